@@ -1,0 +1,110 @@
+/*
+ * librehip: MI355X (gfx950) fused GGUF dequant-matmul behind a C ABI.
+ *
+ * Drop-in for the quantized projection path of platinoff/rusty-engine:
+ *   QMat::matvec  src/qmat.rs:80     -> re_qmat_matvec
+ *   QMat::matmul  src/qmat.rs:169    -> re_qmat_matmul
+ *   QMat::from_bytes / from_model    -> re_qmat_create   (src/qmat.rs:52-59, 312-330)
+ *   quant::dequant src/quant.rs:363  -> re_dequant        (bit-exact, quant types)
+ *   moe expert FFN + combine          -> re_moe_forward    (src/moe.rs:288-300, 360-388)
+ *
+ * Conventions (from the reference):
+ *   - W is m x n row-major; each row is a run of GGUF blocks (kernel.rs:51, 329). GGUF dims
+ *     are [n, m] (qmat.rs:310-311).
+ *   - X is rows x n row-major f32; Y is rows x m row-major f32, Y[row*m + r] (kernel.rs:1508).
+ *   - ggml types: 2 Q4_0, 6 Q5_0, 8 Q8_0, 12 Q4_K, 13 Q5_K, 14 Q6_K (quant.rs:75-88).
+ *   - n must be a multiple of 32. When n is not a multiple of the type's block size (the
+ *     K-quants at n = 896), each row holds ceil(n/256) whole super-blocks and the elements
+ *     past n are ignored.
+ *
+ * Every entry point returns 0 on success or an RE_ERR_* code; re_last_error() gives the
+ * message of the calling thread's last failure. Nothing panics or throws across the ABI.
+ * Host-pointer entry points are synchronous and thread-safe (calls on one matrix serialize).
+ * Device-pointer entry points (*_dev) enqueue on the caller's HIP stream and return at once;
+ * calls on the same matrix object must not overlap in time (they share its split scratch).
+ */
+#ifndef REHIP_H
+#define REHIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RE_OK 0
+#define RE_ERR_TYPE 1      /* unknown / unsupported ggml type (kernel.rs:2006, 2027 panic) */
+#define RE_ERR_SIZE 2      /* byte count or shape mismatch (quant.rs:402-447) */
+#define RE_ERR_ARG 3       /* null pointer or invalid argument */
+#define RE_ERR_HIP 4       /* HIP runtime failure */
+#define RE_ERR_NODEV 5     /* no usable gfx950 device */
+
+#define RE_MODE_BF16 0     /* GEMM: bf16 MFMA, f32 accumulate (|err| <= 1e-2 rel-to-norm) */
+#define RE_MODE_F32 1      /* GEMM: f32 MFMA strict mode (|err| <= 2^-10 sum|w*x|) */
+
+typedef struct re_qmat re_qmat;
+typedef struct re_moe re_moe;
+
+/* Library state. re_init selects the current HIP device; it is called implicitly. */
+int re_init(void);
+const char *re_last_error(void);
+const char *re_version(void);
+
+/* ---- layout (host only; no GPU needed) ------------------------------------------------ */
+/* Bytes of one padded GGUF row: ceil(n/QK) * block_bytes (kernel.rs:1983-1993, padded). */
+int re_row_bytes(uint32_t ggml_type, size_t n, size_t *out);
+/* Size of the GPU-resident tiled layout of an m x n matrix. */
+int re_tiled_bytes(uint32_t ggml_type, size_t m, size_t n, size_t *out);
+/* Repack GGUF rows into the tiled layout on the host (out holds re_tiled_bytes bytes). */
+int re_repack(uint32_t ggml_type, const uint8_t *bytes, size_t nbytes, size_t m, size_t n,
+              uint8_t *out, size_t out_len);
+
+/* ---- QMat (src/qmat.rs:30-42) ---------------------------------------------------------- */
+/* Upload and repack once. nbytes must equal m * re_row_bytes(type, n). */
+int re_qmat_create(uint32_t ggml_type, const uint8_t *bytes, size_t nbytes, size_t m, size_t n,
+                   re_qmat **out);
+void re_qmat_destroy(re_qmat *q);
+size_t re_qmat_rows(const re_qmat *q);   /* m (qmat.rs:62-66) */
+size_t re_qmat_cols(const re_qmat *q);   /* n (qmat.rs:69-73) */
+uint32_t re_qmat_type(const re_qmat *q);
+
+/* y[m] = W x[n] (qmat.rs:80). Host pointers, synchronous. f32 accumulation. */
+int re_qmat_matvec(re_qmat *q, const float *x, float *y);
+/* Y[rows x m] = X[rows x n] W^T (qmat.rs:169). Host pointers, synchronous. rows == 1 runs
+ * the GEMV; otherwise the MFMA GEMM in the given mode. */
+int re_qmat_matmul(re_qmat *q, const float *x, size_t rows, float *y, int mode);
+
+/* Device-pointer variants; `stream` is a hipStream_t (NULL = default stream). */
+int re_qmat_matvec_dev(re_qmat *q, const float *d_x, float *d_y, void *stream);
+int re_qmat_matmul_dev(re_qmat *q, const float *d_x, size_t rows, float *d_y, int mode,
+                       void *stream);
+/* Dequantize the resident weights to d_out[m x n] f32, bit-exact with quant::dequant. */
+int re_qmat_dequant_dev(re_qmat *q, float *d_out, void *stream);
+
+/* Flat-stream dequant on the GPU (quant::dequant, src/quant.rs:363-453) for the six quant
+ * types: out receives nbytes / block_bytes * QK floats. Same length errors as the reference. */
+int re_dequant(uint32_t ggml_type, const uint8_t *bytes, size_t nbytes, float *out, size_t out_len);
+
+/* ---- MoE expert FFN (src/moe.rs:288-300, 360-388) ------------------------------------- */
+/* Experts stored like a GGUF expert tensor: gate/up are n_experts x inter x hidden, down is
+ * n_experts x hidden x inter, each expert's rows as GGUF blocks. */
+int re_moe_create(uint32_t gate_type, const uint8_t *gate, size_t gate_bytes,
+                  uint32_t up_type, const uint8_t *up, size_t up_bytes,
+                  uint32_t down_type, const uint8_t *down, size_t down_bytes,
+                  size_t n_experts, size_t hidden, size_t inter, re_moe **out);
+void re_moe_destroy(re_moe *e);
+/* out[t] = sum_j weights[t*k+j] * down_e(silu(gate_e x_t) * up_e x_t), e = ids[t*k+j], summed
+ * in routing order j = 0..k-1 (moe.rs:376-383). Routing comes from the host router
+ * (moe.rs:75-125). Host pointers, synchronous. */
+int re_moe_forward(re_moe *e, const float *x, size_t tokens, size_t top_k, const uint32_t *ids,
+                   const float *weights, float *out, int mode);
+/* Device x/out; ids and weights stay on the host (they shape the grouped launch). */
+int re_moe_forward_dev(re_moe *e, const float *d_x, size_t tokens, size_t top_k,
+                       const uint32_t *ids, const float *weights, float *d_out, int mode,
+                       void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* REHIP_H */

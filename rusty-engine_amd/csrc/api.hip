@@ -1,0 +1,513 @@
+// C ABI of librehip (include/rehip.h): weight upload and repack, GEMV/GEMM dispatch, the
+// bit-exact dequant and the grouped MoE expert FFN.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <new>
+#include <vector>
+
+#include "../../include/rehip.h"
+#include "common.hpp"
+#include "kernels.hpp"
+
+using namespace rehip;
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof g_err, fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+#define HIP_TRY(expr)                                                                      \
+  do {                                                                                     \
+    hipError_t e_ = (expr);                                                                \
+    if (e_ != hipSuccess) return fail(RE_ERR_HIP, "%s: %s", #expr, hipGetErrorString(e_)); \
+  } while (0)
+
+const char* type_name(uint32_t t) {
+  switch (t) {
+    case T_Q4_0: return "Q4_0";
+    case T_Q5_0: return "Q5_0";
+    case T_Q8_0: return "Q8_0";
+    case T_Q4_K: return "Q4_K";
+    case T_Q5_K: return "Q5_K";
+    case T_Q6_K: return "Q6_K";
+    default: return "?";
+  }
+}
+
+std::once_flag g_init_once;
+int g_init_rc = RE_OK;
+char g_init_msg[512] = "";
+
+int do_init() {
+  std::call_once(g_init_once, [] {
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n == 0) {
+      g_init_rc = RE_ERR_NODEV;
+      snprintf(g_init_msg, sizeof g_init_msg, "no HIP device (%s)", hipGetErrorString(e));
+      return;
+    }
+    hipDeviceProp_t prop;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&prop, dev) != hipSuccess) {
+      g_init_rc = RE_ERR_NODEV;
+      snprintf(g_init_msg, sizeof g_init_msg, "cannot query HIP device");
+      return;
+    }
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+      g_init_rc = RE_ERR_NODEV;
+      snprintf(g_init_msg, sizeof g_init_msg, "device %d is %s, librehip is built for gfx950", dev,
+               prop.gcnArchName);
+    }
+  });
+  if (g_init_rc != RE_OK) return fail(g_init_rc, "%s", g_init_msg);
+  return RE_OK;
+}
+
+// Geometry checks shared by every entry point taking GGUF rows.
+int check_matrix(uint32_t type, size_t nbytes, size_t m, size_t n, MatGeom* g) {
+  const TypeInfo* ti = type_info(type);
+  if (!ti) return fail(RE_ERR_TYPE, "no fused kernel for ggml type %u", type);
+  if (m == 0 || n == 0) return fail(RE_ERR_SIZE, "empty matrix %zu x %zu", m, n);
+  if (n % 32 != 0) return fail(RE_ERR_SIZE, "n = %zu must be a multiple of 32", n);
+  if (m > (1u << 30) || n > (1u << 24)) return fail(RE_ERR_SIZE, "matrix %zu x %zu too large", m, n);
+  make_geom(type, m, n, g);
+  const size_t want = m * g->kb * (size_t)g->bb;
+  if (nbytes != want)
+    return fail(RE_ERR_SIZE, "%s weight %zu x %zu needs %zu bytes, got %zu", type_name(type), m, n, want,
+                nbytes);
+  return RE_OK;
+}
+
+struct Staging {
+  void* p = nullptr;
+  size_t cap = 0;
+  int ensure(size_t bytes) {
+    if (bytes <= cap) return RE_OK;
+    if (p) (void)hipFree(p);
+    p = nullptr;
+    cap = 0;
+    HIP_TRY(hipMalloc(&p, bytes));
+    cap = bytes;
+    return RE_OK;
+  }
+  void release() {
+    if (p) (void)hipFree(p);
+    p = nullptr;
+    cap = 0;
+  }
+};
+
+}  // namespace
+
+struct re_qmat {
+  MatGeom g{};
+  uint8_t* d_w = nullptr;
+  float* d_partial = nullptr;
+  unsigned* d_counters = nullptr;
+  int splits = 1, kb_per_split = 1, waves = 4;
+  std::mutex mu;
+  hipStream_t stream = nullptr;
+  Staging sx, sy;
+};
+
+struct re_moe {
+  size_t n_experts = 0, hidden = 0, inter = 0;
+  MatGeom gg{}, gu{}, gd{};
+  uint8_t *d_gate = nullptr, *d_up = nullptr, *d_down = nullptr;
+  std::mutex mu;
+  hipStream_t stream = nullptr;
+  Staging sx, sout, sg, su, sh, syp, smeta;
+};
+
+namespace {
+
+// GEMV launch shape: enough workgroups to cover the chip (the split count grows until about
+// 1024 workgroups exist or every block column is its own split).
+void plan_gemv(re_qmat* q) {
+  const size_t tiles = q->g.tiles, kb = q->g.kb;
+  size_t want = (1024 + tiles - 1) / tiles;
+  want = std::max<size_t>(1, std::min(want, kb));
+  size_t per = (kb + want - 1) / want;
+  q->kb_per_split = (int)per;
+  q->splits = (int)((kb + per - 1) / per);
+  q->waves = per >= 4 ? 4 : 1;
+}
+
+int upload_tiled(const MatGeom& g, const uint8_t* bytes, uint8_t* d_dst) {
+  std::vector<uint8_t> tiled;
+  try {
+    tiled.resize(g.bytes);
+  } catch (const std::bad_alloc&) {
+    return fail(RE_ERR_ARG, "host out of memory for %zu-byte repack", g.bytes);
+  }
+  repack_host(g, bytes, tiled.data());
+  HIP_TRY(hipMemcpy(d_dst, tiled.data(), g.bytes, hipMemcpyHostToDevice));
+  return RE_OK;
+}
+
+int gemv_enqueue(re_qmat* q, const float* d_x, float* d_y, hipStream_t s) {
+  GemvArgs a{};
+  a.W = q->d_w;
+  a.x = d_x;
+  a.y = d_y;
+  a.partial = q->d_partial;
+  a.counters = q->d_counters;
+  a.m = (int)q->g.m;
+  a.m_pad = (int)(q->g.tiles * kTileRows);
+  a.K = (int)q->g.n;
+  a.KB = (int)q->g.kb;
+  a.tiles = (int)q->g.tiles;
+  a.kb_per_split = q->kb_per_split;
+  a.splits = q->splits;
+  HIP_TRY(launch_gemv(q->g.type, a, q->waves, s));
+  return RE_OK;
+}
+
+int gemm_enqueue(re_qmat* q, const float* d_x, size_t rows, float* d_y, int mode, hipStream_t s) {
+  GemmArgs a{};
+  a.W = q->d_w;
+  a.w_stride = 0;
+  a.X = d_x;
+  a.Y = d_y;
+  a.m = (int)q->g.m;
+  a.K = (int)q->g.n;
+  a.KB = (int)q->g.kb;
+  a.tiles = (int)q->g.tiles;
+  a.N = (int)rows;
+  a.ldy = (int)q->g.m;
+  a.tasks = nullptr;
+  a.xrow = nullptr;
+  HIP_TRY(launch_gemm(q->g.type, mode, a, 0, s));
+  return RE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int re_init(void) { return do_init(); }
+
+const char* re_last_error(void) { return g_err; }
+
+const char* re_version(void) { return "librehip 0.1 (gfx950)"; }
+
+int re_row_bytes(uint32_t ggml_type, size_t n, size_t* out) {
+  const TypeInfo* ti = type_info(ggml_type);
+  if (!ti) return fail(RE_ERR_TYPE, "no fused kernel for ggml type %u", ggml_type);
+  if (!out) return fail(RE_ERR_ARG, "null out");
+  *out = (n + ti->qk - 1) / ti->qk * ti->bb;
+  return RE_OK;
+}
+
+int re_tiled_bytes(uint32_t ggml_type, size_t m, size_t n, size_t* out) {
+  MatGeom g;
+  if (!type_info(ggml_type)) return fail(RE_ERR_TYPE, "no fused kernel for ggml type %u", ggml_type);
+  if (!out || !make_geom(ggml_type, m, n, &g)) return fail(RE_ERR_ARG, "bad shape or null out");
+  *out = g.bytes;
+  return RE_OK;
+}
+
+int re_repack(uint32_t ggml_type, const uint8_t* bytes, size_t nbytes, size_t m, size_t n, uint8_t* out,
+              size_t out_len) {
+  MatGeom g;
+  int rc = check_matrix(ggml_type, nbytes, m, n, &g);
+  if (rc) return rc;
+  if (!bytes || !out) return fail(RE_ERR_ARG, "null pointer");
+  if (out_len != g.bytes) return fail(RE_ERR_SIZE, "tiled layout needs %zu bytes, got %zu", g.bytes, out_len);
+  repack_host(g, bytes, out);
+  return RE_OK;
+}
+
+int re_qmat_create(uint32_t ggml_type, const uint8_t* bytes, size_t nbytes, size_t m, size_t n,
+                   re_qmat** out) {
+  if (!out || !bytes) return fail(RE_ERR_ARG, "null pointer");
+  *out = nullptr;
+  MatGeom g;
+  int rc = check_matrix(ggml_type, nbytes, m, n, &g);
+  if (rc) return rc;
+  if ((rc = do_init())) return rc;
+  re_qmat* q = new (std::nothrow) re_qmat();
+  if (!q) return fail(RE_ERR_ARG, "out of memory");
+  q->g = g;
+  plan_gemv(q);
+  auto cleanup = [&](int code) {
+    re_qmat_destroy(q);
+    return code;
+  };
+  if (hipMalloc(&q->d_w, g.bytes) != hipSuccess) return cleanup(fail(RE_ERR_HIP, "hipMalloc(%zu) failed", g.bytes));
+  if ((rc = upload_tiled(g, bytes, q->d_w))) return cleanup(rc);
+  const size_t m_pad = g.tiles * kTileRows;
+  if (q->splits > 1) {
+    if (hipMalloc(&q->d_partial, (size_t)q->splits * m_pad * sizeof(float)) != hipSuccess ||
+        hipMalloc(&q->d_counters, g.tiles * sizeof(unsigned)) != hipSuccess)
+      return cleanup(fail(RE_ERR_HIP, "hipMalloc of split scratch failed"));
+    if (hipMemset(q->d_counters, 0, g.tiles * sizeof(unsigned)) != hipSuccess)
+      return cleanup(fail(RE_ERR_HIP, "hipMemset of split counters failed"));
+  }
+  if (hipStreamCreateWithFlags(&q->stream, hipStreamNonBlocking) != hipSuccess)
+    return cleanup(fail(RE_ERR_HIP, "hipStreamCreate failed"));
+  *out = q;
+  return RE_OK;
+}
+
+void re_qmat_destroy(re_qmat* q) {
+  if (!q) return;
+  if (q->stream) (void)hipStreamSynchronize(q->stream);
+  if (q->d_w) (void)hipFree(q->d_w);
+  if (q->d_partial) (void)hipFree(q->d_partial);
+  if (q->d_counters) (void)hipFree(q->d_counters);
+  q->sx.release();
+  q->sy.release();
+  if (q->stream) (void)hipStreamDestroy(q->stream);
+  delete q;
+}
+
+size_t re_qmat_rows(const re_qmat* q) { return q ? q->g.m : 0; }
+size_t re_qmat_cols(const re_qmat* q) { return q ? q->g.n : 0; }
+uint32_t re_qmat_type(const re_qmat* q) { return q ? q->g.type : 0; }
+
+int re_qmat_matvec_dev(re_qmat* q, const float* d_x, float* d_y, void* stream) {
+  if (!q || !d_x || !d_y) return fail(RE_ERR_ARG, "null pointer");
+  return gemv_enqueue(q, d_x, d_y, (hipStream_t)stream);
+}
+
+int re_qmat_matmul_dev(re_qmat* q, const float* d_x, size_t rows, float* d_y, int mode, void* stream) {
+  if (!q || (rows && (!d_x || !d_y))) return fail(RE_ERR_ARG, "null pointer");
+  if (mode != RE_MODE_BF16 && mode != RE_MODE_F32) return fail(RE_ERR_ARG, "unknown mode %d", mode);
+  if (rows == 0) return RE_OK;
+  if (rows > (1u << 24)) return fail(RE_ERR_SIZE, "rows = %zu too large", rows);
+  if (rows == 1) return gemv_enqueue(q, d_x, d_y, (hipStream_t)stream);
+  return gemm_enqueue(q, d_x, rows, d_y, mode, (hipStream_t)stream);
+}
+
+int re_qmat_matvec(re_qmat* q, const float* x, float* y) {
+  if (!q || !x || !y) return fail(RE_ERR_ARG, "null pointer");
+  return re_qmat_matmul(q, x, 1, y, RE_MODE_F32);
+}
+
+int re_qmat_matmul(re_qmat* q, const float* x, size_t rows, float* y, int mode) {
+  if (!q || (rows && (!x || !y))) return fail(RE_ERR_ARG, "null pointer");
+  if (mode != RE_MODE_BF16 && mode != RE_MODE_F32) return fail(RE_ERR_ARG, "unknown mode %d", mode);
+  if (rows == 0) return RE_OK;
+  std::lock_guard<std::mutex> lk(q->mu);
+  const size_t xb = rows * q->g.n * sizeof(float), yb = rows * q->g.m * sizeof(float);
+  int rc;
+  if ((rc = q->sx.ensure(xb)) || (rc = q->sy.ensure(yb))) return rc;
+  HIP_TRY(hipMemcpyAsync(q->sx.p, x, xb, hipMemcpyHostToDevice, q->stream));
+  if ((rc = re_qmat_matmul_dev(q, (const float*)q->sx.p, rows, (float*)q->sy.p, mode, q->stream))) return rc;
+  HIP_TRY(hipMemcpyAsync(y, q->sy.p, yb, hipMemcpyDeviceToHost, q->stream));
+  HIP_TRY(hipStreamSynchronize(q->stream));
+  return RE_OK;
+}
+
+int re_qmat_dequant_dev(re_qmat* q, float* d_out, void* stream) {
+  if (!q || !d_out) return fail(RE_ERR_ARG, "null pointer");
+  HIP_TRY(launch_dequant(q->g.type, q->d_w, d_out, (int)q->g.m, (int)q->g.n, (int)q->g.kb, (int)q->g.tiles,
+                         (hipStream_t)stream));
+  return RE_OK;
+}
+
+int re_dequant(uint32_t ggml_type, const uint8_t* bytes, size_t nbytes, float* out, size_t out_len) {
+  const TypeInfo* ti = type_info(ggml_type);
+  if (!ti) return fail(RE_ERR_TYPE, "no scalar dequant for ggml type %u", ggml_type);
+  if (nbytes % ti->bb)
+    return fail(RE_ERR_SIZE, "%s data len %zu not a multiple of %d", type_name(ggml_type), nbytes, ti->bb);
+  const size_t blocks = nbytes / ti->bb;
+  if (out_len != blocks * ti->qk) return fail(RE_ERR_SIZE, "out needs %zu floats, got %zu", blocks * ti->qk, out_len);
+  if (blocks == 0) return RE_OK;
+  if (!bytes || !out) return fail(RE_ERR_ARG, "null pointer");
+  // a flat stream is a (blocks x QK) matrix with one block per row
+  re_qmat* q = nullptr;
+  int rc = re_qmat_create(ggml_type, bytes, nbytes, blocks, ti->qk, &q);
+  if (rc) return rc;
+  float* d_out = nullptr;
+  if (hipMalloc(&d_out, blocks * ti->qk * sizeof(float)) != hipSuccess) {
+    re_qmat_destroy(q);
+    return fail(RE_ERR_HIP, "hipMalloc failed");
+  }
+  rc = re_qmat_dequant_dev(q, d_out, q->stream);
+  if (!rc && hipMemcpyAsync(out, d_out, blocks * ti->qk * sizeof(float), hipMemcpyDeviceToHost, q->stream) != hipSuccess)
+    rc = fail(RE_ERR_HIP, "copy back failed");
+  if (!rc && hipStreamSynchronize(q->stream) != hipSuccess) rc = fail(RE_ERR_HIP, "sync failed");
+  (void)hipFree(d_out);
+  re_qmat_destroy(q);
+  return rc;
+}
+
+// ---- MoE ---------------------------------------------------------------------------------
+int re_moe_create(uint32_t gate_type, const uint8_t* gate, size_t gate_bytes, uint32_t up_type, const uint8_t* up,
+                  size_t up_bytes, uint32_t down_type, const uint8_t* down, size_t down_bytes, size_t n_experts,
+                  size_t hidden, size_t inter, re_moe** out) {
+  if (!out || !gate || !up || !down) return fail(RE_ERR_ARG, "null pointer");
+  *out = nullptr;
+  if (n_experts == 0 || n_experts > 65536) return fail(RE_ERR_SIZE, "n_experts = %zu", n_experts);
+  MatGeom gg, gu, gd;
+  int rc;
+  if (gate_bytes % n_experts || up_bytes % n_experts || down_bytes % n_experts)
+    return fail(RE_ERR_SIZE, "expert tensors must hold n_experts equal slices");
+  if ((rc = check_matrix(gate_type, gate_bytes / n_experts, inter, hidden, &gg))) return rc;
+  if ((rc = check_matrix(up_type, up_bytes / n_experts, inter, hidden, &gu))) return rc;
+  if ((rc = check_matrix(down_type, down_bytes / n_experts, hidden, inter, &gd))) return rc;
+  if ((rc = do_init())) return rc;
+  re_moe* e = new (std::nothrow) re_moe();
+  if (!e) return fail(RE_ERR_ARG, "out of memory");
+  e->n_experts = n_experts;
+  e->hidden = hidden;
+  e->inter = inter;
+  e->gg = gg;
+  e->gu = gu;
+  e->gd = gd;
+  auto cleanup = [&](int code) {
+    re_moe_destroy(e);
+    return code;
+  };
+  struct P { const MatGeom* g; const uint8_t* src; size_t slice; uint8_t** dst; };
+  P parts[3] = {{&gg, gate, gate_bytes / n_experts, &e->d_gate}, {&gu, up, up_bytes / n_experts, &e->d_up},
+                {&gd, down, down_bytes / n_experts, &e->d_down}};
+  for (auto& pt : parts) {
+    if (hipMalloc(pt.dst, pt.g->bytes * n_experts) != hipSuccess)
+      return cleanup(fail(RE_ERR_HIP, "hipMalloc(%zu) failed", pt.g->bytes * n_experts));
+    for (size_t x = 0; x < n_experts; ++x)
+      if ((rc = upload_tiled(*pt.g, pt.src + x * pt.slice, *pt.dst + x * pt.g->bytes))) return cleanup(rc);
+  }
+  if (hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking) != hipSuccess)
+    return cleanup(fail(RE_ERR_HIP, "hipStreamCreate failed"));
+  *out = e;
+  return RE_OK;
+}
+
+void re_moe_destroy(re_moe* e) {
+  if (!e) return;
+  if (e->stream) (void)hipStreamSynchronize(e->stream);
+  if (e->d_gate) (void)hipFree(e->d_gate);
+  if (e->d_up) (void)hipFree(e->d_up);
+  if (e->d_down) (void)hipFree(e->d_down);
+  for (Staging* s : {&e->sx, &e->sout, &e->sg, &e->su, &e->sh, &e->syp, &e->smeta}) s->release();
+  if (e->stream) (void)hipStreamDestroy(e->stream);
+  delete e;
+}
+
+int re_moe_forward_dev(re_moe* e, const float* d_x, size_t tokens, size_t top_k, const uint32_t* ids,
+                       const float* weights, float* d_out, int mode, void* stream) {
+  if (!e) return fail(RE_ERR_ARG, "null moe");
+  if (mode != RE_MODE_BF16 && mode != RE_MODE_F32) return fail(RE_ERR_ARG, "unknown mode %d", mode);
+  if (tokens == 0) return RE_OK;
+  if (!d_x || !d_out || !ids || !weights || top_k == 0) return fail(RE_ERR_ARG, "null pointer or top_k = 0");
+  const size_t pairs = tokens * top_k;
+  if (pairs > (1u << 24)) return fail(RE_ERR_SIZE, "too many (token, expert) pairs");
+  for (size_t p = 0; p < pairs; ++p)
+    if (ids[p] >= e->n_experts) return fail(RE_ERR_ARG, "expert id %u out of range (%zu experts)", ids[p], e->n_experts);
+  hipStream_t s = (hipStream_t)stream;
+
+  // group the pairs by expert, keeping (token, slot) order inside an expert
+  std::vector<int> count(e->n_experts + 1, 0), start(e->n_experts + 1, 0);
+  for (size_t p = 0; p < pairs; ++p) count[ids[p]]++;
+  for (size_t x = 0; x < e->n_experts; ++x) start[x + 1] = start[x] + count[x];
+  std::vector<int> fill(start.begin(), start.end() - 1);
+  std::vector<int> xrow(pairs), pos(pairs);
+  for (size_t p = 0; p < pairs; ++p) {
+    const int at = fill[ids[p]]++;
+    xrow[at] = (int)(p / top_k);
+    pos[p] = at;
+  }
+  std::vector<GemmTask> t_gu, t_d;
+  const int mt_gu = (int)((e->inter + kGemmBM - 1) / kGemmBM), mt_d = (int)((e->hidden + kGemmBM - 1) / kGemmBM);
+  for (size_t x = 0; x < e->n_experts; ++x) {
+    for (int r = 0; r < count[x]; r += kGemmBN) {
+      const int rn = std::min(kGemmBN, count[x] - r);
+      for (int mt = 0; mt < mt_gu; ++mt) t_gu.push_back({(int)x, mt, start[x] + r, rn});
+      for (int mt = 0; mt < mt_d; ++mt) t_d.push_back({(int)x, mt, start[x] + r, rn});
+    }
+  }
+  // metadata block: xrow | pos | weights | tasks_gu | tasks_d
+  const size_t off_pos = pairs * sizeof(int), off_w = 2 * pairs * sizeof(int);
+  const size_t off_tgu = (off_w + pairs * sizeof(float) + 15) / 16 * 16;
+  const size_t off_td = off_tgu + t_gu.size() * sizeof(GemmTask);
+  const size_t meta_bytes = off_td + t_d.size() * sizeof(GemmTask);
+  std::vector<uint8_t> meta(meta_bytes);
+  std::memcpy(meta.data(), xrow.data(), pairs * sizeof(int));
+  std::memcpy(meta.data() + off_pos, pos.data(), pairs * sizeof(int));
+  std::memcpy(meta.data() + off_w, weights, pairs * sizeof(float));
+  std::memcpy(meta.data() + off_tgu, t_gu.data(), t_gu.size() * sizeof(GemmTask));
+  std::memcpy(meta.data() + off_td, t_d.data(), t_d.size() * sizeof(GemmTask));
+
+  int rc;
+  const size_t act = pairs * e->inter * sizeof(float);
+  if ((rc = e->smeta.ensure(meta_bytes)) || (rc = e->sg.ensure(act)) || (rc = e->su.ensure(act)) ||
+      (rc = e->sh.ensure(act)) || (rc = e->syp.ensure(pairs * e->hidden * sizeof(float))))
+    return rc;
+  uint8_t* dm = (uint8_t*)e->smeta.p;
+  // the metadata is uploaded with a synchronous copy so the host vectors may go out of scope
+  HIP_TRY(hipStreamSynchronize(s));
+  HIP_TRY(hipMemcpy(dm, meta.data(), meta_bytes, hipMemcpyHostToDevice));
+
+  GemmArgs a{};
+  a.X = d_x;
+  a.tasks = (const GemmTask*)(dm + off_tgu);
+  a.xrow = (const int*)dm;
+  a.m = (int)e->inter;
+  a.K = (int)e->hidden;
+  a.KB = (int)e->gg.kb;
+  a.tiles = (int)e->gg.tiles;
+  a.ldy = (int)e->inter;
+  a.W = e->d_gate;
+  a.w_stride = e->gg.bytes;
+  a.Y = (float*)e->sg.p;
+  HIP_TRY(launch_gemm(e->gg.type, mode, a, (int)t_gu.size(), s));
+  a.W = e->d_up;
+  a.w_stride = e->gu.bytes;
+  a.KB = (int)e->gu.kb;
+  a.tiles = (int)e->gu.tiles;
+  a.Y = (float*)e->su.p;
+  HIP_TRY(launch_gemm(e->gu.type, mode, a, (int)t_gu.size(), s));
+  HIP_TRY(launch_swiglu((const float*)e->sg.p, (const float*)e->su.p, (float*)e->sh.p, pairs * e->inter, s));
+  GemmArgs d{};
+  d.W = e->d_down;
+  d.w_stride = e->gd.bytes;
+  d.X = (const float*)e->sh.p;
+  d.Y = (float*)e->syp.p;
+  d.m = (int)e->hidden;
+  d.K = (int)e->inter;
+  d.KB = (int)e->gd.kb;
+  d.tiles = (int)e->gd.tiles;
+  d.ldy = (int)e->hidden;
+  d.tasks = (const GemmTask*)(dm + off_td);
+  d.xrow = nullptr;
+  HIP_TRY(launch_gemm(e->gd.type, mode, d, (int)t_d.size(), s));
+  HIP_TRY(launch_combine((const float*)e->syp.p, (const int*)(dm + off_pos), (const float*)(dm + off_w), d_out,
+                         (int)tokens, (int)top_k, (int)e->hidden, s));
+  return RE_OK;
+}
+
+int re_moe_forward(re_moe* e, const float* x, size_t tokens, size_t top_k, const uint32_t* ids,
+                   const float* weights, float* out, int mode) {
+  if (!e) return fail(RE_ERR_ARG, "null moe");
+  if (tokens == 0) return RE_OK;
+  if (!x || !out) return fail(RE_ERR_ARG, "null pointer");
+  std::lock_guard<std::mutex> lk(e->mu);
+  int rc;
+  const size_t xb = tokens * e->hidden * sizeof(float);
+  if ((rc = e->sx.ensure(xb)) || (rc = e->sout.ensure(xb))) return rc;
+  HIP_TRY(hipMemcpyAsync(e->sx.p, x, xb, hipMemcpyHostToDevice, e->stream));
+  if ((rc = re_moe_forward_dev(e, (const float*)e->sx.p, tokens, top_k, ids, weights, (float*)e->sout.p, mode,
+                               e->stream)))
+    return rc;
+  HIP_TRY(hipMemcpyAsync(out, e->sout.p, xb, hipMemcpyDeviceToHost, e->stream));
+  HIP_TRY(hipStreamSynchronize(e->stream));
+  return RE_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,311 @@
+// Device-side block decoding for the tiled-slab layout (common.hpp).
+//
+// Every block is read as "chunks" of 32 quants. A chunk is two runs of 16 elements, run A at
+// element offset eA and run B at eB inside the block; each run has an affine map
+//     value = scale * q - offset,   q an unsigned integer quant (0..255)
+// which reproduces the reference dequantizers (src/quant.rs:106-357) exactly: every product
+// involved is exact in f32 and the subtraction rounds once, where the reference rounds.
+//   Q4_0  d*(q-8)        -> scale d,       offset 8d          (1 chunk, runs 0/16)
+//   Q5_0  d*(q-16)       -> scale d,       offset 16d         (1 chunk, runs 0/16)
+//   Q8_0  d*qs (signed)  -> q = qs+128,    offset 128d        (1 chunk, runs 0/16)
+//   Q4_K  d*sc*q - dmin*m                                     (8 chunks)
+//   Q5_K  same with the 5th bit                               (8 chunks)
+//   Q6_K  d*sc*(q-32)    -> scale d*sc,    offset 32*d*sc     (8 chunks)
+// The affine form lets a dot product factor the scale out of the 16-element sum:
+//   sum(v_i x_i) = scale * sum(q_i x_i) - offset * sum(x_i).
+// Quants are delivered four per dword (one byte each) so they convert with v_cvt_f32_ubyte.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <cstdint>
+
+#include "common.hpp"
+
+namespace rehip {
+
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
+  // src/quant.rs:25-45 (exact widening incl. subnormals; NaN payload kept)
+  const uint32_t sign = (h & 0x8000u) << 16;
+  const uint32_t exp = (h >> 10) & 0x1Fu;
+  const uint32_t frac = h & 0x3FFu;
+  uint32_t bits;
+  if (exp == 0x1F) {
+    bits = sign | 0x7F800000u | (frac << 13);
+  } else if (exp != 0) {
+    bits = sign | ((exp + 112u) << 23) | (frac << 13);
+  } else if (frac == 0) {
+    bits = sign;
+  } else {
+    // subnormal: frac * 2^-24, normalised (leading one at bit 10)
+    const int lz = __builtin_clz(frac) - 21;   // shifts to bring bit 10 to the top
+    bits = sign | ((uint32_t)(113 - lz) << 23) | (((frac << lz) & 0x3FFu) << 13);
+  }
+  return __uint_as_float(bits);
+}
+
+template <int T> struct Blk;
+
+struct Run {
+  uint32_t q[4];    // 16 quants, one per byte, element order
+  float scale, offset;
+  int e;            // element offset of the run inside the block
+};
+
+// Quant bias of the types whose reference formula multiplies a signed quant, (q - bias) * d
+// (Q4_0 8, Q5_0 16, Q8_0 128, Q6_K 32); 0 for Q4_K/Q5_K (d*sc*q - dmin*m).
+template <int T> inline constexpr int kBias = 0;
+template <> inline constexpr int kBias<T_Q4_0> = 8;
+template <> inline constexpr int kBias<T_Q5_0> = 16;
+template <> inline constexpr int kBias<T_Q8_0> = 128;
+template <> inline constexpr int kBias<T_Q6_K> = 32;
+
+// Plane slab offsets: plane p of a 64-row slab starts at 64 * (sum of widths before p).
+//
+// Each Blk<T> offers two ways in:
+//   chunk(slab, lane, c, a, b)   loads only the planes chunk c needs, then decodes it
+//                                (GEMM staging and the dequant kernel, c may be a runtime value);
+//   load(slab, lane, r) + decode(r, c, a, b)
+//                                loads every plane of the block into registers first, then
+//                                decodes chunk after chunk (GEMV; c is a compile-time constant
+//                                after unrolling, so r.p[...] stays in registers).
+
+__device__ __forceinline__ uint4 ld16(const uint8_t* p) { return *reinterpret_cast<const uint4*>(p); }
+__device__ __forceinline__ uint32_t ld4(const uint8_t* p) { return *reinterpret_cast<const uint32_t*>(p); }
+__device__ __forceinline__ uint32_t ld2(const uint8_t* p) { return *reinterpret_cast<const uint16_t*>(p); }
+
+// nibble split of 16 quant bytes: low nibbles -> run a, high nibbles -> run b
+__device__ __forceinline__ void split_nibbles(const uint4& qs, Run& a, Run& b) {
+  const uint32_t w[4] = {qs.x, qs.y, qs.z, qs.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) { a.q[i] = w[i] & 0x0F0F0F0Fu; b.q[i] = (w[i] >> 4) & 0x0F0F0F0Fu; }
+}
+
+template <> struct Blk<T_Q4_0> {
+  static constexpr int QK = 32, BB = 18, NCH = 1, NP = 1;
+  static constexpr int SLAB = 64 * BB;
+  struct R { uint4 p[NP]; uint32_t t0, t1; };
+  __device__ static void load(const uint8_t* slab, int lane, R& r) {
+    r.p[0] = ld16(slab + lane * 16);
+    r.t0 = ld2(slab + 1024 + lane * 2);
+    r.t1 = 0;
+  }
+  __device__ static void decode(const R& r, int c, Run& a, Run& b) {
+    (void)c;
+    split_nibbles(r.p[0], a, b);
+    const float d = f16_bits_to_f32(r.t0);
+    a.scale = b.scale = d;
+    a.offset = b.offset = 8.0f * d;
+    a.e = 0; b.e = 16;
+  }
+  __device__ static void chunk(const uint8_t* slab, int lane, int c, Run& a, Run& b) {
+    R r; load(slab, lane, r); decode(r, c, a, b);
+  }
+};
+
+// spread bits 0..3 of v to bit 4 of bytes 0..3
+__device__ __forceinline__ uint32_t bits4_to_byte_bit4(uint32_t v) {
+  return ((v & 0xFu) * 0x00204081u & 0x01010101u) << 4;
+}
+
+template <> struct Blk<T_Q5_0> {
+  static constexpr int QK = 32, BB = 22, NCH = 1, NP = 1;
+  static constexpr int SLAB = 64 * BB;
+  struct R { uint4 p[NP]; uint32_t t0, t1; };
+  __device__ static void load(const uint8_t* slab, int lane, R& r) {
+    r.p[0] = ld16(slab + lane * 16);
+    r.t0 = ld4(slab + 1024 + lane * 4);      // qh
+    r.t1 = ld2(slab + 1280 + lane * 2);      // d
+  }
+  __device__ static void decode(const R& r, int c, Run& a, Run& b) {
+    (void)c;
+    const uint32_t w[4] = {r.p[0].x, r.p[0].y, r.p[0].z, r.p[0].w};
+    const uint32_t qh = r.t0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      a.q[i] = (w[i] & 0x0F0F0F0Fu) | bits4_to_byte_bit4(qh >> (4 * i));
+      b.q[i] = ((w[i] >> 4) & 0x0F0F0F0Fu) | bits4_to_byte_bit4(qh >> (16 + 4 * i));
+    }
+    const float d = f16_bits_to_f32(r.t1);
+    a.scale = b.scale = d;
+    a.offset = b.offset = 16.0f * d;
+    a.e = 0; b.e = 16;
+  }
+  __device__ static void chunk(const uint8_t* slab, int lane, int c, Run& a, Run& b) {
+    R r; load(slab, lane, r); decode(r, c, a, b);
+  }
+};
+
+template <> struct Blk<T_Q8_0> {
+  static constexpr int QK = 32, BB = 34, NCH = 1, NP = 2;
+  static constexpr int SLAB = 64 * BB;
+  struct R { uint4 p[NP]; uint32_t t0, t1; };
+  __device__ static void load(const uint8_t* slab, int lane, R& r) {
+    r.p[0] = ld16(slab + lane * 16);
+    r.p[1] = ld16(slab + 1024 + lane * 16);
+    r.t0 = ld2(slab + 2048 + lane * 2);
+    r.t1 = 0;
+  }
+  __device__ static void decode(const R& r, int c, Run& a, Run& b) {
+    (void)c;
+    a.q[0] = r.p[0].x ^ 0x80808080u; a.q[1] = r.p[0].y ^ 0x80808080u;
+    a.q[2] = r.p[0].z ^ 0x80808080u; a.q[3] = r.p[0].w ^ 0x80808080u;
+    b.q[0] = r.p[1].x ^ 0x80808080u; b.q[1] = r.p[1].y ^ 0x80808080u;
+    b.q[2] = r.p[1].z ^ 0x80808080u; b.q[3] = r.p[1].w ^ 0x80808080u;
+    const float d = f16_bits_to_f32(r.t0);
+    a.scale = b.scale = d;
+    a.offset = b.offset = 128.0f * d;
+    a.e = 0; b.e = 16;
+  }
+  __device__ static void chunk(const uint8_t* slab, int lane, int c, Run& a, Run& b) {
+    R r; load(slab, lane, r); decode(r, c, a, b);
+  }
+};
+
+// src/quant.rs:250-258 on the 12 scale bytes held in three dwords s0 (bytes 0-3), s1 (4-7),
+// s2 (8-11) of the head plane.
+__device__ __forceinline__ void scale_min_k4(int j, uint32_t s0, uint32_t s1, uint32_t s2,
+                                             uint32_t& sc, uint32_t& m) {
+  if (j < 4) {
+    sc = (s0 >> (8 * j)) & 63u;
+    m = (s1 >> (8 * j)) & 63u;
+  } else {
+    const int k = j - 4;
+    const uint32_t hi = (s2 >> (8 * k)) & 0xFFu;
+    sc = (hi & 0xFu) | (((s0 >> (8 * k + 6)) & 3u) << 4);
+    m = (hi >> 4) | (((s1 >> (8 * k + 6)) & 3u) << 4);
+  }
+}
+
+// Q4_K/Q5_K head plane: d, dmin and the packed (scale, min) of sub-blocks 2g, 2g+1
+__device__ __forceinline__ void k4_scales(const uint4& head, int g, Run& a, Run& b) {
+  const float d = f16_bits_to_f32(head.x & 0xFFFFu);
+  const float dmin = f16_bits_to_f32(head.x >> 16);
+  uint32_t sc0, m0, sc1, m1;
+  scale_min_k4(2 * g, head.y, head.z, head.w, sc0, m0);
+  scale_min_k4(2 * g + 1, head.y, head.z, head.w, sc1, m1);
+  a.scale = d * (float)sc0; a.offset = dmin * (float)m0;
+  b.scale = d * (float)sc1; b.offset = dmin * (float)m1;
+}
+
+template <> struct Blk<T_Q4_K> {
+  static constexpr int QK = 256, BB = 144, NCH = 8, NP = 9;
+  static constexpr int SLAB = 64 * BB;
+  struct R { uint4 p[NP]; uint32_t t0, t1; };
+  // chunk c = 2g + h: qs bytes 32g + 16h .. +16 (plane 1 + c); low nibbles -> elements
+  // 64g + 16h + i (sub-block 2g), high nibbles -> 64g + 32 + 16h + i (sub-block 2g + 1)
+  __device__ static void dec(const uint4& head, const uint4& qs, int c, Run& a, Run& b) {
+    const int g = c >> 1, h = c & 1;
+    split_nibbles(qs, a, b);
+    k4_scales(head, g, a, b);
+    a.e = 64 * g + 16 * h; b.e = a.e + 32;
+  }
+  __device__ static void load(const uint8_t* slab, int lane, R& r) {
+#pragma unroll
+    for (int p = 0; p < NP; ++p) r.p[p] = ld16(slab + 1024 * p + lane * 16);
+    r.t0 = r.t1 = 0;
+  }
+  __device__ static void decode(const R& r, int c, Run& a, Run& b) { dec(r.p[0], r.p[1 + c], c, a, b); }
+  __device__ static void chunk(const uint8_t* slab, int lane, int c, Run& a, Run& b) {
+    dec(ld16(slab + lane * 16), ld16(slab + 1024 * (1 + c) + lane * 16), c, a, b);
+  }
+};
+
+template <> struct Blk<T_Q5_K> {
+  static constexpr int QK = 256, BB = 176, NCH = 8, NP = 11;
+  static constexpr int SLAB = 64 * BB;
+  struct R { uint4 p[NP]; uint32_t t0, t1; };
+  // planes: head(0) qh(1,2) qs(3..10); chunk c = 2g + h as Q4_K plus the 5th bit, which for
+  // element l of group g (l = 16h + i) is bit 2g (low run) / 2g+1 (high run) of qh[l]
+  __device__ static void dec(const uint4& head, const uint4& qh, const uint4& qs, int c, Run& a, Run& b) {
+    const int g = c >> 1, h = c & 1;
+    const uint32_t w[4] = {qs.x, qs.y, qs.z, qs.w};
+    const uint32_t hw[4] = {qh.x, qh.y, qh.z, qh.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      a.q[i] = (w[i] & 0x0F0F0F0Fu) | (((hw[i] >> (2 * g)) & 0x01010101u) << 4);
+      b.q[i] = ((w[i] >> 4) & 0x0F0F0F0Fu) | (((hw[i] >> (2 * g + 1)) & 0x01010101u) << 4);
+    }
+    k4_scales(head, g, a, b);
+    a.e = 64 * g + 16 * h; b.e = a.e + 32;
+  }
+  __device__ static void load(const uint8_t* slab, int lane, R& r) {
+#pragma unroll
+    for (int p = 0; p < NP; ++p) r.p[p] = ld16(slab + 1024 * p + lane * 16);
+    r.t0 = r.t1 = 0;
+  }
+  __device__ static void decode(const R& r, int c, Run& a, Run& b) {
+    dec(r.p[0], r.p[1 + (c & 1)], r.p[3 + c], c, a, b);
+  }
+  __device__ static void chunk(const uint8_t* slab, int lane, int c, Run& a, Run& b) {
+    dec(ld16(slab + lane * 16), ld16(slab + 1024 * (1 + (c & 1)) + lane * 16),
+        ld16(slab + 1024 * (3 + c) + lane * 16), c, a, b);
+  }
+};
+
+template <> struct Blk<T_Q6_K> {
+  static constexpr int QK = 256, BB = 210, NCH = 8, NP = 13;
+  static constexpr int SLAB = 64 * BB;
+  struct R { uint4 p[NP]; uint32_t t0, t1; };
+  // planes: ql(0..7) qh(8..11) sc(12) d(13, 2 bytes). Chunk c = ql plane c: half hh = c/4,
+  // byte l = 16(c%2) + i of the half's ql[32*ih + l] with ih = (c%4)/2. Low nibble -> element
+  // 128hh + 32ih + l (qh bits 2ih, scale 8hh + l/16 + 2ih); high nibble -> element + 64
+  // (qh bits 2ih + 4, scale index + 4). qh byte = qh[32hh + l] = plane 8 + 2hh + c%2.
+  __device__ static void dec(const uint4& ql, const uint4& qh, const uint4& sc, uint32_t dbits, int c,
+                             Run& a, Run& b) {
+    const int hh = c >> 2, ih = (c >> 1) & 1, lo = c & 1;
+    const float d = f16_bits_to_f32(dbits);
+    const int ia = 8 * hh + lo + 2 * ih, ib = ia + 4;
+    const uint32_t scw[4] = {sc.x, sc.y, sc.z, sc.w};
+    const float sca = (float)(int8_t)(scw[ia >> 2] >> (8 * (ia & 3)));
+    const float scb = (float)(int8_t)(scw[ib >> 2] >> (8 * (ib & 3)));
+    const uint32_t w[4] = {ql.x, ql.y, ql.z, ql.w};
+    const uint32_t hw[4] = {qh.x, qh.y, qh.z, qh.w};
+    const int sha = 2 * ih, shb = 2 * ih + 4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      a.q[i] = (w[i] & 0x0F0F0F0Fu) | (((hw[i] >> sha) & 0x03030303u) << 4);
+      b.q[i] = ((w[i] >> 4) & 0x0F0F0F0Fu) | (((hw[i] >> shb) & 0x03030303u) << 4);
+    }
+    a.scale = d * sca; a.offset = 32.0f * a.scale;
+    b.scale = d * scb; b.offset = 32.0f * b.scale;
+    a.e = 128 * hh + 32 * ih + 16 * lo; b.e = a.e + 64;
+  }
+  __device__ static void load(const uint8_t* slab, int lane, R& r) {
+#pragma unroll
+    for (int p = 0; p < NP; ++p) r.p[p] = ld16(slab + 1024 * p + lane * 16);
+    r.t0 = ld2(slab + 1024 * 13 + lane * 2);
+    r.t1 = 0;
+  }
+  __device__ static void decode(const R& r, int c, Run& a, Run& b) {
+    dec(r.p[c], r.p[8 + 2 * (c >> 2) + (c & 1)], r.p[12], r.t0, c, a, b);
+  }
+  __device__ static void chunk(const uint8_t* slab, int lane, int c, Run& a, Run& b) {
+    dec(ld16(slab + 1024 * c + lane * 16), ld16(slab + 1024 * (8 + 2 * (c >> 2) + (c & 1)) + lane * 16),
+        ld16(slab + 1024 * 12 + lane * 16), ld2(slab + 1024 * 13 + lane * 2), c, a, b);
+  }
+};
+
+__device__ __forceinline__ float qbyte(const uint32_t* q, int i) {
+  return (float)((q[i >> 2] >> (8 * (i & 3))) & 0xFFu);
+}
+
+// Value of element i of a run as scale*q - offset: exact for every type, signed zeros aside
+// (used where values are summed).
+__device__ __forceinline__ float run_value(const Run& r, int i) {
+  return __builtin_fmaf(r.scale, qbyte(r.q, i), -r.offset);
+}
+
+// Value of element i with the reference's own operation order, bit for bit including the sign
+// of zero: scale * (q - bias) for the biased types (quant.rs:113, 138, 153, 348-351), and
+// (d*sc)*q - dmin*m for Q4_K/Q5_K (quant.rs:280-284, 314-318).
+template <int T>
+__device__ __forceinline__ float run_value_exact(const Run& r, int i) {
+  const uint32_t q = (r.q[i >> 2] >> (8 * (i & 3))) & 0xFFu;
+  if constexpr (kBias<T> != 0) {
+    return r.scale * (float)((int)q - kBias<T>);
+  } else {
+    return __builtin_fmaf(r.scale, (float)q, -r.offset);
+  }
+}
+
+}  // namespace rehip

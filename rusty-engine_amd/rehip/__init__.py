@@ -1,0 +1,250 @@
+"""Python mirror of rusty-engine's quantized-matrix interface over librehip's C ABI.
+
+`QMat` follows src/qmat.rs: `QMat.from_bytes(ggml_type, bytes, m, n)` (qmat.rs:52-59),
+`.matvec(x)` (qmat.rs:80), `.matmul(x, rows)` (qmat.rs:169), `.rows()` / `.cols()`
+(qmat.rs:62-73). Errors the reference reports by panicking (unknown type, kernel.rs:2006, 2027) or
+through `EngineError` (sizes, quant.rs:402-447) raise `RehipError` with the library's message.
+`MoeExperts.forward` mirrors the expert half of moe_layer_forward (moe.rs:360-388) on
+router-chosen experts.
+
+The compute runs only on the GPU through librehip.so; there is no CPU fallback. Importing this
+module without the built library raises, and every call on a machine without a gfx950 GPU
+returns RE_ERR_NODEV.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+_PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(_PKG, "librehip.so")
+
+Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K = 2, 6, 8, 12, 13, 14
+QUANT_TYPES = (Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K)
+GEOM = {Q4_0: (32, 18), Q5_0: (32, 22), Q8_0: (32, 34), Q4_K: (256, 144), Q5_K: (256, 176),
+        Q6_K: (256, 210)}
+TYPE_NAMES = {Q4_0: "Q4_0", Q5_0: "Q5_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K"}
+
+RE_OK, RE_ERR_TYPE, RE_ERR_SIZE, RE_ERR_ARG, RE_ERR_HIP, RE_ERR_NODEV = 0, 1, 2, 3, 4, 5
+MODE_BF16, MODE_F32 = 0, 1
+
+# every symbol include/rehip.h declares
+EXPORTS = ("re_init", "re_last_error", "re_version", "re_row_bytes", "re_tiled_bytes", "re_repack",
+           "re_qmat_create", "re_qmat_destroy", "re_qmat_rows", "re_qmat_cols", "re_qmat_type",
+           "re_qmat_matvec", "re_qmat_matmul", "re_qmat_matvec_dev", "re_qmat_matmul_dev",
+           "re_qmat_dequant_dev", "re_dequant", "re_moe_create", "re_moe_destroy", "re_moe_forward",
+           "re_moe_forward_dev")
+
+
+class RehipError(RuntimeError):
+    def __init__(self, code: int, message: str):
+        super().__init__(f"[{code}] {message}")
+        self.code = code
+        self.message = message
+
+
+_lib = None
+_sz = C.c_size_t
+_vp = C.c_void_p
+
+
+def lib() -> C.CDLL:
+    """Load librehip.so (built by `make -C rusty-engine_amd`)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RehipError(RE_ERR_ARG, f"{LIB_PATH} is not built (run __graft_entry__.build())")
+        L = C.CDLL(LIB_PATH)
+        L.re_init.restype = C.c_int
+        L.re_last_error.restype = C.c_char_p
+        L.re_version.restype = C.c_char_p
+        L.re_row_bytes.argtypes = [C.c_uint32, _sz, C.POINTER(_sz)]
+        L.re_tiled_bytes.argtypes = [C.c_uint32, _sz, _sz, C.POINTER(_sz)]
+        L.re_repack.argtypes = [C.c_uint32, _vp, _sz, _sz, _sz, _vp, _sz]
+        L.re_qmat_create.argtypes = [C.c_uint32, _vp, _sz, _sz, _sz, C.POINTER(_vp)]
+        L.re_qmat_destroy.argtypes = [_vp]
+        L.re_qmat_destroy.restype = None
+        for f in ("re_qmat_rows", "re_qmat_cols"):
+            getattr(L, f).argtypes = [_vp]
+            getattr(L, f).restype = _sz
+        L.re_qmat_type.argtypes = [_vp]
+        L.re_qmat_type.restype = C.c_uint32
+        L.re_qmat_matvec.argtypes = [_vp, _vp, _vp]
+        L.re_qmat_matmul.argtypes = [_vp, _vp, _sz, _vp, C.c_int]
+        L.re_qmat_matvec_dev.argtypes = [_vp, _vp, _vp, _vp]
+        L.re_qmat_matmul_dev.argtypes = [_vp, _vp, _sz, _vp, C.c_int, _vp]
+        L.re_qmat_dequant_dev.argtypes = [_vp, _vp, _vp]
+        L.re_dequant.argtypes = [C.c_uint32, _vp, _sz, _vp, _sz]
+        L.re_moe_create.argtypes = [C.c_uint32, _vp, _sz, C.c_uint32, _vp, _sz, C.c_uint32, _vp, _sz,
+                                    _sz, _sz, _sz, C.POINTER(_vp)]
+        L.re_moe_destroy.argtypes = [_vp]
+        L.re_moe_destroy.restype = None
+        L.re_moe_forward.argtypes = [_vp, _vp, _sz, _sz, _vp, _vp, _vp, C.c_int]
+        L.re_moe_forward_dev.argtypes = [_vp, _vp, _sz, _sz, _vp, _vp, _vp, C.c_int, _vp]
+        _lib = L
+    return _lib
+
+
+def _check(rc: int) -> None:
+    if rc != RE_OK:
+        raise RehipError(rc, lib().re_last_error().decode())
+
+
+def _u8(a) -> np.ndarray:
+    if isinstance(a, (bytes, bytearray, memoryview)):
+        return np.frombuffer(a, np.uint8)
+    return np.ascontiguousarray(a, np.uint8).reshape(-1)
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, np.float32).reshape(-1)
+
+
+def init() -> None:
+    _check(lib().re_init())
+
+
+def version() -> str:
+    return lib().re_version().decode()
+
+
+def row_bytes(ggml_type: int, n: int) -> int:
+    out = _sz()
+    _check(lib().re_row_bytes(ggml_type, n, C.byref(out)))
+    return out.value
+
+
+def tiled_bytes(ggml_type: int, m: int, n: int) -> int:
+    out = _sz()
+    _check(lib().re_tiled_bytes(ggml_type, m, n, C.byref(out)))
+    return out.value
+
+
+def repack(ggml_type: int, data, m: int, n: int) -> np.ndarray:
+    """Host-side repack into the GPU tiled layout (no GPU needed)."""
+    src = _u8(data)
+    out = np.empty(tiled_bytes(ggml_type, m, n), np.uint8)
+    _check(lib().re_repack(ggml_type, src.ctypes.data, src.size, m, n, out.ctypes.data, out.size))
+    return out
+
+
+def dequant(ggml_type: int, data) -> np.ndarray:
+    """GPU dequant of a flat block stream (quant::dequant, src/quant.rs:363)."""
+    src = _u8(data)
+    qk, bb = GEOM.get(ggml_type, (1, 1))
+    n = src.size // bb * qk if ggml_type in GEOM else 0
+    out = np.empty(max(n, 1), np.float32)
+    _check(lib().re_dequant(ggml_type, src.ctypes.data, src.size, out.ctypes.data, n))
+    return out[:n]
+
+
+def _dev_ptr(t) -> int:
+    """Device address of a torch tensor (plumbing for the *_dev entry points)."""
+    return int(t.data_ptr())
+
+
+def _stream_ptr(stream) -> int | None:
+    if stream is None:
+        return None
+    return int(getattr(stream, "cuda_stream", stream))
+
+
+class QMat:
+    """GPU-resident quantized matrix W[m x n] (src/qmat.rs:30-42, Quant variant)."""
+
+    def __init__(self, handle: int, ggml_type: int, m: int, n: int):
+        self._h = C.c_void_p(handle)
+        self.ggml_type, self.m, self.n = ggml_type, m, n
+
+    @classmethod
+    def from_bytes(cls, ggml_type: int, data, m: int, n: int) -> "QMat":
+        src = _u8(data)
+        h = _vp()
+        _check(lib().re_qmat_create(ggml_type, src.ctypes.data, src.size, m, n, C.byref(h)))
+        return cls(h.value, ggml_type, m, n)
+
+    def rows(self) -> int:
+        return lib().re_qmat_rows(self._h)
+
+    def cols(self) -> int:
+        return lib().re_qmat_cols(self._h)
+
+    def matvec(self, x) -> np.ndarray:
+        xv = _f32(x)
+        if xv.size != self.n:
+            raise RehipError(RE_ERR_SIZE, f"matvec: x has {xv.size} values, want {self.n}")
+        y = np.empty(self.m, np.float32)
+        _check(lib().re_qmat_matvec(self._h, xv.ctypes.data, y.ctypes.data))
+        return y
+
+    def matmul(self, x, rows: int, mode: int = MODE_BF16) -> np.ndarray:
+        xv = _f32(x)
+        if xv.size != rows * self.n:
+            raise RehipError(RE_ERR_SIZE, f"matmul: X has {xv.size} values, want {rows}x{self.n}")
+        y = np.empty(max(rows * self.m, 1), np.float32)
+        _check(lib().re_qmat_matmul(self._h, xv.ctypes.data, rows, y.ctypes.data, mode))
+        return y[:rows * self.m]
+
+    # device-resident variants (torch tensors as plumbing for HBM buffers and streams)
+    def matvec_dev(self, x_dev, y_dev, stream=None) -> None:
+        _check(lib().re_qmat_matvec_dev(self._h, _dev_ptr(x_dev), _dev_ptr(y_dev), _stream_ptr(stream)))
+
+    def matmul_dev(self, x_dev, rows: int, y_dev, mode: int = MODE_BF16, stream=None) -> None:
+        _check(lib().re_qmat_matmul_dev(self._h, _dev_ptr(x_dev), rows, _dev_ptr(y_dev), mode,
+                                        _stream_ptr(stream)))
+
+    def dequant_dev(self, out_dev, stream=None) -> None:
+        _check(lib().re_qmat_dequant_dev(self._h, _dev_ptr(out_dev), _stream_ptr(stream)))
+
+    def close(self) -> None:
+        if self._h:
+            lib().re_qmat_destroy(self._h)
+            self._h = C.c_void_p(0)
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class MoeExperts:
+    """All experts of one MoE layer resident on the GPU (gate/up inter x hidden, down hidden x inter)."""
+
+    def __init__(self, gate_type, gate, up_type, up, down_type, down, n_experts, hidden, inter):
+        g, u, d = _u8(gate), _u8(up), _u8(down)
+        h = _vp()
+        _check(lib().re_moe_create(gate_type, g.ctypes.data, g.size, up_type, u.ctypes.data, u.size,
+                                   down_type, d.ctypes.data, d.size, n_experts, hidden, inter, C.byref(h)))
+        self._h = h
+        self.n_experts, self.hidden, self.inter = n_experts, hidden, inter
+
+    def forward(self, x, tokens: int, top_k: int, ids, weights, mode: int = MODE_BF16) -> np.ndarray:
+        xv = _f32(x)
+        idv = np.ascontiguousarray(ids, np.uint32).reshape(-1)
+        wv = _f32(weights)
+        if xv.size != tokens * self.hidden or idv.size != tokens * top_k or wv.size != tokens * top_k:
+            raise RehipError(RE_ERR_SIZE, "moe forward: shape mismatch")
+        out = np.empty(max(tokens * self.hidden, 1), np.float32)
+        _check(lib().re_moe_forward(self._h, xv.ctypes.data, tokens, top_k, idv.ctypes.data, wv.ctypes.data,
+                                    out.ctypes.data, mode))
+        return out[:tokens * self.hidden]
+
+    def forward_dev(self, x_dev, tokens, top_k, ids, weights, out_dev, mode=MODE_BF16, stream=None) -> None:
+        idv = np.ascontiguousarray(ids, np.uint32).reshape(-1)
+        wv = _f32(weights)
+        _check(lib().re_moe_forward_dev(self._h, _dev_ptr(x_dev), tokens, top_k, idv.ctypes.data,
+                                        wv.ctypes.data, _dev_ptr(out_dev), mode, _stream_ptr(stream)))
+
+    def close(self) -> None:
+        if self._h:
+            lib().re_moe_destroy(self._h)
+            self._h = C.c_void_p(0)
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

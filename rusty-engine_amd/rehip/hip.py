@@ -1,0 +1,138 @@
+"""Minimal ctypes plumbing over the HIP runtime that librehip.so links (libamdhip64.so.7 from
+/opt/rocm): device buffers, copies, streams and events for the device-pointer entry points,
+the benchmark and the tests.
+
+torch is deliberately not used in processes that load librehip: torch bundles its own HIP
+runtime under the same soname, and two HIP runtimes in one process do not initialise.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from . import lib as _rehip_lib
+
+_hip = None
+
+
+def hip() -> C.CDLL:
+    global _hip
+    if _hip is None:
+        _rehip_lib()                    # loads libamdhip64.so.7 through librehip's RUNPATH
+        H = C.CDLL("libamdhip64.so.7")
+        H.hipGetErrorString.restype = C.c_char_p
+        H.hipMalloc.argtypes = [C.POINTER(C.c_void_p), C.c_size_t]
+        H.hipFree.argtypes = [C.c_void_p]
+        H.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+        H.hipMemcpyAsync.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int, C.c_void_p]
+        H.hipMemset.argtypes = [C.c_void_p, C.c_int, C.c_size_t]
+        H.hipDeviceSynchronize.argtypes = []
+        H.hipStreamCreate.argtypes = [C.POINTER(C.c_void_p)]
+        H.hipStreamDestroy.argtypes = [C.c_void_p]
+        H.hipStreamSynchronize.argtypes = [C.c_void_p]
+        H.hipEventCreate.argtypes = [C.POINTER(C.c_void_p)]
+        H.hipEventDestroy.argtypes = [C.c_void_p]
+        H.hipEventRecord.argtypes = [C.c_void_p, C.c_void_p]
+        H.hipEventSynchronize.argtypes = [C.c_void_p]
+        H.hipEventElapsedTime.argtypes = [C.POINTER(C.c_float), C.c_void_p, C.c_void_p]
+        H.hipGetDeviceCount.argtypes = [C.POINTER(C.c_int)]
+        _hip = H
+    return _hip
+
+
+H2D, D2H, D2D = 1, 2, 3
+
+
+def check(rc: int) -> None:
+    if rc != 0:
+        raise RuntimeError(f"HIP error {rc}: {hip().hipGetErrorString(rc).decode()}")
+
+
+def device_count() -> int:
+    n = C.c_int(0)
+    rc = hip().hipGetDeviceCount(C.byref(n))
+    return n.value if rc == 0 else 0
+
+
+class DeviceBuffer:
+    """Owned device allocation of `nbytes` bytes."""
+
+    def __init__(self, nbytes: int):
+        self.nbytes = int(nbytes)
+        p = C.c_void_p()
+        check(hip().hipMalloc(C.byref(p), max(self.nbytes, 1)))
+        self.ptr = p.value
+
+    @classmethod
+    def from_array(cls, a: np.ndarray) -> "DeviceBuffer":
+        a = np.ascontiguousarray(a)
+        b = cls(a.nbytes)
+        b.upload(a)
+        return b
+
+    def data_ptr(self) -> int:
+        return self.ptr
+
+    def upload(self, a: np.ndarray) -> None:
+        a = np.ascontiguousarray(a)
+        assert a.nbytes <= self.nbytes
+        check(hip().hipMemcpy(C.c_void_p(self.ptr), a.ctypes.data, a.nbytes, H2D))
+
+    def download(self, dtype=np.float32, count: int | None = None) -> np.ndarray:
+        itemsize = np.dtype(dtype).itemsize
+        n = self.nbytes // itemsize if count is None else count
+        out = np.empty(n, dtype)
+        check(hip().hipMemcpy(out.ctypes.data, C.c_void_p(self.ptr), n * itemsize, D2H))
+        return out
+
+    def zero(self) -> None:
+        check(hip().hipMemset(C.c_void_p(self.ptr), 0, self.nbytes))
+
+    def free(self) -> None:
+        if self.ptr:
+            hip().hipFree(C.c_void_p(self.ptr))
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Stream:
+    def __init__(self):
+        s = C.c_void_p()
+        check(hip().hipStreamCreate(C.byref(s)))
+        self.cuda_stream = s.value
+
+    def synchronize(self) -> None:
+        check(hip().hipStreamSynchronize(C.c_void_p(self.cuda_stream)))
+
+    def destroy(self) -> None:
+        if self.cuda_stream:
+            hip().hipStreamDestroy(C.c_void_p(self.cuda_stream))
+            self.cuda_stream = None
+
+
+class Event:
+    def __init__(self):
+        e = C.c_void_p()
+        check(hip().hipEventCreate(C.byref(e)))
+        self.ev = e.value
+
+    def record(self, stream: Stream | None = None) -> None:
+        check(hip().hipEventRecord(C.c_void_p(self.ev), C.c_void_p(stream.cuda_stream if stream else None)))
+
+    def synchronize(self) -> None:
+        check(hip().hipEventSynchronize(C.c_void_p(self.ev)))
+
+    def elapsed_ms(self, end: "Event") -> float:
+        ms = C.c_float()
+        check(hip().hipEventElapsedTime(C.byref(ms), C.c_void_p(self.ev), C.c_void_p(end.ev)))
+        return ms.value
+
+
+def synchronize() -> None:
+    check(hip().hipDeviceSynchronize())

@@ -1,0 +1,244 @@
+"""GPU parity of librehip against the CPU oracle, through the C ABI.
+
+Bars (from the task's parity contract):
+  - dequant: bit-exact with quant::dequant (src/quant.rs:363-453);
+  - GEMV and f32-mode GEMM: |y - y_oracle| <= 2^-10 * sum_k |w_rk x_k| per output;
+  - bf16-mode GEMM and MoE: ||y - y_oracle|| / ||y_oracle|| <= 1e-2.
+Full-size shapes compare against an f64 product of the oracle-dequantized weights (the
+dequantized values are exact, so this is the exact product up to f64 rounding).
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+import rehip
+from blockpack import k_blocks, q4_blocks, q5_blocks, q8_blocks
+from rehip import hip, synth
+
+pytestmark = pytest.mark.gpu
+
+F32_TOL = 2.0 ** -10
+BF16_TOL = 1e-2
+
+
+def qmat(t, w, m, n):
+    return rehip.QMat.from_bytes(t, w, m, n)
+
+
+def f64_product(t, w, m, n, x, rows):
+    qk, _ = rehip.GEOM[t]
+    nb = (n + qk - 1) // qk
+    deq = O.dequant(t, w).reshape(m, nb * qk)[:, :n].astype(np.float64)
+    xx = x.reshape(rows, n).astype(np.float64)
+    return xx @ deq.T, np.abs(xx) @ np.abs(deq).T
+
+
+# ---- dequant: bit-exact ---------------------------------------------------------------------
+def random_blocks_all_scales(rng, t, nb):
+    """Random block bytes whose f16 scales span normal, subnormal, zero and negative values."""
+    qk, bb = rehip.GEOM[t]
+    raw = rng.integers(0, 256, (nb, bb), dtype=np.uint8)
+    h = rng.integers(0, 0x7C00, nb).astype(np.uint16)              # finite, any sign below
+    h[::7] = rng.integers(0, 0x400, len(h[::7]))                      # subnormals
+    h[::11] = 0
+    h[1::3] |= 0x8000                                                 # negative scales
+    hb = h.view(np.uint8).reshape(nb, 2)
+    if t == rehip.Q6_K:
+        raw[:, 208:210] = hb
+    else:
+        raw[:, 0:2] = hb
+        if t in (rehip.Q4_K, rehip.Q5_K):
+            raw[:, 2:4] = hb[::-1]
+    return raw.reshape(-1)
+
+
+@pytest.mark.parametrize("t", rehip.QUANT_TYPES)
+def test_dequant_bit_exact_random_blocks(t):
+    rng = np.random.default_rng(100 + t)
+    data = random_blocks_all_scales(rng, t, 1000)
+    want = O.dequant(t, data)
+    got = rehip.dequant(t, data)
+    assert got.shape == want.shape
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("t,data", [(rehip.Q4_0, q4_blocks(67)), (rehip.Q5_0, q5_blocks(67)),
+                                    (rehip.Q8_0, q8_blocks(67)), (rehip.Q4_K, k_blocks(0, 9)),
+                                    (rehip.Q5_K, k_blocks(1, 9)), (rehip.Q6_K, k_blocks(2, 9))],
+                         ids=["q4_blocks", "q5_blocks", "q8_blocks", "k_blocks0", "k_blocks1", "k_blocks2"])
+def test_dequant_bit_exact_reference_fixtures(t, data):
+    assert np.array_equal(rehip.dequant(t, data).view(np.uint32), O.dequant(t, data).view(np.uint32))
+
+
+def test_dequant_errors_mirror_reference():
+    with pytest.raises(rehip.RehipError) as e:
+        rehip.dequant(rehip.Q4_K, bytes(143))
+    assert e.value.message == "Q4_K data len 143 not a multiple of 144"
+    assert rehip.dequant(rehip.Q6_K, b"").size == 0
+
+
+@pytest.mark.parametrize("t", rehip.QUANT_TYPES)
+def test_resident_dequant_matches_flat_dequant(t):
+    rng = np.random.default_rng(7 + t)
+    m, n = 130, 896
+    w = synth.weight_bytes(rng, t, m, n)
+    q = qmat(t, w, m, n)
+    out = hip.DeviceBuffer(m * n * 4)
+    q.dequant_dev(out)
+    hip.synchronize()
+    qk, _ = rehip.GEOM[t]
+    nb = (n + qk - 1) // qk
+    want = O.dequant(t, w).reshape(m, nb * qk)[:, :n].reshape(-1)
+    assert np.array_equal(out.download().view(np.uint32), want.view(np.uint32))
+
+
+def test_device_entry_points_match_host_entry_points():
+    rng = np.random.default_rng(17)
+    t, m, n, rows = rehip.Q4_K, 256, 1024, 33
+    w = synth.weight_bytes(rng, t, m, n)
+    x = synth.activations(rng, rows, n)
+    q = qmat(t, w, m, n)
+    dx = hip.DeviceBuffer.from_array(x)
+    dy = hip.DeviceBuffer(rows * m * 4)
+    s = hip.Stream()
+    q.matmul_dev(dx, rows, dy, rehip.MODE_BF16, stream=s)
+    s.synchronize()
+    assert np.array_equal(dy.download(), q.matmul(x, rows, rehip.MODE_BF16))
+    q.matvec_dev(dx, dy, stream=s)
+    s.synchronize()
+    assert np.array_equal(dy.download(count=m), q.matvec(x[:n]))
+    s.destroy()
+
+
+# ---- GEMV --------------------------------------------------------------------------------
+GEMV_SHAPES = [(1, 256), (5, 512), (64, 256), (70, 896), (130, 1024), (896, 4864), (4864, 896)]
+
+
+@pytest.mark.parametrize("t", rehip.QUANT_TYPES)
+@pytest.mark.parametrize("m,n", GEMV_SHAPES)
+def test_gemv_parity(t, m, n):
+    rng = np.random.default_rng(1000 * t + m + n)
+    w = synth.weight_bytes(rng, t, m, n)
+    x = synth.activations(rng, 1, n)
+    got = qmat(t, w, m, n).matvec(x)
+    want = O.qmat_matvec(t, w, m, n, x)
+    absd = O.qmat_absdot(t, w, m, n, x, 1)
+    err = np.abs(got.astype(np.float64) - want)
+    assert np.all(err <= F32_TOL * absd), f"max err/bound {np.max(err / (absd + 1e-30))}"
+
+
+def test_gemv_reference_fixtures_match_scalar_kernels():
+    # kernel.rs fixtures; the oracle's matvec is the reference's scalar GEMV
+    for t, w, m, n in [(rehip.Q4_0, q4_blocks(3 * 64 // 32), 3, 64), (rehip.Q5_0, q5_blocks(3 * 64 // 32), 3, 64),
+                       (rehip.Q8_0, q8_blocks(2), 2, 32), (rehip.Q4_K, k_blocks(0, 4), 2, 512),
+                       (rehip.Q5_K, k_blocks(1, 4), 2, 512), (rehip.Q6_K, k_blocks(2, 4), 2, 512)]:
+        x = (np.arange(n, dtype=np.float32) * np.float32(0.01) - np.float32(1.3)).astype(np.float32)
+        got = qmat(t, w, m, n).matvec(x)
+        want = O.matvec(t, w, m, n, x)
+        assert np.all(np.abs(got - want) <= np.abs(want) * 1e-4 + 1e-4), t
+
+
+def test_gemv_is_deterministic_and_equals_rows1_matmul():
+    rng = np.random.default_rng(3)
+    t, m, n = rehip.Q6_K, 896, 4864
+    w = synth.weight_bytes(rng, t, m, n)
+    x = synth.activations(rng, 1, n)
+    q = qmat(t, w, m, n)
+    a, b = q.matvec(x), q.matvec(x)
+    assert np.array_equal(a, b)
+    assert np.array_equal(q.matmul(x, 1, rehip.MODE_BF16), a)
+
+
+def test_lm_head_gemv_q8_0_full_size():
+    rng = np.random.default_rng(305)
+    t, m, n = rehip.Q8_0, 151936, 896
+    w = synth.weight_bytes(rng, t, m, n)
+    x = synth.activations(rng, 1, n)
+    got = qmat(t, w, m, n).matvec(x)
+    exact, absd = f64_product(t, w, m, n, x, 1)
+    assert np.all(np.abs(got - exact[0]) <= F32_TOL * absd[0])
+
+
+# ---- GEMM --------------------------------------------------------------------------------
+GEMM_SHAPES = [(5, 256, 2), (70, 512, 3), (128, 896, 64), (200, 1024, 70), (896, 4864, 129)]
+
+
+@pytest.mark.parametrize("t", rehip.QUANT_TYPES)
+@pytest.mark.parametrize("m,n,rows", GEMM_SHAPES)
+def test_gemm_parity_both_modes(t, m, n, rows):
+    rng = np.random.default_rng(2000 * t + m + n + rows)
+    w = synth.weight_bytes(rng, t, m, n)
+    x = synth.activations(rng, rows, n)
+    q = qmat(t, w, m, n)
+    exact, absd = f64_product(t, w, m, n, x, rows)
+    exact, absd = exact.reshape(-1), absd.reshape(-1)
+    got32 = q.matmul(x, rows, rehip.MODE_F32)
+    assert np.all(np.abs(got32 - exact) <= F32_TOL * absd)
+    got16 = q.matmul(x, rows, rehip.MODE_BF16)
+    assert np.linalg.norm(got16 - exact) / np.linalg.norm(exact) <= BF16_TOL
+    if m * n * rows <= 1 << 22:
+        want = O.qmat_matmul(t, w, m, n, x, rows)
+        assert np.all(np.abs(got32 - want) <= F32_TOL * absd)
+
+
+@pytest.mark.parametrize("name,t,m,n", [("C1 Q5_0 4864x896", rehip.Q5_0, 4864, 896),
+                                        ("C2 Q6_K 896x4864", rehip.Q6_K, 896, 4864)])
+def test_prefill_961_rows_full_size(name, t, m, n):
+    rng = np.random.default_rng(101 if t == rehip.Q5_0 else 201 + 961)
+    w = synth.weight_bytes(rng, t, m, n)
+    x = synth.activations(rng, 961, n)
+    q = qmat(t, w, m, n)
+    exact, absd = f64_product(t, w, m, n, x, 961)
+    exact, absd = exact.reshape(-1), absd.reshape(-1)
+    got16 = q.matmul(x, 961, rehip.MODE_BF16)
+    assert np.linalg.norm(got16 - exact) / np.linalg.norm(exact) <= BF16_TOL
+    got32 = q.matmul(x, 961, rehip.MODE_F32)
+    assert np.all(np.abs(got32 - exact) <= F32_TOL * absd)
+    assert np.array_equal(q.matmul(x, 961, rehip.MODE_BF16), got16)      # deterministic
+
+
+# ---- MoE ---------------------------------------------------------------------------------
+def moe_case(seed, E, hidden, inter, T, k, gt=rehip.Q4_K, dt=rehip.Q6_K):
+    rng = np.random.default_rng(seed)
+    gate = np.concatenate([synth.weight_bytes(rng, gt, inter, hidden) for _ in range(E)])
+    up = np.concatenate([synth.weight_bytes(rng, gt, inter, hidden) for _ in range(E)])
+    down = np.concatenate([synth.weight_bytes(rng, dt, hidden, inter) for _ in range(E)])
+    x = synth.activations(rng, T, hidden)
+    logits = rng.standard_normal((T, E)).astype(np.float32)
+    ids = np.zeros((T, k), np.uint32)
+    wts = np.zeros((T, k), np.float32)
+    for i in range(T):
+        ids[i], wts[i] = O.top_k(logits[i], k)        # the reference router (moe.rs:75-93)
+    return gate, up, down, x, ids.reshape(-1), wts.reshape(-1)
+
+
+@pytest.mark.parametrize("T", [1, 5, 40])
+def test_moe_grouped_ffn_parity(T):
+    E, hidden, inter, k = 16, 512, 256, 4
+    gate, up, down, x, ids, wts = moe_case(400 + T, E, hidden, inter, T, k)
+    want = O.moe_ffn(rehip.Q4_K, gate, rehip.Q4_K, up, rehip.Q6_K, down, E, hidden, inter, x, T, k, ids, wts)
+    moe = rehip.MoeExperts(rehip.Q4_K, gate, rehip.Q4_K, up, rehip.Q6_K, down, E, hidden, inter)
+    for mode, tol in [(rehip.MODE_F32, 1e-4), (rehip.MODE_BF16, BF16_TOL)]:
+        got = moe.forward(x, T, k, ids, wts, mode)
+        rel = np.linalg.norm(got - want) / np.linalg.norm(want)
+        assert rel <= tol, (mode, rel)
+
+
+def test_moe_qwen3_shape_t32():
+    E, hidden, inter, k, T = 128, 2048, 768, 8, 32
+    gate, up, down, x, ids, wts = moe_case(401, E, hidden, inter, T, k)
+    want = O.moe_ffn(rehip.Q4_K, gate, rehip.Q4_K, up, rehip.Q6_K, down, E, hidden, inter, x, T, k, ids, wts)
+    moe = rehip.MoeExperts(rehip.Q4_K, gate, rehip.Q4_K, up, rehip.Q6_K, down, E, hidden, inter)
+    got = moe.forward(x, T, k, ids, wts, rehip.MODE_BF16)
+    assert np.linalg.norm(got - want) / np.linalg.norm(want) <= BF16_TOL
+    got32 = moe.forward(x, T, k, ids, wts, rehip.MODE_F32)
+    assert np.linalg.norm(got32 - want) / np.linalg.norm(want) <= 1e-4
+
+
+def test_moe_rejects_bad_expert_id():
+    E, hidden, inter = 2, 256, 256
+    gate, up, down, x, ids, wts = moe_case(9, E, hidden, inter, 1, 1)
+    moe = rehip.MoeExperts(rehip.Q4_K, gate, rehip.Q4_K, up, rehip.Q6_K, down, E, hidden, inter)
+    with pytest.raises(rehip.RehipError) as e:
+        moe.forward(x, 1, 1, np.array([5], np.uint32), wts)
+    assert e.value.code == rehip.RE_ERR_ARG
