@@ -1,0 +1,185 @@
+"""Benchmark of the fused GGUF dequant-matmul on one MI355X.
+
+Workload (the configuration the headline metric is quoted on): the Q6_K down projection
+W[896 x 4864] (K = 4864, 256-element super-blocks of 210 B) with f32 activations X[N x 4864],
+N = 1 (decode GEMV), 64 and 961 (prefill GEMM). Synthetic, seeded (numpy PCG64, seed 201 + N),
+inputs resident in HBM before timing.
+
+A "step" is one N = 1 GEMV over one weight copy. The timed region replays a HIP graph of `steps`
+back-to-back GEMV launches that rotate over enough copies of W (> 512 MiB) that every launch
+reads its weights from HBM, not from the 256 MiB MALL. `value` = algorithmic bytes per launch
+(stored GGUF weight bytes + f32 x + f32 y) / average launch time. The N = 961 and N = 64 GEMMs
+(bf16 MFMA mode) are timed the same way and reported under "gemm".
+
+The CPU baseline is the oracle's restatement of the reference's pooled AVX2 kernels
+(matmul_reuse + QMat split policy + persistent pool), timed on this host on a bounded sample.
+
+Prints one JSON line.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "rusty-engine_amd"))
+sys.path.insert(0, ROOT)
+
+import numpy as np  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+F32_MFMA_PEAK_TFLOPS = 157.3
+M, K = 896, 4864
+MALL_BYTES = 256 << 20
+
+
+def algorithmic_bytes(t, m, k, n):
+    import rehip
+    qk, bb = rehip.GEOM[t]
+    return m * k // qk * bb + 4 * n * k + 4 * n * m
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--gemm-steps", type=int, default=200)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="bound on the CPU-baseline sample")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import rehip
+    from rehip import hip, synth
+
+    t = rehip.Q6_K
+    rehip.init()
+    stream = hip.Stream()
+
+    # ---- N = 1 GEMV over rotated weight copies -------------------------------------------------
+    rng = np.random.default_rng(201 + 1)
+    w = synth.weight_bytes(rng, t, M, K)
+    x1 = synth.activations(rng, 1, K)
+    copies = int(np.ceil(2 * MALL_BYTES / w.size))
+    qs = [rehip.QMat.from_bytes(t, w, M, K) for _ in range(copies)]
+    dx = hip.DeviceBuffer.from_array(x1)
+    dy = hip.DeviceBuffer(M * 4)
+    steps, warmup = args.steps, args.warmup
+
+    def gemv_run(n):
+        for i in range(n):
+            qs[i % copies].matvec_dev(dx, dy, stream=stream)
+
+    gw = hip.Graph(stream, lambda: gemv_run(warmup))
+    gt = hip.Graph(stream, lambda: gemv_run(steps))
+    gw.launch()
+    stream.synchronize()
+    e0, e1 = hip.Event(), hip.Event()
+    e0.record(stream)
+    gt.launch()
+    e1.record(stream)
+    e1.synchronize()
+    gemv_ms = e0.elapsed_ms(e1) / steps
+    # parity spot check of the timed kernel against the oracle
+    y_gpu = dy.download()
+    import oracle
+    y_ref = oracle.qmat_matvec(t, w, M, K, x1)
+    absd = oracle.qmat_absdot(t, w, M, K, x1, 1)
+    parity_ok = bool(np.all(np.abs(y_gpu - y_ref) <= 2.0 ** -10 * absd))
+    gemv_bytes = algorithmic_bytes(t, M, K, 1)
+    gemv_gbs = gemv_bytes / (gemv_ms * 1e-3) / 1e9
+    gw.destroy()
+    gt.destroy()
+    for q in qs[1:]:
+        q.close()
+
+    # ---- N = 64 and N = 961 GEMM (bf16 MFMA) -----------------------------------------------------
+    gemm = {}
+    for n in (64, 961):
+        rng = np.random.default_rng(201 + n)
+        wn = synth.weight_bytes(rng, t, M, K)
+        xn = synth.activations(rng, n, K)
+        q = rehip.QMat.from_bytes(t, wn, M, K)
+        dxn = hip.DeviceBuffer.from_array(xn)
+        dyn = hip.DeviceBuffer(n * M * 4)
+        gs = args.gemm_steps
+        g = hip.Graph(stream, lambda: [q.matmul_dev(dxn, n, dyn, rehip.MODE_BF16, stream=stream) for _ in range(gs)])
+        g.launch()
+        stream.synchronize()
+        e0.record(stream)
+        g.launch()
+        e1.record(stream)
+        e1.synchronize()
+        ms = e0.elapsed_ms(e1) / gs
+        g.destroy()
+        flops = 2.0 * n * M * K
+        nbytes = algorithmic_bytes(t, M, K, n)
+        y = dyn.download()
+        deq = oracle.dequant(t, wn).reshape(M, K).astype(np.float64)
+        exact = (xn.reshape(n, K).astype(np.float64) @ deq.T).reshape(-1)
+        rel = float(np.linalg.norm(y - exact) / np.linalg.norm(exact))
+        gemm[f"n{n}"] = {"ms": ms, "tflops": flops / (ms * 1e-3) / 1e12, "gbs": nbytes / (ms * 1e-3) / 1e9,
+                         "frac_bf16_peak": flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
+                         "frac_hbm_peak": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                         "rel_err_vs_f64": rel, "flop": flops, "bytes": nbytes}
+        q.close()
+
+    # ---- CPU baseline (reference-restated pooled AVX2 kernels) on a bounded sample --------------
+    cpu = None
+    if not args.no_cpu and oracle.cpu_has_avx2():
+        threads = int(os.environ.get("RE_THREADS", "0")) or min(os.cpu_count() or 1, 16)
+        oracle.cpu_matvec(t, w, M, K, x1, threads)
+        budget = args.cpu_seconds / 2
+        reps, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < budget:
+            oracle.cpu_matvec(t, w, M, K, x1, threads)
+            reps += 1
+        cpu_gemv_s = (time.perf_counter() - t0) / reps
+        rng = np.random.default_rng(201 + 961)
+        wn = synth.weight_bytes(rng, t, M, K)
+        xn = synth.activations(rng, 961, K)
+        oracle.cpu_matmul(t, wn, M, K, xn, 961, threads)
+        reps2, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < budget:
+            oracle.cpu_matmul(t, wn, M, K, xn, 961, threads)
+            reps2 += 1
+        cpu_gemm_s = (time.perf_counter() - t0) / reps2
+        cpu = {"value": gemv_bytes / cpu_gemv_s / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+               "sample": f"Q6_K 896x4864: N=1 GEMV x{reps} ({cpu_gemv_s * 1e3:.3f} ms each), "
+                         f"N=961 GEMM x{reps2} ({cpu_gemm_s * 1e3:.1f} ms each = "
+                         f"{2.0 * 961 * M * K / cpu_gemm_s / 1e9:.1f} GFLOP/s)",
+               "n961_gflops": 2.0 * 961 * M * K / cpu_gemm_s / 1e9}
+
+    out = {
+        "metric": "Q-matmul GB/s (N=1) & TFLOP/s (N=961) as % roofline; decode tok/s",
+        "value": round(gemv_gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": gemv_ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded PCG64 GGUF Q6_K blocks, finite f16 scales; X ~ N(0,1))",
+        "config": {"workload": "Q6_K down projection W[896x4864], X[N x 4864] f32, N=1 GEMV (+ N=64/961 GEMM)",
+                   "weight_copies_rotated": copies, "graph_replay": True},
+        "roofline": {"bound": "hbm", "achieved": round(gemv_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gemv_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "algorithmic_bytes_per_launch": gemv_bytes, "avg_launch_us": gemv_ms * 1e3},
+        "gemm": gemm,
+        "parity_ok": parity_ok and all(v["rel_err_vs_f64"] <= 1e-2 for v in gemm.values()),
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

@@ -4,6 +4,7 @@
 
 #include <algorithm>
 #include <cstdarg>
+#include <cstdlib>
 #include <cstdio>
 #include <cstring>
 #include <mutex>
@@ -136,10 +137,21 @@ namespace {
 
 // GEMV launch shape: enough workgroups to cover the chip (the split count grows until about
 // 1024 workgroups exist or every block column is its own split).
+size_t env_size(const char* name, size_t dflt) {
+  const char* v = std::getenv(name);
+  return (v && *v) ? (size_t)std::strtoull(v, nullptr, 10) : dflt;
+}
+
 void plan_gemv(re_qmat* q) {
   const size_t tiles = q->g.tiles, kb = q->g.kb;
   size_t want = (1024 + tiles - 1) / tiles;
-  want = std::max<size_t>(1, std::min(want, kb));
+  // a cross-workgroup split costs an agent-scope release per workgroup (an L2 write-back on
+  // gfx950), so rows are split only when they are long and the tiles too few to fill the chip
+  if (q->g.n < 2048) want = 1;
+  want = std::min(want, env_size("REHIP_GEMV_MAX_SPLITS", want));
+  // a split stages its slice of x in LDS: keep it within 64 KiB (16384 floats)
+  const size_t max_per = std::max<size_t>(1, 16384 / (size_t)q->g.qk);
+  want = std::max<size_t>({(size_t)1, std::min(want, kb), (kb + max_per - 1) / max_per});
   size_t per = (kb + want - 1) / want;
   q->kb_per_split = (int)per;
   q->splits = (int)((kb + per - 1) / per);
@@ -190,7 +202,7 @@ int gemm_enqueue(re_qmat* q, const float* d_x, size_t rows, float* d_y, int mode
   a.ldy = (int)q->g.m;
   a.tasks = nullptr;
   a.xrow = nullptr;
-  HIP_TRY(launch_gemm(q->g.type, mode, a, 0, s));
+  HIP_TRY(launch_gemm(q->g.type, mode, a, 0, gemm_tile_for((int)q->g.m, (int)rows), s));
   return RE_OK;
 }
 
@@ -424,10 +436,10 @@ int re_moe_forward_dev(re_moe* e, const float* d_x, size_t tokens, size_t top_k,
     pos[p] = at;
   }
   std::vector<GemmTask> t_gu, t_d;
-  const int mt_gu = (int)((e->inter + kGemmBM - 1) / kGemmBM), mt_d = (int)((e->hidden + kGemmBM - 1) / kGemmBM);
+  const int mt_gu = (int)((e->inter + kMoeTile - 1) / kMoeTile), mt_d = (int)((e->hidden + kMoeTile - 1) / kMoeTile);
   for (size_t x = 0; x < e->n_experts; ++x) {
-    for (int r = 0; r < count[x]; r += kGemmBN) {
-      const int rn = std::min(kGemmBN, count[x] - r);
+    for (int r = 0; r < count[x]; r += kMoeTile) {
+      const int rn = std::min(kMoeTile, count[x] - r);
       for (int mt = 0; mt < mt_gu; ++mt) t_gu.push_back({(int)x, mt, start[x] + r, rn});
       for (int mt = 0; mt < mt_d; ++mt) t_d.push_back({(int)x, mt, start[x] + r, rn});
     }
@@ -466,13 +478,13 @@ int re_moe_forward_dev(re_moe* e, const float* d_x, size_t tokens, size_t top_k,
   a.W = e->d_gate;
   a.w_stride = e->gg.bytes;
   a.Y = (float*)e->sg.p;
-  HIP_TRY(launch_gemm(e->gg.type, mode, a, (int)t_gu.size(), s));
+  HIP_TRY(launch_gemm(e->gg.type, mode, a, (int)t_gu.size(), kMoeTile, s));
   a.W = e->d_up;
   a.w_stride = e->gu.bytes;
   a.KB = (int)e->gu.kb;
   a.tiles = (int)e->gu.tiles;
   a.Y = (float*)e->su.p;
-  HIP_TRY(launch_gemm(e->gu.type, mode, a, (int)t_gu.size(), s));
+  HIP_TRY(launch_gemm(e->gu.type, mode, a, (int)t_gu.size(), kMoeTile, s));
   HIP_TRY(launch_swiglu((const float*)e->sg.p, (const float*)e->su.p, (float*)e->sh.p, pairs * e->inter, s));
   GemmArgs d{};
   d.W = e->d_down;
@@ -486,7 +498,7 @@ int re_moe_forward_dev(re_moe* e, const float* d_x, size_t tokens, size_t top_k,
   d.ldy = (int)e->hidden;
   d.tasks = (const GemmTask*)(dm + off_td);
   d.xrow = nullptr;
-  HIP_TRY(launch_gemm(e->gd.type, mode, d, (int)t_d.size(), s));
+  HIP_TRY(launch_gemm(e->gd.type, mode, d, (int)t_d.size(), kMoeTile, s));
   HIP_TRY(launch_combine((const float*)e->syp.p, (const int*)(dm + off_pos), (const float*)(dm + off_w), d_out,
                          (int)tokens, (int)top_k, (int)e->hidden, s));
   return RE_OK;

@@ -97,6 +97,10 @@ template <> struct Blk<T_Q4_0> {
     a.offset = b.offset = 8.0f * d;
     a.e = 0; b.e = 16;
   }
+  // raw data of one chunk (the whole block for 32-element types)
+  using CR = R;
+  __device__ static void load_chunk(const uint8_t* slab, int lane, int c, CR& r) { (void)c; load(slab, lane, r); }
+  __device__ static void decode_chunk(const CR& r, int c, Run& a, Run& b) { decode(r, c, a, b); }
   __device__ static void chunk(const uint8_t* slab, int lane, int c, Run& a, Run& b) {
     R r; load(slab, lane, r); decode(r, c, a, b);
   }
@@ -130,6 +134,10 @@ template <> struct Blk<T_Q5_0> {
     a.offset = b.offset = 16.0f * d;
     a.e = 0; b.e = 16;
   }
+  // raw data of one chunk (the whole block for 32-element types)
+  using CR = R;
+  __device__ static void load_chunk(const uint8_t* slab, int lane, int c, CR& r) { (void)c; load(slab, lane, r); }
+  __device__ static void decode_chunk(const CR& r, int c, Run& a, Run& b) { decode(r, c, a, b); }
   __device__ static void chunk(const uint8_t* slab, int lane, int c, Run& a, Run& b) {
     R r; load(slab, lane, r); decode(r, c, a, b);
   }
@@ -156,6 +164,10 @@ template <> struct Blk<T_Q8_0> {
     a.offset = b.offset = 128.0f * d;
     a.e = 0; b.e = 16;
   }
+  // raw data of one chunk (the whole block for 32-element types)
+  using CR = R;
+  __device__ static void load_chunk(const uint8_t* slab, int lane, int c, CR& r) { (void)c; load(slab, lane, r); }
+  __device__ static void decode_chunk(const CR& r, int c, Run& a, Run& b) { decode(r, c, a, b); }
   __device__ static void chunk(const uint8_t* slab, int lane, int c, Run& a, Run& b) {
     R r; load(slab, lane, r); decode(r, c, a, b);
   }
@@ -205,8 +217,14 @@ template <> struct Blk<T_Q4_K> {
     r.t0 = r.t1 = 0;
   }
   __device__ static void decode(const R& r, int c, Run& a, Run& b) { dec(r.p[0], r.p[1 + c], c, a, b); }
+  struct CR { uint4 head, qs; };
+  __device__ static void load_chunk(const uint8_t* slab, int lane, int c, CR& r) {
+    r.head = ld16(slab + lane * 16);
+    r.qs = ld16(slab + 1024 * (1 + c) + lane * 16);
+  }
+  __device__ static void decode_chunk(const CR& r, int c, Run& a, Run& b) { dec(r.head, r.qs, c, a, b); }
   __device__ static void chunk(const uint8_t* slab, int lane, int c, Run& a, Run& b) {
-    dec(ld16(slab + lane * 16), ld16(slab + 1024 * (1 + c) + lane * 16), c, a, b);
+    CR r; load_chunk(slab, lane, c, r); decode_chunk(r, c, a, b);
   }
 };
 
@@ -236,9 +254,15 @@ template <> struct Blk<T_Q5_K> {
   __device__ static void decode(const R& r, int c, Run& a, Run& b) {
     dec(r.p[0], r.p[1 + (c & 1)], r.p[3 + c], c, a, b);
   }
+  struct CR { uint4 head, qh, qs; };
+  __device__ static void load_chunk(const uint8_t* slab, int lane, int c, CR& r) {
+    r.head = ld16(slab + lane * 16);
+    r.qh = ld16(slab + 1024 * (1 + (c & 1)) + lane * 16);
+    r.qs = ld16(slab + 1024 * (3 + c) + lane * 16);
+  }
+  __device__ static void decode_chunk(const CR& r, int c, Run& a, Run& b) { dec(r.head, r.qh, r.qs, c, a, b); }
   __device__ static void chunk(const uint8_t* slab, int lane, int c, Run& a, Run& b) {
-    dec(ld16(slab + lane * 16), ld16(slab + 1024 * (1 + (c & 1)) + lane * 16),
-        ld16(slab + 1024 * (3 + c) + lane * 16), c, a, b);
+    CR r; load_chunk(slab, lane, c, r); decode_chunk(r, c, a, b);
   }
 };
 
@@ -279,9 +303,16 @@ template <> struct Blk<T_Q6_K> {
   __device__ static void decode(const R& r, int c, Run& a, Run& b) {
     dec(r.p[c], r.p[8 + 2 * (c >> 2) + (c & 1)], r.p[12], r.t0, c, a, b);
   }
+  struct CR { uint4 ql, qh, sc; uint32_t d; };
+  __device__ static void load_chunk(const uint8_t* slab, int lane, int c, CR& r) {
+    r.ql = ld16(slab + 1024 * c + lane * 16);
+    r.qh = ld16(slab + 1024 * (8 + 2 * (c >> 2) + (c & 1)) + lane * 16);
+    r.sc = ld16(slab + 1024 * 12 + lane * 16);
+    r.d = ld2(slab + 1024 * 13 + lane * 2);
+  }
+  __device__ static void decode_chunk(const CR& r, int c, Run& a, Run& b) { dec(r.ql, r.qh, r.sc, r.d, c, a, b); }
   __device__ static void chunk(const uint8_t* slab, int lane, int c, Run& a, Run& b) {
-    dec(ld16(slab + 1024 * c + lane * 16), ld16(slab + 1024 * (8 + 2 * (c >> 2) + (c & 1)) + lane * 16),
-        ld16(slab + 1024 * 12 + lane * 16), ld2(slab + 1024 * 13 + lane * 2), c, a, b);
+    CR r; load_chunk(slab, lane, c, r); decode_chunk(r, c, a, b);
   }
 };
 

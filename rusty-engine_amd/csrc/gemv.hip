@@ -20,33 +20,49 @@
 
 namespace rehip {
 
-// x is read through the constant address space: it is not written while a kernel runs, and
-// wave-uniform loads from that space compile to scalar loads (s_load) into SGPRs.
-typedef const __attribute__((address_space(4))) float cfloat;
-
+// x comes from LDS: every lane of the wave reads the same address (a broadcast), so a run of
+// 16 activations is four ds_read_b128.
 template <int T, bool GUARD>
-__device__ __forceinline__ float block_dot(const typename Blk<T>::R& r, cfloat* __restrict__ xb,
+__device__ __forceinline__ float block_dot(const typename Blk<T>::R& r, const float* __restrict__ xb,
                                            const float* __restrict__ xs, int valid) {
   using B = Blk<T>;
   float acc = 0.0f;
 #pragma unroll
   for (int c = 0; c < B::NCH; ++c) {
-    // keeps each chunk's wave-uniform x loads (scalar loads) next to their use, so a
-    // 256-element super-block never holds all of its x in SGPRs at once
+    // one chunk's 32 activations live at a time: stops the scheduler from hoisting all of a
+    // super-block's LDS reads (256 values) above the first chunk
     if (B::NCH > 1) asm volatile("" ::: "memory");
     Run a, b;
     B::decode(r, c, a, b);
+    // ... and the same for the quant-to-float conversions: pin this chunk's quant words here
+    if (B::NCH > 1)
+      asm volatile("" : "+v"(a.q[0]), "+v"(a.q[1]), "+v"(a.q[2]), "+v"(a.q[3]),
+                        "+v"(b.q[0]), "+v"(b.q[1]), "+v"(b.q[2]), "+v"(b.q[3]));
     // K is a multiple of 32, so a 16-element run is either wholly inside K or wholly past it
     if (!GUARD || a.e < valid) {
+      const float4* xv = reinterpret_cast<const float4*>(xb + a.e);
       float sa = 0.0f;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) sa = __builtin_fmaf(qbyte(a.q, i), xb[a.e + i], sa);
+      for (int v = 0; v < 4; ++v) {
+        const float4 q = xv[v];
+        sa = __builtin_fmaf(qbyte(a.q, 4 * v + 0), q.x, sa);
+        sa = __builtin_fmaf(qbyte(a.q, 4 * v + 1), q.y, sa);
+        sa = __builtin_fmaf(qbyte(a.q, 4 * v + 2), q.z, sa);
+        sa = __builtin_fmaf(qbyte(a.q, 4 * v + 3), q.w, sa);
+      }
       acc += __builtin_fmaf(a.scale, sa, -a.offset * xs[a.e >> 4]);
     }
     if (!GUARD || b.e < valid) {
+      const float4* xv = reinterpret_cast<const float4*>(xb + b.e);
       float sb = 0.0f;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) sb = __builtin_fmaf(qbyte(b.q, i), xb[b.e + i], sb);
+      for (int v = 0; v < 4; ++v) {
+        const float4 q = xv[v];
+        sb = __builtin_fmaf(qbyte(b.q, 4 * v + 0), q.x, sb);
+        sb = __builtin_fmaf(qbyte(b.q, 4 * v + 1), q.y, sb);
+        sb = __builtin_fmaf(qbyte(b.q, 4 * v + 2), q.z, sb);
+        sb = __builtin_fmaf(qbyte(b.q, 4 * v + 3), q.w, sb);
+      }
       acc += __builtin_fmaf(b.scale, sb, -b.offset * xs[b.e >> 4]);
     }
   }
@@ -56,39 +72,52 @@ __device__ __forceinline__ float block_dot(const typename Blk<T>::R& r, cfloat* 
 template <int T, int WAVES>
 __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs p) {
   using B = Blk<T>;
-  extern __shared__ float smem[];          // xs16[kb_per_split * QK/16], then red[WAVES*64]
+  // LDS: x[kb_per_split * QK] (zero past K), xs16[kb_per_split * QK / 16], red[WAVES * 64]
+  extern __shared__ __attribute__((aligned(16))) float smem[];
   const int tile = blockIdx.x;
   const int split = blockIdx.y;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int kb0 = split * p.kb_per_split;
   const int kb1 = min(p.KB, kb0 + p.kb_per_split);
-  float* xs16 = smem;
-  float* red = smem + p.kb_per_split * (B::QK / 16);
+  const int nx = p.kb_per_split * B::QK;
+  float* xl = smem;
+  float* xs16 = smem + nx;
+  float* red = xs16 + nx / 16;
 
-  // per-16 sums of x over this split's columns (zero beyond K)
-  const int n16 = (kb1 - kb0) * (B::QK / 16);
-  for (int i = threadIdx.x; i < n16; i += WAVES * 64) {
-    const int k = kb0 * B::QK + 16 * i;
+  // the first block's planes go out before anything else
+  const uint8_t* tbase = p.W + (size_t)tile * p.KB * B::SLAB;
+  int kb = kb0 + wave;
+  typename B::R cur, nxt;
+  if (kb < kb1) B::load(tbase + (size_t)kb * B::SLAB, lane, cur);
+
+  // stage this split's x (float4, zero past K) and its per-16 sums
+  const int x0 = kb0 * B::QK;
+  const int nv = (kb1 - kb0) * B::QK / 4;
+  for (int i = threadIdx.x; i < nv; i += WAVES * 64) {
+    const int k = x0 + 4 * i;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (k < p.K) v = *reinterpret_cast<const float4*>(p.x + k);
+    reinterpret_cast<float4*>(xl)[i] = v;
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < nv / 4; i += WAVES * 64) {
+    const float4* q = reinterpret_cast<const float4*>(xl + 16 * i);
     float s = 0.0f;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) s += (k + j < p.K) ? p.x[k + j] : 0.0f;
+    for (int v = 0; v < 4; ++v) { const float4 t = q[v]; s += t.x; s += t.y; s += t.z; s += t.w; }
     xs16[i] = s;
   }
   __syncthreads();
 
-  const uint8_t* tbase = p.W + (size_t)tile * p.KB * B::SLAB;
   const int kb_full = min(kb1, p.K / B::QK);   // columns with no element beyond K
   float acc = 0.0f;
-  int kb = kb0 + wave;
   // software pipeline: the planes of the next block column are in flight while this one
   // is decoded
-  typename B::R cur, nxt;
-  if (kb < kb1) B::load(tbase + (size_t)kb * B::SLAB, lane, cur);
   for (; kb < kb1; kb += WAVES) {
     const int kn = kb + WAVES;
     if (kn < kb1) B::load(tbase + (size_t)kn * B::SLAB, lane, nxt);
-    cfloat* xb = (cfloat*)(p.x + (size_t)kb * B::QK);
+    const float* xb = xl + (kb - kb0) * B::QK;
     const float* xs = xs16 + (kb - kb0) * (B::QK / 16);
     if (kb < kb_full) acc += block_dot<T, false>(cur, xb, xs, B::QK);
     else acc += block_dot<T, true>(cur, xb, xs, p.K - kb * B::QK);
@@ -121,12 +150,14 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs p) {
   }
   __syncthreads();
   if (!last) return;
-  __threadfence();
+  // acquire: the agent-scope fence invalidates this CU's vector L1, so the plain loads below
+  // see every split's partial (all published before their arrival increment)
+  __atomic_thread_fence(__ATOMIC_ACQUIRE);
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   if (wave == 0) {
+    const float* part = p.partial + row;
     float s = 0.0f;
-    for (int sp = 0; sp < p.splits; ++sp)
-      s += __hip_atomic_load(&p.partial[(size_t)sp * p.m_pad + row], __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
+    for (int sp = 0; sp < p.splits; ++sp) s += part[(size_t)sp * p.m_pad];
     if (row < p.m) p.y[row] = s;
   }
   if (threadIdx.x == 0) p.counters[tile] = 0u;
@@ -157,7 +188,8 @@ __global__ __launch_bounds__(64) void dequant_kernel(const uint8_t* __restrict__
 
 template <int T>
 static hipError_t launch_gemv_t(const GemvArgs& a, int waves, hipStream_t s) {
-  const int xs = a.kb_per_split * (Blk<T>::QK / 16);
+  const int nx = a.kb_per_split * Blk<T>::QK;
+  const int xs = nx + nx / 16;
   dim3 grid((unsigned)a.tiles, (unsigned)a.splits);
   if (waves == 4) {
     const size_t shm = (size_t)(xs + 4 * 64) * sizeof(float);

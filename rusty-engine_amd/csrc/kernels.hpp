@@ -21,8 +21,9 @@ hipError_t launch_gemv(uint32_t type, const GemvArgs& a, int waves, hipStream_t 
 hipError_t launch_dequant(uint32_t type, const uint8_t* W, float* out, int m, int n, int KB, int tiles,
                           hipStream_t s);
 
-// GEMM tile geometry: BM weight rows x BN activation rows per workgroup, K steps of 128.
-constexpr int kGemmBM = 128, kGemmBN = 128, kGemmBK = 128;
+// GEMM: K steps of 128 elements; square tiles of 128 or 64 (weight rows x activation rows).
+constexpr int kGemmBK = 128;
+constexpr int kMoeTile = 64;   // tile of the grouped (MoE) launches
 
 // Work item of a grouped launch (MoE): one BM x BN output tile of one expert.
 struct GemmTask {
@@ -44,8 +45,10 @@ struct GemmArgs {
   const int* xrow;         // grouped: X row of gathered row p (nullptr = p itself)
 };
 
-// mode 0 = bf16 MFMA with f32 accumulation, 1 = f32 MFMA (strict parity)
-hipError_t launch_gemm(uint32_t type, int mode, const GemmArgs& a, int ntasks, hipStream_t s);
+// mode 0 = bf16 MFMA with f32 accumulation, 1 = f32 MFMA (strict parity); tile 128 or 64
+hipError_t launch_gemm(uint32_t type, int mode, const GemmArgs& a, int ntasks, int tile, hipStream_t s);
+// tile a dense m x n-row launch uses
+int gemm_tile_for(int m, int n);
 
 // MoE helpers
 hipError_t launch_swiglu(const float* g, const float* u, float* h, size_t n, hipStream_t s);

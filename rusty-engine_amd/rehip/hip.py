@@ -37,6 +37,12 @@ def hip() -> C.CDLL:
         H.hipEventSynchronize.argtypes = [C.c_void_p]
         H.hipEventElapsedTime.argtypes = [C.POINTER(C.c_float), C.c_void_p, C.c_void_p]
         H.hipGetDeviceCount.argtypes = [C.POINTER(C.c_int)]
+        H.hipStreamBeginCapture.argtypes = [C.c_void_p, C.c_int]
+        H.hipStreamEndCapture.argtypes = [C.c_void_p, C.POINTER(C.c_void_p)]
+        H.hipGraphInstantiate.argtypes = [C.POINTER(C.c_void_p), C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t]
+        H.hipGraphLaunch.argtypes = [C.c_void_p, C.c_void_p]
+        H.hipGraphExecDestroy.argtypes = [C.c_void_p]
+        H.hipGraphDestroy.argtypes = [C.c_void_p]
         _hip = H
     return _hip
 
@@ -132,6 +138,35 @@ class Event:
         ms = C.c_float()
         check(hip().hipEventElapsedTime(C.byref(ms), C.c_void_p(self.ev), C.c_void_p(end.ev)))
         return ms.value
+
+
+class Graph:
+    """A HIP graph captured from the calls `fn()` makes on `stream` (stream capture), then
+    instantiated for replay. Captured work must not contain memset nodes."""
+
+    def __init__(self, stream: Stream, fn):
+        H = hip()
+        check(H.hipStreamBeginCapture(C.c_void_p(stream.cuda_stream), 0))   # hipStreamCaptureModeGlobal
+        try:
+            fn()
+        finally:
+            g = C.c_void_p()
+            rc = H.hipStreamEndCapture(C.c_void_p(stream.cuda_stream), C.byref(g))
+        check(rc)
+        self.graph = g.value
+        ex = C.c_void_p()
+        check(H.hipGraphInstantiate(C.byref(ex), C.c_void_p(self.graph), None, None, 0))
+        self.exec = ex.value
+        self.stream = stream
+
+    def launch(self) -> None:
+        check(hip().hipGraphLaunch(C.c_void_p(self.exec), C.c_void_p(self.stream.cuda_stream)))
+
+    def destroy(self) -> None:
+        if self.exec:
+            hip().hipGraphExecDestroy(C.c_void_p(self.exec))
+            hip().hipGraphDestroy(C.c_void_p(self.graph))
+            self.exec = self.graph = None
 
 
 def synchronize() -> None:
