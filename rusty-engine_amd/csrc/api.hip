@@ -117,7 +117,6 @@ struct re_qmat {
   MatGeom g{};
   uint8_t* d_w = nullptr;
   float* d_partial = nullptr;
-  unsigned* d_counters = nullptr;
   int splits = 1, kb_per_split = 1, waves = 4;
   std::mutex mu;
   hipStream_t stream = nullptr;
@@ -142,20 +141,27 @@ size_t env_size(const char* name, size_t dflt) {
   return (v && *v) ? (size_t)std::strtoull(v, nullptr, 10) : dflt;
 }
 
+// GEMV launch shape. Work units are 32-quant chunks of a 64-row tile (KB * chunks-per-block per
+// tile); one unit costs a wave about 110 VALU instructions (~450 cycles). A tile's units are
+// split over several workgroups (partials + reduce kernel, ~2.5 us extra) only when one CU would
+// otherwise spend more than ~6000 cycles on them; waves per workgroup are chosen so that every
+// wave holds at most 4 units (all of them in flight at once) where 16 waves allow it.
 void plan_gemv(re_qmat* q) {
-  const size_t tiles = q->g.tiles, kb = q->g.kb;
-  size_t want = (1024 + tiles - 1) / tiles;
-  // a cross-workgroup split costs an agent-scope release per workgroup (an L2 write-back on
-  // gfx950), so rows are split only when they are long and the tiles too few to fill the chip
-  if (q->g.n < 2048) want = 1;
-  want = std::min(want, env_size("REHIP_GEMV_MAX_SPLITS", want));
+  const size_t kb = q->g.kb;
+  const size_t nch = q->g.qk == 256 ? 8 : 1;
+  const size_t units = kb * nch;
+  const size_t cycles = units * 112;              // per-CU VALU cycles for one tile (4 SIMDs)
+  size_t want = cycles > 6000 ? (cycles + 2399) / 2400 : 1;
   // a split stages its slice of x in LDS: keep it within 64 KiB (16384 floats)
   const size_t max_per = std::max<size_t>(1, 16384 / (size_t)q->g.qk);
   want = std::max<size_t>({(size_t)1, std::min(want, kb), (kb + max_per - 1) / max_per});
-  size_t per = (kb + want - 1) / want;
+  want = std::min(want, std::max<size_t>(1, env_size("REHIP_GEMV_MAX_SPLITS", want)));
+  const size_t per = (kb + want - 1) / want;
   q->kb_per_split = (int)per;
   q->splits = (int)((kb + per - 1) / per);
-  q->waves = per >= 4 ? 4 : 1;
+  const size_t per_wg = per * nch;
+  q->waves = per_wg <= 16 ? 4 : per_wg <= 32 ? 8 : 16;
+  if (const size_t w = env_size("REHIP_GEMV_WAVES", 0)) q->waves = (int)w;
 }
 
 int upload_tiled(const MatGeom& g, const uint8_t* bytes, uint8_t* d_dst) {
@@ -176,7 +182,6 @@ int gemv_enqueue(re_qmat* q, const float* d_x, float* d_y, hipStream_t s) {
   a.x = d_x;
   a.y = d_y;
   a.partial = q->d_partial;
-  a.counters = q->d_counters;
   a.m = (int)q->g.m;
   a.m_pad = (int)(q->g.tiles * kTileRows);
   a.K = (int)q->g.n;
@@ -263,11 +268,8 @@ int re_qmat_create(uint32_t ggml_type, const uint8_t* bytes, size_t nbytes, size
   if ((rc = upload_tiled(g, bytes, q->d_w))) return cleanup(rc);
   const size_t m_pad = g.tiles * kTileRows;
   if (q->splits > 1) {
-    if (hipMalloc(&q->d_partial, (size_t)q->splits * m_pad * sizeof(float)) != hipSuccess ||
-        hipMalloc(&q->d_counters, g.tiles * sizeof(unsigned)) != hipSuccess)
+    if (hipMalloc(&q->d_partial, (size_t)q->splits * m_pad * sizeof(float)) != hipSuccess)
       return cleanup(fail(RE_ERR_HIP, "hipMalloc of split scratch failed"));
-    if (hipMemset(q->d_counters, 0, g.tiles * sizeof(unsigned)) != hipSuccess)
-      return cleanup(fail(RE_ERR_HIP, "hipMemset of split counters failed"));
   }
   if (hipStreamCreateWithFlags(&q->stream, hipStreamNonBlocking) != hipSuccess)
     return cleanup(fail(RE_ERR_HIP, "hipStreamCreate failed"));
@@ -280,7 +282,6 @@ void re_qmat_destroy(re_qmat* q) {
   if (q->stream) (void)hipStreamSynchronize(q->stream);
   if (q->d_w) (void)hipFree(q->d_w);
   if (q->d_partial) (void)hipFree(q->d_partial);
-  if (q->d_counters) (void)hipFree(q->d_counters);
   q->sx.release();
   q->sy.release();
   if (q->stream) (void)hipStreamDestroy(q->stream);

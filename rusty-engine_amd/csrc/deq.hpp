@@ -51,6 +51,12 @@ struct Run {
   int e;            // element offset of the run inside the block
 };
 
+// Quants of at most 4 bits (Q4_0, Q4_K): a byte 0000qqqq read as an OCP E4M3 value is exactly
+// q * 2^-9 (subnormal for q < 8, exponent 1 for q >= 8), so v_cvt_pk_f32_fp8 turns two of them
+// into floats with one instruction; the 2^9 goes into the run's scale (exact).
+template <int T> inline constexpr bool kNibble = (T == T_Q4_0 || T == T_Q4_K);
+constexpr float kNibbleUnit = 1.0f / 512.0f;
+
 // Quant bias of the types whose reference formula multiplies a signed quant, (q - bias) * d
 // (Q4_0 8, Q5_0 16, Q8_0 128, Q6_K 32); 0 for Q4_K/Q5_K (d*sc*q - dmin*m).
 template <int T> inline constexpr int kBias = 0;

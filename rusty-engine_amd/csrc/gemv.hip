@@ -6,13 +6,14 @@
 // same element), so it is fetched with scalar loads; only the weight planes use vector loads,
 // each a contiguous 1 KiB (16-byte planes) / 256 B / 128 B per wavefront.
 //
-// Per block the lane decodes chunk after chunk (deq.hpp) and folds
+// Per 32-quant chunk the lane folds
 //   scale * sum(q_i x_i) - offset * sum(x_i)
 // where sum(x_i) over each 16-element run comes from a per-workgroup table in LDS.
 //
-// Split reduction is deterministic: each split writes its partial row sums, the last workgroup
-// of a tile (arrival counter) adds the partials in split order, writes y and re-arms the
-// counter for the next launch.
+// Long rows of small matrices are split over several workgroups so the whole chip works on
+// them. Each split writes its partial row sums with plain stores and a second small kernel adds
+// them in split order (deterministic): the kernel boundary publishes the partials, which is far
+// cheaper on gfx950 than an agent-scope release per workgroup (an L2 write-back).
 #include <hip/hip_runtime.h>
 
 #include "deq.hpp"
@@ -20,58 +21,47 @@
 
 namespace rehip {
 
-// x comes from LDS: every lane of the wave reads the same address (a broadcast), so a run of
-// 16 activations is four ds_read_b128.
-template <int T, bool GUARD>
-__device__ __forceinline__ float block_dot(const typename Blk<T>::R& r, const float* __restrict__ xb,
-                                           const float* __restrict__ xs, int valid) {
-  using B = Blk<T>;
-  float acc = 0.0f;
+typedef __attribute__((__vector_size__(2 * sizeof(float)))) float f32x2_t;
+
+// Dot of one decoded run (16 quants) with x from LDS: every lane of the wave reads the same
+// address (a broadcast), so 16 activations are four ds_read_b128.
+template <int T>
+__device__ __forceinline__ float run_dot(const Run& r, const float* __restrict__ xb,
+                                         const float* __restrict__ xs) {
+  const float4* xv = reinterpret_cast<const float4*>(xb + r.e);
+  float s = 0.0f;
 #pragma unroll
-  for (int c = 0; c < B::NCH; ++c) {
-    // one chunk's 32 activations live at a time: stops the scheduler from hoisting all of a
-    // super-block's LDS reads (256 values) above the first chunk
-    if (B::NCH > 1) asm volatile("" ::: "memory");
-    Run a, b;
-    B::decode(r, c, a, b);
-    // ... and the same for the quant-to-float conversions: pin this chunk's quant words here
-    if (B::NCH > 1)
-      asm volatile("" : "+v"(a.q[0]), "+v"(a.q[1]), "+v"(a.q[2]), "+v"(a.q[3]),
-                        "+v"(b.q[0]), "+v"(b.q[1]), "+v"(b.q[2]), "+v"(b.q[3]));
-    // K is a multiple of 32, so a 16-element run is either wholly inside K or wholly past it
-    if (!GUARD || a.e < valid) {
-      const float4* xv = reinterpret_cast<const float4*>(xb + a.e);
-      float sa = 0.0f;
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const float4 q = xv[v];
-        sa = __builtin_fmaf(qbyte(a.q, 4 * v + 0), q.x, sa);
-        sa = __builtin_fmaf(qbyte(a.q, 4 * v + 1), q.y, sa);
-        sa = __builtin_fmaf(qbyte(a.q, 4 * v + 2), q.z, sa);
-        sa = __builtin_fmaf(qbyte(a.q, 4 * v + 3), q.w, sa);
-      }
-      acc += __builtin_fmaf(a.scale, sa, -a.offset * xs[a.e >> 4]);
-    }
-    if (!GUARD || b.e < valid) {
-      const float4* xv = reinterpret_cast<const float4*>(xb + b.e);
-      float sb = 0.0f;
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const float4 q = xv[v];
-        sb = __builtin_fmaf(qbyte(b.q, 4 * v + 0), q.x, sb);
-        sb = __builtin_fmaf(qbyte(b.q, 4 * v + 1), q.y, sb);
-        sb = __builtin_fmaf(qbyte(b.q, 4 * v + 2), q.z, sb);
-        sb = __builtin_fmaf(qbyte(b.q, 4 * v + 3), q.w, sb);
-      }
-      acc += __builtin_fmaf(b.scale, sb, -b.offset * xs[b.e >> 4]);
+  for (int v = 0; v < 4; ++v) {
+    const float4 q = xv[v];
+    if constexpr (kNibble<T>) {
+      const f32x2_t lo = __builtin_amdgcn_cvt_pk_f32_fp8(r.q[v], false);   // quants 4v, 4v+1
+      const f32x2_t hi = __builtin_amdgcn_cvt_pk_f32_fp8(r.q[v], true);    // quants 4v+2, 4v+3
+      s = __builtin_fmaf(lo[0], q.x, s);
+      s = __builtin_fmaf(lo[1], q.y, s);
+      s = __builtin_fmaf(hi[0], q.z, s);
+      s = __builtin_fmaf(hi[1], q.w, s);
+    } else {
+      s = __builtin_fmaf(qbyte(r.q, 4 * v + 0), q.x, s);
+      s = __builtin_fmaf(qbyte(r.q, 4 * v + 1), q.y, s);
+      s = __builtin_fmaf(qbyte(r.q, 4 * v + 2), q.z, s);
+      s = __builtin_fmaf(qbyte(r.q, 4 * v + 3), q.w, s);
     }
   }
-  return acc;
+  const float scale = kNibble<T> ? r.scale * 512.0f : r.scale;
+  return __builtin_fmaf(scale, s, -r.offset * xs[r.e >> 4]);
 }
+
+// Work unit = one 32-quant chunk (two 16-element runs) of one block column for the 64 rows of
+// a tile. Units of a tile are numbered u = kb * NCH + c; a workgroup owns the units of its
+// block-column range, its waves take every WAVES-th unit, and each wave keeps DEPTH units'
+// raw planes in flight (a ring of registers) so small matrices issue every load up front.
+constexpr int kGemvDepth = 4;
 
 template <int T, int WAVES>
 __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs p) {
   using B = Blk<T>;
+  constexpr int NCH = B::NCH;
+  constexpr int D = kGemvDepth;
   // LDS: x[kb_per_split * QK] (zero past K), xs16[kb_per_split * QK / 16], red[WAVES * 64]
   extern __shared__ __attribute__((aligned(16))) float smem[];
   const int tile = blockIdx.x;
@@ -85,11 +75,16 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs p) {
   float* xs16 = smem + nx;
   float* red = xs16 + nx / 16;
 
-  // the first block's planes go out before anything else
+  // the first DEPTH units' planes go out before anything else
   const uint8_t* tbase = p.W + (size_t)tile * p.KB * B::SLAB;
-  int kb = kb0 + wave;
-  typename B::R cur, nxt;
-  if (kb < kb1) B::load(tbase + (size_t)kb * B::SLAB, lane, cur);
+  const int u_end = kb1 * NCH;
+  const int u0 = kb0 * NCH + wave;
+  typename B::CR ring[D];
+#pragma unroll
+  for (int i = 0; i < D; ++i) {
+    const int u = u0 + i * WAVES;
+    if (u < u_end) B::load_chunk(tbase + (size_t)(u / NCH) * B::SLAB, lane, u % NCH, ring[i]);
+  }
 
   // stage this split's x (float4, zero past K) and its per-16 sums
   const int x0 = kb0 * B::QK;
@@ -110,57 +105,51 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs p) {
   }
   __syncthreads();
 
-  const int kb_full = min(kb1, p.K / B::QK);   // columns with no element beyond K
   float acc = 0.0f;
-  // software pipeline: the planes of the next block column are in flight while this one
-  // is decoded
-  for (; kb < kb1; kb += WAVES) {
-    const int kn = kb + WAVES;
-    if (kn < kb1) B::load(tbase + (size_t)kn * B::SLAB, lane, nxt);
-    const float* xb = xl + (kb - kb0) * B::QK;
-    const float* xs = xs16 + (kb - kb0) * (B::QK / 16);
-    if (kb < kb_full) acc += block_dot<T, false>(cur, xb, xs, B::QK);
-    else acc += block_dot<T, true>(cur, xb, xs, p.K - kb * B::QK);
-    cur = nxt;
+  for (int base = u0; base < u_end; base += D * WAVES) {
+#pragma unroll
+    for (int i = 0; i < D; ++i) {
+      const int u = base + i * WAVES;
+      if (u < u_end) {
+        const int kb = u / NCH, c = u - kb * NCH;
+        Run a, b;
+        B::decode_chunk(ring[i], c, a, b);
+        const int un = u + D * WAVES;
+        if (un < u_end) B::load_chunk(tbase + (size_t)(un / NCH) * B::SLAB, lane, un % NCH, ring[i]);
+        const float* xb = xl + (kb - kb0) * B::QK;
+        const float* xs = xs16 + (kb - kb0) * (B::QK / 16);
+        const int valid = p.K - kb * B::QK;   // K is a multiple of 32: a run is wholly in or out
+        if (a.e < valid) acc += run_dot<T>(a, xb, xs);
+        if (b.e < valid) acc += run_dot<T>(b, xb, xs);
+      }
+    }
   }
 
   // fixed-order reduction over the waves
   red[threadIdx.x] = acc;
   __syncthreads();
-  const int row = tile * 64 + lane;
-  if (p.splits == 1) {
-    if (wave == 0) {
-      float s = red[lane];
-      for (int w = 1; w < WAVES; ++w) s += red[w * 64 + lane];
-      if (row < p.m) p.y[row] = s;
-    }
-    return;
-  }
   if (wave == 0) {
     float s = red[lane];
+#pragma unroll
     for (int w = 1; w < WAVES; ++w) s += red[w * 64 + lane];
-    p.partial[(size_t)split * p.m_pad + row] = s;
+    const int row = tile * 64 + lane;
+    if (p.splits == 1) {
+      if (row < p.m) p.y[row] = s;
+    } else {
+      p.partial[(size_t)split * p.m_pad + row] = s;
+    }
   }
-  __threadfence();
-  __syncthreads();
-  __shared__ int last;
-  if (threadIdx.x == 0) {
-    const unsigned prev = atomicAdd(&p.counters[tile], 1u);
-    last = (prev == (unsigned)(p.splits - 1));
-  }
-  __syncthreads();
-  if (!last) return;
-  // acquire: the agent-scope fence invalidates this CU's vector L1, so the plain loads below
-  // see every split's partial (all published before their arrival increment)
-  __atomic_thread_fence(__ATOMIC_ACQUIRE);
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-  if (wave == 0) {
-    const float* part = p.partial + row;
-    float s = 0.0f;
-    for (int sp = 0; sp < p.splits; ++sp) s += part[(size_t)sp * p.m_pad];
-    if (row < p.m) p.y[row] = s;
-  }
-  if (threadIdx.x == 0) p.counters[tile] = 0u;
+}
+
+// y[r] = sum over splits, in split order, of partial[split][r]
+__global__ __launch_bounds__(256) void gemv_reduce_kernel(const float* __restrict__ partial,
+                                                          float* __restrict__ y, int m, int m_pad,
+                                                          int splits) {
+  const int r = blockIdx.x * 256 + threadIdx.x;
+  if (r >= m) return;
+  float s = 0.0f;
+  for (int sp = 0; sp < splits; ++sp) s += partial[(size_t)sp * m_pad + r];
+  y[r] = s;
 }
 
 // Bit-exact dequant of the tiled weights into a row-major f32 matrix [m x n].
@@ -191,13 +180,17 @@ static hipError_t launch_gemv_t(const GemvArgs& a, int waves, hipStream_t s) {
   const int nx = a.kb_per_split * Blk<T>::QK;
   const int xs = nx + nx / 16;
   dim3 grid((unsigned)a.tiles, (unsigned)a.splits);
-  if (waves == 4) {
-    const size_t shm = (size_t)(xs + 4 * 64) * sizeof(float);
-    hipLaunchKernelGGL((gemv_kernel<T, 4>), grid, dim3(256), shm, s, a);
+  if (waves == 16) {
+    hipLaunchKernelGGL((gemv_kernel<T, 16>), grid, dim3(1024), (size_t)(xs + 16 * 64) * sizeof(float), s, a);
+  } else if (waves == 8) {
+    hipLaunchKernelGGL((gemv_kernel<T, 8>), grid, dim3(512), (size_t)(xs + 8 * 64) * sizeof(float), s, a);
   } else {
-    const size_t shm = (size_t)(xs + 64) * sizeof(float);
-    hipLaunchKernelGGL((gemv_kernel<T, 1>), grid, dim3(64), shm, s, a);
+    hipLaunchKernelGGL((gemv_kernel<T, 4>), grid, dim3(256), (size_t)(xs + 4 * 64) * sizeof(float), s, a);
   }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || a.splits == 1) return e;
+  hipLaunchKernelGGL(gemv_reduce_kernel, dim3((unsigned)((a.m + 255) / 256)), dim3(256), 0, s, a.partial, a.y,
+                     a.m, a.m_pad, a.splits);
   return hipGetLastError();
 }
 

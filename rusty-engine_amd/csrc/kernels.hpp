@@ -11,12 +11,12 @@ struct GemvArgs {
   const uint8_t* W;      // tiled slabs of one matrix
   const float* x;        // K floats
   float* y;              // m floats
-  float* partial;        // splits * m_pad floats (splits > 1)
-  unsigned* counters;    // tiles counters, zero between launches (splits > 1)
+  float* partial;        // splits * m_pad floats (splits > 1), reduced by a second kernel
   int m, m_pad, K, KB, tiles;
   int kb_per_split, splits;
 };
 
+// waves per workgroup: 4 or 8
 hipError_t launch_gemv(uint32_t type, const GemvArgs& a, int waves, hipStream_t s);
 hipError_t launch_dequant(uint32_t type, const uint8_t* W, float* out, int m, int n, int KB, int tiles,
                           hipStream_t s);

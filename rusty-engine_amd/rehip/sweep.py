@@ -18,7 +18,7 @@ import numpy as np
 from . import GEOM, QMat, TYPE_NAMES, init
 from . import hip, synth
 
-PROJECTIONS = [("q", 896, 896), ("o", 896, 896), ("k", 128, 896), ("v", 128, 896),
+PROJECTIONS = [("tiny", 64, 32), ("q", 896, 896), ("o", 896, 896), ("k", 128, 896), ("v", 128, 896),
                ("gate", 4864, 896), ("up", 4864, 896), ("down", 896, 4864), ("lm_head", 151936, 896)]
 HBM_PEAK_GBS = 8000.0
 
