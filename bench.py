@@ -35,6 +35,19 @@ M, K = 896, 4864
 MALL_BYTES = 256 << 20
 
 
+def measured_traffic():
+    """HBM bytes per GEMV launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE passes
+    (profiles/gemv_q6k_896x4864_traffic.txt, copy-calibrated), or None."""
+    path = os.path.join(ROOT, "profiles", "gemv_q6k_896x4864_traffic.txt")
+    try:
+        for line in open(path):
+            if line.startswith("gemv_traffic_bytes_per_launch="):
+                return int(line.split("=")[1].split()[0])
+    except OSError:
+        pass
+    return None
+
+
 def algorithmic_bytes(t, m, k, n):
     import rehip
     qk, bb = rehip.GEOM[t]
@@ -49,6 +62,8 @@ def main():
     ap.add_argument("--gemm-steps", type=int, default=200)
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="bound on the CPU-baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="first run one 256 MiB device-to-device copy (calibrates profiler byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
@@ -61,6 +76,12 @@ def main():
     t = rehip.Q6_K
     rehip.init()
     stream = hip.Stream()
+    if args.copy_probe:
+        src, dst = hip.DeviceBuffer(256 << 20), hip.DeviceBuffer(256 << 20)
+        hip.check(hip.hip().hipMemcpy(hip.C.c_void_p(dst.ptr), hip.C.c_void_p(src.ptr), 256 << 20, hip.D2D))
+        hip.synchronize()
+        src.free()
+        dst.free()
 
     # ---- N = 1 GEMV over rotated weight copies -------------------------------------------------
     rng = np.random.default_rng(201 + 1)
@@ -172,7 +193,7 @@ def main():
         "config": {"workload": "Q6_K down projection W[896x4864], X[N x 4864] f32, N=1 GEMV (+ N=64/961 GEMM)",
                    "weight_copies_rotated": copies, "graph_replay": True},
         "roofline": {"bound": "hbm", "achieved": round(gemv_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gemv_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(gemv_gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                      "algorithmic_bytes_per_launch": gemv_bytes, "avg_launch_us": gemv_ms * 1e3},
         "gemm": gemm,
         "parity_ok": parity_ok and all(v["rel_err_vs_f64"] <= 1e-2 for v in gemm.values()),

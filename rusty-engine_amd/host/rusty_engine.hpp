@@ -1,0 +1,202 @@
+// C++ host-side mirror of rusty-engine's quantized-matrix interface, over librehip's C ABI.
+//
+// Callers written against the reference keep their shape:
+//   QMat::from_bytes(ggml_type, bytes, m, n)   src/qmat.rs:52-59 (uploads and repacks once)
+//   q.matvec(x) -> y[m]                        src/qmat.rs:80
+//   q.matmul(x, rows) -> Y[rows x m]           src/qmat.rs:169
+//   q.rows(), q.cols()                         src/qmat.rs:62-73
+//   top_k / top_k_sigmoid / route / silu       src/moe.rs:44-125 (host router)
+//   moe_layer_forward(...)                     src/moe.rs:360-388, experts on the GPU
+// Failures surface as EngineError (src/core.rs:56-68) thrown with librehip's message; the
+// reference panics on unknown types at call time, this layer throws at construction.
+#pragma once
+
+#include <algorithm>
+#include <cmath>
+#include <cstdint>
+#include <memory>
+#include <numeric>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "../../include/rehip.h"
+
+namespace rusty_engine {
+
+struct EngineError : std::runtime_error {
+  int code;
+  EngineError(int c, const std::string& m) : std::runtime_error(m), code(c) {}
+};
+
+inline void check(int rc) {
+  if (rc != RE_OK) throw EngineError(rc, re_last_error());
+}
+
+enum class Precision { Bf16Mfma = RE_MODE_BF16, F32Strict = RE_MODE_F32 };
+
+// A GPU-resident quantized weight matrix W[m x n] (the Quant variant of QMat, qmat.rs:30-42).
+class QMat {
+ public:
+  static QMat from_bytes(uint32_t ggml_type, const std::vector<uint8_t>& bytes, size_t m, size_t n) {
+    re_qmat* h = nullptr;
+    check(re_qmat_create(ggml_type, bytes.data(), bytes.size(), m, n, &h));
+    return QMat(h);
+  }
+
+  size_t rows() const { return re_qmat_rows(h_.get()); }
+  size_t cols() const { return re_qmat_cols(h_.get()); }
+  uint32_t ggml_type() const { return re_qmat_type(h_.get()); }
+
+  // W[m x n] * x[n] -> out[m]; f32 accumulation on the GPU
+  std::vector<float> matvec(const std::vector<float>& x) const {
+    if (x.size() != cols()) throw EngineError(RE_ERR_SIZE, "matvec: input width mismatch");
+    std::vector<float> y(rows());
+    check(re_qmat_matvec(h_.get(), x.data(), y.data()));
+    return y;
+  }
+
+  // W[m x n] * X[rows x n] -> Out[rows x m] (row-major, out[row*m + r])
+  std::vector<float> matmul(const std::vector<float>& x, size_t nrows,
+                            Precision prec = Precision::Bf16Mfma) const {
+    if (x.size() != nrows * cols()) throw EngineError(RE_ERR_SIZE, "matmul: X rows x n mismatch");
+    std::vector<float> y(nrows * rows());
+    check(re_qmat_matmul(h_.get(), x.data(), nrows, y.data(), static_cast<int>(prec)));
+    return y;
+  }
+
+  re_qmat* raw() const { return h_.get(); }
+
+ private:
+  explicit QMat(re_qmat* h) : h_(h, re_qmat_destroy) {}
+  std::shared_ptr<re_qmat> h_;
+};
+
+// ---- router (src/moe.rs:11-125) -------------------------------------------------------------
+struct ExpertScore {
+  size_t id;
+  float weight;
+};
+
+enum class Gate { Softmax, Sigmoid };
+
+struct RouterConfig {
+  Gate gate = Gate::Softmax;
+  size_t top_k = 2;
+};
+
+inline float sigmoid(float x) { return 1.0f / (1.0f + std::exp(-x)); }
+inline float silu(float x) { return x * sigmoid(x); }
+
+inline void softmax_in_place(std::vector<float>& v) {
+  float mx = -INFINITY;
+  for (float a : v) mx = std::fmax(mx, a);
+  for (float& a : v) a = std::exp(a - mx);
+  float sum = -0.0f;
+  for (float a : v) sum = sum + a;
+  if (sum != 0.0f)
+    for (float& a : v) a /= sum;
+}
+
+// indices by score, descending, ties in ascending index order (a stable sort)
+inline std::vector<size_t> order_desc(const std::vector<float>& s) {
+  std::vector<size_t> idx(s.size());
+  std::iota(idx.begin(), idx.end(), 0);
+  std::stable_sort(idx.begin(), idx.end(), [&](size_t a, size_t b) { return s[a] > s[b]; });
+  return idx;
+}
+
+// keep the k best, weights = softmax over the chosen scores (moe.rs:75-93)
+inline std::vector<ExpertScore> top_k(const std::vector<float>& scores, size_t k) {
+  if (scores.empty()) return {};
+  k = std::min(k, scores.size());
+  const auto idx = order_desc(scores);
+  std::vector<float> w(k);
+  for (size_t i = 0; i < k; ++i) w[i] = scores[idx[i]];
+  softmax_in_place(w);
+  std::vector<ExpertScore> out(k);
+  for (size_t i = 0; i < k; ++i) out[i] = {idx[i], w[i]};
+  return out;
+}
+
+// per-expert sigmoid, keep k, renormalize over the chosen (moe.rs:97-117)
+inline std::vector<ExpertScore> top_k_sigmoid(const std::vector<float>& scores, size_t k) {
+  if (scores.empty()) return {};
+  std::vector<float> sig(scores.size());
+  for (size_t i = 0; i < scores.size(); ++i) sig[i] = sigmoid(scores[i]);
+  k = std::min(k, sig.size());
+  const auto idx = order_desc(sig);
+  float wsum = -0.0f;
+  for (size_t i = 0; i < k; ++i) wsum = wsum + sig[idx[i]];
+  std::vector<ExpertScore> out(k);
+  for (size_t i = 0; i < k; ++i) out[i] = {idx[i], wsum == 0.0f ? 0.0f : sig[idx[i]] / wsum};
+  return out;
+}
+
+inline std::vector<ExpertScore> route(const std::vector<float>& logits, RouterConfig cfg) {
+  return cfg.gate == Gate::Softmax ? top_k(logits, cfg.top_k) : top_k_sigmoid(logits, cfg.top_k);
+}
+
+// ---- MoE experts on the GPU --------------------------------------------------------------------
+// Expert tensors as GGUF stores them: gate/up [n_experts][inter][hidden], down
+// [n_experts][hidden][inter], each row a run of blocks.
+class MoeExperts {
+ public:
+  MoeExperts(uint32_t gate_t, const std::vector<uint8_t>& gate, uint32_t up_t, const std::vector<uint8_t>& up,
+             uint32_t down_t, const std::vector<uint8_t>& down, size_t n_experts, size_t hidden, size_t inter)
+      : n_experts_(n_experts), hidden_(hidden), inter_(inter) {
+    re_moe* h = nullptr;
+    check(re_moe_create(gate_t, gate.data(), gate.size(), up_t, up.data(), up.size(), down_t, down.data(),
+                        down.size(), n_experts, hidden, inter, &h));
+    h_.reset(h, re_moe_destroy);
+  }
+
+  size_t n_experts() const { return n_experts_; }
+  size_t hidden() const { return hidden_; }
+  size_t inter() const { return inter_; }
+
+  // tokens x hidden activations, tokens x k routing -> tokens x hidden
+  std::vector<float> forward(const std::vector<float>& x, size_t tokens, size_t k, const std::vector<uint32_t>& ids,
+                             const std::vector<float>& weights, Precision prec = Precision::Bf16Mfma) const {
+    if (x.size() != tokens * hidden_ || ids.size() != tokens * k || weights.size() != tokens * k)
+      throw EngineError(RE_ERR_SIZE, "moe forward: shape mismatch");
+    std::vector<float> out(tokens * hidden_);
+    check(re_moe_forward(h_.get(), x.data(), tokens, k, ids.data(), weights.data(), out.data(),
+                         static_cast<int>(prec)));
+    return out;
+  }
+
+ private:
+  std::shared_ptr<re_moe> h_;
+  size_t n_experts_, hidden_, inter_;
+};
+
+// One MoE FFN layer on `tokens` hidden vectors (moe.rs:360-388): router logits on the host
+// (router_w is n_experts x hidden f32, `matvec` of moe.rs:271-277), route, then the routed
+// experts' SwiGLU FFNs and the weighted combine in routing order on the GPU.
+inline std::vector<float> moe_layer_forward(const std::vector<float>& hidden, size_t tokens,
+                                            const std::vector<float>& router_w, const MoeExperts& experts,
+                                            RouterConfig cfg, Precision prec = Precision::Bf16Mfma) {
+  const size_t d = experts.hidden(), e = experts.n_experts();
+  if (hidden.size() != tokens * d || router_w.size() != e * d)
+    throw EngineError(RE_ERR_SIZE, "moe_layer_forward: shape mismatch");
+  const size_t k = std::min(cfg.top_k, e);
+  std::vector<uint32_t> ids(tokens * k);
+  std::vector<float> w(tokens * k);
+  std::vector<float> logits(e);
+  for (size_t t = 0; t < tokens; ++t) {
+    for (size_t r = 0; r < e; ++r) {
+      float s = -0.0f;
+      for (size_t c = 0; c < d; ++c) s = s + router_w[r * d + c] * hidden[t * d + c];
+      logits[r] = s;
+    }
+    const auto chosen = route(logits, cfg);
+    for (size_t j = 0; j < k; ++j) {
+      ids[t * k + j] = static_cast<uint32_t>(chosen[j].id);
+      w[t * k + j] = chosen[j].weight;
+    }
+  }
+  return experts.forward(hidden, tokens, k, ids, w, prec);
+}
+
+}  // namespace rusty_engine

@@ -8,6 +8,7 @@ runtime under the same soname, and two HIP runtimes in one process do not initia
 from __future__ import annotations
 
 import ctypes as C
+import ctypes  # noqa: F401  (re-exported for callers building raw calls)
 
 import numpy as np
 

@@ -1,0 +1,208 @@
+// C++ parity tests of the host-side mirror (rusty_engine.hpp) on the GPU, written like the
+// reference's own unit tests (src/qmat.rs:333-399, src/kernel.rs:2080-2584, src/moe.rs:624-801).
+// The CPU oracle (oracle/oracle.h) is the checker. Exit status 0 = all passed.
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <random>
+#include <vector>
+
+#include "../../oracle/oracle.h"
+#include "../../rusty-engine_amd/host/rusty_engine.hpp"
+
+using namespace rusty_engine;
+
+static int g_failed = 0;
+#define CHECK(cond, ...)                                   \
+  do {                                                     \
+    if (!(cond)) {                                         \
+      std::printf("  FAIL %s:%d: ", __FILE__, __LINE__);   \
+      std::printf(__VA_ARGS__);                            \
+      std::printf("\n");                                   \
+      ++g_failed;                                          \
+    }                                                      \
+  } while (0)
+
+// qmat.rs:370-381 fixture: Q8_0 blocks, d = 1, i8 ((bi*31 + j*7) % 251) - 125
+static std::vector<uint8_t> q8_blocks(size_t m, size_t n) {
+  std::vector<uint8_t> a(m * n / 32 * 34);
+  for (size_t bi = 0; bi < m * n / 32; ++bi) {
+    a[bi * 34] = 0x00;
+    a[bi * 34 + 1] = 0x3C;
+    for (int j = 0; j < 32; ++j) a[bi * 34 + 2 + j] = (uint8_t)(int8_t)(((bi * 31 + j * 7) % 251) - 125);
+  }
+  return a;
+}
+
+static std::vector<uint8_t> random_blocks(std::mt19937& g, uint32_t t, size_t m, size_t n) {
+  size_t qk = 0, bb = 0;
+  orc_block_info(t, &qk, &bb);
+  const size_t nb = m * ((n + qk - 1) / qk);
+  std::vector<uint8_t> a(nb * bb);
+  for (auto& v : a) v = (uint8_t)(g() & 0xFF);
+  std::normal_distribution<float> nd(0.f, 1.f);
+  for (size_t b = 0; b < nb; ++b) {
+    uint8_t* blk = &a[b * bb];
+    const uint16_t d = orc_f32_to_f16(std::fabs(nd(g)) * (qk == 32 ? 0.01f : 0.001f));
+    const size_t off = t == ORC_Q6_K ? 208 : 0;
+    blk[off] = d & 0xFF;
+    blk[off + 1] = d >> 8;
+    if (t == ORC_Q4_K || t == ORC_Q5_K) { blk[2] = d & 0xFF; blk[3] = d >> 8; }
+  }
+  return a;
+}
+
+static std::vector<float> randn(std::mt19937& g, size_t n) {
+  std::normal_distribution<float> nd(0.f, 1.f);
+  std::vector<float> v(n);
+  for (auto& x : v) x = nd(g);
+  return v;
+}
+
+// |got - want| <= 2^-10 * sum|w x| per output
+static bool within_f32_bound(uint32_t t, const std::vector<uint8_t>& w, size_t m, size_t n,
+                             const std::vector<float>& x, size_t rows, const std::vector<float>& got,
+                             const std::vector<float>& want) {
+  std::vector<double> absd(rows * m);
+  orc_qmat_absdot(t, w.data(), w.size(), m, n, x.data(), rows, absd.data());
+  for (size_t i = 0; i < rows * m; ++i)
+    if (std::fabs((double)got[i] - (double)want[i]) > std::ldexp(absd[i], -10)) return false;
+  return true;
+}
+
+static void test_matmul_matches_rowwise_matvec() {  // qmat.rs:357-367
+  std::printf("matmul_matches_rowwise_matvec\n");
+  const size_t m = 64, n = 4096, rows = 8;
+  const auto w = q8_blocks(m, n);
+  const auto q = QMat::from_bytes(ORC_Q8_0, w, m, n);
+  CHECK(q.rows() == m && q.cols() == n, "rows/cols");
+  std::vector<float> x(rows * n);
+  for (size_t i = 0; i < x.size(); ++i) x[i] = (float)i * 0.0007f - 1.5f;
+  const auto got = q.matmul(x, rows, Precision::F32Strict);
+  std::vector<float> rowwise;
+  for (size_t r = 0; r < rows; ++r) {
+    const auto y = q.matvec(std::vector<float>(x.begin() + r * n, x.begin() + (r + 1) * n));
+    rowwise.insert(rowwise.end(), y.begin(), y.end());
+  }
+  CHECK(within_f32_bound(ORC_Q8_0, w, m, n, x, rows, got, rowwise), "matmul vs rowwise matvec");
+}
+
+static void test_matvec_is_deterministic() {  // qmat.rs:385-391 (bit-identical whatever the split)
+  std::printf("matvec_is_deterministic_and_matches_serial_oracle\n");
+  const size_t m = 64, n = 4096;
+  const auto w = q8_blocks(m, n);
+  const auto q = QMat::from_bytes(ORC_Q8_0, w, m, n);
+  std::vector<float> x(n);
+  for (size_t i = 0; i < n; ++i) x[i] = (float)i * 0.001f - 2.0f;
+  const auto a = q.matvec(x), b = q.matvec(x);
+  CHECK(std::memcmp(a.data(), b.data(), a.size() * 4) == 0, "two calls differ");
+  std::vector<float> want(m);
+  orc_matvec(ORC_Q8_0, w.data(), m, n, x.data(), want.data());
+  CHECK(within_f32_bound(ORC_Q8_0, w, m, n, x, 1, a, want), "matvec vs oracle");
+}
+
+static void test_every_type_against_oracle() {
+  std::printf("qmat_every_type_matvec_and_matmul_against_oracle\n");
+  std::mt19937 g(42);
+  const uint32_t types[] = {ORC_Q4_0, ORC_Q5_0, ORC_Q8_0, ORC_Q4_K, ORC_Q5_K, ORC_Q6_K};
+  for (uint32_t t : types) {
+    const size_t m = 200, n = 896, rows = 37;
+    const auto w = random_blocks(g, t, m, n);
+    const auto x = randn(g, rows * n);
+    const auto q = QMat::from_bytes(t, w, m, n);
+    std::vector<float> want(rows * m);
+    orc_qmat_matmul(t, w.data(), w.size(), m, n, x.data(), rows, want.data());
+    const auto got32 = q.matmul(x, rows, Precision::F32Strict);
+    CHECK(within_f32_bound(t, w, m, n, x, rows, got32, want), "type %u f32 matmul", t);
+    const auto got16 = q.matmul(x, rows, Precision::Bf16Mfma);
+    double num = 0, den = 0;
+    for (size_t i = 0; i < want.size(); ++i) {
+      num += ((double)got16[i] - want[i]) * ((double)got16[i] - want[i]);
+      den += (double)want[i] * want[i];
+    }
+    CHECK(std::sqrt(num / den) <= 1e-2, "type %u bf16 matmul rel %g", t, std::sqrt(num / den));
+    const auto y = q.matvec(std::vector<float>(x.begin(), x.begin() + n));
+    CHECK(within_f32_bound(t, w, m, n, std::vector<float>(x.begin(), x.begin() + n), 1, y,
+                           std::vector<float>(want.begin(), want.begin() + m)),
+          "type %u matvec", t);
+  }
+}
+
+static void test_unknown_type_is_an_error() {  // kernel.rs:2006, 2027 panic -> EngineError
+  std::printf("unknown_type_is_an_error\n");
+  bool threw = false;
+  try {
+    (void)QMat::from_bytes(99, std::vector<uint8_t>(34), 1, 32);
+  } catch (const EngineError& e) {
+    threw = e.code == RE_ERR_TYPE;
+  }
+  CHECK(threw, "no EngineError for type 99");
+}
+
+static void test_router_matches_oracle() {  // moe.rs:631-662
+  std::printf("router_top_k_matches_oracle\n");
+  auto s = top_k({0.1f, 0.9f, 0.2f, 0.8f}, 2);
+  CHECK(s.size() == 2 && s[0].id == 1 && s[1].id == 3, "top_k ids");
+  CHECK(std::fabs(s[0].weight + s[1].weight - 1.0f) < 1e-5f, "top_k weights sum");
+  CHECK(top_k({0.5f, 0.4f}, 8).size() == 2, "clamp k");
+  auto sg = top_k_sigmoid({1.0f, 5.0f, 2.0f, 4.0f}, 2);
+  CHECK(sg[0].id == 1 && sg[1].id == 3, "top_k_sigmoid ids");
+  std::mt19937 g(5);
+  for (int rep = 0; rep < 50; ++rep) {
+    const auto logits = randn(g, 128);
+    const auto mine = top_k(logits, 8);
+    uint32_t ids[8];
+    float w[8];
+    orc_top_k(logits.data(), logits.size(), 8, ids, w);
+    for (int j = 0; j < 8; ++j)
+      CHECK(mine[j].id == ids[j] && mine[j].weight == w[j], "router differs at %d", j);
+  }
+}
+
+// 32 x 32 Q8_0 matrix, d = 1, quant `q` on the diagonal
+static std::vector<uint8_t> q8_identity(int q) {
+  std::vector<uint8_t> a(32 * 34, 0);
+  for (int r = 0; r < 32; ++r) {
+    a[r * 34] = 0x00;
+    a[r * 34 + 1] = 0x3C;
+    a[r * 34 + 2 + r] = (uint8_t)(int8_t)q;
+  }
+  return a;
+}
+
+static void test_moe_layer_routes_to_best_expert() {  // moe.rs:784-796
+  std::printf("moe_layer_routes_to_best_expert\n");
+  auto ident = q8_identity(1), dbl = q8_identity(2);
+  std::vector<uint8_t> gate = ident, down = ident;
+  gate.insert(gate.end(), ident.begin(), ident.end());
+  down.insert(down.end(), dbl.begin(), dbl.end());
+  MoeExperts ex(ORC_Q8_0, gate, ORC_Q8_0, gate, ORC_Q8_0, down, 2, 32, 32);
+  std::vector<float> router_w(2 * 32, 0.0f);
+  router_w[32] = 10.0f;  // expert 1 scores 10 on hidden[0]
+  std::vector<float> h(32, 0.0f);
+  h[0] = 1.0f;
+  for (Precision p : {Precision::F32Strict, Precision::Bf16Mfma}) {
+    const auto out = moe_layer_forward(h, 1, router_w, ex, RouterConfig{Gate::Softmax, 1}, p);
+    CHECK(std::fabs(out[0] - 2.0f * silu(1.0f)) < 1e-2f, "out[0] = %g", out[0]);
+    float rest = 0;
+    for (int i = 1; i < 32; ++i) rest += std::fabs(out[i]);
+    CHECK(rest < 1e-5f, "off-diagonal %g", rest);
+  }
+}
+
+int main() {
+  try {
+    check(re_init());
+    test_unknown_type_is_an_error();
+    test_matmul_matches_rowwise_matvec();
+    test_matvec_is_deterministic();
+    test_every_type_against_oracle();
+    test_router_matches_oracle();
+    test_moe_layer_routes_to_best_expert();
+  } catch (const EngineError& e) {
+    std::printf("EngineError %d: %s\n", e.code, e.what());
+    return 2;
+  }
+  std::printf(g_failed ? "FAILED (%d)\n" : "ALL PASSED\n", g_failed);
+  return g_failed ? 1 : 0;
+}
