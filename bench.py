@@ -130,6 +130,8 @@ def main():
         dxn = hip.DeviceBuffer.from_array(xn)
         dyn = hip.DeviceBuffer(n * M * 4)
         gs = args.gemm_steps
+        q.matmul_dev(dxn, n, dyn, rehip.MODE_BF16, stream=stream)     # sizes the split-K buffer
+        stream.synchronize()
         g = hip.Graph(stream, lambda: [q.matmul_dev(dxn, n, dyn, rehip.MODE_BF16, stream=stream) for _ in range(gs)])
         g.launch()
         stream.synchronize()

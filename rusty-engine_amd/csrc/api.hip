@@ -120,7 +120,7 @@ struct re_qmat {
   int splits = 1, kb_per_split = 1, waves = 4;
   std::mutex mu;
   hipStream_t stream = nullptr;
-  Staging sx, sy;
+  Staging sx, sy, spart;
 };
 
 struct re_moe {
@@ -194,10 +194,27 @@ int gemv_enqueue(re_qmat* q, const float* d_x, float* d_y, hipStream_t s) {
 }
 
 int gemm_enqueue(re_qmat* q, const float* d_x, size_t rows, float* d_y, int mode, hipStream_t s) {
+  const size_t xbytes = rows * q->g.n * sizeof(float);
+  if (xbytes >= (1ull << 31) || q->g.bytes >= (1ull << 31))
+    return fail(RE_ERR_SIZE, "GEMM operands must stay below 2 GiB (X %zu B, W %zu B)", xbytes, q->g.bytes);
+  GemmPlan pl = plan_gemm((int)q->g.m, (int)rows, (int)q->g.n, mode);
+  const size_t part_bytes = (size_t)pl.splits * rows * q->g.m * sizeof(float);
+  if (pl.splits > 1 && part_bytes > q->spart.cap) {
+    // the partial-sum buffer grows on first use; under stream capture nothing may be allocated,
+    // so an un-warmed shape runs unsplit (same result up to summation order)
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    HIP_TRY(hipStreamIsCapturing(s, &cs));
+    if (cs != hipStreamCaptureStatusNone) {
+      pl.splits = 1;
+      pl.steps_per_split = (int)((q->g.n + kGemmBK - 1) / kGemmBK);
+    }
+  }
   GemmArgs a{};
   a.W = q->d_w;
+  a.w_bytes = (uint32_t)q->g.bytes;
   a.w_stride = 0;
   a.X = d_x;
+  a.x_bytes = (uint32_t)xbytes;
   a.Y = d_y;
   a.m = (int)q->g.m;
   a.K = (int)q->g.n;
@@ -205,9 +222,16 @@ int gemm_enqueue(re_qmat* q, const float* d_x, size_t rows, float* d_y, int mode
   a.tiles = (int)q->g.tiles;
   a.N = (int)rows;
   a.ldy = (int)q->g.m;
+  a.splits = pl.splits;
+  a.steps_per_split = pl.steps_per_split;
   a.tasks = nullptr;
   a.xrow = nullptr;
-  HIP_TRY(launch_gemm(q->g.type, mode, a, 0, gemm_tile_for((int)q->g.m, (int)rows), s));
+  if (pl.splits > 1) {
+    int rc = q->spart.ensure(part_bytes);
+    if (rc) return rc;
+    a.partial = (float*)q->spart.p;
+  }
+  HIP_TRY(launch_gemm(q->g.type, mode, a, 0, pl.tile, s));
   return RE_OK;
 }
 
@@ -284,6 +308,7 @@ void re_qmat_destroy(re_qmat* q) {
   if (q->d_partial) (void)hipFree(q->d_partial);
   q->sx.release();
   q->sy.release();
+  q->spart.release();
   if (q->stream) (void)hipStreamDestroy(q->stream);
   delete q;
 }
@@ -467,8 +492,14 @@ int re_moe_forward_dev(re_moe* e, const float* d_x, size_t tokens, size_t top_k,
   HIP_TRY(hipStreamSynchronize(s));
   HIP_TRY(hipMemcpy(dm, meta.data(), meta_bytes, hipMemcpyHostToDevice));
 
+  if (tokens * e->hidden * sizeof(float) >= (1ull << 31) || e->gg.bytes * e->n_experts >= (1ull << 31) ||
+      e->gd.bytes * e->n_experts >= (1ull << 31) || pairs * e->inter * sizeof(float) >= (1ull << 31))
+    return fail(RE_ERR_SIZE, "MoE operands must stay below 2 GiB");
   GemmArgs a{};
   a.X = d_x;
+  a.x_bytes = (uint32_t)(tokens * e->hidden * sizeof(float));
+  a.splits = 1;
+  a.steps_per_split = 1 << 30;
   a.tasks = (const GemmTask*)(dm + off_tgu);
   a.xrow = (const int*)dm;
   a.m = (int)e->inter;
@@ -477,20 +508,26 @@ int re_moe_forward_dev(re_moe* e, const float* d_x, size_t tokens, size_t top_k,
   a.tiles = (int)e->gg.tiles;
   a.ldy = (int)e->inter;
   a.W = e->d_gate;
+  a.w_bytes = (uint32_t)(e->gg.bytes * e->n_experts);
   a.w_stride = e->gg.bytes;
   a.Y = (float*)e->sg.p;
-  HIP_TRY(launch_gemm(e->gg.type, mode, a, (int)t_gu.size(), kMoeTile, s));
+  HIP_TRY(launch_gemm(e->gg.type, mode, a, (int)t_gu.size(), GemmTile::k64x64, s));
   a.W = e->d_up;
+  a.w_bytes = (uint32_t)(e->gu.bytes * e->n_experts);
   a.w_stride = e->gu.bytes;
   a.KB = (int)e->gu.kb;
   a.tiles = (int)e->gu.tiles;
   a.Y = (float*)e->su.p;
-  HIP_TRY(launch_gemm(e->gu.type, mode, a, (int)t_gu.size(), kMoeTile, s));
+  HIP_TRY(launch_gemm(e->gu.type, mode, a, (int)t_gu.size(), GemmTile::k64x64, s));
   HIP_TRY(launch_swiglu((const float*)e->sg.p, (const float*)e->su.p, (float*)e->sh.p, pairs * e->inter, s));
   GemmArgs d{};
   d.W = e->d_down;
+  d.w_bytes = (uint32_t)(e->gd.bytes * e->n_experts);
   d.w_stride = e->gd.bytes;
   d.X = (const float*)e->sh.p;
+  d.x_bytes = (uint32_t)(pairs * e->inter * sizeof(float));
+  d.splits = 1;
+  d.steps_per_split = 1 << 30;
   d.Y = (float*)e->syp.p;
   d.m = (int)e->hidden;
   d.K = (int)e->inter;
@@ -499,7 +536,7 @@ int re_moe_forward_dev(re_moe* e, const float* d_x, size_t tokens, size_t top_k,
   d.ldy = (int)e->hidden;
   d.tasks = (const GemmTask*)(dm + off_td);
   d.xrow = nullptr;
-  HIP_TRY(launch_gemm(e->gd.type, mode, d, (int)t_d.size(), kMoeTile, s));
+  HIP_TRY(launch_gemm(e->gd.type, mode, d, (int)t_d.size(), GemmTile::k64x64, s));
   HIP_TRY(launch_combine((const float*)e->syp.p, (const int*)(dm + off_pos), (const float*)(dm + off_w), d_out,
                          (int)tokens, (int)top_k, (int)e->hidden, s));
   return RE_OK;

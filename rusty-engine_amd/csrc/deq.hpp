@@ -76,6 +76,24 @@ template <> inline constexpr int kBias<T_Q6_K> = 32;
 //                                after unrolling, so r.p[...] stays in registers).
 
 __device__ __forceinline__ uint4 ld16(const uint8_t* p) { return *reinterpret_cast<const uint4*>(p); }
+
+// Raw buffer loads through a resource covering a whole matrix (or all experts): byte offsets are
+// 32-bit and a read past num_records returns zero, so padding rows/columns need no branches
+// (zero bytes decode to zero weights for every type: every scale is then 0).
+typedef __attribute__((__vector_size__(4 * sizeof(int)))) int i32x4_t;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ uint4 bld16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const i32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+  return make_uint4((uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]);
+}
+__device__ __forceinline__ uint32_t bld4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
+}
+__device__ __forceinline__ uint32_t bld2(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, 0);
+}
 __device__ __forceinline__ uint32_t ld4(const uint8_t* p) { return *reinterpret_cast<const uint32_t*>(p); }
 __device__ __forceinline__ uint32_t ld2(const uint8_t* p) { return *reinterpret_cast<const uint16_t*>(p); }
 
@@ -93,6 +111,12 @@ template <> struct Blk<T_Q4_0> {
   __device__ static void load(const uint8_t* slab, int lane, R& r) {
     r.p[0] = ld16(slab + lane * 16);
     r.t0 = ld2(slab + 1024 + lane * 2);
+    r.t1 = 0;
+  }
+  __device__ static void bload_chunk(__amdgpu_buffer_rsrc_t rs, uint32_t slab, int lane, int c, R& r) {
+    (void)c;
+    r.p[0] = bld16(rs, slab + lane * 16);
+    r.t0 = bld2(rs, slab + 1024 + lane * 2);
     r.t1 = 0;
   }
   __device__ static void decode(const R& r, int c, Run& a, Run& b) {
@@ -126,6 +150,12 @@ template <> struct Blk<T_Q5_0> {
     r.t0 = ld4(slab + 1024 + lane * 4);      // qh
     r.t1 = ld2(slab + 1280 + lane * 2);      // d
   }
+  __device__ static void bload_chunk(__amdgpu_buffer_rsrc_t rs, uint32_t slab, int lane, int c, R& r) {
+    (void)c;
+    r.p[0] = bld16(rs, slab + lane * 16);
+    r.t0 = bld4(rs, slab + 1024 + lane * 4);
+    r.t1 = bld2(rs, slab + 1280 + lane * 2);
+  }
   __device__ static void decode(const R& r, int c, Run& a, Run& b) {
     (void)c;
     const uint32_t w[4] = {r.p[0].x, r.p[0].y, r.p[0].z, r.p[0].w};
@@ -157,6 +187,13 @@ template <> struct Blk<T_Q8_0> {
     r.p[0] = ld16(slab + lane * 16);
     r.p[1] = ld16(slab + 1024 + lane * 16);
     r.t0 = ld2(slab + 2048 + lane * 2);
+    r.t1 = 0;
+  }
+  __device__ static void bload_chunk(__amdgpu_buffer_rsrc_t rs, uint32_t slab, int lane, int c, R& r) {
+    (void)c;
+    r.p[0] = bld16(rs, slab + lane * 16);
+    r.p[1] = bld16(rs, slab + 1024 + lane * 16);
+    r.t0 = bld2(rs, slab + 2048 + lane * 2);
     r.t1 = 0;
   }
   __device__ static void decode(const R& r, int c, Run& a, Run& b) {
@@ -228,6 +265,10 @@ template <> struct Blk<T_Q4_K> {
     r.head = ld16(slab + lane * 16);
     r.qs = ld16(slab + 1024 * (1 + c) + lane * 16);
   }
+  __device__ static void bload_chunk(__amdgpu_buffer_rsrc_t rs, uint32_t slab, int lane, int c, CR& r) {
+    r.head = bld16(rs, slab + lane * 16);
+    r.qs = bld16(rs, slab + 1024 * (1 + c) + lane * 16);
+  }
   __device__ static void decode_chunk(const CR& r, int c, Run& a, Run& b) { dec(r.head, r.qs, c, a, b); }
   __device__ static void chunk(const uint8_t* slab, int lane, int c, Run& a, Run& b) {
     CR r; load_chunk(slab, lane, c, r); decode_chunk(r, c, a, b);
@@ -265,6 +306,11 @@ template <> struct Blk<T_Q5_K> {
     r.head = ld16(slab + lane * 16);
     r.qh = ld16(slab + 1024 * (1 + (c & 1)) + lane * 16);
     r.qs = ld16(slab + 1024 * (3 + c) + lane * 16);
+  }
+  __device__ static void bload_chunk(__amdgpu_buffer_rsrc_t rs, uint32_t slab, int lane, int c, CR& r) {
+    r.head = bld16(rs, slab + lane * 16);
+    r.qh = bld16(rs, slab + 1024 * (1 + (c & 1)) + lane * 16);
+    r.qs = bld16(rs, slab + 1024 * (3 + c) + lane * 16);
   }
   __device__ static void decode_chunk(const CR& r, int c, Run& a, Run& b) { dec(r.head, r.qh, r.qs, c, a, b); }
   __device__ static void chunk(const uint8_t* slab, int lane, int c, Run& a, Run& b) {
@@ -315,6 +361,12 @@ template <> struct Blk<T_Q6_K> {
     r.qh = ld16(slab + 1024 * (8 + 2 * (c >> 2) + (c & 1)) + lane * 16);
     r.sc = ld16(slab + 1024 * 12 + lane * 16);
     r.d = ld2(slab + 1024 * 13 + lane * 2);
+  }
+  __device__ static void bload_chunk(__amdgpu_buffer_rsrc_t rs, uint32_t slab, int lane, int c, CR& r) {
+    r.ql = bld16(rs, slab + 1024 * c + lane * 16);
+    r.qh = bld16(rs, slab + 1024 * (8 + 2 * (c >> 2) + (c & 1)) + lane * 16);
+    r.sc = bld16(rs, slab + 1024 * 12 + lane * 16);
+    r.d = bld2(rs, slab + 1024 * 13 + lane * 2);
   }
   __device__ static void decode_chunk(const CR& r, int c, Run& a, Run& b) { dec(r.ql, r.qh, r.sc, r.d, c, a, b); }
   __device__ static void chunk(const uint8_t* slab, int lane, int c, Run& a, Run& b) {

@@ -21,34 +21,46 @@ hipError_t launch_gemv(uint32_t type, const GemvArgs& a, int waves, hipStream_t 
 hipError_t launch_dequant(uint32_t type, const uint8_t* W, float* out, int m, int n, int KB, int tiles,
                           hipStream_t s);
 
-// GEMM: K steps of 128 elements; square tiles of 128 or 64 (weight rows x activation rows).
+// GEMM: K steps of 128 elements.
 constexpr int kGemmBK = 128;
-constexpr int kMoeTile = 64;   // tile of the grouped (MoE) launches
+constexpr int kMoeTile = 64;   // tile of the grouped (MoE) launches (64 x 64, four waves)
 
-// Work item of a grouped launch (MoE): one BM x BN output tile of one expert.
+enum class GemmTile { k64x64, k128x128, k128x256 };
+
+// Work item of a grouped launch (MoE): one tile of one expert.
 struct GemmTask {
   int expert;     // weight matrix index (byte offset expert * w_stride)
-  int mtile;      // BM tile along the weight rows
+  int mtile;      // weight-row tile
   int r0;         // first gathered row of the tile
-  int rn;         // valid rows in the tile (<= BN)
+  int rn;         // valid rows in the tile (<= tile)
 };
 
 struct GemmArgs {
   const uint8_t* W;        // tiled slabs (expert 0)
+  uint32_t w_bytes;        // bytes readable from W (all experts); < 2 GiB
   size_t w_stride;         // bytes between experts
   const float* X;          // activations, row-major, K floats per row
+  uint32_t x_bytes;        // bytes readable from X; < 2 GiB
   float* Y;                // output, row stride ldy
   int m, K, KB, tiles;     // weight geometry (per expert)
   int N;                   // activation rows (dense launch)
   int ldy;
-  const GemmTask* tasks;   // grouped launch: one task per workgroup (nullptr = dense 2-D grid)
+  int splits;              // dense: K steps divided over this many workgroups (>= 1)
+  int steps_per_split;
+  float* partial;          // splits > 1: splits * N * ldy floats, summed by a second kernel
+  const GemmTask* tasks;   // grouped launch: one task per workgroup (nullptr = dense grid)
   const int* xrow;         // grouped: X row of gathered row p (nullptr = p itself)
 };
 
-// mode 0 = bf16 MFMA with f32 accumulation, 1 = f32 MFMA (strict parity); tile 128 or 64
-hipError_t launch_gemm(uint32_t type, int mode, const GemmArgs& a, int ntasks, int tile, hipStream_t s);
-// tile a dense m x n-row launch uses
-int gemm_tile_for(int m, int n);
+struct GemmPlan {
+  GemmTile tile = GemmTile::k64x64;
+  int splits = 1;
+  int steps_per_split = 1;
+};
+
+// tile and K split of a dense m x n-row launch over K (mode 0 bf16, 1 f32)
+GemmPlan plan_gemm(int m, int n, int K, int mode);
+hipError_t launch_gemm(uint32_t type, int mode, const GemmArgs& a, int ntasks, GemmTile tile, hipStream_t s);
 
 // MoE helpers
 hipError_t launch_swiglu(const float* g, const float* u, float* h, size_t n, hipStream_t s);

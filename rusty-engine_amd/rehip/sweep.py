@@ -69,6 +69,8 @@ def time_gemm(t: int, m: int, k: int, n: int, mode: int, launches: int, seed: in
     dx = hip.DeviceBuffer.from_array(x)
     dy = hip.DeviceBuffer(n * m * 4)
     s = hip.Stream()
+    q.matmul_dev(dx, n, dy, mode, stream=s)     # eager first call sizes the split-K buffer
+    s.synchronize()
     g = hip.Graph(s, lambda: [q.matmul_dev(dx, n, dy, mode, stream=s) for _ in range(launches)])
     g.launch()
     s.synchronize()

@@ -181,6 +181,23 @@ def test_gemm_parity_both_modes(t, m, n, rows):
         assert np.all(np.abs(got32 - want) <= F32_TOL * absd)
 
 
+@pytest.mark.parametrize("t", [rehip.Q4_0, rehip.Q8_0, rehip.Q4_K, rehip.Q6_K])
+def test_gemm_large_tiles_ragged_edges(t):
+    # 3136 weight rows (not a multiple of 128) x 2085 activation rows (not a multiple of 256):
+    # enough tiles for the 128 x 256 bf16 tile and the 128 x 128 f32 tile, with partial edge tiles
+    m, n, rows = 3136, 512, 2085
+    rng = np.random.default_rng(77 + t)
+    w = synth.weight_bytes(rng, t, m, n)
+    x = synth.activations(rng, rows, n)
+    q = qmat(t, w, m, n)
+    exact, absd = f64_product(t, w, m, n, x, rows)
+    exact, absd = exact.reshape(-1), absd.reshape(-1)
+    got16 = q.matmul(x, rows, rehip.MODE_BF16)
+    assert np.linalg.norm(got16 - exact) / np.linalg.norm(exact) <= BF16_TOL
+    got32 = q.matmul(x, rows, rehip.MODE_F32)
+    assert np.all(np.abs(got32 - exact) <= F32_TOL * absd)
+
+
 @pytest.mark.parametrize("name,t,m,n", [("C1 Q5_0 4864x896", rehip.Q5_0, 4864, 896),
                                         ("C2 Q6_K 896x4864", rehip.Q6_K, 896, 4864)])
 def test_prefill_961_rows_full_size(name, t, m, n):
