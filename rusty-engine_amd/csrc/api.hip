@@ -118,6 +118,7 @@ struct re_qmat {
   uint8_t* d_w = nullptr;
   float* d_partial = nullptr;
   int splits = 1, kb_per_split = 1, waves = 4;
+  int rows_per_group = 0, groups = 0;   // row-group GEMV launch (0 = split launch)
   std::mutex mu;
   hipStream_t stream = nullptr;
   Staging sx, sy, spart;
@@ -141,19 +142,41 @@ size_t env_size(const char* name, size_t dflt) {
   return (v && *v) ? (size_t)std::strtoull(v, nullptr, 10) : dflt;
 }
 
-// GEMV launch shape. Work units are 32-quant chunks of a 64-row tile (KB * chunks-per-block per
-// tile); one unit costs a wave about 110 VALU instructions (~450 cycles). A tile's units are
-// split over several workgroups (partials + reduce kernel, ~2.5 us extra) only when one CU would
-// otherwise spend more than ~6000 cycles on them; waves per workgroup are chosen so that every
-// wave holds at most 4 units (all of them in flight at once) where 16 waves allow it.
+// GEMV launch shape. Work units are 32-quant chunks (KB * chunks-per-block per row).
+// Rows up to kGemvRowsMaxK long use the row-group kernel: the rows per workgroup are the largest
+// of 64/16/8/4 that still give >= 512 workgroups (two per CU), and the waves per workgroup are
+// the fewest of 4/8/16 that leave each lane-group slot at most 2 units (4 for 64-row groups), so
+// a slot's loads are all in flight at once. Longer rows split the row over workgroups (partials
+// + a reduce kernel). Measured on MI355X over the Qwen2.5-0.5B projections in all six types.
 void plan_gemv(re_qmat* q) {
   const size_t kb = q->g.kb;
   const size_t nch = q->g.qk == 256 ? 8 : 1;
   const size_t units = kb * nch;
+  q->rows_per_group = 0;
+  q->groups = 0;
+  if (q->g.n <= (size_t)kGemvRowsMaxK) {
+    int r = 64;
+    for (int c : {64, 16, 8, 4}) {
+      r = c;
+      if (q->g.tiles * 64 / (size_t)c >= 512) break;
+    }
+    if (const size_t e = env_size("REHIP_GEMV_ROWS", 0); e == 64 || e == 16 || e == 8 || e == 4) r = (int)e;
+    const size_t per_slot = r == 64 ? 4 : 2;
+    const size_t slots = (units + per_slot - 1) / per_slot;
+    const size_t per_wave = 64 / (size_t)r;
+    const size_t w = (slots + per_wave - 1) / per_wave;
+    q->waves = w <= 4 ? 4 : w <= 8 ? 8 : 16;
+    if (const size_t e = env_size("REHIP_GEMV_WAVES", 0); e == 4 || e == 8 || e == 16) q->waves = (int)e;
+    q->rows_per_group = r;
+    q->groups = (int)(q->g.tiles * 64 / (size_t)r);
+    q->splits = 1;
+    q->kb_per_split = (int)kb;
+    return;
+  }
   const size_t cycles = units * 112;              // per-CU VALU cycles for one tile (4 SIMDs)
   size_t want = cycles > 6000 ? (cycles + 2399) / 2400 : 1;
-  // a split stages its slice of x in LDS: keep it within 64 KiB (16384 floats)
-  const size_t max_per = std::max<size_t>(1, 16384 / (size_t)q->g.qk);
+  // a split stages its slice of x in LDS
+  const size_t max_per = std::max<size_t>(1, (size_t)kGemvRowsMaxK / (size_t)q->g.qk);
   want = std::max<size_t>({(size_t)1, std::min(want, kb), (kb + max_per - 1) / max_per});
   want = std::min(want, std::max<size_t>(1, env_size("REHIP_GEMV_MAX_SPLITS", want)));
   const size_t per = (kb + want - 1) / want;
@@ -161,7 +184,7 @@ void plan_gemv(re_qmat* q) {
   q->splits = (int)((kb + per - 1) / per);
   const size_t per_wg = per * nch;
   q->waves = per_wg <= 16 ? 4 : per_wg <= 32 ? 8 : 16;
-  if (const size_t w = env_size("REHIP_GEMV_WAVES", 0)) q->waves = (int)w;
+  if (const size_t w = env_size("REHIP_GEMV_WAVES", 0); w == 4 || w == 8 || w == 16) q->waves = (int)w;
 }
 
 int upload_tiled(const MatGeom& g, const uint8_t* bytes, uint8_t* d_dst) {
@@ -189,6 +212,8 @@ int gemv_enqueue(re_qmat* q, const float* d_x, float* d_y, hipStream_t s) {
   a.tiles = (int)q->g.tiles;
   a.kb_per_split = q->kb_per_split;
   a.splits = q->splits;
+  a.rows_per_group = q->rows_per_group;
+  a.groups = q->groups;
   HIP_TRY(launch_gemv(q->g.type, a, q->waves, s));
   return RE_OK;
 }

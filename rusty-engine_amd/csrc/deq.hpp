@@ -330,10 +330,12 @@ template <> struct Blk<T_Q6_K> {
                              Run& a, Run& b) {
     const int hh = c >> 2, ih = (c >> 1) & 1, lo = c & 1;
     const float d = f16_bits_to_f32(dbits);
-    const int ia = 8 * hh + lo + 2 * ih, ib = ia + 4;
-    const uint32_t scw[4] = {sc.x, sc.y, sc.z, sc.w};
-    const float sca = (float)(int8_t)(scw[ia >> 2] >> (8 * (ia & 3)));
-    const float scb = (float)(int8_t)(scw[ib >> 2] >> (8 * (ib & 3)));
+    // sub-scale ia = 8hh + 2ih + lo is byte (c & 3) of dword 2hh; ib = ia + 4 the same byte of
+    // dword 2hh + 1 (selected, not indexed: a runtime index into a register array goes to scratch)
+    const uint32_t wa = hh ? sc.z : sc.x, wb = hh ? sc.w : sc.y;
+    const int sh = 24 - 8 * (c & 3);
+    const float sca = (float)((int)(wa << sh) >> 24);
+    const float scb = (float)((int)(wb << sh) >> 24);
     const uint32_t w[4] = {ql.x, ql.y, ql.z, ql.w};
     const uint32_t hw[4] = {qh.x, qh.y, qh.z, qh.w};
     const int sha = 2 * ih, shb = 2 * ih + 4;

@@ -141,6 +141,96 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs p) {
   }
 }
 
+// Row-group GEMV: a workgroup owns R consecutive rows of one 64-row tile (R = 64, 16, 8 or 4)
+// and the whole row length, so a matrix with few rows still spreads over hundreds of
+// workgroups and needs no second reduction kernel. Lane l of a wave serves row l % R of the
+// group; the 64 / R lane groups of every wave ("slots") take the units of the row in turn, so
+// one load instruction reads 64 / R runs of R * 16 contiguous bytes. Partial sums are folded
+// over the lane groups with a fixed xor-shuffle tree, then over the waves in wave order
+// (deterministic). Row groups that share cache lines are given to the same XCD (workgroup w
+// runs on XCD w % 8).
+template <int T, int R, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void gemv_rows_kernel(GemvArgs p) {
+  using B = Blk<T>;
+  constexpr int NCH = B::NCH;
+  constexpr int D = WAVES == 16 ? 2 : kGemvDepth;   // 16 waves: 128 VGPRs per lane
+  constexpr int G = 64 / R;              // lane groups per wave
+  constexpr int S = WAVES * G;           // slots per workgroup
+  // LDS: x[KB * QK] (zero past K), xs16[KB * QK / 16], red[WAVES * R]
+  extern __shared__ __attribute__((aligned(16))) float smem[];
+  const int per = (p.groups + 7) / 8;
+  const int gi = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
+  if (gi >= p.groups) return;
+  constexpr int GPT = 64 / R;            // row groups per tile
+  const int tile = gi / GPT;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int rr = (gi - tile * GPT) * R + (lane % R);    // row inside the tile
+  const int slot = wave * G + lane / R;
+  const int nx = p.KB * B::QK;
+  float* xl = smem;
+  float* xs16 = smem + nx;
+  float* red = xs16 + nx / 16;
+
+  const uint8_t* tbase = p.W + (size_t)tile * p.KB * B::SLAB;
+  const int u_end = p.KB * NCH;
+  typename B::CR ring[D];
+#pragma unroll
+  for (int i = 0; i < D; ++i) {
+    const int u = slot + i * S;
+    if (u < u_end) B::load_chunk(tbase + (size_t)(u / NCH) * B::SLAB, rr, u % NCH, ring[i]);
+  }
+
+  const int nv = nx / 4;
+  for (int i = threadIdx.x; i < nv; i += WAVES * 64) {
+    const int k = 4 * i;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (k < p.K) v = *reinterpret_cast<const float4*>(p.x + k);
+    reinterpret_cast<float4*>(xl)[i] = v;
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < nv / 4; i += WAVES * 64) {
+    const float4* q = reinterpret_cast<const float4*>(xl + 16 * i);
+    float s = 0.0f;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) { const float4 t = q[v]; s += t.x; s += t.y; s += t.z; s += t.w; }
+    xs16[i] = s;
+  }
+  __syncthreads();
+
+  float acc = 0.0f;
+  for (int base = slot; base < u_end; base += D * S) {
+#pragma unroll
+    for (int i = 0; i < D; ++i) {
+      const int u = base + i * S;
+      if (u < u_end) {
+        const int kb = u / NCH, c = u - kb * NCH;
+        Run a, b;
+        B::decode_chunk(ring[i], c, a, b);
+        const int un = u + D * S;
+        if (un < u_end) B::load_chunk(tbase + (size_t)(un / NCH) * B::SLAB, rr, un % NCH, ring[i]);
+        const float* xb = xl + kb * B::QK;
+        const float* xs = xs16 + kb * (B::QK / 16);
+        const int valid = p.K - kb * B::QK;   // K is a multiple of 32: a run is wholly in or out
+        if (a.e < valid) acc += run_dot<T>(a, xb, xs);
+        if (b.e < valid) acc += run_dot<T>(b, xb, xs);
+      }
+    }
+  }
+
+#pragma unroll
+  for (int off = R; off < 64; off *= 2) acc += __shfl_xor(acc, off, 64);
+  if (lane < R) red[wave * R + lane] = acc;
+  __syncthreads();
+  if (threadIdx.x < R) {
+    float s = red[threadIdx.x];
+#pragma unroll
+    for (int w = 1; w < WAVES; ++w) s += red[w * R + threadIdx.x];
+    const int row = tile * 64 + rr;
+    if (row < p.m) p.y[row] = s;
+  }
+}
+
 // y[r] = sum over splits, in split order, of partial[split][r]
 __global__ __launch_bounds__(256) void gemv_reduce_kernel(const float* __restrict__ partial,
                                                           float* __restrict__ y, int m, int m_pad,
@@ -175,8 +265,31 @@ __global__ __launch_bounds__(64) void dequant_kernel(const uint8_t* __restrict__
   }
 }
 
+template <int T, int R>
+static hipError_t launch_rows(const GemvArgs& a, int waves, hipStream_t s) {
+  const size_t lds = ((size_t)a.KB * Blk<T>::QK * 17 / 16 + 16 * R) * sizeof(float);
+  const unsigned grid = (unsigned)((a.groups + 7) / 8 * 8);
+  if (waves == 16) {
+    hipLaunchKernelGGL((gemv_rows_kernel<T, R, 16>), dim3(grid), dim3(1024), lds, s, a);
+  } else if (waves == 8) {
+    hipLaunchKernelGGL((gemv_rows_kernel<T, R, 8>), dim3(grid), dim3(512), lds, s, a);
+  } else {
+    hipLaunchKernelGGL((gemv_rows_kernel<T, R, 4>), dim3(grid), dim3(256), lds, s, a);
+  }
+  return hipGetLastError();
+}
+
 template <int T>
 static hipError_t launch_gemv_t(const GemvArgs& a, int waves, hipStream_t s) {
+  if (a.rows_per_group) {
+    switch (a.rows_per_group) {
+      case 64: return launch_rows<T, 64>(a, waves, s);
+      case 16: return launch_rows<T, 16>(a, waves, s);
+      case 8: return launch_rows<T, 8>(a, waves, s);
+      case 4: return launch_rows<T, 4>(a, waves, s);
+      default: return hipErrorInvalidValue;
+    }
+  }
   const int nx = a.kb_per_split * Blk<T>::QK;
   const int xs = nx + nx / 16;
   dim3 grid((unsigned)a.tiles, (unsigned)a.splits);

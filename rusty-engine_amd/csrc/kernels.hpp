@@ -13,10 +13,16 @@ struct GemvArgs {
   float* y;              // m floats
   float* partial;        // splits * m_pad floats (splits > 1), reduced by a second kernel
   int m, m_pad, K, KB, tiles;
-  int kb_per_split, splits;
+  int kb_per_split, splits;     // split launch (rows_per_group == 0)
+  int rows_per_group;           // row-group launch: 64, 16, 8 or 4 rows per workgroup; 0 = split launch
+  int groups;                   // row-group launch: tiles * 64 / rows_per_group
 };
 
-// waves per workgroup: 4 or 8
+// longest row (elements) a GEMV workgroup stages in LDS: x, its per-16 sums and the wave
+// partials stay under 64 KiB of dynamic LDS
+constexpr int kGemvRowsMaxK = 12288;
+
+// waves per workgroup: 4, 8 or 16
 hipError_t launch_gemv(uint32_t type, const GemvArgs& a, int waves, hipStream_t s);
 hipError_t launch_dequant(uint32_t type, const uint8_t* W, float* out, int m, int n, int KB, int tiles,
                           hipStream_t s);

@@ -111,7 +111,8 @@ def test_device_entry_points_match_host_entry_points():
 
 
 # ---- GEMV --------------------------------------------------------------------------------
-GEMV_SHAPES = [(1, 256), (5, 512), (64, 256), (70, 896), (130, 1024), (896, 4864), (4864, 896)]
+GEMV_SHAPES = [(1, 256), (5, 512), (64, 256), (70, 896), (130, 1024), (896, 4864), (4864, 896),
+               (96, 14336)]     # the last row is longer than one workgroup stages: split launch
 
 
 @pytest.mark.parametrize("t", rehip.QUANT_TYPES)
@@ -125,6 +126,26 @@ def test_gemv_parity(t, m, n):
     absd = O.qmat_absdot(t, w, m, n, x, 1)
     err = np.abs(got.astype(np.float64) - want)
     assert np.all(err <= F32_TOL * absd), f"max err/bound {np.max(err / (absd + 1e-30))}"
+
+
+@pytest.mark.parametrize("t", [rehip.Q5_0, rehip.Q8_0, rehip.Q4_K, rehip.Q6_K])
+@pytest.mark.parametrize("rows_per_group", [64, 16, 8, 4])
+@pytest.mark.parametrize("waves", [4, 8, 16])
+def test_gemv_launch_shapes(t, rows_per_group, waves, monkeypatch):
+    # every row-group / wave-count kernel variant on a ragged shape (3 tiles, last one partial)
+    monkeypatch.setenv("REHIP_GEMV_ROWS", str(rows_per_group))
+    monkeypatch.setenv("REHIP_GEMV_WAVES", str(waves))
+    m, n = 150, 2560
+    rng = np.random.default_rng(5000 + 10 * t + rows_per_group + waves)
+    w = synth.weight_bytes(rng, t, m, n)
+    x = synth.activations(rng, 1, n)
+    q = qmat(t, w, m, n)
+    got = q.matvec(x)
+    want = O.qmat_matvec(t, w, m, n, x)
+    absd = O.qmat_absdot(t, w, m, n, x, 1)
+    assert np.all(np.abs(got.astype(np.float64) - want) <= F32_TOL * absd)
+    assert np.array_equal(q.matvec(x), got)
+    q.close()
 
 
 def test_gemv_reference_fixtures_match_scalar_kernels():
