@@ -62,6 +62,10 @@ def main():
     ap.add_argument("--gemm-steps", type=int, default=200)
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="bound on the CPU-baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-e2e", action="store_true", help="skip the end-to-end decoder run")
+    ap.add_argument("--e2e-steps", type=int, default=256, help="greedy decode steps of the end-to-end run")
+    ap.add_argument("--e2e-cpu-steps", type=int, default=64,
+                    help="decode steps of the CPU-matmul end-to-end run (parity and CPU tok/s)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="first run one 256 MiB device-to-device copy (calibrates profiler byte counters)")
     args = ap.parse_args()
@@ -179,6 +183,8 @@ def main():
                          f"{2.0 * 961 * M * K / cpu_gemm_s / 1e9:.1f} GFLOP/s)",
                "n961_gflops": 2.0 * 961 * M * K / cpu_gemm_s / 1e9}
 
+    e2e = None if args.no_e2e else run_e2e(args, cpu_ok=not args.no_cpu and oracle.cpu_has_avx2())
+
     out = {
         "metric": "Q-matmul GB/s (N=1) & TFLOP/s (N=961) as % roofline; decode tok/s",
         "value": round(gemv_gbs, 2),
@@ -200,8 +206,50 @@ def main():
         "gemm": gemm,
         "parity_ok": parity_ok and all(v["rel_err_vs_f64"] <= 1e-2 for v in gemm.values()),
         "cpu_baseline": cpu,
+        "e2e": e2e,
     }
+    if e2e and e2e.get("greedy_identical") is False:
+        out["parity_ok"] = False
     print(json.dumps(out))
+
+
+def run_e2e(args, cpu_ok):
+    """Seeded random-init Qwen2.5-0.5B-shaped model (24 layers, Q4_K_M mix): 961-token prefill and
+    greedy decode with every projection on the GPU (f32 mode), the host steps on the CPU; then the
+    same with the reference-restated CPU kernels for the first e2e_cpu_steps tokens."""
+    import rehip
+    from rehip import qwen
+
+    mb = qwen.synth_model(501)
+    prompt = np.random.default_rng(502).integers(0, mb.n_vocab, 961)
+
+    def decode(backend, steps):
+        r = qwen.DenseRunner(mb, backend)
+        dec = qwen.DenseDecoder(r, len(prompt) + steps)
+        t0 = time.perf_counter()
+        logits = dec.prefill(prompt)
+        t1 = time.perf_counter()
+        toks = [qwen.argmax_last(logits)]
+        for _ in range(steps - 1):
+            toks.append(qwen.argmax_last(dec.step(toks[-1])))
+        t2 = time.perf_counter()
+        if hasattr(r, "close"):
+            r.close()
+        return toks, t1 - t0, (steps - 1) / (t2 - t1) if steps > 1 else None
+
+    toks, pre_s, tps = decode(qwen.HipBackend(rehip.MODE_F32), args.e2e_steps)
+    res = {"model": "Qwen2.5-0.5B-shaped (24 layers, 896/14/2 heads, d_ff 4864, vocab 151936), Q4_K_M mix, "
+                    "random init seed 501",
+           "prompt_tokens": len(prompt), "decode_steps": args.e2e_steps, "matmul_mode": "f32",
+           "prefill_s_hip": pre_s, "decode_tok_s_hip": tps,
+           "host_steps": "attention/norm/RoPE/argmax on the host (numpy), projections through the backend"}
+    if cpu_ok:
+        from oracle.backend import CpuBackend
+        n = min(args.e2e_cpu_steps, args.e2e_steps)
+        ctoks, cpre_s, ctps = decode(CpuBackend(), n)
+        res.update({"prefill_s_cpu": cpre_s, "decode_tok_s_cpu": ctps, "cpu_decode_steps": n,
+                    "greedy_identical": ctoks == toks[:n], "greedy_compared_steps": n})
+    return res
 
 
 if __name__ == "__main__":

@@ -13,6 +13,9 @@
  *   folds the block into an 8-lane FMA accumulator (the reference's fused AVX2 dots,
  *   kernel.rs:488-954, follow the same per-block dequant + FMA structure).
  * - Pool: OpenMP's persistent team stands in for src/pool.rs:145-163.
+ * Rows whose length n is not a multiple of the block size are stored as whole blocks (the padded
+ * row rule of the GPU library and of orc_qmat_*); only the first n dequantized elements of a row
+ * enter a dot. n must be a multiple of 32.
  */
 #include <immintrin.h>
 #include <stdlib.h>
@@ -61,12 +64,12 @@ static void dot_x4x2(const float *a0, const float *a1, const float *const b[4], 
 }
 
 /* matmul_reuse with tile 96, group 4, w_rows 2, r_block 1024 (kernel.rs:1383-1477).
- * W is m x n (whole blocks), X rows x n, out rows x m with row stride ldo. */
+ * W is m rows of ceil(n/qk) blocks, X rows x n, out rows x m with row stride ldo. */
 static void matmul_reuse_avx2(const uint8_t *w, size_t m, size_t n, const float *x, size_t rows,
                               float *out, size_t ldo, size_t qk, size_t bb,
                               void (*dq)(const uint8_t *, float *), float *rb0b, float *rb1b) {
     const size_t tile = 96, r_block = 1024;
-    size_t blocks = n / qk, row_bytes = blocks * bb;
+    size_t blocks = (n + qk - 1) / qk, row_bytes = blocks * bb;
     for (size_t rb0 = 0; rb0 < m; rb0 += r_block) {
         size_t rb1 = rb0 + r_block < m ? rb0 + r_block : m;
         for (size_t r0 = 0; r0 < rows; r0 += tile) {
@@ -111,21 +114,22 @@ int orc_cpu_matmul(uint32_t t, const uint8_t *w, size_t m, size_t n, const float
     size_t qk, bb;
     void (*dq)(const uint8_t *, float *);
     if (quant_geom_raw(t, &qk, &bb, &dq)) return ORC_ERR_TYPE;
-    if (n % qk) return ORC_ERR_SIZE;
+    if (n % 32) return ORC_ERR_SIZE;
     int th = nthreads(threads);
-    size_t row_bytes = n / qk * bb;
+    size_t blocks = (n + qk - 1) / qk, row_bytes = blocks * bb;
     int split_w = rows * n * 4 > 6u * 1024 * 1024;             /* MATMUL_X_L3_BUDGET, qmat.rs:18 */
     size_t span = split_w ? m : rows;
     size_t chunk = (span + (size_t)th - 1) / (size_t)th;
     size_t jobs = (span + chunk - 1) / chunk;
 #pragma omp parallel for num_threads(th) schedule(static, 1)
     for (size_t j = 0; j < jobs; ++j) {
-        float *bufs = (float *)aligned_alloc(64, ((2 * n * sizeof(float)) + 63) / 64 * 64);
+        const size_t nb = blocks * qk;
+        float *bufs = (float *)aligned_alloc(64, ((2 * nb * sizeof(float)) + 63) / 64 * 64);
         size_t lo = j * chunk, cnt = chunk < span - lo ? chunk : span - lo;
         if (split_w)   /* qmat.rs:256-262: weight-row slice, whole X, strided stitch */
-            matmul_reuse_avx2(w + lo * row_bytes, cnt, n, x, rows, out + lo, m, qk, bb, dq, bufs, bufs + n);
+            matmul_reuse_avx2(w + lo * row_bytes, cnt, n, x, rows, out + lo, m, qk, bb, dq, bufs, bufs + nb);
         else           /* qmat.rs:206-217: activation-row slice */
-            matmul_reuse_avx2(w, m, n, x + lo * n, cnt, out + lo * m, m, qk, bb, dq, bufs, bufs + n);
+            matmul_reuse_avx2(w, m, n, x + lo * n, cnt, out + lo * m, m, qk, bb, dq, bufs, bufs + nb);
         free(bufs);
     }
     return ORC_OK;
@@ -137,9 +141,9 @@ int orc_cpu_matvec(uint32_t t, const uint8_t *w, size_t m, size_t n, const float
     size_t qk, bb;
     void (*dq)(const uint8_t *, float *);
     if (quant_geom_raw(t, &qk, &bb, &dq)) return ORC_ERR_TYPE;
-    if (n % qk) return ORC_ERR_SIZE;
+    if (n % 32) return ORC_ERR_SIZE;
     int th = nthreads(threads);
-    size_t blocks = n / qk, row_bytes = blocks * bb;
+    size_t blocks = (n + qk - 1) / qk, row_bytes = blocks * bb;
 #pragma omp parallel for num_threads(th) schedule(static)
     for (size_t r = 0; r < m; ++r) {
         float buf[256] __attribute__((aligned(32)));
@@ -148,7 +152,8 @@ int orc_cpu_matvec(uint32_t t, const uint8_t *w, size_t m, size_t n, const float
         for (size_t b = 0; b < blocks; ++b) {
             dq(row + b * bb, buf);
             const float *xb = x + b * qk;
-            for (size_t i = 0; i < qk; i += 8)
+            const size_t len = n - b * qk < qk ? n - b * qk : qk;
+            for (size_t i = 0; i < len; i += 8)
                 acc = _mm256_fmadd_ps(_mm256_load_ps(buf + i), _mm256_loadu_ps(xb + i), acc);
         }
         out[r] = hsum256(acc);

@@ -1,0 +1,366 @@
+"""Dense Qwen2-architecture decoder over a pluggable quantized-matmul backend.
+
+This restates the reference's dense runner (src/runner.rs:105-282) and transformer block
+(src/forward.rs:100-586) on the host, with every projection going through a backend object
+that exposes `matvec(x)` / `matmul(x, rows)` like `QMat` (src/qmat.rs:80, 169):
+
+  * `HipBackend` routes each projection through librehip (`rehip.QMat`), which is the drop-in
+    the reference would make in `QMat::Quant`;
+  * any other object with `make(ggml_type, bytes, m, n)` returning such a matrix and
+    `dequant(ggml_type, bytes)` can be passed in (the measurement and parity code passes the
+    CPU kernels this way).
+
+Attention, RMS-norm, RoPE, SwiGLU and argmax stay on the host, as in the reference's
+configuration for this workload. They are vectorised numpy restatements of:
+  rmsnorm            infer.rs:72-82    x * (1 / sqrt(mean(x^2) + eps)) * w
+  rope (NeoX)        infer.rs:90-139   angle = pos * base^(-2i/d); (x0 c - x1 s, x1 c + x0 s)
+  attention          forward.rs:232-277, 437-470   softmax(q.k / sqrt(hd)) over 0..=pos, p.v
+  softmax            moe.rs:61-72      exp(x - max) / sum (no division when the sum is 0)
+  silu / swiglu      moe.rs:44-51, 280-283         g * (1 / (1 + exp(-g))) * u
+  argmax             infer.rs:217-223  the last index among equal maxima (Iterator::max_by)
+  decoder            runner.rs:205-282 batched prefill that fills rotated K/V, then one
+                                       position per step over the cache.
+Sums inside these host steps use numpy's order, not the reference's sequential f32 order;
+both backends share this host code, so a greedy comparison between them isolates the matmuls.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import MODE_F32, Q4_K, Q6_K, Q8_0, QMat, dequant
+from . import synth
+
+
+@dataclass(frozen=True)
+class Geometry:
+    """forward.rs:17-55."""
+    d_model: int = 896
+    n_heads: int = 14
+    n_kv_heads: int = 2
+    d_ff: int = 4864
+    rope_freq_base: float = 1e6
+    rms_eps: float = 1e-6
+
+    @property
+    def head_dim(self) -> int:
+        return self.d_model // self.n_heads
+
+
+QWEN25_05B = Geometry()
+QWEN25_05B_LAYERS = 24
+QWEN25_05B_VOCAB = 151936
+
+
+class HipBackend:
+    """Projections on the GPU through librehip; `mode` selects bf16 MFMA or f32 GEMM."""
+
+    name = "hip"
+
+    def __init__(self, mode: int = MODE_F32):
+        self.mode = mode
+
+    @staticmethod
+    def dequant(ggml_type: int, data: np.ndarray) -> np.ndarray:
+        return dequant(ggml_type, data)
+
+    def make(self, ggml_type: int, data: np.ndarray, m: int, n: int):
+        q = QMat.from_bytes(ggml_type, data, m, n)
+        mode = self.mode
+
+        class _M:
+            def rows(self_):
+                return m
+
+            def cols(self_):
+                return n
+
+            def matvec(self_, x):
+                return q.matvec(x)
+
+            def matmul(self_, x, rows):
+                return q.matmul(x, rows, mode)
+
+            def close(self_):
+                q.close()
+
+        return _M()
+
+
+# ---- host steps ---------------------------------------------------------------------------
+def rmsnorm_rows(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    x = x.reshape(-1, w.size)
+    ms = np.einsum("ij,ij->i", x, x, dtype=np.float32) / np.float32(w.size)
+    inv = np.float32(1.0) / np.sqrt(ms + np.float32(eps), dtype=np.float32)
+    return (x * inv[:, None] * w[None, :]).astype(np.float32)
+
+
+def rope_freqs(d: int, base: float) -> np.ndarray:
+    i = np.arange(d // 2, dtype=np.float32)
+    return (np.float32(1.0) / np.power(np.float32(base), np.float32(2.0) * i / np.float32(d))).astype(np.float32)
+
+
+def rope_table(seq: int, pos_start: int, d: int, base: float):
+    f = rope_freqs(d, base)
+    ang = (np.arange(pos_start, pos_start + seq, dtype=np.float32)[:, None] * f[None, :]).astype(np.float32)
+    return np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+
+
+def rope_rows(x: np.ndarray, heads: int, hd: int, cos: np.ndarray, sin: np.ndarray) -> np.ndarray:
+    """NeoX rotate-half of a (seq, heads * hd) buffer with per-row (cos, sin) tables."""
+    v = x.reshape(-1, heads, hd)
+    half = hd // 2
+    x0, x1 = v[:, :, :half], v[:, :, half:]
+    c, s = cos[:, None, :], sin[:, None, :]
+    out = np.empty_like(v)
+    out[:, :, :half] = x0 * c - x1 * s
+    out[:, :, half:] = x1 * c + x0 * s
+    return out.reshape(x.shape)
+
+
+def softmax_rows(s: np.ndarray) -> np.ndarray:
+    mx = np.max(s, axis=-1, keepdims=True)
+    e = np.exp(s - mx).astype(np.float32)
+    tot = np.sum(e, axis=-1, keepdims=True, dtype=np.float32)
+    return np.where(tot != 0, e / np.where(tot != 0, tot, 1), e).astype(np.float32)
+
+
+def attention(q: np.ndarray, kc: np.ndarray, vc: np.ndarray, g: Geometry, pos_start: int) -> np.ndarray:
+    """Causal GQA attention of `seq` rotated query rows at positions pos_start.. over the cache
+    rows 0..pos_start+seq (forward.rs:232-277)."""
+    hd, nh, nkv = g.head_dim, g.n_heads, g.n_kv_heads
+    seq = q.shape[0] // (nh * hd) if q.ndim == 1 else q.shape[0]
+    q = q.reshape(seq, nh, hd)
+    total = pos_start + seq
+    k = kc[:total].reshape(total, nkv, hd)
+    v = vc[:total].reshape(total, nkv, hd)
+    scale = np.float32(1.0) / np.sqrt(np.float32(hd))
+    ctx = np.empty((seq, nh, hd), np.float32)
+    grp = nh // nkv                       # query heads h with h * nkv // nh == kv are contiguous
+    rows = 128                            # query rows per pass: temporaries stay cache-sized
+    for kv in range(nkv):
+        qg = np.ascontiguousarray(q[:, kv * grp:(kv + 1) * grp, :].transpose(1, 0, 2))   # grp, seq, hd
+        kt = np.ascontiguousarray(k[:, kv, :].T)
+        vv = np.ascontiguousarray(v[:, kv, :])
+        for r0 in range(0, seq, rows):
+            r1 = min(seq, r0 + rows)
+            end = pos_start + r1                           # keys 0..end-1 cover every row here
+            s = np.matmul(qg[:, r0:r1, :], kt[:, :end]) * scale                             # grp, r, end
+            if r1 - r0 > 1 or end > pos_start + r0 + 1:
+                later = np.arange(end)[None, :] > (pos_start + np.arange(r0, r1))[:, None]
+                s[:, later] = -np.inf
+            p = softmax_rows(s)
+            ctx[r0:r1, kv * grp:(kv + 1) * grp, :] = np.matmul(p, vv[:end]).transpose(1, 0, 2)
+    return ctx.reshape(seq, nh * hd)
+
+
+def silu(x: np.ndarray) -> np.ndarray:
+    with np.errstate(over="ignore"):      # exp(-x) = inf for x < -88 gives silu = -0, as in f32
+        return (x * (np.float32(1.0) / (np.float32(1.0) + np.exp(-x)))).astype(np.float32)
+
+
+def argmax_last(logits: np.ndarray) -> int:
+    """Index of the maximum; among equal maxima the last one (infer.rs:217-223)."""
+    mx = np.max(logits)
+    return int(np.flatnonzero(logits == mx)[-1])
+
+
+# ---- weights ------------------------------------------------------------------------------
+@dataclass
+class BlockBytes:
+    q: np.ndarray
+    k: np.ndarray
+    v: np.ndarray
+    o: np.ndarray
+    gate: np.ndarray
+    up: np.ndarray
+    down: np.ndarray
+    attn_norm: np.ndarray
+    ffn_norm: np.ndarray
+    q_bias: np.ndarray
+    k_bias: np.ndarray
+    v_bias: np.ndarray
+
+
+@dataclass
+class ModelBytes:
+    geom: Geometry
+    n_vocab: int
+    embed: np.ndarray          # Q8_0 token_embd bytes, n_vocab x d_model
+    output: np.ndarray         # Q8_0 output (lm_head) bytes, n_vocab x d_model
+    output_norm: np.ndarray
+    blocks: list
+    attn_type: int = Q4_K
+    ffn_type: int = Q4_K
+    down_type: int = Q6_K
+    embed_type: int = Q8_0
+
+
+# standard deviation of one block's (scale-free) value, d = 1: Q4_K sc*q - 7.5*m with sc, m
+# uniform in 0..63 and q in 0..15 (zero mean); Q6_K sc*(q - 32) with sc in -64..63, q in 0..63;
+# Q8_0 qs uniform in -128..127
+_UNIT_STD = {Q4_K: 257.2, Q6_K: 682.4, Q8_0: 73.9}
+
+
+def conditioned_weight_bytes(rng: np.random.Generator, t: int, m: int, n: int, std: float) -> np.ndarray:
+    """Random GGUF block bytes (synth.weight_bytes) whose f16 scales are re-drawn as
+    |N(0,1)| * std / unit_std(t), so the dequantized weights have about zero mean and the given
+    standard deviation (Q4_K: dmin = 7.5 d cancels the mean of d*sc*q)."""
+    raw = synth.weight_bytes(rng, t, m, n)
+    qk, bb = {Q4_K: (256, 144), Q6_K: (256, 210), Q8_0: (32, 34)}[t]
+    blocks = raw.reshape(-1, bb)
+    nb = blocks.shape[0]
+    d = (np.abs(rng.standard_normal(nb)) * (std / _UNIT_STD[t])).astype(np.float16)
+    if t == Q4_K:
+        blocks[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
+        blocks[:, 2:4] = (d.astype(np.float32) * 7.5).astype(np.float16).view(np.uint8).reshape(nb, 2)
+    elif t == Q6_K:
+        blocks[:, 208:210] = d.view(np.uint8).reshape(nb, 2)
+    else:
+        blocks[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
+    return raw
+
+
+def synth_model(seed: int, geom: Geometry = QWEN25_05B, n_layers: int = QWEN25_05B_LAYERS,
+                n_vocab: int = QWEN25_05B_VOCAB) -> ModelBytes:
+    """Seeded random-init weights of the Q4_K_M mix: Q4_K attention and gate/up, Q6_K down,
+    Q8_0 embedding and output (untied: a tied random model locks onto one token). Projection weights have about zero mean and standard deviation
+    1/sqrt(K) (activations stay of order one through the layers), embedding entries 0.1; norm
+    weights are 1 + N(0, 0.1^2), q/k/v biases N(0, 0.1^2)."""
+    rng = np.random.default_rng(seed)
+    d, kv, ff = geom.d_model, geom.n_kv_heads * geom.head_dim, geom.d_ff
+    wd, wf = 1.0 / np.sqrt(d), 1.0 / np.sqrt(ff)
+    blocks = []
+    for _ in range(n_layers):
+        blocks.append(BlockBytes(
+            q=conditioned_weight_bytes(rng, Q4_K, d, d, wd), k=conditioned_weight_bytes(rng, Q4_K, kv, d, wd),
+            v=conditioned_weight_bytes(rng, Q4_K, kv, d, wd), o=conditioned_weight_bytes(rng, Q4_K, d, d, wd),
+            gate=conditioned_weight_bytes(rng, Q4_K, ff, d, wd), up=conditioned_weight_bytes(rng, Q4_K, ff, d, wd),
+            down=conditioned_weight_bytes(rng, Q6_K, d, ff, wf),
+            attn_norm=(1 + 0.1 * rng.standard_normal(d)).astype(np.float32),
+            ffn_norm=(1 + 0.1 * rng.standard_normal(d)).astype(np.float32),
+            q_bias=(0.1 * rng.standard_normal(d)).astype(np.float32),
+            k_bias=(0.1 * rng.standard_normal(kv)).astype(np.float32),
+            v_bias=(0.1 * rng.standard_normal(kv)).astype(np.float32)))
+    embed = conditioned_weight_bytes(rng, Q8_0, n_vocab, d, 0.1)
+    output = conditioned_weight_bytes(rng, Q8_0, n_vocab, d, 0.1)
+    output_norm = (1 + 0.1 * rng.standard_normal(d)).astype(np.float32)
+    return ModelBytes(geom, n_vocab, embed, output, output_norm, blocks)
+
+
+class _Block:
+    def __init__(self, b: BlockBytes, mb: ModelBytes, backend):
+        g = mb.geom
+        d, kv, ff = g.d_model, g.n_kv_heads * g.head_dim, g.d_ff
+        self.q = backend.make(mb.attn_type, b.q, d, d)
+        self.k = backend.make(mb.attn_type, b.k, kv, d)
+        self.v = backend.make(mb.attn_type, b.v, kv, d)
+        self.o = backend.make(mb.attn_type, b.o, d, d)
+        self.gate = backend.make(mb.ffn_type, b.gate, ff, d)
+        self.up = backend.make(mb.ffn_type, b.up, ff, d)
+        self.down = backend.make(mb.down_type, b.down, d, ff)
+        self.attn_norm, self.ffn_norm = b.attn_norm, b.ffn_norm
+        self.q_bias, self.k_bias, self.v_bias = b.q_bias, b.k_bias, b.v_bias
+
+    def mats(self):
+        return (self.q, self.k, self.v, self.o, self.gate, self.up, self.down)
+
+
+class DenseRunner:
+    """runner.rs:11-120: the embedding table is dequantized once (the backend's bit-exact
+    dequant); the output projection is a quantized matrix like the others."""
+
+    def __init__(self, mb: ModelBytes, backend):
+        self.geom = mb.geom
+        self.n_vocab = mb.n_vocab
+        self.embed = backend.dequant(mb.embed_type, mb.embed).reshape(mb.n_vocab, mb.geom.d_model)
+        self.blocks = [_Block(b, mb, backend) for b in mb.blocks]
+        self.output_norm = mb.output_norm
+        self.output = backend.make(mb.embed_type, mb.output, mb.n_vocab, mb.geom.d_model)
+
+    def close(self):
+        for b in self.blocks:
+            for m in b.mats():
+                if hasattr(m, "close"):
+                    m.close()
+        if hasattr(self.output, "close"):
+            self.output.close()
+
+
+class DenseDecoder:
+    """runner.rs:205-282: per-layer rotated K/V caches; batched prefill, then one position per
+    step."""
+
+    def __init__(self, runner: DenseRunner, max_seq: int):
+        self.r = runner
+        g = runner.geom
+        kv = g.n_kv_heads * g.head_dim
+        self.kc = [np.zeros((max_seq, kv), np.float32) for _ in runner.blocks]
+        self.vc = [np.zeros((max_seq, kv), np.float32) for _ in runner.blocks]
+        self.seq_len = 0
+
+    def _block(self, l: int, blk: _Block, x: np.ndarray, seq: int, pos_start: int) -> np.ndarray:
+        g = self.r.geom
+        hd = g.head_dim
+        d = g.d_model
+        n = rmsnorm_rows(x, blk.attn_norm, g.rms_eps).reshape(-1)
+        if seq == 1:
+            q, k, v = blk.q.matvec(n), blk.k.matvec(n), blk.v.matvec(n)
+        else:
+            q, k, v = blk.q.matmul(n, seq), blk.k.matmul(n, seq), blk.v.matmul(n, seq)
+        q = (q.reshape(seq, -1) + blk.q_bias).astype(np.float32)
+        k = (k.reshape(seq, -1) + blk.k_bias).astype(np.float32)
+        v = (v.reshape(seq, -1) + blk.v_bias).astype(np.float32)
+        cos, sin = rope_table(seq, pos_start, hd, g.rope_freq_base)
+        q = rope_rows(q, g.n_heads, hd, cos, sin)
+        k = rope_rows(k, g.n_kv_heads, hd, cos, sin)
+        self.kc[l][pos_start:pos_start + seq] = k
+        self.vc[l][pos_start:pos_start + seq] = v
+        ctx = attention(q, self.kc[l], self.vc[l], g, pos_start).reshape(-1)
+        o = blk.o.matvec(ctx) if seq == 1 else blk.o.matmul(ctx, seq)
+        y = (x.reshape(seq, d) + o.reshape(seq, d)).astype(np.float32)
+        yn = rmsnorm_rows(y, blk.ffn_norm, g.rms_eps).reshape(-1)
+        if seq == 1:
+            gt, up = blk.gate.matvec(yn), blk.up.matvec(yn)
+        else:
+            gt, up = blk.gate.matmul(yn, seq), blk.up.matmul(yn, seq)
+        act = (silu(gt) * up).astype(np.float32)
+        dn = blk.down.matvec(act) if seq == 1 else blk.down.matmul(act, seq)
+        return (y + dn.reshape(seq, d)).astype(np.float32)
+
+    def _logits(self, last: np.ndarray) -> np.ndarray:
+        g = self.r.geom
+        normed = rmsnorm_rows(last, self.r.output_norm, g.rms_eps).reshape(-1)
+        return self.r.output.matvec(normed)
+
+    def prefill(self, prompt) -> np.ndarray:
+        prompt = np.asarray(prompt, dtype=np.int64)
+        seq = prompt.size
+        x = self.r.embed[prompt].astype(np.float32)
+        pos_start = self.seq_len
+        for l, blk in enumerate(self.r.blocks):
+            x = self._block(l, blk, x, seq, pos_start)
+        self.seq_len += seq
+        return self._logits(x[-1])
+
+    def step(self, tok: int) -> np.ndarray:
+        x = self.r.embed[tok][None, :].astype(np.float32)
+        pos = self.seq_len
+        for l, blk in enumerate(self.r.blocks):
+            x = self._block(l, blk, x, 1, pos)
+        self.seq_len += 1
+        return self._logits(x[0])
+
+    def generate(self, prompt, max_new: int, on_token=None):
+        """runner.rs:262-282 without an EOS token: prefill, then argmax / step."""
+        logits = self.prefill(prompt)
+        out = []
+        for i in range(max_new):
+            t = argmax_last(logits)
+            out.append(t)
+            if on_token:
+                on_token(i, t)
+            if i + 1 < max_new:
+                logits = self.step(t)
+        return out

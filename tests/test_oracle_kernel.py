@@ -253,3 +253,21 @@ def test_cpu_baseline_matches_oracle(t):
     mv = O.cpu_matvec(t, w, m, n, x[:n], threads=4)
     absd = O.qmat_absdot(t, w, m, n, x[:n], 1)
     assert np.all(np.abs(mv - O.matvec(t, w, m, n, x[:n])) <= 2 * n * 2.0 ** -24 * absd)
+
+
+@pytest.mark.parametrize("t", [O.Q4_K, O.Q5_K, O.Q6_K])
+def test_cpu_baseline_padded_k_quant_rows(t):
+    # K = 896 is not a multiple of 256: rows are stored as 4 whole super-blocks and only the
+    # first 896 elements enter the dot (the padded-row rule of the QMat oracle)
+    if not O.cpu_has_avx2():
+        pytest.skip("host has no AVX2+FMA")
+    rng = np.random.default_rng(70 + t)
+    m, n, rows = 40, 896, 6
+    w = random_rows(rng, t, m, n)
+    assert w.size == m * O.qmat_row_bytes(t, n)
+    x = rng.standard_normal(rows * n).astype(np.float32)
+    got = O.cpu_matmul(t, w, m, n, x, rows, threads=3)
+    absd = O.qmat_absdot(t, w, m, n, x, rows)
+    assert np.all(np.abs(got - O.qmat_matmul(t, w, m, n, x, rows)) <= 2 * n * 2.0 ** -24 * absd)
+    mv = O.cpu_matvec(t, w, m, n, x[:n], threads=3)
+    assert np.all(np.abs(mv - O.qmat_matvec(t, w, m, n, x[:n])) <= 2 * n * 2.0 ** -24 * absd[:m])
