@@ -223,6 +223,16 @@ int gemm_enqueue(re_qmat* q, const float* d_x, size_t rows, float* d_y, int mode
   if (xbytes >= (1ull << 31) || q->g.bytes >= (1ull << 31))
     return fail(RE_ERR_SIZE, "GEMM operands must stay below 2 GiB (X %zu B, W %zu B)", xbytes, q->g.bytes);
   GemmPlan pl = plan_gemm((int)q->g.m, (int)rows, (int)q->g.n, mode);
+  // tuning knobs: REHIP_GEMM_TILE (1 64x64, 2 128x128, 3 128x256, 4 256x128), REHIP_GEMM_KG,
+  // REHIP_GEMM_SPLITS; a combination the library does not build fails at launch
+  if (const size_t t = env_size("REHIP_GEMM_TILE", 0); t >= 1 && t <= 4) {
+    pl.tile = (GemmTile)(t - 1);
+    pl.kgroups = (int)env_size("REHIP_GEMM_KG", 1);
+    const int steps = (int)((q->g.n + kGemmBK - 1) / kGemmBK);
+    const int sp = std::max(1, std::min(steps, (int)env_size("REHIP_GEMM_SPLITS", 1)));
+    pl.steps_per_split = (steps + sp - 1) / sp;
+    pl.splits = (steps + pl.steps_per_split - 1) / pl.steps_per_split;
+  }
   const size_t part_bytes = (size_t)pl.splits * rows * q->g.m * sizeof(float);
   if (pl.splits > 1 && part_bytes > q->spart.cap) {
     // the partial-sum buffer grows on first use; under stream capture nothing may be allocated,
@@ -256,7 +266,7 @@ int gemm_enqueue(re_qmat* q, const float* d_x, size_t rows, float* d_y, int mode
     if (rc) return rc;
     a.partial = (float*)q->spart.p;
   }
-  HIP_TRY(launch_gemm(q->g.type, mode, a, 0, pl.tile, s));
+  HIP_TRY(launch_gemm(q->g.type, mode, a, 0, pl.tile, pl.kgroups, s));
   return RE_OK;
 }
 
@@ -536,14 +546,16 @@ int re_moe_forward_dev(re_moe* e, const float* d_x, size_t tokens, size_t top_k,
   a.w_bytes = (uint32_t)(e->gg.bytes * e->n_experts);
   a.w_stride = e->gg.bytes;
   a.Y = (float*)e->sg.p;
-  HIP_TRY(launch_gemm(e->gg.type, mode, a, (int)t_gu.size(), GemmTile::k64x64, s));
+  const int kg_gu = gemm_kgroups(GemmTile::k64x64, mode, (long)t_gu.size(), (int)((e->hidden + kGemmBK - 1) / kGemmBK));
+  const int kg_d = gemm_kgroups(GemmTile::k64x64, mode, (long)t_d.size(), (int)((e->inter + kGemmBK - 1) / kGemmBK));
+  HIP_TRY(launch_gemm(e->gg.type, mode, a, (int)t_gu.size(), GemmTile::k64x64, kg_gu, s));
   a.W = e->d_up;
   a.w_bytes = (uint32_t)(e->gu.bytes * e->n_experts);
   a.w_stride = e->gu.bytes;
   a.KB = (int)e->gu.kb;
   a.tiles = (int)e->gu.tiles;
   a.Y = (float*)e->su.p;
-  HIP_TRY(launch_gemm(e->gu.type, mode, a, (int)t_gu.size(), GemmTile::k64x64, s));
+  HIP_TRY(launch_gemm(e->gu.type, mode, a, (int)t_gu.size(), GemmTile::k64x64, kg_gu, s));
   HIP_TRY(launch_swiglu((const float*)e->sg.p, (const float*)e->su.p, (float*)e->sh.p, pairs * e->inter, s));
   GemmArgs d{};
   d.W = e->d_down;
@@ -561,7 +573,7 @@ int re_moe_forward_dev(re_moe* e, const float* d_x, size_t tokens, size_t top_k,
   d.ldy = (int)e->hidden;
   d.tasks = (const GemmTask*)(dm + off_td);
   d.xrow = nullptr;
-  HIP_TRY(launch_gemm(e->gd.type, mode, d, (int)t_d.size(), GemmTile::k64x64, s));
+  HIP_TRY(launch_gemm(e->gd.type, mode, d, (int)t_d.size(), GemmTile::k64x64, kg_d, s));
   HIP_TRY(launch_combine((const float*)e->syp.p, (const int*)(dm + off_pos), (const float*)(dm + off_w), d_out,
                          (int)tokens, (int)top_k, (int)e->hidden, s));
   return RE_OK;

@@ -23,24 +23,12 @@
 
 namespace rehip {
 
+// binary16 -> f32 (src/quant.rs:25-45): v_cvt_f32_f16 widens every finite value and infinity
+// exactly, subnormals included (f16 denormals are kept in the kernel float mode). A signalling NaN
+// comes out quieted with its payload; the reference's value keeps the signalling bit, but every
+// dequantized value multiplies the scale, and that multiplication quiets it on both sides.
 __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
-  // src/quant.rs:25-45 (exact widening incl. subnormals; NaN payload kept)
-  const uint32_t sign = (h & 0x8000u) << 16;
-  const uint32_t exp = (h >> 10) & 0x1Fu;
-  const uint32_t frac = h & 0x3FFu;
-  uint32_t bits;
-  if (exp == 0x1F) {
-    bits = sign | 0x7F800000u | (frac << 13);
-  } else if (exp != 0) {
-    bits = sign | ((exp + 112u) << 23) | (frac << 13);
-  } else if (frac == 0) {
-    bits = sign;
-  } else {
-    // subnormal: frac * 2^-24, normalised (leading one at bit 10)
-    const int lz = __builtin_clz(frac) - 21;   // shifts to bring bit 10 to the top
-    bits = sign | ((uint32_t)(113 - lz) << 23) | (((frac << lz) & 0x3FFu) << 13);
-  }
-  return __uint_as_float(bits);
+  return (float)__builtin_bit_cast(_Float16, (unsigned short)h);
 }
 
 template <int T> struct Blk;
@@ -136,9 +124,9 @@ template <> struct Blk<T_Q4_0> {
   }
 };
 
-// spread bits 0..3 of v to bit 4 of bytes 0..3
+// spread bits 0..3 of v to bit 4 of bytes 0..3 (a 24-bit multiply: full rate, unlike v_mul_lo_u32)
 __device__ __forceinline__ uint32_t bits4_to_byte_bit4(uint32_t v) {
-  return ((v & 0xFu) * 0x00204081u & 0x01010101u) << 4;
+  return (__umul24(v & 0xFu, 0x00204081u) & 0x01010101u) << 4;
 }
 
 template <> struct Blk<T_Q5_0> {

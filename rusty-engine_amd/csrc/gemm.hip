@@ -11,8 +11,12 @@
 //     bf16 (RNE) into LDS.
 // Both are fetched with raw buffer loads: 32-bit offsets, and a read past the end of the buffer
 // returns zero, so missing rows and columns cost no branches (zero weight bytes decode to 0).
-// Global loads are double-buffered in registers: the raw chunks and X of step s+1 are in flight
-// while the MFMAs of step s run; decoding happens when they are written to LDS. LDS rows are
+// Software pipeline (one LDS stage per K-group, two barriers per step): while the MFMAs of step s
+// read LDS, the same waves decode the weight chunks of step s+1 (loaded one step earlier) into
+// registers, and the raw chunks of step s+2 and the activations of step s+1 are in flight; after
+// the MFMAs the decoded step s+1 is written to LDS. The dequantization VALU work thereby runs
+// under the matrix-core time of the previous step. Steps past the end of a K range load from
+// an out-of-range offset (zeros), so every iteration has the same branch-free body. LDS rows are
 // padded by 16 bytes so the 32 lanes reading one k-slice hit different banks.
 //
 // Dense launches use a 1-D grid ordered so that each of the 8 XCDs (workgroup w runs on XCD
@@ -60,58 +64,84 @@ __device__ __forceinline__ void run_values(const Run& r, float v[16]) {
   }
 }
 
-// 16 decoded values of a run -> LDS (two 16-byte bf16 stores, or four float4 stores)
+// A decoded chunk held in registers: runs a and b, 16 values each (bf16 or f32)
+template <bool F32> struct DecChunk;
+template <> struct DecChunk<false> { bf16x8_t v[4]; int ea, eb; };
+template <> struct DecChunk<true> { float4 v[8]; int ea, eb; };
+
 template <int T, bool F32>
-__device__ __forceinline__ void store_run(typename Elem<F32>::T* dst, const Run& r) {
+__device__ __forceinline__ void pack_run(const Run& r, DecChunk<F32>& d, int h) {
   float v[16];
   run_values<T>(r, v);
   if constexpr (F32) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      reinterpret_cast<float4*>(dst)[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+    for (int i = 0; i < 4; ++i) d.v[4 * h + i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
   } else {
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
+    for (int k = 0; k < 2; ++k) {
       bf16x8_t o;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) o[i] = (__bf16)v[8 * h + i];
-      reinterpret_cast<bf16x8_t*>(dst)[h] = o;
+      for (int i = 0; i < 8; ++i) o[i] = (__bf16)v[8 * k + i];
+      d.v[2 * h + k] = o;
     }
   }
 }
 
 template <bool F32>
-__device__ __forceinline__ void store4(typename Elem<F32>::T* dst, float4 v) {
+__device__ __forceinline__ void store_dec(typename Elem<F32>::T* row, const DecChunk<F32>& d) {
   if constexpr (F32) {
-    *reinterpret_cast<float4*>(dst) = v;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) reinterpret_cast<float4*>(row + d.ea)[i] = d.v[i];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) reinterpret_cast<float4*>(row + d.eb)[i] = d.v[4 + i];
+  } else {
+    reinterpret_cast<bf16x8_t*>(row + d.ea)[0] = d.v[0];
+    reinterpret_cast<bf16x8_t*>(row + d.ea)[1] = d.v[1];
+    reinterpret_cast<bf16x8_t*>(row + d.eb)[0] = d.v[2];
+    reinterpret_cast<bf16x8_t*>(row + d.eb)[1] = d.v[3];
+  }
+}
+
+template <bool F32> struct DecX;
+template <> struct DecX<false> { using T = bf16x4_t; };
+template <> struct DecX<true> { using T = float4; };
+
+template <bool F32>
+__device__ __forceinline__ typename DecX<F32>::T cvt_x(float4 v) {
+  if constexpr (F32) {
+    return v;
   } else {
     bf16x4_t o;
     o[0] = (__bf16)v.x; o[1] = (__bf16)v.y; o[2] = (__bf16)v.z; o[3] = (__bf16)v.w;
-    *reinterpret_cast<bf16x4_t*>(dst) = o;
+    return o;
   }
 }
 
 constexpr uint32_t kOob = 0x80000000u;   // a byte offset past every buffer: the load returns 0
 
-template <int T, bool F32, bool GROUPED, int BM, int BN, int WM, int WN>
-__global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs p) {
+template <int T, bool F32, bool GROUPED, int BM, int BN, int WM, int WN, int KG>
+__global__ __launch_bounds__(WM* WN * 64 * KG) void gemm_kernel(GemmArgs p) {
   using B = Blk<T>;
   using E = typename Elem<F32>::T;
-  constexpr int NT = WM * WN * 64;                 // threads
+  constexpr int GT = WM * WN * 64;                 // threads of one K-group
   constexpr int BK = kGemmBK;
   constexpr int LD = BK + Elem<F32>::PAD;          // LDS row stride (elements)
-  constexpr int WJOBS = BM * 4 / NT;               // (row, chunk) jobs per thread per step
-  constexpr int XV = BN * BK / 4 / NT;             // 16-byte X loads per thread per step
-  constexpr int XR = NT / 32;                      // X rows covered by one pass of the workgroup
+  constexpr int WJOBS = BM * 4 / GT;               // (row, chunk) jobs per thread per step
+  constexpr int XV = BN * BK / 4 / GT;             // 16-byte X loads per thread per step
+  constexpr int XR = GT / 32;                      // X rows covered by one pass of a group
   constexpr int TM = BM / WM / 32, TN = BN / WN / 32;
+  constexpr int STAGE = (BM + BN) * LD;            // LDS elements of one group
   static_assert(WJOBS >= 1 && XV >= 1 && TM >= 1 && TN >= 1, "tile shape");
-  __shared__ __attribute__((aligned(16))) E Ws[BM * LD];
-  __shared__ __attribute__((aligned(16))) E Xs[BN * LD];
+  static_assert((KG - 1) * BM * BN * 4 <= KG * STAGE * (int)sizeof(E), "K-group partials fit in LDS");
+  __shared__ __attribute__((aligned(16))) E smem[KG * STAGE];
 
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int grp = __builtin_amdgcn_readfirstlane(threadIdx.x / GT);
+  const int tid = threadIdx.x - grp * GT;          // thread inside the K-group
+  const int lane = threadIdx.x & 63;
+  const int wave = tid >> 6;                       // wave inside the K-group
   const int wm = wave / WN, wn = wave % WN;
+  E* const Ws = smem + grp * STAGE;
+  E* const Xs = Ws + BM * LD;
 
   int mtile, r0, rn, split = 0;
   uint32_t wbase = 0;
@@ -138,6 +168,10 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs p) {
   const int steps_all = (p.K + BK - 1) / BK;
   const int s_begin = split * p.steps_per_split;
   const int s_end = min(steps_all, s_begin + p.steps_per_split);
+  // K-group g takes steps s_begin + g, s_begin + g + KG, ...; every group runs `iters`
+  // iterations (barriers are workgroup-wide); a step past s_end loads zeros and adds nothing
+  const int iters = (s_end - s_begin + KG - 1) / KG;
+  const int s0 = s_begin + grp;
 
   const __amdgpu_buffer_rsrc_t wr = make_rsrc(p.W, p.w_bytes);
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(p.X, p.x_bytes);
@@ -150,94 +184,137 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs p) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  // activation rows this thread stages: rows XR*jj + tid/32, k offset 4*(tid%32)
+  // activation rows this thread stages: rows XR*jj + tid/32, k offset 4*(tid%32). Dense launches
+  // address row r0 + XR*jj + tid/32 as one per-thread offset plus a scalar jj*XR*K*4 (rows past
+  // N lie past the end of X and read zeros); grouped launches gather rows through xrow.
   const int xk = 4 * (tid & 31);
-  uint32_t xoff[XV];
+  constexpr int XOFFS = GROUPED ? XV : 1;
+  uint32_t xoff[XOFFS];
+  if constexpr (GROUPED) {
 #pragma unroll
-  for (int jj = 0; jj < XV; ++jj) {
-    const int rl = XR * jj + (tid >> 5);
-    uint32_t o = kOob;
-    if (rl < rn) {
-      const int g = r0 + rl;
-      const int row = (GROUPED && p.xrow) ? p.xrow[g] : g;
-      o = (uint32_t)row * (uint32_t)p.K * 4u + (uint32_t)xk * 4u;
+    for (int jj = 0; jj < XV; ++jj) {
+      const int rl = XR * jj + (tid >> 5);
+      uint32_t o = kOob;
+      if (rl < rn) {
+        const int row = p.xrow ? p.xrow[r0 + rl] : r0 + rl;
+        o = (uint32_t)row * (uint32_t)p.K * 4u + (uint32_t)xk * 4u;
+      }
+      xoff[jj] = o;
     }
-    xoff[jj] = o;
+  } else {
+    xoff[0] = (uint32_t)(r0 + (tid >> 5)) * (uint32_t)p.K * 4u + (uint32_t)xk * 4u;
   }
+  const uint32_t xrow_step = (uint32_t)XR * (uint32_t)p.K * 4u;   // bytes between a thread's rows
   // weight jobs: row rl = j % BM of tile (BM/64)*mtile + rl/64, chunk c = j / BM
   uint32_t wrow[WJOBS];
   int wc[WJOBS];
 #pragma unroll
   for (int rep = 0; rep < WJOBS; ++rep) {
-    const int j = tid + NT * rep;
+    const int j = tid + GT * rep;
     const int rl = j % BM;
     const int tile = BM / 64 * mtile + (rl >> 6);
     wc[rep] = j / BM;
     wrow[rep] = tile < p.tiles ? wbase + (uint32_t)tile * (uint32_t)p.KB * (uint32_t)B::SLAB : kOob;
   }
 
-  typename B::CR wraw[WJOBS];
-  float4 xraw[XV];
-
-  auto prefetch = [&](int s) {
+  auto load_w = [&](int s, typename B::CR (&raw)[WJOBS]) {
+    const bool in = s < s_end;
 #pragma unroll
     for (int rep = 0; rep < WJOBS; ++rep) {
-      const int j = tid + NT * rep;
+      const int j = tid + GT * rep;
       const int tl = (j % BM) & 63;
       int kb, cc;
       if constexpr (B::QK == 32) { kb = 4 * s + wc[rep]; cc = 0; }
       else { kb = s >> 1; cc = 4 * (s & 1) + wc[rep]; }
-      const uint32_t slab = (kb < p.KB && wrow[rep] != kOob) ? wrow[rep] + (uint32_t)kb * (uint32_t)B::SLAB : kOob;
-      B::bload_chunk(wr, slab, tl, cc, wraw[rep]);
-    }
-    const bool kin = s * BK + xk < p.K;
-#pragma unroll
-    for (int jj = 0; jj < XV; ++jj) {
-      const uint32_t o = (kin && xoff[jj] != kOob) ? xoff[jj] + (uint32_t)(s * BK) * 4u : kOob;
-      const i32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(xr, (int)o, 0, 0);
-      xraw[jj] = make_float4(__int_as_float(v[0]), __int_as_float(v[1]), __int_as_float(v[2]), __int_as_float(v[3]));
+      const uint32_t slab = (in && kb < p.KB) ? wrow[rep] + (uint32_t)kb * (uint32_t)B::SLAB : kOob;
+      B::bload_chunk(wr, slab, tl, cc, raw[rep]);
     }
   };
-
-  auto commit = [&](int s) {
+  auto load_x = [&](int s, float4 (&xv)[XV]) {
+    const bool in = s < s_end && s * BK + xk < p.K;
+#pragma unroll
+    for (int jj = 0; jj < XV; ++jj) {
+      i32x4_t v;
+      if constexpr (GROUPED) {
+        const uint32_t o = in ? xoff[jj] + (uint32_t)(s * BK) * 4u : kOob;
+        v = __builtin_amdgcn_raw_buffer_load_b128(xr, (int)o, 0, 0);
+      } else {
+        const uint32_t o = in ? xoff[0] + (uint32_t)(s * BK) * 4u : kOob;
+        v = __builtin_amdgcn_raw_buffer_load_b128(xr, (int)o, (int)(jj * xrow_step), 0);
+      }
+      xv[jj] = make_float4(__int_as_float(v[0]), __int_as_float(v[1]), __int_as_float(v[2]), __int_as_float(v[3]));
+    }
+  };
+  auto decode = [&](int s, const typename B::CR (&raw)[WJOBS], DecChunk<F32> (&dec)[WJOBS]) {
 #pragma unroll
     for (int rep = 0; rep < WJOBS; ++rep) {
-      const int j = tid + NT * rep;
-      const int rl = j % BM, c = j / BM;
-      E* dst = Ws + rl * LD;
+      const int c = (tid + GT * rep) / BM;
       int cc, kl;
       if constexpr (B::QK == 32) { cc = 0; kl = 32 * c; }
       else { cc = 4 * (s & 1) + c; kl = -128 * (s & 1); }
       Run a, b;
-      B::decode_chunk(wraw[rep], cc, a, b);
-      store_run<T, F32>(dst + kl + a.e, a);
-      store_run<T, F32>(dst + kl + b.e, b);
+      B::decode_chunk(raw[rep], cc, a, b);
+      pack_run<T, F32>(a, dec[rep], 0);
+      pack_run<T, F32>(b, dec[rep], 1);
+      dec[rep].ea = kl + a.e;
+      dec[rep].eb = kl + b.e;
     }
+  };
+  auto write_lds = [&](const DecChunk<F32> (&dec)[WJOBS], const typename DecX<F32>::T (&xd)[XV]) {
 #pragma unroll
-    for (int jj = 0; jj < XV; ++jj) store4<F32>(Xs + (XR * jj + (tid >> 5)) * LD + xk, xraw[jj]);
+    for (int rep = 0; rep < WJOBS; ++rep) store_dec<F32>(Ws + ((tid + GT * rep) % BM) * LD, dec[rep]);
+#pragma unroll
+    for (int jj = 0; jj < XV; ++jj)
+      *reinterpret_cast<typename DecX<F32>::T*>(Xs + (XR * jj + (tid >> 5)) * LD + xk) = xd[jj];
   };
 
-  if (s_begin < s_end) prefetch(s_begin);
-  for (int s = s_begin; s < s_end; ++s) {
-    if (s > s_begin) __syncthreads();    // previous step's MFMA reads are done
-    commit(s);
-    __syncthreads();
-    if (s + 1 < s_end) prefetch(s + 1);  // in flight during the MFMAs below
+  typename B::CR rawA[WJOBS], rawB[WJOBS];
+  DecChunk<F32> dec[WJOBS];
+  float4 xraw[XV];
+  typename DecX<F32>::T xdec[XV];
+
+  // prologue: step s0 into LDS, raw chunks of s0 + KG in flight
+  load_w(s0, rawA);
+  load_x(s0, xraw);
+  load_w(s0 + KG, rawB);
+  decode(s0, rawA, dec);
+#pragma unroll
+  for (int jj = 0; jj < XV; ++jj) xdec[jj] = cvt_x<F32>(xraw[jj]);
+  write_lds(dec, xdec);
+#pragma unroll
+  for (int rep = 0; rep < WJOBS; ++rep) rawA[rep] = rawB[rep];
+  __syncthreads();
+
+  for (int it = 0; it < iters; ++it) {
+    const int s = s0 + KG * it;
+    load_x(s + KG, xraw);
+    load_w(s + 2 * KG, rawB);
+    decode(s + KG, rawA, dec);             // VALU under the MFMAs below
     if constexpr (!F32) {
+      // operands of k-slice kk+1 are read from LDS while the MFMAs of slice kk run
+      const E* wsrc = Ws + (BM / WM * wm + (lane & 31)) * LD + 8 * (lane >> 5);
+      const E* xsrc = Xs + (BN / WN * wn + (lane & 31)) * LD + 8 * (lane >> 5);
+      bf16x8_t av[2][TM], bv[2][TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) av[0][i] = *reinterpret_cast<const bf16x8_t*>(wsrc + 32 * i * LD);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) bv[0][j] = *reinterpret_cast<const bf16x8_t*>(xsrc + 32 * j * LD);
 #pragma unroll
       for (int kk = 0; kk < BK / 16; ++kk) {
-        bf16x8_t av[TM], bv[TN];
+        const int cur = kk & 1, nxt = cur ^ 1;
+        if (kk + 1 < BK / 16) {
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
-          av[i] = *reinterpret_cast<const bf16x8_t*>(Ws + (BM / WM * wm + 32 * i + (lane & 31)) * LD + 16 * kk + 8 * (lane >> 5));
+          for (int i = 0; i < TM; ++i)
+            av[nxt][i] = *reinterpret_cast<const bf16x8_t*>(wsrc + 32 * i * LD + 16 * (kk + 1));
 #pragma unroll
-        for (int j = 0; j < TN; ++j)
-          bv[j] = *reinterpret_cast<const bf16x8_t*>(Xs + (BN / WN * wn + 32 * j + (lane & 31)) * LD + 16 * kk + 8 * (lane >> 5));
+          for (int j = 0; j < TN; ++j)
+            bv[nxt][j] = *reinterpret_cast<const bf16x8_t*>(xsrc + 32 * j * LD + 16 * (kk + 1));
+        }
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
           for (int j = 0; j < TN; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[i], bv[j], acc[i][j], 0, 0, 0);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[cur][i], bv[cur][j], acc[i][j], 0, 0, 0);
       }
     } else {
 #pragma unroll 8
@@ -254,29 +331,79 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs p) {
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i], bv[j], acc[i][j], 0, 0, 0);
       }
     }
+#pragma unroll
+    for (int jj = 0; jj < XV; ++jj) xdec[jj] = cvt_x<F32>(xraw[jj]);
+    __syncthreads();                      // every wave is done reading step s
+    write_lds(dec, xdec);                 // step s + KG (zeros past the end)
+    __syncthreads();
+#pragma unroll
+    for (int rep = 0; rep < WJOBS; ++rep) rawA[rep] = rawB[rep];
   }
 
-  // ---- epilogue: D[i][j] of a 32x32 tile sits in lane j + 32*((i/4)%2), register 4*(i/8) + i%4
+  if constexpr (KG > 1) {
+    // fold the K-groups into group 0 in group order (deterministic), through LDS
+    float* red = reinterpret_cast<float*>(smem);
+    constexpr int WG_ACC = TM * TN * 16 * 64;   // accumulator floats of one wave
+    if (grp > 0) {
+      float* dst = red + ((grp - 1) * (WM * WN) + wave) * WG_ACC;
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) dst[((i * TN + j) * 16 + r) * 64 + lane] = acc[i][j][r];
+    }
+    __syncthreads();
+    if (grp > 0) return;
+#pragma unroll 1
+    for (int g = 1; g < KG; ++g) {
+      const float* src = red + ((g - 1) * (WM * WN) + wave) * WG_ACC;
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[i][j][r] += src[((i * TN + j) * 16 + r) * 64 + lane];
+    }
+  }
+
+  // ---- epilogue: D[i][j] of a 32x32 tile sits in lane j + 32*((i/4)%2), register 4*(i/8) + i%4,
+  // i.e. a lane holds 4-float pieces of one output row. Each wave turns its tiles around through
+  // its own LDS scratch (32 rows x 36 floats, past the K-group partials) so that 8 consecutive
+  // lanes store one output row's 128 contiguous bytes.
   float* Y = p.splits > 1 ? p.partial + (size_t)split * p.N * p.ldy : p.Y;
+  constexpr int SROW = 36;
+  static_assert((KG - 1) * BM * BN * 4 + WM * WN * 32 * SROW * 4 <= KG * STAGE * (int)sizeof(E),
+                "epilogue scratch fits in LDS");
+  float* scr = reinterpret_cast<float*>(smem) + (KG - 1) * BM * BN + wave * 32 * SROW;
+  const int xr8 = lane >> 3, c4 = 4 * (lane & 7);
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
-      const int xl = BN / WN * wn + 32 * j + (lane & 31);
-      if (xl >= rn) continue;
-      float* yrow = Y + (size_t)(r0 + xl) * p.ldy;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int wr0 = BM * mtile + BM / WM * wm + 32 * i + 8 * q + 4 * (lane >> 5);
-        if (wr0 + 3 < p.m) {
-          *reinterpret_cast<float4*>(yrow + wr0) =
-              make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
-        } else {
+      for (int q = 0; q < 4; ++q)
+        *reinterpret_cast<float4*>(scr + (lane & 31) * SROW + 8 * q + 4 * (lane >> 5)) =
+            make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
+      __builtin_amdgcn_wave_barrier();
+      const int xl0 = BN / WN * wn + 32 * j;
+      const int wr = BM * mtile + BM / WM * wm + 32 * i + c4;
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (wr0 + e < p.m) yrow[wr0 + e] = acc[i][j][4 * q + e];
+      for (int t = 0; t < 4; ++t) {
+        const int xr = 8 * t + xr8;
+        const float4 v = *reinterpret_cast<const float4*>(scr + xr * SROW + c4);
+        if (xl0 + xr < rn) {
+          float* yrow = Y + (size_t)(r0 + xl0 + xr) * p.ldy;
+          if (wr + 3 < p.m) {
+            *reinterpret_cast<float4*>(yrow + wr) = v;
+          } else {
+            if (wr < p.m) yrow[wr] = v.x;
+            if (wr + 1 < p.m) yrow[wr + 1] = v.y;
+            if (wr + 2 < p.m) yrow[wr + 2] = v.z;
+          }
         }
       }
+      __builtin_amdgcn_wave_barrier();
     }
   }
 }
@@ -291,39 +418,64 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(const float* __restric
   y[i] = s;
 }
 
-template <int T, bool F32, int BM, int BN, int WM, int WN>
+template <int T, bool F32, int BM, int BN, int WM, int WN, int KG, bool GROUPED>
 static hipError_t launch_shape(const GemmArgs& a, int ntasks, hipStream_t s) {
-  constexpr int NT = WM * WN * 64;
-  if (a.tasks) {
-    hipLaunchKernelGGL((gemm_kernel<T, F32, true, BM, BN, WM, WN>), dim3((unsigned)ntasks), dim3(NT), 0, s, a);
+  constexpr int NT = WM * WN * 64 * KG;
+  if constexpr (GROUPED) {
+    hipLaunchKernelGGL((gemm_kernel<T, F32, true, BM, BN, WM, WN, KG>), dim3((unsigned)ntasks), dim3(NT), 0, s, a);
+    return hipGetLastError();
+  } else {
+    const int total = ((a.m + BM - 1) / BM) * ((a.N + BN - 1) / BN) * a.splits;
+    const int grid = (total + 7) / 8 * 8;
+    hipLaunchKernelGGL((gemm_kernel<T, F32, false, BM, BN, WM, WN, KG>), dim3((unsigned)grid), dim3(NT), 0, s, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || a.splits == 1) return e;
+    const size_t n = (size_t)a.N * a.ldy;
+    hipLaunchKernelGGL(gemm_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a.partial, a.Y, n,
+                       a.splits);
     return hipGetLastError();
   }
-  const int total = ((a.m + BM - 1) / BM) * ((a.N + BN - 1) / BN) * a.splits;
-  const int grid = (total + 7) / 8 * 8;
-  hipLaunchKernelGGL((gemm_kernel<T, F32, false, BM, BN, WM, WN>), dim3((unsigned)grid), dim3(NT), 0, s, a);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess || a.splits == 1) return e;
-  const size_t n = (size_t)a.N * a.ldy;
-  hipLaunchKernelGGL(gemm_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a.partial, a.Y, n,
-                     a.splits);
-  return hipGetLastError();
 }
 
+// tile x K-group instances: dense 64x64 (KG 1/2) and 128x128 (1) in both modes, 128x256 and
+// 256x128 (1) in bf16; grouped (MoE) 64x64 (KG 1/2) in both modes.
 template <int T, bool F32>
-static hipError_t launch_t(const GemmArgs& a, int ntasks, GemmTile tile, hipStream_t s) {
+static hipError_t launch_t(const GemmArgs& a, int ntasks, GemmTile tile, int kg, hipStream_t s) {
+  if (a.tasks) {
+    if (tile != GemmTile::k64x64) return hipErrorInvalidValue;
+    if (kg == 1) return launch_shape<T, F32, 64, 64, 2, 2, 1, true>(a, ntasks, s);
+    if (kg == 2) return launch_shape<T, F32, 64, 64, 2, 2, 2, true>(a, ntasks, s);
+    return hipErrorInvalidValue;
+  }
   switch (tile) {
     case GemmTile::k128x256:
-      // bf16 only: the f32 tile pair would need 198 KiB of LDS
+      if constexpr (F32) return hipErrorInvalidValue;   // the f32 tile pair would need 198 KiB of LDS
+      else return kg != 1 ? hipErrorInvalidValue : launch_shape<T, F32, 128, 256, 2, 4, 1, false>(a, ntasks, s);
+    case GemmTile::k256x128:
       if constexpr (F32) return hipErrorInvalidValue;
-      else return launch_shape<T, F32, 128, 256, 2, 4>(a, ntasks, s);
-    case GemmTile::k128x128: return launch_shape<T, F32, 128, 128, 2, 2>(a, ntasks, s);
-    default: return launch_shape<T, F32, 64, 64, 2, 2>(a, ntasks, s);
+      else return kg != 1 ? hipErrorInvalidValue : launch_shape<T, F32, 256, 128, 4, 2, 1, false>(a, ntasks, s);
+    case GemmTile::k128x128:
+      return kg != 1 ? hipErrorInvalidValue : launch_shape<T, F32, 128, 128, 2, 2, 1, false>(a, ntasks, s);
+    default:
+      if (kg == 1) return launch_shape<T, F32, 64, 64, 2, 2, 1, false>(a, ntasks, s);
+      if (kg == 2) return launch_shape<T, F32, 64, 64, 2, 2, 2, false>(a, ntasks, s);
+      return hipErrorInvalidValue;
   }
 }
 
 template <int T>
-static hipError_t launch_mode(int mode, const GemmArgs& a, int ntasks, GemmTile tile, hipStream_t s) {
-  return mode == 1 ? launch_t<T, true>(a, ntasks, tile, s) : launch_t<T, false>(a, ntasks, tile, s);
+static hipError_t launch_mode(int mode, const GemmArgs& a, int ntasks, GemmTile tile, int kg, hipStream_t s) {
+  return mode == 1 ? launch_t<T, true>(a, ntasks, tile, kg, s) : launch_t<T, false>(a, ntasks, tile, kg, s);
+}
+
+int gemm_kgroups(GemmTile tile, int mode, long workgroups, int steps) {
+  // K-groups multiply the waves of a workgroup so that small grids still put ~4 waves on
+  // every SIMD; each group keeps at least 2 K steps
+  const int cap = tile == GemmTile::k64x64 ? 2 : 1;
+  const long waves_per_group = tile == GemmTile::k64x64 ? 4 : (tile == GemmTile::k128x128 ? 4 : 8);
+  int kg = 1;
+  while (kg * 2 <= cap && workgroups * waves_per_group * kg * 2 <= 4096 && steps >= 2 * kg * 2) kg *= 2;
+  return kg;
 }
 
 GemmPlan plan_gemm(int m, int n, int K, int mode) {
@@ -332,16 +484,30 @@ GemmPlan plan_gemm(int m, int n, int K, int mode) {
   const long t128 = (long)((m + 127) / 128) * ((n + 127) / 128);
   const long t256 = (long)((m + 127) / 128) * ((n + 255) / 256);
   const long t64 = (long)((m + 63) / 64) * ((n + 63) / 64);
-  if (mode == 0 && n >= 512 && t256 >= 200) {
+  if (mode == 0 && n >= 384) {
+    // bf16 with many activation rows: 128 weight rows x 256 activation rows, 8 waves (the
+    // 256 x 128 transpose measured no faster on the prefill shapes). Split K over workgroups
+    // until ~200 workgroups run, while the partial tiles stay <= 32 MiB.
     pl.tile = GemmTile::k128x256;
+    pl.kgroups = 1;
+    const long tw = t256;
+    if (tw < 200 && steps >= 4) {
+      long splits = std::min<long>((200 + tw - 1) / tw, steps / 2);
+      while (splits > 1 && splits * (long)n * m * 4 > (32l << 20)) --splits;
+      pl.splits = (int)std::max<long>(1, splits);
+    }
   } else if (t128 >= 200) {
     pl.tile = GemmTile::k128x128;
+    pl.kgroups = gemm_kgroups(pl.tile, mode, t128, steps);
   } else {
     pl.tile = GemmTile::k64x64;
-    // few tiles over a deep K: split the K steps when the partial tiles stay small
-    if (t64 < 128 && steps >= 8) {
-      long splits = (256 + t64 - 1) / t64;
-      splits = std::min<long>(splits, steps / 2);
+    pl.kgroups = gemm_kgroups(pl.tile, mode, t64, steps);
+    // few tiles over a deep K: also split the K steps over workgroups when the partial tiles stay
+    // small (each split keeps >= 2 steps per K-group)
+    const long groups = t64 * pl.kgroups;
+    if (groups < 512 && steps >= 4 * pl.kgroups) {
+      long splits = (512 + groups - 1) / groups;
+      splits = std::min<long>(splits, steps / (2 * pl.kgroups));
       const long partial_bytes = splits * (long)n * m * 4;
       if (partial_bytes <= (16l << 20) && splits > 1) pl.splits = (int)splits;
     }
@@ -351,14 +517,15 @@ GemmPlan plan_gemm(int m, int n, int K, int mode) {
   return pl;
 }
 
-hipError_t launch_gemm(uint32_t type, int mode, const GemmArgs& a, int ntasks, GemmTile tile, hipStream_t s) {
+hipError_t launch_gemm(uint32_t type, int mode, const GemmArgs& a, int ntasks, GemmTile tile, int kgroups,
+                       hipStream_t s) {
   switch (type) {
-    case T_Q4_0: return launch_mode<T_Q4_0>(mode, a, ntasks, tile, s);
-    case T_Q5_0: return launch_mode<T_Q5_0>(mode, a, ntasks, tile, s);
-    case T_Q8_0: return launch_mode<T_Q8_0>(mode, a, ntasks, tile, s);
-    case T_Q4_K: return launch_mode<T_Q4_K>(mode, a, ntasks, tile, s);
-    case T_Q5_K: return launch_mode<T_Q5_K>(mode, a, ntasks, tile, s);
-    case T_Q6_K: return launch_mode<T_Q6_K>(mode, a, ntasks, tile, s);
+    case T_Q4_0: return launch_mode<T_Q4_0>(mode, a, ntasks, tile, kgroups, s);
+    case T_Q5_0: return launch_mode<T_Q5_0>(mode, a, ntasks, tile, kgroups, s);
+    case T_Q8_0: return launch_mode<T_Q8_0>(mode, a, ntasks, tile, kgroups, s);
+    case T_Q4_K: return launch_mode<T_Q4_K>(mode, a, ntasks, tile, kgroups, s);
+    case T_Q5_K: return launch_mode<T_Q5_K>(mode, a, ntasks, tile, kgroups, s);
+    case T_Q6_K: return launch_mode<T_Q6_K>(mode, a, ntasks, tile, kgroups, s);
     default: return hipErrorInvalidValue;
   }
 }

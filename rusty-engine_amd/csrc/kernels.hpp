@@ -31,7 +31,7 @@ hipError_t launch_dequant(uint32_t type, const uint8_t* W, float* out, int m, in
 constexpr int kGemmBK = 128;
 constexpr int kMoeTile = 64;   // tile of the grouped (MoE) launches (64 x 64, four waves)
 
-enum class GemmTile { k64x64, k128x128, k128x256 };
+enum class GemmTile { k64x64, k128x128, k128x256, k256x128 };
 
 // Work item of a grouped launch (MoE): one tile of one expert.
 struct GemmTask {
@@ -60,13 +60,17 @@ struct GemmArgs {
 
 struct GemmPlan {
   GemmTile tile = GemmTile::k64x64;
-  int splits = 1;
+  int kgroups = 1;         // K-groups per workgroup (1 or 2): waves that share a tile, split K
+  int splits = 1;          // K split over workgroups (partials + reduce kernel)
   int steps_per_split = 1;
 };
 
-// tile and K split of a dense m x n-row launch over K (mode 0 bf16, 1 f32)
+// tile, K-groups and K split of a dense m x n-row launch over K (mode 0 bf16, 1 f32)
 GemmPlan plan_gemm(int m, int n, int K, int mode);
-hipError_t launch_gemm(uint32_t type, int mode, const GemmArgs& a, int ntasks, GemmTile tile, hipStream_t s);
+// K-groups for `workgroups` tiles of `tile` over `steps` K steps
+int gemm_kgroups(GemmTile tile, int mode, long workgroups, int steps);
+hipError_t launch_gemm(uint32_t type, int mode, const GemmArgs& a, int ntasks, GemmTile tile, int kgroups,
+                       hipStream_t s);
 
 // MoE helpers
 hipError_t launch_swiglu(const float* g, const float* u, float* h, size_t n, hipStream_t s);

@@ -90,6 +90,44 @@ def time_gemm(t: int, m: int, k: int, n: int, mode: int, launches: int, seed: in
             "frac_peak": tf / peak, "gbs": algorithmic_bytes(t, m, k) / (us * 1e-6) / 1e9}
 
 
+MOE = {"n_experts": 128, "hidden": 2048, "inter": 768, "top_k": 8}
+
+
+def time_moe(tokens: int, mode: int, reps: int, seed: int = 401):
+    """Qwen3-30B-A3B-like expert FFN (config 4): Q4_K gate/up 768x2048, Q6_K down 2048x768 for
+    128 experts, top-8 softmax routing of f32 N(0,1) logits. Times re_moe_forward_dev (host
+    grouping + metadata upload + grouped GEMMs + SwiGLU + combine) per call."""
+    import time as _time
+    from . import MoeExperts, Q4_K, Q6_K
+    E, H, I, k = MOE["n_experts"], MOE["hidden"], MOE["inter"], MOE["top_k"]
+    rng = np.random.default_rng(seed)
+    gate = np.concatenate([synth.weight_bytes(rng, Q4_K, I, H) for _ in range(E)])
+    up = np.concatenate([synth.weight_bytes(rng, Q4_K, I, H) for _ in range(E)])
+    down = np.concatenate([synth.weight_bytes(rng, Q6_K, H, I) for _ in range(E)])
+    ids, wts, _ = synth.router(np.random.default_rng(seed + 1), tokens, E, k)
+    x = synth.activations(np.random.default_rng(seed + 2), tokens, H)
+    moe = MoeExperts(Q4_K, gate, Q4_K, up, Q6_K, down, E, H, I)
+    dx = hip.DeviceBuffer.from_array(x)
+    dy = hip.DeviceBuffer(tokens * H * 4)
+    s = hip.Stream()
+    moe.forward_dev(dx, tokens, k, ids, wts, dy, mode, stream=s)
+    s.synchronize()
+    t0 = _time.perf_counter()
+    for _ in range(reps):
+        moe.forward_dev(dx, tokens, k, ids, wts, dy, mode, stream=s)
+    s.synchronize()
+    us = (_time.perf_counter() - t0) / reps * 1e6
+    moe.close()
+    s.destroy()
+    hit = len(np.unique(ids))
+    per_expert = (gate.size + up.size + down.size) // E
+    nbytes = hit * per_expert + 2 * tokens * H * 4
+    flop = 2.0 * tokens * k * 3 * H * I
+    return {"tokens": tokens, "pairs": tokens * k, "experts_hit": int(hit), "mode": "f32" if mode == 1 else "bf16",
+            "us": us, "bytes": int(nbytes), "gbs": nbytes / (us * 1e-6) / 1e9,
+            "frac_hbm": nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, "tflops": flop / (us * 1e-6) / 1e12}
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--types", default="Q4_0,Q5_0,Q8_0,Q4_K,Q5_K,Q6_K")
@@ -97,13 +135,34 @@ def main(argv=None) -> int:
     ap.add_argument("--only", default="", help="comma list of projection names")
     ap.add_argument("--json", default="")
     ap.add_argument("--gemm", action="store_true", help="time the prefill GEMMs instead")
+    ap.add_argument("--moe", action="store_true", help="time the MoE expert FFN (config 4) instead")
+    ap.add_argument("--rows", default="64,961", help="GEMM activation-row counts")
+    ap.add_argument("--modes", default="bf16,f32", help="GEMM modes")
     args = ap.parse_args(argv)
     init()
+    only = set(filter(None, args.only.split(",")))
+    if args.moe:
+        rows = []
+        for tokens in (1, 32, 512):
+            for mode in (0, 1):
+                r = time_moe(tokens, mode, reps=50 if tokens < 512 else 20)
+                rows.append(r)
+                print(f"MoE T={tokens:4d} pairs={r['pairs']:5d} experts={r['experts_hit']:3d} {r['mode']:4s} "
+                      f"{r['us']:9.1f} us {r['gbs']:8.1f} GB/s ({100 * r['frac_hbm']:5.1f}% of HBM) "
+                      f"{r['tflops']:7.2f} TFLOP/s", flush=True)
+        if args.json:
+            with open(args.json, "w") as f:
+                json.dump(rows, f, indent=1)
+        return 0
     if args.gemm:
         rows = []
+        ns = [int(v) for v in args.rows.split(",") if v]
+        modes = [{"bf16": 0, "f32": 1}[v] for v in args.modes.split(",") if v]
         for name, t, m, k in GEMMS:
-            for n in (64, 961):
-                for mode in (0, 1):
+            if only and not any(o in name for o in only):
+                continue
+            for n in ns:
+                for mode in modes:
                     r = time_gemm(t, m, k, n, mode, max(20, args.launches // 10), seed=101 + n)
                     r["name"] = name
                     rows.append(r)
@@ -115,7 +174,6 @@ def main(argv=None) -> int:
         return 0
     by_name = {v: k for k, v in TYPE_NAMES.items()}
     types = [by_name[s] for s in args.types.split(",") if s]
-    only = set(filter(None, args.only.split(",")))
     rows = []
     for ti, t in enumerate(types):
         for pi, (name, m, k) in enumerate(PROJECTIONS):

@@ -181,7 +181,7 @@ def test_lm_head_gemv_q8_0_full_size():
 
 
 # ---- GEMM --------------------------------------------------------------------------------
-GEMM_SHAPES = [(5, 256, 2), (70, 512, 3), (128, 896, 64), (200, 1024, 70), (896, 4864, 129)]
+GEMM_SHAPES = [(5, 256, 2), (70, 512, 3), (128, 896, 64), (200, 1024, 70), (896, 4864, 129), (300, 1024, 500)]
 
 
 @pytest.mark.parametrize("t", rehip.QUANT_TYPES)
