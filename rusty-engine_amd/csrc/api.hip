@@ -131,12 +131,16 @@ struct re_moe {
   std::mutex mu;
   hipStream_t stream = nullptr;
   Staging sx, sout, sg, su, sh, syp, smeta;
+  // pinned host staging of the per-call routing metadata, reused once its last upload is done
+  void* hmeta = nullptr;
+  size_t hmeta_cap = 0;
+  hipEvent_t meta_ev = nullptr;
+  bool meta_pending = false;
 };
 
 namespace {
 
-// GEMV launch shape: enough workgroups to cover the chip (the split count grows until about
-// 1024 workgroups exist or every block column is its own split).
+// integer tuning knob from the environment (dflt when unset or empty)
 size_t env_size(const char* name, size_t dflt) {
   const char* v = std::getenv(name);
   return (v && *v) ? (size_t)std::strtoull(v, nullptr, 10) : dflt;
@@ -458,6 +462,8 @@ int re_moe_create(uint32_t gate_type, const uint8_t* gate, size_t gate_bytes, ui
   }
   if (hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking) != hipSuccess)
     return cleanup(fail(RE_ERR_HIP, "hipStreamCreate failed"));
+  if (hipEventCreateWithFlags(&e->meta_ev, hipEventDisableTiming) != hipSuccess)
+    return cleanup(fail(RE_ERR_HIP, "hipEventCreate failed"));
   *out = e;
   return RE_OK;
 }
@@ -469,6 +475,9 @@ void re_moe_destroy(re_moe* e) {
   if (e->d_up) (void)hipFree(e->d_up);
   if (e->d_down) (void)hipFree(e->d_down);
   for (Staging* s : {&e->sx, &e->sout, &e->sg, &e->su, &e->sh, &e->syp, &e->smeta}) s->release();
+  if (e->meta_ev) (void)hipEventSynchronize(e->meta_ev);
+  if (e->meta_ev) (void)hipEventDestroy(e->meta_ev);
+  if (e->hmeta) (void)hipHostFree(e->hmeta);
   if (e->stream) (void)hipStreamDestroy(e->stream);
   delete e;
 }
@@ -489,6 +498,8 @@ int re_moe_forward_dev(re_moe* e, const float* d_x, size_t tokens, size_t top_k,
   std::vector<int> count(e->n_experts + 1, 0), start(e->n_experts + 1, 0);
   for (size_t p = 0; p < pairs; ++p) count[ids[p]]++;
   for (size_t x = 0; x < e->n_experts; ++x) start[x + 1] = start[x] + count[x];
+  size_t touched = 0;
+  for (size_t x = 0; x < e->n_experts; ++x) touched += count[x] > 0;
   std::vector<int> fill(start.begin(), start.end() - 1);
   std::vector<int> xrow(pairs), pos(pairs);
   for (size_t p = 0; p < pairs; ++p) {
@@ -496,84 +507,160 @@ int re_moe_forward_dev(re_moe* e, const float* d_x, size_t tokens, size_t top_k,
     xrow[at] = (int)(p / top_k);
     pos[p] = at;
   }
-  std::vector<GemmTask> t_gu, t_d;
-  const int mt_gu = (int)((e->inter + kMoeTile - 1) / kMoeTile), mt_d = (int)((e->hidden + kMoeTile - 1) / kMoeTile);
-  for (size_t x = 0; x < e->n_experts; ++x) {
-    for (int r = 0; r < count[x]; r += kMoeTile) {
-      const int rn = std::min(kMoeTile, count[x] - r);
-      for (int mt = 0; mt < mt_gu; ++mt) t_gu.push_back({(int)x, mt, start[x] + r, rn});
-      for (int mt = 0; mt < mt_d; ++mt) t_d.push_back({(int)x, mt, start[x] + r, rn});
-    }
-  }
-  // metadata block: xrow | pos | weights | tasks_gu | tasks_d
-  const size_t off_pos = pairs * sizeof(int), off_w = 2 * pairs * sizeof(int);
-  const size_t off_tgu = (off_w + pairs * sizeof(float) + 15) / 16 * 16;
-  const size_t off_td = off_tgu + t_gu.size() * sizeof(GemmTask);
-  const size_t meta_bytes = off_td + t_d.size() * sizeof(GemmTask);
-  std::vector<uint8_t> meta(meta_bytes);
-  std::memcpy(meta.data(), xrow.data(), pairs * sizeof(int));
-  std::memcpy(meta.data() + off_pos, pos.data(), pairs * sizeof(int));
-  std::memcpy(meta.data() + off_w, weights, pairs * sizeof(float));
-  std::memcpy(meta.data() + off_tgu, t_gu.data(), t_gu.size() * sizeof(GemmTask));
-  std::memcpy(meta.data() + off_td, t_d.data(), t_d.size() * sizeof(GemmTask));
-
-  int rc;
-  const size_t act = pairs * e->inter * sizeof(float);
-  if ((rc = e->smeta.ensure(meta_bytes)) || (rc = e->sg.ensure(act)) || (rc = e->su.ensure(act)) ||
-      (rc = e->sh.ensure(act)) || (rc = e->syp.ensure(pairs * e->hidden * sizeof(float))))
-    return rc;
-  uint8_t* dm = (uint8_t*)e->smeta.p;
-  // the metadata is uploaded with a synchronous copy so the host vectors may go out of scope
-  HIP_TRY(hipStreamSynchronize(s));
-  HIP_TRY(hipMemcpy(dm, meta.data(), meta_bytes, hipMemcpyHostToDevice));
-
   if (tokens * e->hidden * sizeof(float) >= (1ull << 31) || e->gg.bytes * e->n_experts >= (1ull << 31) ||
       e->gd.bytes * e->n_experts >= (1ull << 31) || pairs * e->inter * sizeof(float) >= (1ull << 31))
     return fail(RE_ERR_SIZE, "MoE operands must stay below 2 GiB");
-  GemmArgs a{};
-  a.X = d_x;
-  a.x_bytes = (uint32_t)(tokens * e->hidden * sizeof(float));
-  a.splits = 1;
-  a.steps_per_split = 1 << 30;
-  a.tasks = (const GemmTask*)(dm + off_tgu);
-  a.xrow = (const int*)dm;
-  a.m = (int)e->inter;
-  a.K = (int)e->hidden;
-  a.KB = (int)e->gg.kb;
-  a.tiles = (int)e->gg.tiles;
-  a.ldy = (int)e->inter;
-  a.W = e->d_gate;
-  a.w_bytes = (uint32_t)(e->gg.bytes * e->n_experts);
-  a.w_stride = e->gg.bytes;
-  a.Y = (float*)e->sg.p;
-  const int kg_gu = gemm_kgroups(GemmTile::k64x64, mode, (long)t_gu.size(), (int)((e->hidden + kGemmBK - 1) / kGemmBK));
-  const int kg_d = gemm_kgroups(GemmTile::k64x64, mode, (long)t_d.size(), (int)((e->inter + kGemmBK - 1) / kGemmBK));
-  HIP_TRY(launch_gemm(e->gg.type, mode, a, (int)t_gu.size(), GemmTile::k64x64, kg_gu, s));
-  a.W = e->d_up;
-  a.w_bytes = (uint32_t)(e->gu.bytes * e->n_experts);
-  a.w_stride = e->gu.bytes;
-  a.KB = (int)e->gu.kb;
-  a.tiles = (int)e->gu.tiles;
-  a.Y = (float*)e->su.p;
-  HIP_TRY(launch_gemm(e->gu.type, mode, a, (int)t_gu.size(), GemmTile::k64x64, kg_gu, s));
-  HIP_TRY(launch_swiglu((const float*)e->sg.p, (const float*)e->su.p, (float*)e->sh.p, pairs * e->inter, s));
-  GemmArgs d{};
-  d.W = e->d_down;
-  d.w_bytes = (uint32_t)(e->gd.bytes * e->n_experts);
-  d.w_stride = e->gd.bytes;
-  d.X = (const float*)e->sh.p;
-  d.x_bytes = (uint32_t)(pairs * e->inter * sizeof(float));
-  d.splits = 1;
-  d.steps_per_split = 1 << 30;
-  d.Y = (float*)e->syp.p;
-  d.m = (int)e->hidden;
-  d.K = (int)e->inter;
-  d.KB = (int)e->gd.kb;
-  d.tiles = (int)e->gd.tiles;
-  d.ldy = (int)e->hidden;
-  d.tasks = (const GemmTask*)(dm + off_td);
-  d.xrow = nullptr;
-  HIP_TRY(launch_gemm(e->gd.type, mode, d, (int)t_d.size(), GemmTile::k64x64, kg_d, s));
+
+  // Few rows per expert (decode-sized batches): grouped GEMV tasks that read each weight once
+  // per kMoeGemvBatch rows. Otherwise MFMA tiles of kMoeTile gathered rows.
+  const bool gemv = pairs <= (size_t)kMoeGemvBatch * touched;
+  std::vector<MoeGemvTask> v_gu, v_d;
+  std::vector<GemmTask> t_gu, t_d;
+  if (gemv) {
+    for (size_t x = 0; x < e->n_experts; ++x)
+      for (int r = 0; r < count[x]; r += kMoeGemvBatch) {
+        const int np = std::min(kMoeGemvBatch, count[x] - r);
+        for (size_t row = 0; row < e->inter; row += kMoeGemvRows) v_gu.push_back({(int)x, (int)row, start[x] + r, np});
+        for (size_t row = 0; row < e->hidden; row += kMoeGemvRows) v_d.push_back({(int)x, (int)row, start[x] + r, np});
+      }
+  } else {
+    const int mt_gu = (int)((e->inter + kMoeTile - 1) / kMoeTile), mt_d = (int)((e->hidden + kMoeTile - 1) / kMoeTile);
+    for (size_t x = 0; x < e->n_experts; ++x) {
+      for (int r = 0; r < count[x]; r += kMoeTile) {
+        const int rn = std::min(kMoeTile, count[x] - r);
+        for (int mt = 0; mt < mt_gu; ++mt) t_gu.push_back({(int)x, mt, start[x] + r, rn});
+        for (int mt = 0; mt < mt_d; ++mt) t_d.push_back({(int)x, mt, start[x] + r, rn});
+      }
+    }
+  }
+  // metadata block: xrow | pos | weights | tasks_gu | tasks_d
+  const size_t task_sz = gemv ? sizeof(MoeGemvTask) : sizeof(GemmTask);
+  const size_t n_gu = gemv ? v_gu.size() : t_gu.size(), n_d = gemv ? v_d.size() : t_d.size();
+  const size_t off_pos = pairs * sizeof(int), off_w = 2 * pairs * sizeof(int);
+  const size_t off_tgu = (off_w + pairs * sizeof(float) + 15) / 16 * 16;
+  const size_t off_td = off_tgu + n_gu * task_sz;
+  const size_t meta_bytes = off_td + n_d * task_sz;
+
+  int rc;
+  const size_t act = pairs * e->inter * sizeof(float);
+  if ((rc = e->smeta.ensure(meta_bytes)) || (rc = e->sh.ensure(act)) ||
+      (rc = e->syp.ensure(pairs * e->hidden * sizeof(float))))
+    return rc;
+  const bool dual = gemv && e->gg.type == e->gu.type;
+  if (!dual && ((rc = e->sg.ensure(act)) || (rc = e->su.ensure(act)))) return rc;
+  // the pinned staging is rewritten once its previous upload has completed
+  if (e->meta_pending) {
+    HIP_TRY(hipEventSynchronize(e->meta_ev));
+    e->meta_pending = false;
+  }
+  if (meta_bytes > e->hmeta_cap) {
+    if (e->hmeta) (void)hipHostFree(e->hmeta);
+    e->hmeta = nullptr;
+    e->hmeta_cap = 0;
+    HIP_TRY(hipHostMalloc(&e->hmeta, meta_bytes, hipHostMallocDefault));
+    e->hmeta_cap = meta_bytes;
+  }
+  uint8_t* meta = (uint8_t*)e->hmeta;
+  std::memcpy(meta, xrow.data(), pairs * sizeof(int));
+  std::memcpy(meta + off_pos, pos.data(), pairs * sizeof(int));
+  std::memcpy(meta + off_w, weights, pairs * sizeof(float));
+  std::memcpy(meta + off_tgu, gemv ? (const void*)v_gu.data() : (const void*)t_gu.data(), n_gu * task_sz);
+  std::memcpy(meta + off_td, gemv ? (const void*)v_d.data() : (const void*)t_d.data(), n_d * task_sz);
+  uint8_t* dm = (uint8_t*)e->smeta.p;
+  HIP_TRY(hipMemcpyAsync(dm, meta, meta_bytes, hipMemcpyHostToDevice, s));
+  HIP_TRY(hipEventRecord(e->meta_ev, s));
+  e->meta_pending = true;
+
+  if (gemv) {
+    int max_rows = 0;
+    for (size_t x = 0; x < e->n_experts; ++x) max_rows = std::max(max_rows, std::min(count[x], kMoeGemvBatch));
+    MoeGemvArgs g{};
+    g.max_rows = max_rows;
+    g.X = d_x;
+    g.xrow = (const int*)dm;
+    g.tasks = (const MoeGemvTask*)(dm + off_tgu);
+    g.m = (int)e->inter;
+    g.K = (int)e->hidden;
+    g.KB = (int)e->gg.kb;
+    g.ldy = (int)e->inter;
+    g.w_stride = e->gg.bytes;
+    if (dual) {
+      g.W0 = e->d_gate;
+      g.W1 = e->d_up;
+      g.Y = (float*)e->sh.p;
+      HIP_TRY(launch_moe_gemv(e->gg.type, true, g, (int)n_gu, s));
+    } else {
+      g.W0 = e->d_gate;
+      g.Y = (float*)e->sg.p;
+      HIP_TRY(launch_moe_gemv(e->gg.type, false, g, (int)n_gu, s));
+      g.W0 = e->d_up;
+      g.w_stride = e->gu.bytes;
+      g.KB = (int)e->gu.kb;
+      g.Y = (float*)e->su.p;
+      HIP_TRY(launch_moe_gemv(e->gu.type, false, g, (int)n_gu, s));
+      HIP_TRY(launch_swiglu((const float*)e->sg.p, (const float*)e->su.p, (float*)e->sh.p, pairs * e->inter, s));
+    }
+    MoeGemvArgs d{};
+    d.max_rows = max_rows;
+    d.W0 = e->d_down;
+    d.w_stride = e->gd.bytes;
+    d.X = (const float*)e->sh.p;
+    d.xrow = nullptr;
+    d.Y = (float*)e->syp.p;
+    d.tasks = (const MoeGemvTask*)(dm + off_td);
+    d.m = (int)e->hidden;
+    d.K = (int)e->inter;
+    d.KB = (int)e->gd.kb;
+    d.ldy = (int)e->hidden;
+    HIP_TRY(launch_moe_gemv(e->gd.type, false, d, (int)n_d, s));
+  } else {
+    GemmArgs a{};
+    a.X = d_x;
+    a.x_bytes = (uint32_t)(tokens * e->hidden * sizeof(float));
+    a.splits = 1;
+    a.steps_per_split = 1 << 30;
+    a.tasks = (const GemmTask*)(dm + off_tgu);
+    a.xrow = (const int*)dm;
+    a.m = (int)e->inter;
+    a.K = (int)e->hidden;
+    a.KB = (int)e->gg.kb;
+    a.tiles = (int)e->gg.tiles;
+    a.ldy = (int)e->inter;
+    a.W = e->d_gate;
+    a.w_bytes = (uint32_t)(e->gg.bytes * e->n_experts);
+    a.w_stride = e->gg.bytes;
+    a.Y = (float*)e->sg.p;
+    const int kg_gu = gemm_kgroups(GemmTile::k64x64, mode, (long)n_gu, (int)((e->hidden + kGemmBK - 1) / kGemmBK));
+    const int kg_d = gemm_kgroups(GemmTile::k64x64, mode, (long)n_d, (int)((e->inter + kGemmBK - 1) / kGemmBK));
+    if ((rc = e->sg.ensure(act)) || (rc = e->su.ensure(act))) return rc;
+    a.Y = (float*)e->sg.p;
+    HIP_TRY(launch_gemm(e->gg.type, mode, a, (int)n_gu, GemmTile::k64x64, kg_gu, s));
+    a.W = e->d_up;
+    a.w_bytes = (uint32_t)(e->gu.bytes * e->n_experts);
+    a.w_stride = e->gu.bytes;
+    a.KB = (int)e->gu.kb;
+    a.tiles = (int)e->gu.tiles;
+    a.Y = (float*)e->su.p;
+    HIP_TRY(launch_gemm(e->gu.type, mode, a, (int)n_gu, GemmTile::k64x64, kg_gu, s));
+    HIP_TRY(launch_swiglu((const float*)e->sg.p, (const float*)e->su.p, (float*)e->sh.p, pairs * e->inter, s));
+    GemmArgs d{};
+    d.W = e->d_down;
+    d.w_bytes = (uint32_t)(e->gd.bytes * e->n_experts);
+    d.w_stride = e->gd.bytes;
+    d.X = (const float*)e->sh.p;
+    d.x_bytes = (uint32_t)(pairs * e->inter * sizeof(float));
+    d.splits = 1;
+    d.steps_per_split = 1 << 30;
+    d.Y = (float*)e->syp.p;
+    d.m = (int)e->hidden;
+    d.K = (int)e->inter;
+    d.KB = (int)e->gd.kb;
+    d.tiles = (int)e->gd.tiles;
+    d.ldy = (int)e->hidden;
+    d.tasks = (const GemmTask*)(dm + off_td);
+    d.xrow = nullptr;
+    HIP_TRY(launch_gemm(e->gd.type, mode, d, (int)n_d, GemmTile::k64x64, kg_d, s));
+  }
   HIP_TRY(launch_combine((const float*)e->syp.p, (const int*)(dm + off_pos), (const float*)(dm + off_w), d_out,
                          (int)tokens, (int)top_k, (int)e->hidden, s));
   return RE_OK;

@@ -21,36 +21,6 @@
 
 namespace rehip {
 
-typedef __attribute__((__vector_size__(2 * sizeof(float)))) float f32x2_t;
-
-// Dot of one decoded run (16 quants) with x from LDS: every lane of the wave reads the same
-// address (a broadcast), so 16 activations are four ds_read_b128.
-template <int T>
-__device__ __forceinline__ float run_dot(const Run& r, const float* __restrict__ xb,
-                                         const float* __restrict__ xs) {
-  const float4* xv = reinterpret_cast<const float4*>(xb + r.e);
-  float s = 0.0f;
-#pragma unroll
-  for (int v = 0; v < 4; ++v) {
-    const float4 q = xv[v];
-    if constexpr (kNibble<T>) {
-      const f32x2_t lo = __builtin_amdgcn_cvt_pk_f32_fp8(r.q[v], false);   // quants 4v, 4v+1
-      const f32x2_t hi = __builtin_amdgcn_cvt_pk_f32_fp8(r.q[v], true);    // quants 4v+2, 4v+3
-      s = __builtin_fmaf(lo[0], q.x, s);
-      s = __builtin_fmaf(lo[1], q.y, s);
-      s = __builtin_fmaf(hi[0], q.z, s);
-      s = __builtin_fmaf(hi[1], q.w, s);
-    } else {
-      s = __builtin_fmaf(qbyte(r.q, 4 * v + 0), q.x, s);
-      s = __builtin_fmaf(qbyte(r.q, 4 * v + 1), q.y, s);
-      s = __builtin_fmaf(qbyte(r.q, 4 * v + 2), q.z, s);
-      s = __builtin_fmaf(qbyte(r.q, 4 * v + 3), q.w, s);
-    }
-  }
-  const float scale = kNibble<T> ? r.scale * 512.0f : r.scale;
-  return __builtin_fmaf(scale, s, -r.offset * xs[r.e >> 4]);
-}
-
 // Work unit = one 32-quant chunk (two 16-element runs) of one block column for the 64 rows of
 // a tile. Units of a tile are numbered u = kb * NCH + c; a workgroup owns the units of its
 // block-column range, its waves take every WAVES-th unit, and each wave keeps DEPTH units'

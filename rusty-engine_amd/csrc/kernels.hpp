@@ -72,6 +72,30 @@ int gemm_kgroups(GemmTile tile, int mode, long workgroups, int steps);
 hipError_t launch_gemm(uint32_t type, int mode, const GemmArgs& a, int ntasks, GemmTile tile, int kgroups,
                        hipStream_t s);
 
+// Grouped expert GEMV (few gathered rows per expert): one task per workgroup
+struct MoeGemvTask {
+  int expert;   // expert index
+  int row0;     // first weight row (multiple of kMoeGemvRows, inside one 64-row tile)
+  int p0;       // first gathered row
+  int np;       // gathered rows of the task (1..kMoeGemvBatch)
+};
+struct MoeGemvArgs {
+  const uint8_t* W0;          // tiled slabs of expert 0 (gate, or down)
+  const uint8_t* W1;          // up (dual launch) or nullptr
+  size_t w_stride;            // bytes between experts
+  const float* X;             // activation rows, K floats each
+  const int* xrow;            // X row of gathered row p (nullptr = p itself)
+  float* Y;                   // output row of gathered row p: Y + p * ldy
+  const MoeGemvTask* tasks;
+  int m, K, KB, ldy;          // weight rows and row length (per expert)
+  int max_rows;               // largest np over the tasks
+};
+constexpr int kMoeGemvRows = 16;   // weight rows per task
+constexpr int kMoeGemvWaves = 4;
+constexpr int kMoeGemvBatch = 4;   // gathered rows per task
+// dual: gate and up (W0, W1) with SwiGLU output; else one matrix
+hipError_t launch_moe_gemv(uint32_t type, bool dual, const MoeGemvArgs& a, int ntasks, hipStream_t s);
+
 // MoE helpers
 hipError_t launch_swiglu(const float* g, const float* u, float* h, size_t n, hipStream_t s);
 hipError_t launch_combine(const float* yp, const int* pos, const float* w, float* out, int tokens,

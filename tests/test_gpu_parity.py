@@ -262,6 +262,30 @@ def test_moe_grouped_ffn_parity(T):
         assert rel <= tol, (mode, rel)
 
 
+@pytest.mark.parametrize("T", [1, 3, 60])
+def test_moe_mixed_types_and_padded_rows(T):
+    # gate/up of different types (separate gate and up launches + SwiGLU), K-quant rows padded to
+    # whole super-blocks (hidden 640, inter 384), decode-sized and batch-sized routing
+    E, hidden, inter, k = 8, 640, 384, 2
+    rng = np.random.default_rng(900 + T)
+    gate = np.concatenate([synth.weight_bytes(rng, rehip.Q4_0, inter, hidden) for _ in range(E)])
+    up = np.concatenate([synth.weight_bytes(rng, rehip.Q5_K, inter, hidden) for _ in range(E)])
+    down = np.concatenate([synth.weight_bytes(rng, rehip.Q6_K, hidden, inter) for _ in range(E)])
+    x = synth.activations(rng, T, hidden)
+    logits = rng.standard_normal((T, E)).astype(np.float32)
+    ids = np.zeros((T, k), np.uint32)
+    wts = np.zeros((T, k), np.float32)
+    for i in range(T):
+        ids[i], wts[i] = O.top_k(logits[i], k)
+    ids, wts = ids.reshape(-1), wts.reshape(-1)
+    want = O.moe_ffn(rehip.Q4_0, gate, rehip.Q5_K, up, rehip.Q6_K, down, E, hidden, inter, x, T, k, ids, wts)
+    moe = rehip.MoeExperts(rehip.Q4_0, gate, rehip.Q5_K, up, rehip.Q6_K, down, E, hidden, inter)
+    for mode, tol in [(rehip.MODE_F32, 1e-4), (rehip.MODE_BF16, BF16_TOL)]:
+        got = moe.forward(x, T, k, ids, wts, mode)
+        assert np.linalg.norm(got - want) / np.linalg.norm(want) <= tol, mode
+        assert np.array_equal(moe.forward(x, T, k, ids, wts, mode), got)
+
+
 def test_moe_qwen3_shape_t32():
     E, hidden, inter, k, T = 128, 2048, 768, 8, 32
     gate, up, down, x, ids, wts = moe_case(401, E, hidden, inter, T, k)
