@@ -454,8 +454,6 @@ static hipError_t launch_t(const GemmArgs& a, int ntasks, GemmTile tile, int kg,
     case GemmTile::k256x128:
       if constexpr (F32) return hipErrorInvalidValue;
       else return kg != 1 ? hipErrorInvalidValue : launch_shape<T, F32, 256, 128, 4, 2, 1, false>(a, ntasks, s);
-    case GemmTile::k128x128:
-      return kg != 1 ? hipErrorInvalidValue : launch_shape<T, F32, 128, 128, 2, 2, 1, false>(a, ntasks, s);
     default:
       if (kg == 1) return launch_shape<T, F32, 64, 64, 2, 2, 1, false>(a, ntasks, s);
       if (kg == 2) return launch_shape<T, F32, 64, 64, 2, 2, 2, false>(a, ntasks, s);

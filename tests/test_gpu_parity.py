@@ -202,6 +202,28 @@ def test_gemm_parity_both_modes(t, m, n, rows):
         assert np.all(np.abs(got32 - want) <= F32_TOL * absd)
 
 
+@pytest.mark.parametrize("t", rehip.QUANT_TYPES)
+@pytest.mark.parametrize("tile,kg,splits", [(1, 1, 1), (1, 2, 1), (2, 1, 1), (3, 1, 1), (4, 1, 1), (3, 1, 2),
+                                            (4, 1, 3), (1, 2, 3)])
+def test_gemm_forced_tiles(t, tile, kg, splits, monkeypatch):
+    # every tile / K-group / K-split instance in bf16 mode on a ragged shape: 300 weight rows (a
+    # partial 128- and 256-row tile), 500 activation rows, K = 1280 (5 super-blocks)
+    monkeypatch.setenv("REHIP_GEMM_TILE", str(tile))
+    monkeypatch.setenv("REHIP_GEMM_KG", str(kg))
+    monkeypatch.setenv("REHIP_GEMM_SPLITS", str(splits))
+    m, n, rows = 300, 1280, 500
+    rng = np.random.default_rng(7000 + 10 * t + tile)
+    w = synth.weight_bytes(rng, t, m, n)
+    x = synth.activations(rng, rows, n)
+    q = qmat(t, w, m, n)
+    exact, _ = f64_product(t, w, m, n, x, rows)
+    exact = exact.reshape(-1)
+    got = q.matmul(x, rows, rehip.MODE_BF16)
+    assert np.linalg.norm(got - exact) / np.linalg.norm(exact) <= BF16_TOL
+    assert np.array_equal(q.matmul(x, rows, rehip.MODE_BF16), got)
+    q.close()
+
+
 @pytest.mark.parametrize("t", [rehip.Q4_0, rehip.Q8_0, rehip.Q4_K, rehip.Q6_K])
 def test_gemm_large_tiles_ragged_edges(t):
     # 3136 weight rows (not a multiple of 128) x 2085 activation rows (not a multiple of 256):
