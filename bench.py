@@ -237,18 +237,42 @@ def run_e2e(args, cpu_ok):
             r.close()
         return toks, t1 - t0, (steps - 1) / (t2 - t1) if steps > 1 else None
 
+    def device_decode(steps, mode):
+        """DeviceDecoder: everything on the GPU, one graph replay and a 4-byte read-back per token.
+        The first step (which captures the graph) is not in the decode rate."""
+        dd = qwen.DeviceDecoder(mb, max_seq=len(prompt) + steps, mode=mode, prefill_rows=len(prompt))
+        dd.prefill(prompt[:32])                    # warm-up: GEMM scratch is allocated here
+        dd.close()
+        dd = qwen.DeviceDecoder(mb, max_seq=len(prompt) + steps, mode=mode, prefill_rows=len(prompt))
+        t0 = time.perf_counter()
+        toks = [dd.prefill(prompt)]
+        t1 = time.perf_counter()
+        toks.append(dd.step())
+        t2 = time.perf_counter()
+        for _ in range(steps - 2):
+            toks.append(dd.step())
+        t3 = time.perf_counter()
+        dd.close()
+        return toks, t1 - t0, (steps - 2) / (t3 - t2)
+
+    dtoks, dpre_s, dtps = device_decode(args.e2e_steps, rehip.MODE_F32)
+    _, dpre_bf16, _ = device_decode(3, rehip.MODE_BF16)
     toks, pre_s, tps = decode(qwen.HipBackend(rehip.MODE_F32), args.e2e_steps)
     res = {"model": "Qwen2.5-0.5B-shaped (24 layers, 896/14/2 heads, d_ff 4864, vocab 151936), Q4_K_M mix, "
                     "random init seed 501",
            "prompt_tokens": len(prompt), "decode_steps": args.e2e_steps, "matmul_mode": "f32",
            "prefill_s_hip": pre_s, "decode_tok_s_hip": tps,
-           "host_steps": "attention/norm/RoPE/argmax on the host (numpy), projections through the backend"}
+           "host_steps": "attention/norm/RoPE/argmax on the host (numpy), projections through the backend",
+           "device_resident": {"prefill_s": dpre_s, "prefill_s_bf16_gemm": dpre_bf16, "decode_tok_s": dtps,
+                               "greedy_identical_to_host_step_path": dtoks == toks,
+                               "note": "attention, norms, RoPE, argmax and residuals on the GPU; one HIP graph "
+                                       "replay and a 4-byte token read-back per decode step"}}
     if cpu_ok:
         from oracle.backend import CpuBackend
         n = min(args.e2e_cpu_steps, args.e2e_steps)
         ctoks, cpre_s, ctps = decode(CpuBackend(), n)
         res.update({"prefill_s_cpu": cpre_s, "decode_tok_s_cpu": ctps, "cpu_decode_steps": n,
-                    "greedy_identical": ctoks == toks[:n], "greedy_compared_steps": n})
+                    "greedy_identical": ctoks == toks[:n] and ctoks == dtoks[:n], "greedy_compared_steps": n})
     return res
 
 

@@ -104,6 +104,52 @@ int re_moe_forward_dev(re_moe *e, const float *d_x, size_t tokens, size_t top_k,
                        const uint32_t *ids, const float *weights, float *d_out, int mode,
                        void *stream);
 
+/* ---- device-resident transformer steps (src/forward.rs, src/infer.rs, src/runner.rs) ------
+ * Device pointers, enqueued on `stream`. Positions come from a device int (*d_pos) so that a
+ * captured graph serves every decode step; re_pos_add_dev advances it on the stream. */
+typedef struct re_ffn re_ffn;
+
+/* y = W x + add (add may equal y; NULL = plain matvec): the q/k/v bias add (forward.rs:447-449)
+ * and the residual adds (forward.rs:472-485) folded into the GEMV's store. */
+int re_qmat_matvec_add_dev(re_qmat *q, const float *d_x, const float *d_add, float *d_y, void *stream);
+/* out[r] = x[r] * (1 / sqrt(mean(x[r]^2) + eps)) * w for rows x d (infer.rs:72-82). */
+int re_rmsnorm_dev(const float *d_x, const float *d_w, size_t rows, size_t d, float eps, float *d_out,
+                   void *stream);
+/* NeoX rotate-half of rows x heads x head_dim in place, row r at position *d_pos + pos_offset + r
+ * (infer.rs:90-139, angle = pos * theta^(-2i/head_dim)). */
+int re_rope_dev(float *d_x, size_t rows, size_t heads, size_t head_dim, float theta, const int *d_pos,
+                int pos_offset, void *stream);
+/* Append rows x kv_dim of K and V at cache rows *d_pos + r (the rotated-key cache of
+ * forward.rs:347-363). The caches hold max_seq rows; rows that would land at or past max_seq
+ * are not stored (the caller keeps *d_pos + rows <= max_seq). */
+int re_kv_append_dev(const float *d_k, const float *d_v, size_t rows, size_t kv_dim, float *d_kcache,
+                     float *d_vcache, size_t max_seq, const int *d_pos, void *stream);
+/* Causal GQA attention of rows x n_heads x head_dim queries at positions *d_pos + r over cache
+ * rows 0..position (forward.rs:232-277, 437-470); the scores of one row need max_seq floats of
+ * LDS (max_seq <= 32768) and positions are clamped to the max_seq cache rows. Output rows x
+ * n_heads x head_dim. */
+int re_attention_dev(const float *d_q, const float *d_kcache, const float *d_vcache, size_t rows,
+                     size_t n_heads, size_t n_kv_heads, size_t head_dim, size_t max_seq,
+                     const int *d_pos, float *d_ctx, void *stream);
+/* out[i] = a[i] + b[i % nb] (residual add for nb == n, per-column bias for nb | n). */
+int re_add_dev(const float *d_a, const float *d_b, size_t n, size_t nb, float *d_out, void *stream);
+/* h = silu(g) * u elementwise (moe.rs:44-51, 280-283). */
+int re_swiglu_dev(const float *d_g, const float *d_u, float *d_h, size_t n, void *stream);
+/* *d_idx = index of the largest of n values; the last one among equal maxima (infer.rs:217-223). */
+int re_argmax_dev(const float *d_x, size_t n, int *d_idx, void *stream);
+/* out[r] = table[tok[r]] for rows tokens of an n_vocab x d f32 table (runner.rs:105-122); a token
+ * outside [0, n_vocab) gives a zero row (the host checks prompt ids before upload). */
+int re_embed_dev(const float *d_table, size_t n_vocab, size_t d, const int *d_tok, size_t rows, float *d_out,
+                 void *stream);
+/* *d_pos += delta on the stream. */
+int re_pos_add_dev(int *d_pos, int delta, void *stream);
+/* A gate/up pair (same type and shape, inter x hidden) read side by side for one activation row:
+ * h = silu(gate x) * (up x) in one launch (the SwiGLU FFN input, forward.rs:100-105). The pair
+ * keeps references to the two matrices, which must outlive it. */
+int re_ffn_create(re_qmat *gate, re_qmat *up, re_ffn **out);
+void re_ffn_destroy(re_ffn *f);
+int re_ffn_forward_dev(re_ffn *f, const float *d_x, float *d_h, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

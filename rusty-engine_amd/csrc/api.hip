@@ -203,8 +203,9 @@ int upload_tiled(const MatGeom& g, const uint8_t* bytes, uint8_t* d_dst) {
   return RE_OK;
 }
 
-int gemv_enqueue(re_qmat* q, const float* d_x, float* d_y, hipStream_t s) {
+int gemv_enqueue(re_qmat* q, const float* d_x, float* d_y, hipStream_t s, const float* d_add = nullptr) {
   GemvArgs a{};
+  a.add = d_add;
   a.W = q->d_w;
   a.x = d_x;
   a.y = d_y;
@@ -359,6 +360,11 @@ uint32_t re_qmat_type(const re_qmat* q) { return q ? q->g.type : 0; }
 int re_qmat_matvec_dev(re_qmat* q, const float* d_x, float* d_y, void* stream) {
   if (!q || !d_x || !d_y) return fail(RE_ERR_ARG, "null pointer");
   return gemv_enqueue(q, d_x, d_y, (hipStream_t)stream);
+}
+
+int re_qmat_matvec_add_dev(re_qmat* q, const float* d_x, const float* d_add, float* d_y, void* stream) {
+  if (!q || !d_x || !d_y) return fail(RE_ERR_ARG, "null pointer");
+  return gemv_enqueue(q, d_x, d_y, (hipStream_t)stream, d_add);
 }
 
 int re_qmat_matmul_dev(re_qmat* q, const float* d_x, size_t rows, float* d_y, int mode, void* stream) {
@@ -681,6 +687,144 @@ int re_moe_forward(re_moe* e, const float* x, size_t tokens, size_t top_k, const
     return rc;
   HIP_TRY(hipMemcpyAsync(out, e->sout.p, xb, hipMemcpyDeviceToHost, e->stream));
   HIP_TRY(hipStreamSynchronize(e->stream));
+  return RE_OK;
+}
+
+
+// ---- device-resident transformer steps ----------------------------------------------------------
+struct re_ffn {
+  re_qmat *gate = nullptr, *up = nullptr;
+  MoeGemvTask* d_tasks = nullptr;
+  int ntasks = 0;
+};
+
+int re_rmsnorm_dev(const float* d_x, const float* d_w, size_t rows, size_t d, float eps, float* d_out, void* stream) {
+  if (!d_x || !d_w || !d_out) return fail(RE_ERR_ARG, "null pointer");
+  if (rows == 0) return RE_OK;
+  if (d == 0 || d > (1u << 24) || rows > (1u << 24)) return fail(RE_ERR_SIZE, "rmsnorm shape %zu x %zu", rows, d);
+  HIP_TRY(launch_rmsnorm(d_x, d_w, (int)rows, (int)d, eps, d_out, (hipStream_t)stream));
+  return RE_OK;
+}
+
+int re_rope_dev(float* d_x, size_t rows, size_t heads, size_t head_dim, float theta, const int* d_pos, int pos_offset,
+                void* stream) {
+  if (!d_x || !d_pos) return fail(RE_ERR_ARG, "null pointer");
+  if (rows == 0 || heads == 0) return RE_OK;
+  if (head_dim == 0 || head_dim % 2 || head_dim > 128 || rows > 65535 || heads > 65535)
+    return fail(RE_ERR_SIZE, "rope shape rows %zu heads %zu head_dim %zu (even, <= 128)", rows, heads, head_dim);
+  HIP_TRY(launch_rope(d_x, (int)rows, (int)heads, (int)head_dim, theta, d_pos, pos_offset, (hipStream_t)stream));
+  return RE_OK;
+}
+
+int re_kv_append_dev(const float* d_k, const float* d_v, size_t rows, size_t kv_dim, float* d_kcache, float* d_vcache,
+                     size_t max_seq, const int* d_pos, void* stream) {
+  if (!d_k || !d_v || !d_kcache || !d_vcache || !d_pos) return fail(RE_ERR_ARG, "null pointer");
+  if (rows == 0) return RE_OK;
+  if (kv_dim == 0 || rows > (1u << 24) || max_seq == 0 || max_seq > (1u << 24))
+    return fail(RE_ERR_SIZE, "kv append shape %zu x %zu, %zu cache rows", rows, kv_dim, max_seq);
+  HIP_TRY(launch_kv_append(d_k, d_v, (int)rows, (int)kv_dim, d_kcache, d_vcache, (int)max_seq, d_pos,
+                           (hipStream_t)stream));
+  return RE_OK;
+}
+
+int re_attention_dev(const float* d_q, const float* d_kcache, const float* d_vcache, size_t rows, size_t n_heads,
+                     size_t n_kv_heads, size_t head_dim, size_t max_seq, const int* d_pos, float* d_ctx,
+                     void* stream) {
+  if (!d_q || !d_kcache || !d_vcache || !d_pos || !d_ctx) return fail(RE_ERR_ARG, "null pointer");
+  if (rows == 0) return RE_OK;
+  if (n_heads == 0 || n_kv_heads == 0 || n_heads % n_kv_heads || head_dim == 0 || head_dim % 4 || head_dim > 256 ||
+      max_seq == 0 || max_seq > 32768 || rows > 65535 || n_heads > 65535)
+    return fail(RE_ERR_SIZE, "attention shape heads %zu/%zu head_dim %zu max_seq %zu", n_heads, n_kv_heads, head_dim,
+                max_seq);
+  HIP_TRY(launch_attention(d_q, d_kcache, d_vcache, (int)rows, (int)n_heads, (int)n_kv_heads, (int)head_dim,
+                           (int)max_seq, d_pos, d_ctx, (hipStream_t)stream));
+  return RE_OK;
+}
+
+int re_add_dev(const float* d_a, const float* d_b, size_t n, size_t nb, float* d_out, void* stream) {
+  if (!d_a || !d_b || !d_out) return fail(RE_ERR_ARG, "null pointer");
+  if (n == 0) return RE_OK;
+  if (nb == 0 || n % nb) return fail(RE_ERR_SIZE, "add: %zu values with a %zu-value operand", n, nb);
+  HIP_TRY(launch_add(d_a, d_b, n, nb, d_out, (hipStream_t)stream));
+  return RE_OK;
+}
+
+int re_swiglu_dev(const float* d_g, const float* d_u, float* d_h, size_t n, void* stream) {
+  if (!d_g || !d_u || !d_h) return fail(RE_ERR_ARG, "null pointer");
+  HIP_TRY(launch_swiglu(d_g, d_u, d_h, n, (hipStream_t)stream));
+  return RE_OK;
+}
+
+int re_argmax_dev(const float* d_x, size_t n, int* d_idx, void* stream) {
+  if (!d_x || !d_idx) return fail(RE_ERR_ARG, "null pointer");
+  if (n == 0 || n > (1u << 30)) return fail(RE_ERR_SIZE, "argmax over %zu values", n);
+  HIP_TRY(launch_argmax(d_x, (int)n, d_idx, (hipStream_t)stream));
+  return RE_OK;
+}
+
+int re_embed_dev(const float* d_table, size_t n_vocab, size_t d, const int* d_tok, size_t rows, float* d_out,
+                 void* stream) {
+  if (!d_table || !d_tok || !d_out) return fail(RE_ERR_ARG, "null pointer");
+  if (rows == 0) return RE_OK;
+  if (d == 0 || rows > (1u << 24) || n_vocab == 0 || n_vocab > (1u << 30))
+    return fail(RE_ERR_SIZE, "embed shape %zu x %zu of %zu tokens", rows, d, n_vocab);
+  HIP_TRY(launch_embed(d_table, (int)n_vocab, (int)d, d_tok, (int)rows, d_out, (hipStream_t)stream));
+  return RE_OK;
+}
+
+int re_pos_add_dev(int* d_pos, int delta, void* stream) {
+  if (!d_pos) return fail(RE_ERR_ARG, "null pointer");
+  HIP_TRY(launch_pos_add(d_pos, delta, (hipStream_t)stream));
+  return RE_OK;
+}
+
+int re_ffn_create(re_qmat* gate, re_qmat* up, re_ffn** out) {
+  if (!gate || !up || !out) return fail(RE_ERR_ARG, "null pointer");
+  *out = nullptr;
+  if (gate->g.type != up->g.type || gate->g.m != up->g.m || gate->g.n != up->g.n)
+    return fail(RE_ERR_SIZE, "ffn: gate and up must share type and shape");
+  if (gate->g.n > (size_t)kGemvRowsMaxK) return fail(RE_ERR_SIZE, "ffn: rows longer than %d", kGemvRowsMaxK);
+  std::vector<MoeGemvTask> t;
+  for (size_t row = 0; row < gate->g.m; row += kMoeGemvRows) t.push_back({0, (int)row, 0, 1});
+  re_ffn* f = new (std::nothrow) re_ffn();
+  if (!f) return fail(RE_ERR_ARG, "out of memory");
+  f->gate = gate;
+  f->up = up;
+  f->ntasks = (int)t.size();
+  if (hipMalloc(&f->d_tasks, t.size() * sizeof(MoeGemvTask)) != hipSuccess) {
+    delete f;
+    return fail(RE_ERR_HIP, "hipMalloc of ffn tasks failed");
+  }
+  if (hipMemcpy(f->d_tasks, t.data(), t.size() * sizeof(MoeGemvTask), hipMemcpyHostToDevice) != hipSuccess) {
+    re_ffn_destroy(f);
+    return fail(RE_ERR_HIP, "upload of ffn tasks failed");
+  }
+  *out = f;
+  return RE_OK;
+}
+
+void re_ffn_destroy(re_ffn* f) {
+  if (!f) return;
+  if (f->d_tasks) (void)hipFree(f->d_tasks);
+  delete f;
+}
+
+int re_ffn_forward_dev(re_ffn* f, const float* d_x, float* d_h, void* stream) {
+  if (!f || !d_x || !d_h) return fail(RE_ERR_ARG, "null pointer");
+  MoeGemvArgs g{};
+  g.W0 = f->gate->d_w;
+  g.W1 = f->up->d_w;
+  g.w_stride = 0;
+  g.X = d_x;
+  g.xrow = nullptr;
+  g.Y = d_h;
+  g.tasks = f->d_tasks;
+  g.m = (int)f->gate->g.m;
+  g.K = (int)f->gate->g.n;
+  g.KB = (int)f->gate->g.kb;
+  g.ldy = (int)f->gate->g.m;
+  g.max_rows = 1;
+  HIP_TRY(launch_moe_gemv(f->gate->g.type, true, g, f->ntasks, (hipStream_t)stream));
   return RE_OK;
 }
 

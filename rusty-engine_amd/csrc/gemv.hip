@@ -104,7 +104,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs p) {
     for (int w = 1; w < WAVES; ++w) s += red[w * 64 + lane];
     const int row = tile * 64 + lane;
     if (p.splits == 1) {
-      if (row < p.m) p.y[row] = s;
+      if (row < p.m) p.y[row] = p.add ? s + p.add[row] : s;
     } else {
       p.partial[(size_t)split * p.m_pad + row] = s;
     }
@@ -197,19 +197,19 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_rows_kernel(GemvArgs p) {
 #pragma unroll
     for (int w = 1; w < WAVES; ++w) s += red[w * R + threadIdx.x];
     const int row = tile * 64 + rr;
-    if (row < p.m) p.y[row] = s;
+    if (row < p.m) p.y[row] = p.add ? s + p.add[row] : s;
   }
 }
 
 // y[r] = sum over splits, in split order, of partial[split][r]
 __global__ __launch_bounds__(256) void gemv_reduce_kernel(const float* __restrict__ partial,
-                                                          float* __restrict__ y, int m, int m_pad,
-                                                          int splits) {
+                                                          float* y, int m, int m_pad,
+                                                          int splits, const float* add) {
   const int r = blockIdx.x * 256 + threadIdx.x;
   if (r >= m) return;
   float s = 0.0f;
   for (int sp = 0; sp < splits; ++sp) s += partial[(size_t)sp * m_pad + r];
-  y[r] = s;
+  y[r] = add ? s + add[r] : s;
 }
 
 // Bit-exact dequant of the tiled weights into a row-major f32 matrix [m x n].
@@ -273,7 +273,7 @@ static hipError_t launch_gemv_t(const GemvArgs& a, int waves, hipStream_t s) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || a.splits == 1) return e;
   hipLaunchKernelGGL(gemv_reduce_kernel, dim3((unsigned)((a.m + 255) / 256)), dim3(256), 0, s, a.partial, a.y,
-                     a.m, a.m_pad, a.splits);
+                     a.m, a.m_pad, a.splits, a.add);
   return hipGetLastError();
 }
 

@@ -16,6 +16,7 @@ struct GemvArgs {
   int kb_per_split, splits;     // split launch (rows_per_group == 0)
   int rows_per_group;           // row-group launch: 64, 16, 8 or 4 rows per workgroup; 0 = split launch
   int groups;                   // row-group launch: tiles * 64 / rows_per_group
+  const float* add;             // nullptr, or y[r] = (W x)[r] + add[r] (add may equal y)
 };
 
 // longest row (elements) a GEMV workgroup stages in LDS: x, its per-16 sums and the wave
@@ -95,6 +96,18 @@ constexpr int kMoeGemvWaves = 4;
 constexpr int kMoeGemvBatch = 4;   // gathered rows per task
 // dual: gate and up (W0, W1) with SwiGLU output; else one matrix
 hipError_t launch_moe_gemv(uint32_t type, bool dual, const MoeGemvArgs& a, int ntasks, hipStream_t s);
+
+// Dense transformer steps on device buffers (layer.hip)
+hipError_t launch_rmsnorm(const float* x, const float* w, int rows, int d, float eps, float* out, hipStream_t s);
+hipError_t launch_rope(float* x, int rows, int heads, int hd, float base, const int* pos, int off, hipStream_t s);
+hipError_t launch_kv_append(const float* k, const float* v, int rows, int kv_dim, float* kc, float* vc,
+                            int max_seq, const int* pos, hipStream_t s);
+hipError_t launch_attention(const float* q, const float* kc, const float* vc, int rows, int heads, int kv_heads,
+                            int hd, int max_seq, const int* pos, float* ctx, hipStream_t s);
+hipError_t launch_add(const float* a, const float* b, size_t n, size_t nb, float* out, hipStream_t s);
+hipError_t launch_argmax(const float* x, int n, int* idx, hipStream_t s);
+hipError_t launch_embed(const float* table, int n_vocab, int d, const int* tok, int rows, float* out, hipStream_t s);
+hipError_t launch_pos_add(int* pos, int delta, hipStream_t s);
 
 // MoE helpers
 hipError_t launch_swiglu(const float* g, const float* u, float* h, size_t n, hipStream_t s);

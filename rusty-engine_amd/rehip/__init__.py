@@ -35,7 +35,9 @@ EXPORTS = ("re_init", "re_last_error", "re_version", "re_row_bytes", "re_tiled_b
            "re_qmat_create", "re_qmat_destroy", "re_qmat_rows", "re_qmat_cols", "re_qmat_type",
            "re_qmat_matvec", "re_qmat_matmul", "re_qmat_matvec_dev", "re_qmat_matmul_dev",
            "re_qmat_dequant_dev", "re_dequant", "re_moe_create", "re_moe_destroy", "re_moe_forward",
-           "re_moe_forward_dev")
+           "re_moe_forward_dev", "re_qmat_matvec_add_dev", "re_rmsnorm_dev", "re_rope_dev", "re_kv_append_dev",
+           "re_attention_dev", "re_add_dev", "re_swiglu_dev", "re_argmax_dev", "re_embed_dev", "re_pos_add_dev",
+           "re_ffn_create", "re_ffn_destroy", "re_ffn_forward_dev")
 
 
 class RehipError(RuntimeError):
@@ -83,6 +85,20 @@ def lib() -> C.CDLL:
         L.re_moe_destroy.restype = None
         L.re_moe_forward.argtypes = [_vp, _vp, _sz, _sz, _vp, _vp, _vp, C.c_int]
         L.re_moe_forward_dev.argtypes = [_vp, _vp, _sz, _sz, _vp, _vp, _vp, C.c_int, _vp]
+        L.re_qmat_matvec_add_dev.argtypes = [_vp, _vp, _vp, _vp, _vp]
+        L.re_rmsnorm_dev.argtypes = [_vp, _vp, _sz, _sz, C.c_float, _vp, _vp]
+        L.re_rope_dev.argtypes = [_vp, _sz, _sz, _sz, C.c_float, _vp, C.c_int, _vp]
+        L.re_kv_append_dev.argtypes = [_vp, _vp, _sz, _sz, _vp, _vp, _sz, _vp, _vp]
+        L.re_attention_dev.argtypes = [_vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _vp, _vp, _vp]
+        L.re_add_dev.argtypes = [_vp, _vp, _sz, _sz, _vp, _vp]
+        L.re_swiglu_dev.argtypes = [_vp, _vp, _vp, _sz, _vp]
+        L.re_argmax_dev.argtypes = [_vp, _sz, _vp, _vp]
+        L.re_embed_dev.argtypes = [_vp, _sz, _sz, _vp, _sz, _vp, _vp]
+        L.re_pos_add_dev.argtypes = [_vp, C.c_int, _vp]
+        L.re_ffn_create.argtypes = [_vp, _vp, C.POINTER(_vp)]
+        L.re_ffn_destroy.argtypes = [_vp]
+        L.re_ffn_destroy.restype = None
+        L.re_ffn_forward_dev.argtypes = [_vp, _vp, _vp, _vp]
         _lib = L
     return _lib
 
@@ -141,7 +157,7 @@ def dequant(ggml_type: int, data) -> np.ndarray:
 
 
 def _dev_ptr(t) -> int:
-    """Device address of a torch tensor (plumbing for the *_dev entry points)."""
+    """Device address of a device buffer (rehip.hip.DeviceBuffer or anything with data_ptr())."""
     return int(t.data_ptr())
 
 
@@ -187,9 +203,14 @@ class QMat:
         _check(lib().re_qmat_matmul(self._h, xv.ctypes.data, rows, y.ctypes.data, mode))
         return y[:rows * self.m]
 
-    # device-resident variants (torch tensors as plumbing for HBM buffers and streams)
+    # device-resident variants (rehip.hip device buffers and streams)
     def matvec_dev(self, x_dev, y_dev, stream=None) -> None:
         _check(lib().re_qmat_matvec_dev(self._h, _dev_ptr(x_dev), _dev_ptr(y_dev), _stream_ptr(stream)))
+
+    def matvec_add_dev(self, x_dev, add_dev, y_dev, stream=None) -> None:
+        """y = W x + add (add may be y itself, or None)."""
+        _check(lib().re_qmat_matvec_add_dev(self._h, _dev_ptr(x_dev), _dev_ptr(add_dev) if add_dev is not None else None,
+                                            _dev_ptr(y_dev), _stream_ptr(stream)))
 
     def matmul_dev(self, x_dev, rows: int, y_dev, mode: int = MODE_BF16, stream=None) -> None:
         _check(lib().re_qmat_matmul_dev(self._h, _dev_ptr(x_dev), rows, _dev_ptr(y_dev), mode,
@@ -201,6 +222,73 @@ class QMat:
     def close(self) -> None:
         if self._h:
             lib().re_qmat_destroy(self._h)
+            self._h = C.c_void_p(0)
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+# ---- device-resident transformer steps (src/forward.rs, src/infer.rs) --------------------------
+def _p(b):
+    return _dev_ptr(b) if b is not None else None
+
+
+def rmsnorm_dev(x, w, rows, d, eps, out, stream=None):
+    _check(lib().re_rmsnorm_dev(_p(x), _p(w), rows, d, eps, _p(out), _stream_ptr(stream)))
+
+
+def rope_dev(x, rows, heads, head_dim, theta, pos, pos_offset=0, stream=None):
+    _check(lib().re_rope_dev(_p(x), rows, heads, head_dim, theta, _p(pos), pos_offset, _stream_ptr(stream)))
+
+
+def kv_append_dev(k, v, rows, kv_dim, kcache, vcache, max_seq, pos, stream=None):
+    _check(lib().re_kv_append_dev(_p(k), _p(v), rows, kv_dim, _p(kcache), _p(vcache), max_seq, _p(pos),
+                                  _stream_ptr(stream)))
+
+
+def attention_dev(q, kcache, vcache, rows, n_heads, n_kv_heads, head_dim, max_seq, pos, ctx, stream=None):
+    _check(lib().re_attention_dev(_p(q), _p(kcache), _p(vcache), rows, n_heads, n_kv_heads, head_dim, max_seq,
+                                  _p(pos), _p(ctx), _stream_ptr(stream)))
+
+
+def add_dev(a, b, n, nb, out, stream=None):
+    _check(lib().re_add_dev(_p(a), _p(b), n, nb, _p(out), _stream_ptr(stream)))
+
+
+def swiglu_dev(g, u, h, n, stream=None):
+    _check(lib().re_swiglu_dev(_p(g), _p(u), _p(h), n, _stream_ptr(stream)))
+
+
+def argmax_dev(x, n, idx, stream=None):
+    _check(lib().re_argmax_dev(_p(x), n, _p(idx), _stream_ptr(stream)))
+
+
+def embed_dev(table, n_vocab, d, tok, rows, out, stream=None):
+    _check(lib().re_embed_dev(_p(table), n_vocab, d, _p(tok), rows, _p(out), _stream_ptr(stream)))
+
+
+def pos_add_dev(pos, delta, stream=None):
+    _check(lib().re_pos_add_dev(_p(pos), delta, _stream_ptr(stream)))
+
+
+class Ffn:
+    """A gate/up pair read side by side: h = silu(gate x) * (up x) for one row in one launch."""
+
+    def __init__(self, gate: "QMat", up: "QMat"):
+        h = _vp()
+        _check(lib().re_ffn_create(gate._h, up._h, C.byref(h)))
+        self._h = h
+        self._keep = (gate, up)
+
+    def forward_dev(self, x_dev, h_dev, stream=None) -> None:
+        _check(lib().re_ffn_forward_dev(self._h, _dev_ptr(x_dev), _dev_ptr(h_dev), _stream_ptr(stream)))
+
+    def close(self) -> None:
+        if self._h:
+            lib().re_ffn_destroy(self._h)
             self._h = C.c_void_p(0)
 
     def __del__(self):

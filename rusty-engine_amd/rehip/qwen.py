@@ -364,3 +364,201 @@ class DenseDecoder:
             if i + 1 < max_new:
                 logits = self.step(t)
         return out
+
+
+class DeviceDecoder:
+    """The dense decoder with every step on the GPU (row F1 of the hot-path plan): activations,
+    rotated K/V caches, the position and the sampled token stay in HBM. Each projection is a
+    librehip GEMV (decode) or GEMM (prefill); the q/k/v biases and the residual adds are folded
+    into the GEMV stores; gate and up run as one launch with SwiGLU (`Ffn`). A decode step is
+    captured once as a HIP graph (the position and the token are device integers advanced by
+    the graph itself) and replayed per token, so the host only reads back the token id.
+
+    Same computation as `DenseDecoder` (runner.rs:205-282, forward.rs:347-586); the attention,
+    RMS-norm, RoPE and argmax are librehip kernels instead of host numpy."""
+
+    def __init__(self, mb: ModelBytes, max_seq: int, mode: int = MODE_F32, prefill_rows: int = 1024,
+                 use_graph: bool = True):
+        from . import Ffn, hip
+        self.mb, self.mode, self.max_seq = mb, mode, max_seq
+        self.use_graph = use_graph
+        g = self.g = mb.geom
+        d, hd = g.d_model, g.head_dim
+        kv = g.n_kv_heads * hd
+        self.kv = kv
+        self.cap = max(1, prefill_rows)
+        B = hip.DeviceBuffer
+        self.blocks = []
+        for b in mb.blocks:
+            q = QMat.from_bytes(mb.attn_type, b.q, d, d)
+            k = QMat.from_bytes(mb.attn_type, b.k, kv, d)
+            v = QMat.from_bytes(mb.attn_type, b.v, kv, d)
+            o = QMat.from_bytes(mb.attn_type, b.o, d, d)
+            gate = QMat.from_bytes(mb.ffn_type, b.gate, g.d_ff, d)
+            up = QMat.from_bytes(mb.ffn_type, b.up, g.d_ff, d)
+            down = QMat.from_bytes(mb.down_type, b.down, d, g.d_ff)
+            self.blocks.append(dict(
+                q=q, k=k, v=v, o=o, gate=gate, up=up, down=down,
+                ffn=Ffn(gate, up),
+                attn_norm=B.from_array(b.attn_norm), ffn_norm=B.from_array(b.ffn_norm),
+                q_bias=B.from_array(b.q_bias), k_bias=B.from_array(b.k_bias), v_bias=B.from_array(b.v_bias),
+                kc=B(max_seq * kv * 4), vc=B(max_seq * kv * 4)))
+        self.output = QMat.from_bytes(mb.embed_type, mb.output, mb.n_vocab, d)
+        self.output_norm = B.from_array(mb.output_norm)
+        self.embed = B.from_array(dequant(mb.embed_type, mb.embed))
+        cap = self.cap
+        self.x = B(cap * d * 4)
+        self.n = B(cap * d * 4)
+        self.qb = B(cap * d * 4)
+        self.kb = B(cap * kv * 4)
+        self.vb = B(cap * kv * 4)
+        self.ctx = B(cap * d * 4)
+        self.ob = B(cap * d * 4)
+        self.gb = B(cap * g.d_ff * 4)
+        self.ub = B(cap * g.d_ff * 4)
+        self.hb = B(cap * g.d_ff * 4)
+        self.db = B(cap * d * 4)
+        self.logits_buf = B(mb.n_vocab * 4)
+        self.pos = B.from_array(np.zeros(1, np.int32))
+        self.tok = B.from_array(np.zeros(1, np.int32))
+        self.toks = B(cap * 4)
+        self.stream = hip.Stream()
+        self.graph = None
+        self.seq_len = 0
+
+    # -- helpers ---------------------------------------------------------------------------
+    def _norm(self, src, w, rows, dst):
+        from . import rmsnorm_dev
+        rmsnorm_dev(src, w, rows, self.g.d_model, self.g.rms_eps, dst, self.stream)
+
+    def _logits_and_token(self, last_row_src):
+        from . import argmax_dev
+        self._norm(last_row_src, self.output_norm, 1, self.n)
+        self.output.matvec_dev(self.n, self.logits_buf, stream=self.stream)
+        argmax_dev(self.logits_buf, self.mb.n_vocab, self.tok, self.stream)
+
+    def _step_body(self):
+        """One decode position: token *tok at position *pos -> next token in *tok, *pos + 1."""
+        from . import attention_dev, embed_dev, kv_append_dev, pos_add_dev, rope_dev
+        g, s = self.g, self.stream
+        d, hd = g.d_model, g.head_dim
+        embed_dev(self.embed, self.mb.n_vocab, d, self.tok, 1, self.x, s)
+        for blk in self.blocks:
+            self._norm(self.x, blk["attn_norm"], 1, self.n)
+            blk["q"].matvec_add_dev(self.n, blk["q_bias"], self.qb, stream=s)
+            blk["k"].matvec_add_dev(self.n, blk["k_bias"], self.kb, stream=s)
+            blk["v"].matvec_add_dev(self.n, blk["v_bias"], self.vb, stream=s)
+            rope_dev(self.qb, 1, g.n_heads, hd, g.rope_freq_base, self.pos, 0, s)
+            rope_dev(self.kb, 1, g.n_kv_heads, hd, g.rope_freq_base, self.pos, 0, s)
+            kv_append_dev(self.kb, self.vb, 1, self.kv, blk["kc"], blk["vc"], self.max_seq, self.pos, s)
+            attention_dev(self.qb, blk["kc"], blk["vc"], 1, g.n_heads, g.n_kv_heads, hd, self.max_seq, self.pos,
+                          self.ctx, s)
+            blk["o"].matvec_add_dev(self.ctx, self.x, self.x, stream=s)          # residual
+            self._norm(self.x, blk["ffn_norm"], 1, self.n)
+            blk["ffn"].forward_dev(self.n, self.hb, stream=s)
+            blk["down"].matvec_add_dev(self.hb, self.x, self.x, stream=s)        # residual
+        self._logits_and_token(self.x)
+        pos_add_dev(self.pos, 1, s)
+
+    # -- API -------------------------------------------------------------------------------
+    def prefill(self, prompt) -> int:
+        """Batched prefill of the prompt (runner.rs:236-260); returns the first greedy token."""
+        from . import add_dev, attention_dev, embed_dev, kv_append_dev, pos_add_dev, rope_dev, swiglu_dev
+        g, s = self.g, self.stream
+        d, hd, kv = g.d_model, g.head_dim, self.kv
+        prompt = np.asarray(prompt, np.int32)
+        rows = prompt.size
+        if not (0 < rows <= self.cap and self.seq_len + rows <= self.max_seq):
+            raise ValueError(f"prefill of {rows} rows at position {self.seq_len} (cap {self.cap}, max_seq {self.max_seq})")
+        if prompt.min() < 0 or prompt.max() >= self.mb.n_vocab:
+            raise ValueError("prompt token outside the vocabulary")
+        self.toks.upload(prompt)
+        embed_dev(self.embed, self.mb.n_vocab, d, self.toks, rows, self.x, s)
+        m = self.mode
+        for blk in self.blocks:
+            self._norm(self.x, blk["attn_norm"], rows, self.n)
+            blk["q"].matmul_dev(self.n, rows, self.qb, m, stream=s)
+            blk["k"].matmul_dev(self.n, rows, self.kb, m, stream=s)
+            blk["v"].matmul_dev(self.n, rows, self.vb, m, stream=s)
+            add_dev(self.qb, blk["q_bias"], rows * d, d, self.qb, s)
+            add_dev(self.kb, blk["k_bias"], rows * kv, kv, self.kb, s)
+            add_dev(self.vb, blk["v_bias"], rows * kv, kv, self.vb, s)
+            rope_dev(self.qb, rows, g.n_heads, hd, g.rope_freq_base, self.pos, 0, s)
+            rope_dev(self.kb, rows, g.n_kv_heads, hd, g.rope_freq_base, self.pos, 0, s)
+            kv_append_dev(self.kb, self.vb, rows, kv, blk["kc"], blk["vc"], self.max_seq, self.pos, s)
+            attention_dev(self.qb, blk["kc"], blk["vc"], rows, g.n_heads, g.n_kv_heads, hd, self.max_seq, self.pos,
+                          self.ctx, s)
+            blk["o"].matmul_dev(self.ctx, rows, self.ob, m, stream=s)
+            add_dev(self.x, self.ob, rows * d, rows * d, self.x, s)
+            self._norm(self.x, blk["ffn_norm"], rows, self.n)
+            blk["gate"].matmul_dev(self.n, rows, self.gb, m, stream=s)
+            blk["up"].matmul_dev(self.n, rows, self.ub, m, stream=s)
+            swiglu_dev(self.gb, self.ub, self.hb, rows * g.d_ff, s)
+            blk["down"].matmul_dev(self.hb, rows, self.db, m, stream=s)
+            add_dev(self.x, self.db, rows * d, rows * d, self.x, s)
+        last = _Offset(self.x, (rows - 1) * d * 4)
+        self._logits_and_token(last)
+        pos_add_dev(self.pos, rows, s)
+        self.seq_len += rows
+        self.stream.synchronize()
+        return int(self.tok.download(np.int32, 1)[0])
+
+    def step(self) -> int:
+        """Decode the token in *tok at the next position; returns the following greedy token."""
+        from . import hip
+        if self.seq_len >= self.max_seq:
+            raise ValueError(f"decode past max_seq {self.max_seq}")
+        if not self.use_graph:
+            self._step_body()
+        else:
+            if self.graph is None:
+                self.graph = hip.Graph(self.stream, self._step_body)
+            self.graph.launch()
+        self.seq_len += 1
+        self.stream.synchronize()
+        return int(self.tok.download(np.int32, 1)[0])
+
+    def replay(self, steps: int) -> None:
+        """`steps` decode steps back to back with no host synchronisation in between (the token
+        and position stay on the GPU); waits for the last one."""
+        from . import hip
+        if self.seq_len + steps > self.max_seq:
+            raise ValueError(f"decode past max_seq {self.max_seq}")
+        if self.graph is None:
+            self.graph = hip.Graph(self.stream, self._step_body)
+        for _ in range(steps):
+            self.graph.launch()
+        self.seq_len += steps
+        self.stream.synchronize()
+
+    def logits(self) -> np.ndarray:
+        """The logits of the last position computed (downloaded)."""
+        self.stream.synchronize()
+        return self.logits_buf.download(np.float32, self.mb.n_vocab)
+
+    def generate(self, prompt, max_new: int):
+        out = [self.prefill(prompt)]
+        for _ in range(max_new - 1):
+            out.append(self.step())
+        return out
+
+    def close(self):
+        if self.graph is not None:
+            self.graph.destroy()
+            self.graph = None
+        for blk in self.blocks:
+            blk["ffn"].close()
+            for k in ("q", "k", "v", "o", "gate", "up", "down"):
+                blk[k].close()
+        self.output.close()
+        self.stream.destroy()
+
+
+class _Offset:
+    """A device address inside a buffer (for passing a row of a larger buffer)."""
+
+    def __init__(self, buf, byte_offset: int):
+        self._p = buf.data_ptr() + byte_offset
+
+    def data_ptr(self) -> int:
+        return self._p

@@ -128,6 +128,44 @@ def time_moe(tokens: int, mode: int, reps: int, seed: int = 401):
             "frac_hbm": nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, "tflops": flop / (us * 1e-6) / 1e12}
 
 
+def time_decode(prompt_len: int, steps: int, mode: int, seed: int = 501, use_graph: bool = True):
+    """DeviceDecoder on the Qwen2.5-0.5B-shaped model: prefill, then `steps` graph replays back to
+    back (the token never leaves the GPU), then `steps` replays with a token read-back each."""
+    import time
+
+    from . import qwen
+    mb = qwen.synth_model(seed)
+    prompt = np.random.default_rng(seed + 1).integers(0, mb.n_vocab, prompt_len)
+    print(f"decode: model ready, prompt {prompt_len}, graph {use_graph}", flush=True)
+    dd = qwen.DeviceDecoder(mb, max_seq=prompt_len + 2 * steps + 1, mode=mode, prefill_rows=prompt_len,
+                            use_graph=use_graph)
+    dd.prefill(prompt[:16])
+    dd.close()
+    dd = qwen.DeviceDecoder(mb, max_seq=prompt_len + 2 * steps + 1, mode=mode, prefill_rows=prompt_len,
+                            use_graph=use_graph)
+    print("decode: weights resident", flush=True)
+    t0 = time.perf_counter()
+    dd.prefill(prompt)
+    t1 = time.perf_counter()
+    print("decode: prefill done", flush=True)
+    dd.step()                                    # graph capture
+    t2 = time.perf_counter()
+    print("decode: first step done", flush=True)
+    if use_graph:
+        dd.replay(steps)
+    else:
+        for _ in range(steps):
+            dd.step()
+    t3 = time.perf_counter()
+    for _ in range(steps - 1):
+        dd.step()
+    t4 = time.perf_counter()
+    dd.close()
+    return {"prompt": prompt_len, "steps": steps, "mode": "bf16" if mode == 0 else "f32",
+            "prefill_ms": 1e3 * (t1 - t0), "capture_ms": 1e3 * (t2 - t1),
+            "step_us_device": 1e6 * (t3 - t2) / steps, "step_us_readback": 1e6 * (t4 - t3) / (steps - 1)}
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--types", default="Q4_0,Q5_0,Q8_0,Q4_K,Q5_K,Q6_K")
@@ -138,8 +176,19 @@ def main(argv=None) -> int:
     ap.add_argument("--moe", action="store_true", help="time the MoE expert FFN (config 4) instead")
     ap.add_argument("--rows", default="64,961", help="GEMM activation-row counts")
     ap.add_argument("--modes", default="bf16,f32", help="GEMM modes")
+    ap.add_argument("--decode", action="store_true", help="time the device-resident decoder instead")
+    ap.add_argument("--prompt", type=int, default=961, help="decoder prompt length")
+    ap.add_argument("--steps", type=int, default=128, help="decoder steps")
+    ap.add_argument("--no-graph", action="store_true", help="decoder steps launched eagerly")
     args = ap.parse_args(argv)
     init()
+    if args.decode:
+        for mode in [{"bf16": 0, "f32": 1}[v] for v in args.modes.split(",") if v]:
+            r = time_decode(args.prompt, args.steps, mode, use_graph=not args.no_graph)
+            print(f"decode prompt={r['prompt']} {r['mode']:4s} prefill {r['prefill_ms']:8.2f} ms "
+                  f"capture {r['capture_ms']:7.2f} ms step {r['step_us_device']:8.1f} us (device) "
+                  f"{r['step_us_readback']:8.1f} us (with read-back)", flush=True)
+        return 0
     only = set(filter(None, args.only.split(",")))
     if args.moe:
         rows = []

@@ -1,0 +1,223 @@
+"""Device-resident transformer steps (librehip's re_*_dev layer entry points) against the host
+restatements of the reference's steps (rehip.qwen: infer.rs:72-223, forward.rs:232-586), and the
+device-resident decoder (one HIP graph per token) against the CPU-kernel decoder.
+
+Tolerances: RMS-norm, RoPE, attention and the FFN pair are f32 with a different summation order
+from numpy's, so they are compared at 2e-5 relative to the output scale (RoPE angles at
+positions up to 2048 carry ~1e-4 rad of f32 rounding in both, hence 5e-4 there); argmax, the
+embedding gather, the K/V append and the fused add are exact."""
+import numpy as np
+import pytest
+
+import rehip
+from oracle.backend import CpuBackend
+from rehip import hip, qwen
+
+pytestmark = pytest.mark.gpu
+
+B = hip.DeviceBuffer
+
+
+def dev_i32(a):
+    return B.from_array(np.asarray(a, np.int32))
+
+
+def down(buf, n, dtype=np.float32):
+    hip.synchronize()
+    return buf.download(dtype, n)
+
+
+@pytest.mark.parametrize("rows,d", [(1, 896), (7, 896), (3, 100), (2, 4096)])
+def test_rmsnorm(rows, d):
+    rng = np.random.default_rng(rows * 1000 + d)
+    x = (rng.standard_normal((rows, d)) * 3).astype(np.float32)
+    w = rng.standard_normal(d).astype(np.float32)
+    out = B(rows * d * 4)
+    rehip.rmsnorm_dev(B.from_array(x), B.from_array(w), rows, d, 1e-6, out)
+    got = down(out, rows * d).reshape(rows, d)
+    want = qwen.rmsnorm_rows(x, w, 1e-6)
+    np.testing.assert_allclose(got, want, rtol=0, atol=2e-5 * np.abs(want).max())
+
+
+@pytest.mark.parametrize("rows,heads,hd,pos0,off", [(1, 14, 64, 0, 0), (1, 2, 64, 2047, 0), (9, 14, 64, 100, 3),
+                                                    (4, 4, 128, 5, 0), (3, 1, 2, 0, 0)])
+def test_rope(rows, heads, hd, pos0, off):
+    rng = np.random.default_rng(heads * 7 + hd + pos0)
+    x = rng.standard_normal((rows, heads * hd)).astype(np.float32)
+    xb = B.from_array(x)
+    rehip.rope_dev(xb, rows, heads, hd, 1e6, dev_i32([pos0]), off)
+    got = down(xb, x.size).reshape(rows, -1)
+    cos, sin = qwen.rope_table(rows, pos0 + off, hd, 1e6)
+    want = qwen.rope_rows(x, heads, hd, cos, sin)
+    np.testing.assert_allclose(got, want, rtol=0, atol=5e-4)
+
+
+def test_kv_append_and_bounds():
+    kv, max_seq = 128, 16
+    rng = np.random.default_rng(3)
+    kc, vc = B.from_array(np.zeros((max_seq, kv), np.float32)), B.from_array(np.zeros((max_seq, kv), np.float32))
+    k = rng.standard_normal((5, kv)).astype(np.float32)
+    v = rng.standard_normal((5, kv)).astype(np.float32)
+    # rows 13..15 fit, rows 16 and 17 are past the cache and are dropped
+    rehip.kv_append_dev(B.from_array(k), B.from_array(v), 5, kv, kc, vc, max_seq, dev_i32([13]))
+    gk = down(kc, max_seq * kv).reshape(max_seq, kv)
+    gv = down(vc, max_seq * kv).reshape(max_seq, kv)
+    assert np.array_equal(gk[13:], k[:3]) and np.array_equal(gv[13:], v[:3])
+    assert not gk[:13].any() and not gv[:13].any()
+
+
+@pytest.mark.parametrize("rows,pos0,nh,nkv,hd", [(1, 0, 14, 2, 64), (1, 300, 14, 2, 64), (6, 0, 14, 2, 64),
+                                                 (5, 40, 4, 4, 32), (33, 7, 8, 1, 128)])
+def test_attention(rows, pos0, nh, nkv, hd):
+    g = qwen.Geometry(d_model=nh * hd, n_heads=nh, n_kv_heads=nkv)
+    max_seq = 512
+    rng = np.random.default_rng(rows + pos0 + nh)
+    kvd = nkv * hd
+    kc = np.zeros((max_seq, kvd), np.float32)
+    vc = np.zeros((max_seq, kvd), np.float32)
+    total = pos0 + rows
+    kc[:total] = rng.standard_normal((total, kvd))
+    vc[:total] = rng.standard_normal((total, kvd))
+    q = (rng.standard_normal((rows, nh * hd)) * 2).astype(np.float32)
+    ctx = B(rows * nh * hd * 4)
+    rehip.attention_dev(B.from_array(q), B.from_array(kc), B.from_array(vc), rows, nh, nkv, hd, max_seq,
+                        dev_i32([pos0]), ctx)
+    got = down(ctx, rows * nh * hd).reshape(rows, -1)
+    want = qwen.attention(q, kc, vc, g, pos0)
+    np.testing.assert_allclose(got, want, rtol=0, atol=2e-5 * np.abs(want).max())
+
+
+def test_add_and_bias():
+    rng = np.random.default_rng(9)
+    a = rng.standard_normal(7 * 96).astype(np.float32)
+    b = rng.standard_normal(96).astype(np.float32)
+    out = B(a.nbytes)
+    rehip.add_dev(B.from_array(a), B.from_array(b), a.size, b.size, out)
+    assert np.array_equal(down(out, a.size), (a.reshape(7, 96) + b).reshape(-1))
+    with pytest.raises(rehip.RehipError):
+        rehip.add_dev(B.from_array(a), B.from_array(b), a.size, 97, out)
+
+
+@pytest.mark.parametrize("n", [1, 5, 1000, 151936])
+def test_argmax_last_of_ties(n):
+    rng = np.random.default_rng(n)
+    x = (rng.standard_normal(n) - 5).astype(np.float32)        # all negative
+    if n > 4:
+        top = np.float32(x.max() + 1)
+        x[[1, n // 2, n - 2]] = top                              # ties: the last index wins
+    idx = dev_i32([-7])
+    rehip.argmax_dev(B.from_array(x), n, idx)
+    assert int(down(idx, 1, np.int32)[0]) == qwen.argmax_last(x)
+
+
+def test_embed_gather_and_out_of_range():
+    rng = np.random.default_rng(4)
+    table = rng.standard_normal((50, 96)).astype(np.float32)
+    toks = np.array([3, 0, 49, 50, -1, 3], np.int32)
+    out = B(toks.size * 96 * 4)
+    rehip.embed_dev(B.from_array(table), 50, 96, dev_i32(toks), toks.size, out)
+    got = down(out, toks.size * 96).reshape(toks.size, 96)
+    assert np.array_equal(got[[0, 1, 2, 5]], table[[3, 0, 49, 3]])
+    assert not got[3].any() and not got[4].any()
+
+
+def test_pos_add():
+    p = dev_i32([5])
+    rehip.pos_add_dev(p, 3)
+    rehip.pos_add_dev(p, 961)
+    assert int(down(p, 1, np.int32)[0]) == 969
+
+
+@pytest.mark.parametrize("t,m,n", [(rehip.Q4_K, 896, 896), (rehip.Q6_K, 896, 4864), (rehip.Q8_0, 64, 14336),
+                                   (rehip.Q4_0, 130, 512)])
+def test_matvec_add_is_matvec_plus_add(t, m, n):
+    """The fused add returns the plain GEMV's sum plus `add` exactly, also in place."""
+    rng = np.random.default_rng(m + n)
+    w = qwen.conditioned_weight_bytes(rng, t, m, n, 1.0 / np.sqrt(n)) if t in (rehip.Q4_K, rehip.Q6_K, rehip.Q8_0) \
+        else rng.integers(0, 256, m * rehip.row_bytes(t, n), dtype=np.uint8)
+    if t == rehip.Q4_0:
+        w = w.reshape(m, -1)
+        w[:, 0::18] = 0x00
+        w[:, 1::18] = 0x2c                                      # scale bits of a small f16
+        w = w.reshape(-1)
+    q = rehip.QMat.from_bytes(t, w, m, n)
+    x = rng.standard_normal(n).astype(np.float32)
+    add = rng.standard_normal(m).astype(np.float32)
+    xb, yb, ab = B.from_array(x), B(m * 4), B.from_array(add)
+    q.matvec_dev(xb, yb)
+    plain = down(yb, m)
+    q.matvec_add_dev(xb, ab, yb)
+    assert np.array_equal(down(yb, m), plain + add)
+    q.matvec_add_dev(xb, ab, ab)                                 # y aliases add
+    assert np.array_equal(down(ab, m), plain + add)
+    q.close()
+
+
+@pytest.mark.parametrize("t,inter,hidden", [(rehip.Q4_K, 4864, 896), (rehip.Q8_0, 100, 256), (rehip.Q5_0, 48, 512)])
+def test_ffn_pair(t, inter, hidden):
+    rng = np.random.default_rng(inter)
+    if t in (rehip.Q4_K, rehip.Q8_0):
+        g = qwen.conditioned_weight_bytes(rng, t, inter, hidden, 1.0 / np.sqrt(hidden))
+        u = qwen.conditioned_weight_bytes(rng, t, inter, hidden, 1.0 / np.sqrt(hidden))
+    else:
+        def small(seed):
+            r = np.random.default_rng(seed)
+            w = r.integers(0, 256, inter * rehip.row_bytes(t, hidden), dtype=np.uint8).reshape(inter, -1)
+            w[:, 0::22] = 0x00
+            w[:, 1::22] = 0x24
+            return w.reshape(-1)
+        g, u = small(1), small(2)
+    G, U = rehip.QMat.from_bytes(t, g, inter, hidden), rehip.QMat.from_bytes(t, u, inter, hidden)
+    f = rehip.Ffn(G, U)
+    x = rng.standard_normal(hidden).astype(np.float32)
+    h = B(inter * 4)
+    f.forward_dev(B.from_array(x), h)
+    got = down(h, inter)
+    want = qwen.silu(G.matvec(x)) * U.matvec(x)
+    np.testing.assert_allclose(got, want, rtol=0, atol=2e-5 * np.abs(want).max())
+    f.close()
+    G.close()
+    U.close()
+
+
+def cpu_tokens(mb, prompt, steps):
+    r = qwen.DenseRunner(mb, CpuBackend())
+    dec = qwen.DenseDecoder(r, len(prompt) + steps)
+    logits = dec.prefill(prompt)
+    first = logits.copy()
+    toks = [qwen.argmax_last(logits)]
+    for _ in range(steps - 1):
+        toks.append(qwen.argmax_last(dec.step(toks[-1])))
+    return toks, first
+
+
+TINY = qwen.Geometry(d_model=256, n_heads=4, n_kv_heads=2, d_ff=512, rope_freq_base=1e4, rms_eps=1e-5)
+
+
+@pytest.mark.parametrize("use_graph", [False, True])
+def test_device_decoder_tiny_matches_cpu_path(use_graph):
+    mb = qwen.synth_model(7, TINY, n_layers=3, n_vocab=1000)
+    prompt = [1, 2, 3, 5, 8, 13, 21, 34, 55, 89]
+    want, lg = cpu_tokens(mb, prompt, 20)
+    dd = qwen.DeviceDecoder(mb, max_seq=64, prefill_rows=16, use_graph=use_graph)
+    first = dd.prefill(prompt)
+    np.testing.assert_allclose(dd.logits(), lg, rtol=0, atol=1e-4 * np.abs(lg).max())
+    got = [first] + [dd.step() for _ in range(19)]
+    dd.close()
+    assert got == want
+    with pytest.raises(ValueError):
+        qwen.DeviceDecoder(mb, max_seq=8, prefill_rows=16).prefill(prompt)
+
+
+def test_device_decoder_qwen_shape_64_steps_match_cpu_path():
+    """Qwen2.5-0.5B shape, Q4_K_M mix, 961-token prompt, 64 greedy tokens: the device-resident
+    decoder (GPU attention/norms/RoPE/argmax, graph-replayed steps) against the CPU kernels."""
+    mb = qwen.synth_model(501)
+    prompt = np.random.default_rng(502).integers(0, mb.n_vocab, 961)
+    want, lg = cpu_tokens(mb, prompt, 64)
+    dd = qwen.DeviceDecoder(mb, max_seq=1024, prefill_rows=961)
+    got = [dd.prefill(prompt)]
+    assert np.max(np.abs(dd.logits() - lg)) <= 1e-3 * np.max(np.abs(lg))
+    got += [dd.step() for _ in range(63)]
+    dd.close()
+    assert got == want, next(i for i, (a, b) in enumerate(zip(got, want)) if a != b)
