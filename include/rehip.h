@@ -109,9 +109,17 @@ int re_moe_forward_dev(re_moe *e, const float *d_x, size_t tokens, size_t top_k,
  * captured graph serves every decode step; re_pos_add_dev advances it on the stream. */
 typedef struct re_ffn re_ffn;
 
-/* y = W x + add (add may equal y; NULL = plain matvec): the q/k/v bias add (forward.rs:447-449)
- * and the residual adds (forward.rs:472-485) folded into the GEMV's store. */
-int re_qmat_matvec_add_dev(re_qmat *q, const float *d_x, const float *d_add, float *d_y, void *stream);
+/* y = W norm(x) + add, with the pieces of the transformer block around a projection folded in:
+ *   d_norm_w  NULL, or x is RMS-normalised first, x * (1/sqrt(mean(x^2) + eps)) * norm_w
+ *             (the attention/FFN/output norms, infer.rs:72-82, forward.rs:432, 479, runner.rs:275);
+ *   d_add     NULL, or added to the result (may equal y): the residual adds (forward.rs:472-485);
+ *   d_best    NULL, or RE_ARGMAX_SLOTS uint64 slots that keep the maximum of key(y[r], r) over
+ *             the rows, the key ordering by value and then by index, so the low 32 bits of the
+ *             largest slot end as the greedy token (infer.rs:217-223: the last index among equal
+ *             maxima). The slots must start at 0 (re_decode_advance_dev clears them).
+ * x and norm_w are 16-byte aligned. */
+int re_qmat_matvec_ex_dev(re_qmat *q, const float *d_x, const float *d_norm_w, float eps, const float *d_add,
+                          float *d_y, unsigned long long *d_best, void *stream);
 /* out[r] = x[r] * (1 / sqrt(mean(x[r]^2) + eps)) * w for rows x d (infer.rs:72-82). */
 int re_rmsnorm_dev(const float *d_x, const float *d_w, size_t rows, size_t d, float eps, float *d_out,
                    void *stream);
@@ -125,12 +133,30 @@ int re_rope_dev(float *d_x, size_t rows, size_t heads, size_t head_dim, float th
 int re_kv_append_dev(const float *d_k, const float *d_v, size_t rows, size_t kv_dim, float *d_kcache,
                      float *d_vcache, size_t max_seq, const int *d_pos, void *stream);
 /* Causal GQA attention of rows x n_heads x head_dim queries at positions *d_pos + r over cache
- * rows 0..position (forward.rs:232-277, 437-470); the scores of one row need max_seq floats of
- * LDS (max_seq <= 32768) and positions are clamped to the max_seq cache rows. Output rows x
- * n_heads x head_dim. */
+ * rows 0..position (forward.rs:232-277, 437-470); max_seq <= 32768 cache rows, positions are
+ * clamped to them. Output rows x n_heads x head_dim. Rows >= 8 with head_dim 64 run as f32 MFMA
+ * flash attention; fewer rows use d_work (re_attention_work_bytes bytes; NULL = one workgroup
+ * per head and row, slower for long caches) to split the cache over workgroups. Buffers are
+ * 16-byte aligned. */
+size_t re_attention_work_bytes(size_t rows, size_t n_heads, size_t head_dim, size_t max_seq);
 int re_attention_dev(const float *d_q, const float *d_kcache, const float *d_vcache, size_t rows,
                      size_t n_heads, size_t n_kv_heads, size_t head_dim, size_t max_seq,
-                     const int *d_pos, float *d_ctx, void *stream);
+                     const int *d_pos, float *d_work, size_t work_bytes, float *d_ctx, void *stream);
+/* The q/k/v projections' epilogue (forward.rs:347-363, 437-449): q = q + bq and k = k + bk
+ * rotated (NeoX, as re_rope_dev) at position *d_pos + r, v = v + bv; rotated q written to
+ * d_qout (rows x n_heads x head_dim), k and v appended at cache rows *d_pos + r (rows past
+ * max_seq are not stored). The three inputs are row-strided (ldq/ldk/ldv floats), so they may
+ * be slices of one fused q|k|v projection. Biases may be NULL. */
+int re_qkv_rope_append_dev(const float *d_q, size_t ldq, const float *d_k, size_t ldk, const float *d_v,
+                           size_t ldv, const float *d_bq, const float *d_bk, const float *d_bv, size_t rows,
+                           size_t n_heads, size_t n_kv_heads, size_t head_dim, float theta, const int *d_pos,
+                           float *d_qout, float *d_kcache, float *d_vcache, size_t max_seq, void *stream);
+/* End of a greedy step (runner.rs:262-282): *d_tok = the token in the largest of the
+ * RE_ARGMAX_SLOTS slots at d_best (low 32 bits), *d_pos += delta, d_hist[*d_pos] = *d_tok when
+ * d_hist is given and *d_pos < hist_len, and the slots cleared for the next step. */
+#define RE_ARGMAX_SLOTS 8
+int re_decode_advance_dev(unsigned long long *d_best, int *d_tok, int *d_pos, int delta, int *d_hist,
+                          size_t hist_len, void *stream);
 /* out[i] = a[i] + b[i % nb] (residual add for nb == n, per-column bias for nb | n). */
 int re_add_dev(const float *d_a, const float *d_b, size_t n, size_t nb, float *d_out, void *stream);
 /* h = silu(g) * u elementwise (moe.rs:44-51, 280-283). */
@@ -148,7 +174,8 @@ int re_pos_add_dev(int *d_pos, int delta, void *stream);
  * keeps references to the two matrices, which must outlive it. */
 int re_ffn_create(re_qmat *gate, re_qmat *up, re_ffn **out);
 void re_ffn_destroy(re_ffn *f);
-int re_ffn_forward_dev(re_ffn *f, const float *d_x, float *d_h, void *stream);
+/* d_norm_w: NULL, or x is RMS-normalised first (the FFN norm, forward.rs:479). */
+int re_ffn_forward_dev(re_ffn *f, const float *d_x, const float *d_norm_w, float eps, float *d_h, void *stream);
 
 #ifdef __cplusplus
 }

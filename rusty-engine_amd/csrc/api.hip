@@ -203,9 +203,16 @@ int upload_tiled(const MatGeom& g, const uint8_t* bytes, uint8_t* d_dst) {
   return RE_OK;
 }
 
-int gemv_enqueue(re_qmat* q, const float* d_x, float* d_y, hipStream_t s, const float* d_add = nullptr) {
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+int gemv_enqueue(re_qmat* q, const float* d_x, float* d_y, hipStream_t s, const float* d_add = nullptr,
+                 const float* d_norm = nullptr, float eps = 0.0f, unsigned long long* d_best = nullptr) {
+  if (!aligned16(d_x) || !aligned16(d_norm)) return fail(RE_ERR_ARG, "x and norm weights must be 16-byte aligned");
   GemvArgs a{};
   a.add = d_add;
+  a.norm_w = d_norm;
+  a.norm_eps = eps;
+  a.best = d_best;
   a.W = q->d_w;
   a.x = d_x;
   a.y = d_y;
@@ -362,9 +369,11 @@ int re_qmat_matvec_dev(re_qmat* q, const float* d_x, float* d_y, void* stream) {
   return gemv_enqueue(q, d_x, d_y, (hipStream_t)stream);
 }
 
-int re_qmat_matvec_add_dev(re_qmat* q, const float* d_x, const float* d_add, float* d_y, void* stream) {
+int re_qmat_matvec_ex_dev(re_qmat* q, const float* d_x, const float* d_norm_w, float eps, const float* d_add,
+                          float* d_y, unsigned long long* d_best, void* stream) {
   if (!q || !d_x || !d_y) return fail(RE_ERR_ARG, "null pointer");
-  return gemv_enqueue(q, d_x, d_y, (hipStream_t)stream, d_add);
+  if (d_norm_w && !(eps >= 0.0f)) return fail(RE_ERR_ARG, "norm eps must be >= 0");
+  return gemv_enqueue(q, d_x, d_y, (hipStream_t)stream, d_add, d_norm_w, eps, d_best);
 }
 
 int re_qmat_matmul_dev(re_qmat* q, const float* d_x, size_t rows, float* d_y, int mode, void* stream) {
@@ -727,17 +736,55 @@ int re_kv_append_dev(const float* d_k, const float* d_v, size_t rows, size_t kv_
   return RE_OK;
 }
 
+size_t re_attention_work_bytes(size_t rows, size_t n_heads, size_t head_dim, size_t max_seq) {
+  if (rows == 0 || n_heads == 0 || head_dim == 0 || max_seq == 0 || rows > 65535 || n_heads > 65535 ||
+      head_dim > 256 || max_seq > 32768)
+    return 0;
+  return attention_work_floats((int)rows, (int)n_heads, (int)head_dim, (int)max_seq) * sizeof(float);
+}
+
 int re_attention_dev(const float* d_q, const float* d_kcache, const float* d_vcache, size_t rows, size_t n_heads,
-                     size_t n_kv_heads, size_t head_dim, size_t max_seq, const int* d_pos, float* d_ctx,
-                     void* stream) {
+                     size_t n_kv_heads, size_t head_dim, size_t max_seq, const int* d_pos, float* d_work,
+                     size_t work_bytes, float* d_ctx, void* stream) {
   if (!d_q || !d_kcache || !d_vcache || !d_pos || !d_ctx) return fail(RE_ERR_ARG, "null pointer");
   if (rows == 0) return RE_OK;
   if (n_heads == 0 || n_kv_heads == 0 || n_heads % n_kv_heads || head_dim == 0 || head_dim % 4 || head_dim > 256 ||
       max_seq == 0 || max_seq > 32768 || rows > 65535 || n_heads > 65535)
     return fail(RE_ERR_SIZE, "attention shape heads %zu/%zu head_dim %zu max_seq %zu", n_heads, n_kv_heads, head_dim,
                 max_seq);
+  if (!aligned16(d_q) || !aligned16(d_kcache) || !aligned16(d_vcache) || !aligned16(d_ctx))
+    return fail(RE_ERR_ARG, "attention buffers must be 16-byte aligned");
+  if (d_work && work_bytes < re_attention_work_bytes(rows, n_heads, head_dim, max_seq))
+    return fail(RE_ERR_SIZE, "attention workspace of %zu bytes, need %zu", work_bytes,
+                re_attention_work_bytes(rows, n_heads, head_dim, max_seq));
   HIP_TRY(launch_attention(d_q, d_kcache, d_vcache, (int)rows, (int)n_heads, (int)n_kv_heads, (int)head_dim,
-                           (int)max_seq, d_pos, d_ctx, (hipStream_t)stream));
+                           (int)max_seq, d_pos, d_work, d_ctx, (hipStream_t)stream));
+  return RE_OK;
+}
+
+int re_qkv_rope_append_dev(const float* d_q, size_t ldq, const float* d_k, size_t ldk, const float* d_v, size_t ldv,
+                           const float* d_bq, const float* d_bk, const float* d_bv, size_t rows, size_t n_heads,
+                           size_t n_kv_heads, size_t head_dim, float theta, const int* d_pos, float* d_qout,
+                           float* d_kcache, float* d_vcache, size_t max_seq, void* stream) {
+  if (!d_q || !d_k || !d_v || !d_pos || !d_qout || !d_kcache || !d_vcache) return fail(RE_ERR_ARG, "null pointer");
+  if (rows == 0) return RE_OK;
+  if (n_heads == 0 || n_kv_heads == 0 || head_dim == 0 || head_dim % 2 || head_dim > 256 || rows > 65535 ||
+      n_heads + n_kv_heads > 65535 || max_seq == 0 || max_seq > (1u << 24) || ldq < n_heads * head_dim ||
+      ldk < n_kv_heads * head_dim || ldv < n_kv_heads * head_dim || ldq > (1u << 30) || ldk > (1u << 30) ||
+      ldv > (1u << 30))
+    return fail(RE_ERR_SIZE, "qkv shape rows %zu heads %zu/%zu head_dim %zu strides %zu/%zu/%zu", rows, n_heads,
+                n_kv_heads, head_dim, ldq, ldk, ldv);
+  HIP_TRY(launch_qkv_rope_append(d_q, (int)ldq, d_k, (int)ldk, d_v, (int)ldv, d_bq, d_bk, d_bv, (int)rows,
+                                 (int)n_heads, (int)n_kv_heads, (int)head_dim, theta, d_pos, d_qout, d_kcache,
+                                 d_vcache, (int)max_seq, (hipStream_t)stream));
+  return RE_OK;
+}
+
+int re_decode_advance_dev(unsigned long long* d_best, int* d_tok, int* d_pos, int delta, int* d_hist,
+                          size_t hist_len, void* stream) {
+  if (!d_best || !d_tok || !d_pos) return fail(RE_ERR_ARG, "null pointer");
+  if (hist_len > (1u << 30)) return fail(RE_ERR_SIZE, "history of %zu tokens", hist_len);
+  HIP_TRY(launch_decode_advance(d_best, d_tok, d_pos, delta, d_hist, (int)hist_len, (hipStream_t)stream));
   return RE_OK;
 }
 
@@ -809,9 +856,12 @@ void re_ffn_destroy(re_ffn* f) {
   delete f;
 }
 
-int re_ffn_forward_dev(re_ffn* f, const float* d_x, float* d_h, void* stream) {
+int re_ffn_forward_dev(re_ffn* f, const float* d_x, const float* d_norm_w, float eps, float* d_h, void* stream) {
   if (!f || !d_x || !d_h) return fail(RE_ERR_ARG, "null pointer");
+  if (!aligned16(d_x) || !aligned16(d_norm_w)) return fail(RE_ERR_ARG, "x and norm weights must be 16-byte aligned");
   MoeGemvArgs g{};
+  g.norm_w = d_norm_w;
+  g.norm_eps = eps;
   g.W0 = f->gate->d_w;
   g.W1 = f->up->d_w;
   g.w_stride = 0;

@@ -417,4 +417,19 @@ __device__ __forceinline__ float run_dot(const Run& r, const float* __restrict__
   return __builtin_fmaf(scale, s, -r.offset * xs[r.e >> 4]);
 }
 
+// Sum of one value per thread over a workgroup of WAVES waves: xor tree inside each wave, then
+// the wave sums in wave order (deterministic). `red` holds WAVES floats; all threads get the sum.
+template <int WAVES>
+__device__ __forceinline__ float wg_sum(float v, float* red) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float s = red[0];
+#pragma unroll
+  for (int w = 1; w < WAVES; ++w) s += red[w];
+  return s;
+}
+
 }  // namespace rehip

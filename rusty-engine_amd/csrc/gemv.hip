@@ -59,10 +59,23 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs p) {
   // stage this split's x (float4, zero past K) and its per-16 sums
   const int x0 = kb0 * B::QK;
   const int nv = (kb1 - kb0) * B::QK / 4;
+  float inv = 1.0f;
+  if (p.norm_w) {                        // RMS over the whole row (every split reads all of x)
+    float ss = 0.0f;
+    for (int k = threadIdx.x; k < p.K; k += WAVES * 64) ss = __builtin_fmaf(p.x[k], p.x[k], ss);
+    ss = wg_sum<WAVES>(ss, red);
+    inv = 1.0f / sqrtf(ss / (float)p.K + p.norm_eps);
+  }
   for (int i = threadIdx.x; i < nv; i += WAVES * 64) {
     const int k = x0 + 4 * i;
     float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (k < p.K) v = *reinterpret_cast<const float4*>(p.x + k);
+    if (k < p.K) {
+      v = *reinterpret_cast<const float4*>(p.x + k);
+      if (p.norm_w) {
+        const float4 w = *reinterpret_cast<const float4*>(p.norm_w + k);
+        v = make_float4(v.x * inv * w.x, v.y * inv * w.y, v.z * inv * w.z, v.w * inv * w.w);
+      }
+    }
     reinterpret_cast<float4*>(xl)[i] = v;
   }
   __syncthreads();
@@ -104,7 +117,13 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs p) {
     for (int w = 1; w < WAVES; ++w) s += red[w * 64 + lane];
     const int row = tile * 64 + lane;
     if (p.splits == 1) {
-      if (row < p.m) p.y[row] = p.add ? s + p.add[row] : s;
+      unsigned long long key = 0;
+      if (row < p.m) {
+        const float y = p.add ? s + p.add[row] : s;
+        p.y[row] = y;
+        key = argmax_key(y, row);
+      }
+      if (p.best) wave_argmax_fold(key, p.best);
     } else {
       p.partial[(size_t)split * p.m_pad + row] = s;
     }
@@ -126,7 +145,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_rows_kernel(GemvArgs p) {
   constexpr int D = WAVES == 16 ? 2 : kGemvDepth;   // 16 waves: 128 VGPRs per lane
   constexpr int G = 64 / R;              // lane groups per wave
   constexpr int S = WAVES * G;           // slots per workgroup
-  // LDS: x[KB * QK] (zero past K), xs16[KB * QK / 16], red[WAVES * R]
+  // LDS: x[KB * QK] (zero past K), xs16[KB * QK / 16], red[WAVES * R], ssred[WAVES]
   extern __shared__ __attribute__((aligned(16))) float smem[];
   const int per = (p.groups + 7) / 8;
   const int gi = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
@@ -141,6 +160,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_rows_kernel(GemvArgs p) {
   float* xl = smem;
   float* xs16 = smem + nx;
   float* red = xs16 + nx / 16;
+  float* ssred = red + WAVES * R;
 
   const uint8_t* tbase = p.W + (size_t)tile * p.KB * B::SLAB;
   const int u_end = p.KB * NCH;
@@ -151,11 +171,25 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_rows_kernel(GemvArgs p) {
     if (u < u_end) B::load_chunk(tbase + (size_t)(u / NCH) * B::SLAB, rr, u % NCH, ring[i]);
   }
 
+  // RMS-norm prologue: x * w is staged and the sum of squares kept per thread; the row's
+  // 1/rms multiplies the finished dot (W (x inv w) = inv W (x w)), so the norm adds no pass or
+  // barrier before the weights are consumed.
   const int nv = nx / 4;
+  float ss = 0.0f;
   for (int i = threadIdx.x; i < nv; i += WAVES * 64) {
     const int k = 4 * i;
     float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (k < p.K) v = *reinterpret_cast<const float4*>(p.x + k);
+    if (k < p.K) {
+      v = *reinterpret_cast<const float4*>(p.x + k);
+      if (p.norm_w) {
+        ss = __builtin_fmaf(v.x, v.x, ss);
+        ss = __builtin_fmaf(v.y, v.y, ss);
+        ss = __builtin_fmaf(v.z, v.z, ss);
+        ss = __builtin_fmaf(v.w, v.w, ss);
+        const float4 w = *reinterpret_cast<const float4*>(p.norm_w + k);
+        v = make_float4(v.x * w.x, v.y * w.y, v.z * w.z, v.w * w.w);
+      }
+    }
     reinterpret_cast<float4*>(xl)[i] = v;
   }
   __syncthreads();
@@ -191,25 +225,52 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_rows_kernel(GemvArgs p) {
 #pragma unroll
   for (int off = R; off < 64; off *= 2) acc += __shfl_xor(acc, off, 64);
   if (lane < R) red[wave * R + lane] = acc;
-  __syncthreads();
-  if (threadIdx.x < R) {
-    float s = red[threadIdx.x];
+  if (p.norm_w) {
 #pragma unroll
-    for (int w = 1; w < WAVES; ++w) s += red[w * R + threadIdx.x];
-    const int row = tile * 64 + rr;
-    if (row < p.m) p.y[row] = p.add ? s + p.add[row] : s;
+    for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+    if (lane == 0) ssred[wave] = ss;
+  }
+  __syncthreads();
+  if (wave == 0) {
+    unsigned long long key = 0;
+    float inv = 1.0f;
+    if (p.norm_w) {
+      float t = ssred[0];
+#pragma unroll
+      for (int w = 1; w < WAVES; ++w) t += ssred[w];
+      inv = 1.0f / sqrtf(t / (float)p.K + p.norm_eps);
+    }
+    if (lane < R) {
+      float s = red[lane];
+#pragma unroll
+      for (int w = 1; w < WAVES; ++w) s += red[w * R + lane];
+      if (p.norm_w) s *= inv;
+      const int row = tile * 64 + rr;
+      if (row < p.m) {
+        const float y = p.add ? s + p.add[row] : s;
+        p.y[row] = y;
+        key = argmax_key(y, row);
+      }
+    }
+    if (p.best) wave_argmax_fold(key, p.best);
   }
 }
 
 // y[r] = sum over splits, in split order, of partial[split][r]
 __global__ __launch_bounds__(256) void gemv_reduce_kernel(const float* __restrict__ partial,
                                                           float* y, int m, int m_pad,
-                                                          int splits, const float* add) {
+                                                          int splits, const float* add,
+                                                          unsigned long long* best) {
   const int r = blockIdx.x * 256 + threadIdx.x;
-  if (r >= m) return;
-  float s = 0.0f;
-  for (int sp = 0; sp < splits; ++sp) s += partial[(size_t)sp * m_pad + r];
-  y[r] = add ? s + add[r] : s;
+  unsigned long long key = 0;
+  if (r < m) {
+    float s = 0.0f;
+    for (int sp = 0; sp < splits; ++sp) s += partial[(size_t)sp * m_pad + r];
+    const float v = add ? s + add[r] : s;
+    y[r] = v;
+    key = argmax_key(v, r);
+  }
+  if (best) wave_argmax_fold(key, best);
 }
 
 // Bit-exact dequant of the tiled weights into a row-major f32 matrix [m x n].
@@ -237,7 +298,7 @@ __global__ __launch_bounds__(64) void dequant_kernel(const uint8_t* __restrict__
 
 template <int T, int R>
 static hipError_t launch_rows(const GemvArgs& a, int waves, hipStream_t s) {
-  const size_t lds = ((size_t)a.KB * Blk<T>::QK * 17 / 16 + 16 * R) * sizeof(float);
+  const size_t lds = ((size_t)a.KB * Blk<T>::QK * 17 / 16 + 16 * R + 16) * sizeof(float);
   const unsigned grid = (unsigned)((a.groups + 7) / 8 * 8);
   if (waves == 16) {
     hipLaunchKernelGGL((gemv_rows_kernel<T, R, 16>), dim3(grid), dim3(1024), lds, s, a);
@@ -273,7 +334,7 @@ static hipError_t launch_gemv_t(const GemvArgs& a, int waves, hipStream_t s) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || a.splits == 1) return e;
   hipLaunchKernelGGL(gemv_reduce_kernel, dim3((unsigned)((a.m + 255) / 256)), dim3(256), 0, s, a.partial, a.y,
-                     a.m, a.m_pad, a.splits, a.add);
+                     a.m, a.m_pad, a.splits, a.add, a.best);
   return hipGetLastError();
 }
 

@@ -17,7 +17,39 @@ struct GemvArgs {
   int rows_per_group;           // row-group launch: 64, 16, 8 or 4 rows per workgroup; 0 = split launch
   int groups;                   // row-group launch: tiles * 64 / rows_per_group
   const float* add;             // nullptr, or y[r] = (W x)[r] + add[r] (add may equal y)
+  const float* norm_w;          // nullptr, or x is RMS-normalised first: x * (1/sqrt(mean(x^2)+eps)) * norm_w
+  float norm_eps;
+  unsigned long long* best;     // nullptr, or kArgmaxSlots slots max-folded with argmax_key(y[r], r)
 };
+
+constexpr int kArgmaxSlots = 8;
+
+// Fold one argmax_key per lane of a wave into best[kArgmaxSlots]: the wave's maximum goes to
+// slot blockIdx.x % kArgmaxSlots (the workgroup's XCD under the 1-D grid mapping), and only when
+// it beats the slot's current value (a relaxed read first: slots only grow, so a stale read can
+// only let a needless atomic through). Spreading and filtering keep thousands of workgroups from
+// serialising on one address.
+__device__ __forceinline__ void wave_argmax_fold(unsigned long long key, unsigned long long* best) {
+  unsigned hi = (unsigned)(key >> 32), lo = (unsigned)key;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const unsigned ohi = __shfl_xor(hi, off, 64), olo = __shfl_xor(lo, off, 64);
+    if (ohi > hi || (ohi == hi && olo > lo)) { hi = ohi; lo = olo; }
+  }
+  const unsigned long long k = ((unsigned long long)hi << 32) | lo;
+  unsigned long long* slot = best + (blockIdx.x % kArgmaxSlots);
+  if ((threadIdx.x & 63) == 0 && k > __hip_atomic_load(slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+    atomicMax(slot, k);
+}
+
+
+// Order-preserving key of (value, index): the largest value wins and, among equal values, the
+// largest index (the last maximum, as Iterator::max_by). -0 counts as +0; 0 is below every key.
+__device__ __forceinline__ unsigned long long argmax_key(float v, int i) {
+  unsigned b = __float_as_uint(v == 0.0f ? 0.0f : v);
+  b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  return ((unsigned long long)b << 32) | (unsigned)i;
+}
 
 // longest row (elements) a GEMV workgroup stages in LDS: x, its per-16 sums and the wave
 // partials stay under 64 KiB of dynamic LDS
@@ -90,6 +122,8 @@ struct MoeGemvArgs {
   const MoeGemvTask* tasks;
   int m, K, KB, ldy;          // weight rows and row length (per expert)
   int max_rows;               // largest np over the tasks
+  const float* norm_w;        // nullptr, or each X row is RMS-normalised first (as GemvArgs)
+  float norm_eps;
 };
 constexpr int kMoeGemvRows = 16;   // weight rows per task
 constexpr int kMoeGemvWaves = 4;
@@ -102,8 +136,18 @@ hipError_t launch_rmsnorm(const float* x, const float* w, int rows, int d, float
 hipError_t launch_rope(float* x, int rows, int heads, int hd, float base, const int* pos, int off, hipStream_t s);
 hipError_t launch_kv_append(const float* k, const float* v, int rows, int kv_dim, float* kc, float* vc,
                             int max_seq, const int* pos, hipStream_t s);
+// work: nullptr, or attention_work_floats(...) floats for the key-split path of few rows
+size_t attention_work_floats(int rows, int heads, int hd, int max_seq);
 hipError_t launch_attention(const float* q, const float* kc, const float* vc, int rows, int heads, int kv_heads,
-                            int hd, int max_seq, const int* pos, float* ctx, hipStream_t s);
+                            int hd, int max_seq, const int* pos, float* work, float* ctx, hipStream_t s);
+// q/k/v projections (+ bias) -> rotated q (rows x heads*hd), rotated k and v appended at cache rows *pos + r
+hipError_t launch_qkv_rope_append(const float* qs, int ldq, const float* ks, int ldk, const float* vs, int ldv,
+                                  const float* bq, const float* bk, const float* bv, int rows, int heads,
+                                  int kv_heads, int hd, float base, const int* pos, float* qout, float* kc,
+                                  float* vc, int max_seq, hipStream_t s);
+// *tok = index of *best; *pos += delta; hist[*pos] = *tok (hist may be null); *best = 0
+hipError_t launch_decode_advance(unsigned long long* best, int* tok, int* pos, int delta, int* hist, int hist_len,
+                                 hipStream_t s);
 hipError_t launch_add(const float* a, const float* b, size_t n, size_t nb, float* out, hipStream_t s);
 hipError_t launch_argmax(const float* x, int n, int* idx, hipStream_t s);
 hipError_t launch_embed(const float* table, int n_vocab, int d, const int* tok, int rows, float* out, hipStream_t s);

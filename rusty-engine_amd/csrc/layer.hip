@@ -4,6 +4,8 @@
 // Positions come from a device integer so that one captured graph serves every decode step.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
 #include "kernels.hpp"
 
 namespace rehip {
@@ -71,59 +73,561 @@ __global__ __launch_bounds__(256) void kv_append_kernel(const float* __restrict_
   }
 }
 
-// Causal GQA attention for one (query head, query row) per workgroup (forward.rs:232-277):
-// scores q.k * (1/sqrt(hd)) over keys 0..p (p = *pos + r), softmax as moe.rs:61-72 (exp of
+// Causal GQA attention (forward.rs:232-277, 437-470): query row r at position p = *pos + r
+// attends to cache rows 0..p with scores q.k * (1/sqrt(hd)), softmax as moe.rs:61-72 (exp of
 // x - max, divided by the sum when it is non-zero), then the probability-weighted values.
-__global__ __launch_bounds__(256) void attention_kernel(const float* __restrict__ q, const float* __restrict__ kc,
-                                                        const float* __restrict__ vc, int heads, int kv_heads,
-                                                        int hd, int max_seq, const int* __restrict__ pos,
-                                                        float* __restrict__ ctx) {
-  extern __shared__ float sc[];          // scores[max_seq], then 4 x hd partial sums
-  __shared__ float red[4];
-  __shared__ float qs[256];
+// Cache rows past the last visible one are never read (loads clamp to it), so rows of the cache
+// that were never written do not enter the result.
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// Few rows (decode), or head sizes other than 64: one 1024-thread workgroup per (query head,
+// row). A team of 16 lanes owns one key (a float4 of dimensions per lane and 64-dimension slot,
+// NC slots); the 64 teams cover 64 * U keys per pass with all U * NC loads of a lane in flight.
+// Scores go to LDS (max_seq floats); the p * v pass uses the same teams, and the 16 waves'
+// partials are folded in a fixed order.
+constexpr int kAttnRowsThreads = 1024;
+
+template <int NC>
+__global__ __launch_bounds__(kAttnRowsThreads) void attention_rows_kernel(
+    const float* __restrict__ q, const float* __restrict__ kc, const float* __restrict__ vc, int heads, int kv_heads,
+    int hd, int max_seq, const int* __restrict__ pos, float* __restrict__ ctx) {
+  constexpr int U = 16 / NC;             // keys per team per pass
+  extern __shared__ __attribute__((aligned(16))) float sc[];   // scores[(max_seq + 3) & ~3], 16 x hd partials
+  __shared__ float red[16];
   const int h = blockIdx.x, r = blockIdx.y;
-  const int kvh = h * kv_heads / heads;
+  const int kvh = h / (heads / kv_heads);
   const int kv_dim = kv_heads * hd;
   const int L = min(max(*pos + r + 1, 1), max_seq);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int team = 4 * w + (lane >> 4), tl = lane & 15;
   const float* qh = q + ((size_t)r * heads + h) * hd;
-  for (int i = threadIdx.x; i < hd; i += 256) qs[i] = qh[i];
-  __syncthreads();
-  const float scale = 1.0f / sqrtf((float)hd);
-  float mx = -INFINITY;
-  for (int j = threadIdx.x; j < L; j += 256) {
-    const float* kr = kc + (size_t)j * kv_dim + (size_t)kvh * hd;
-    float s = 0.0f;
-    for (int d = 0; d < hd; d += 4) {
-      const float4 kv = *reinterpret_cast<const float4*>(kr + d);
-      s = __builtin_fmaf(qs[d], kv.x, s);
-      s = __builtin_fmaf(qs[d + 1], kv.y, s);
-      s = __builtin_fmaf(qs[d + 2], kv.z, s);
-      s = __builtin_fmaf(qs[d + 3], kv.w, s);
-    }
-    s *= scale;
-    sc[j] = s;
-    mx = fmaxf(mx, s);
+  float4 qv[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int d = 4 * tl + 64 * c;
+    qv[c] = d < hd ? *reinterpret_cast<const float4*>(qh + d) : make_float4(0.f, 0.f, 0.f, 0.f);
   }
-  mx = block_max256(mx, red);
+  const float scale = 1.0f / sqrtf((float)hd);
+  const float* kbase = kc + (size_t)kvh * hd;
+  const float* vbase = vc + (size_t)kvh * hd;
+  float mx = -INFINITY;
+  for (int base = 0; base < L; base += 64 * U) {
+    float4 kv[U][NC];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const float* kr = kbase + (size_t)min(base + 64 * u + team, L - 1) * kv_dim;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const int d = 4 * tl + 64 * c;
+        kv[u][c] = d < hd ? *reinterpret_cast<const float4*>(kr + d) : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      float a = 0.0f;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        a = __builtin_fmaf(qv[c].x, kv[u][c].x, a);
+        a = __builtin_fmaf(qv[c].y, kv[u][c].y, a);
+        a = __builtin_fmaf(qv[c].z, kv[u][c].z, a);
+        a = __builtin_fmaf(qv[c].w, kv[u][c].w, a);
+      }
+#pragma unroll
+      for (int off = 8; off > 0; off >>= 1) a += __shfl_xor(a, off, 64);
+      const int j = base + 64 * u + team;
+      if (tl == 0 && j < L) {
+        const float v = a * scale;
+        sc[j] = v;
+        mx = fmaxf(mx, v);
+      }
+    }
+  }
+  mx = wave_max(mx);
+  __syncthreads();
+  if (lane == 0) red[w] = mx;
+  __syncthreads();
+  mx = red[0];
+#pragma unroll
+  for (int i = 1; i < 16; ++i) mx = fmaxf(mx, red[i]);
   float sum = 0.0f;
-  for (int j = threadIdx.x; j < L; j += 256) {
+  for (int j = threadIdx.x; j < L; j += kAttnRowsThreads) {
     const float e = expf(sc[j] - mx);
     sc[j] = e;
     sum += e;
   }
-  sum = block_sum256(sum, red);
+  sum = wave_sum(sum);
+  __syncthreads();
+  if (lane == 0) red[w] = sum;
+  __syncthreads();
+  sum = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) sum += red[i];
   const float inv = sum != 0.0f ? 1.0f / sum : 1.0f;
-  // values: thread (g, d) sums keys j = g (mod 4) for dimension d; groups folded in order
-  float* part = sc + ((L + 3) & ~3);
-  const int g = threadIdx.x / 64, dd = threadIdx.x & 63;
-  for (int d = dd; d < hd; d += 64) {
-    float acc = 0.0f;
-    for (int j = g; j < L; j += 4) acc = __builtin_fmaf(sc[j] * inv, vc[(size_t)j * kv_dim + (size_t)kvh * hd + d], acc);
-    part[g * hd + d] = acc;
+  float4 acc[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) acc[c] = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int base = 0; base < L; base += 64 * U) {
+    float4 vv[U][NC];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const float* vr = vbase + (size_t)min(base + 64 * u + team, L - 1) * kv_dim;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const int d = 4 * tl + 64 * c;
+        vv[u][c] = d < hd ? *reinterpret_cast<const float4*>(vr + d) : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int j = base + 64 * u + team;
+      const float p = j < L ? sc[j] * inv : 0.0f;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        acc[c].x = __builtin_fmaf(p, vv[u][c].x, acc[c].x);
+        acc[c].y = __builtin_fmaf(p, vv[u][c].y, acc[c].y);
+        acc[c].z = __builtin_fmaf(p, vv[u][c].z, acc[c].z);
+        acc[c].w = __builtin_fmaf(p, vv[u][c].w, acc[c].w);
+      }
+    }
+  }
+  // fold the four teams of the wave (fixed xor tree), then the 16 waves in order
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+#pragma unroll
+    for (int off = 16; off < 64; off <<= 1) {
+      acc[c].x += __shfl_xor(acc[c].x, off, 64);
+      acc[c].y += __shfl_xor(acc[c].y, off, 64);
+      acc[c].z += __shfl_xor(acc[c].z, off, 64);
+      acc[c].w += __shfl_xor(acc[c].w, off, 64);
+    }
+  }
+  float* part = sc + ((max_seq + 3) & ~3);
+  if ((lane >> 4) == 0) {
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int d = 4 * tl + 64 * c;
+      if (d < hd) *reinterpret_cast<float4*>(part + w * hd + d) = acc[c];
+    }
   }
   __syncthreads();
   float* out = ctx + ((size_t)r * heads + h) * hd;
-  for (int d = threadIdx.x; d < hd; d += 256) out[d] = ((part[d] + part[hd + d]) + part[2 * hd + d]) + part[3 * hd + d];
+  for (int d = threadIdx.x; d < hd; d += kAttnRowsThreads) {
+    float o = part[d];
+#pragma unroll
+    for (int i = 1; i < 16; ++i) o += part[i * hd + d];
+    out[d] = o;
+  }
+}
+
+// Few rows with a workspace: the cache is cut into kAttnSplitKeys-key splits, one 256-thread
+// workgroup per (query head, row, split) -- so a decode step spreads over heads * splits CUs
+// instead of heads -- each writing (max m, sum l of exp(s - m), sum of exp(s - m) * v) for its
+// keys; a second kernel combines the splits in split order:
+//   M = max m_s, L = sum l_s exp(m_s - M), out = sum acc_s exp(m_s - M) / L.
+// Splits past the visible keys write m = -inf and are skipped.
+constexpr int kAttnSplitKeys = 128;      // 16 teams x 8 keys
+constexpr int kAttnMaxSplits = 256;      // 32768 cache rows
+
+template <int NC>
+__global__ __launch_bounds__(256) void attention_split_kernel(const float* __restrict__ q, const float* __restrict__ kc,
+                                                              const float* __restrict__ vc, int heads, int kv_heads,
+                                                              int hd, int max_seq, const int* __restrict__ pos,
+                                                              float* __restrict__ work) {
+  constexpr int U = 8;
+  __shared__ float sc[kAttnSplitKeys];
+  __shared__ float red[4];
+  __shared__ __attribute__((aligned(16))) float part[4 * 256];
+  const int h = blockIdx.x, r = blockIdx.y, sp = blockIdx.z, nsp = gridDim.z;
+  const int kvh = h / (heads / kv_heads);
+  const int kv_dim = kv_heads * hd;
+  const int L = min(max(*pos + r + 1, 1), max_seq);
+  const int j0 = sp * kAttnSplitKeys;
+  float* wp = work + (((size_t)r * heads + h) * nsp + sp) * (hd + 2);
+  if (j0 >= L) {                         // nothing visible in this split
+    if (threadIdx.x == 0) { wp[0] = -INFINITY; wp[1] = 0.0f; }
+    return;
+  }
+  const int jn = min(kAttnSplitKeys, L - j0);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int team = 4 * w + (lane >> 4), tl = lane & 15;
+  const float* qh = q + ((size_t)r * heads + h) * hd;
+  float4 qv[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int d = 4 * tl + 64 * c;
+    qv[c] = d < hd ? *reinterpret_cast<const float4*>(qh + d) : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  const float scale = 1.0f / sqrtf((float)hd);
+  const float* kbase = kc + (size_t)kvh * hd;
+  const float* vbase = vc + (size_t)kvh * hd;
+  // keys j0 + 16 u + team, u < U: all loads of K and V issued up front (V lands under the scores)
+  float4 kv[U][NC], vv[U][NC];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const size_t row = (size_t)(j0 + min(16 * u + team, jn - 1)) * kv_dim;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int d = 4 * tl + 64 * c;
+      kv[u][c] = d < hd ? *reinterpret_cast<const float4*>(kbase + row + d) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const size_t row = (size_t)(j0 + min(16 * u + team, jn - 1)) * kv_dim;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int d = 4 * tl + 64 * c;
+      vv[u][c] = d < hd ? *reinterpret_cast<const float4*>(vbase + row + d) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  }
+  float mx = -INFINITY;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    float a = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      a = __builtin_fmaf(qv[c].x, kv[u][c].x, a);
+      a = __builtin_fmaf(qv[c].y, kv[u][c].y, a);
+      a = __builtin_fmaf(qv[c].z, kv[u][c].z, a);
+      a = __builtin_fmaf(qv[c].w, kv[u][c].w, a);
+    }
+#pragma unroll
+    for (int off = 8; off > 0; off >>= 1) a += __shfl_xor(a, off, 64);
+    const int jj = 16 * u + team;
+    if (tl == 0 && jj < jn) {
+      const float v = a * scale;
+      sc[jj] = v;
+      mx = fmaxf(mx, v);
+    }
+  }
+  mx = wave_max(mx);
+  if (lane == 0) red[w] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  float4 acc[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) acc[c] = make_float4(0.f, 0.f, 0.f, 0.f);
+  float lsum = 0.0f;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int jj = 16 * u + team;
+    const float e = jj < jn ? expf(sc[jj] - mx) : 0.0f;
+    lsum += e;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      acc[c].x = __builtin_fmaf(e, vv[u][c].x, acc[c].x);
+      acc[c].y = __builtin_fmaf(e, vv[u][c].y, acc[c].y);
+      acc[c].z = __builtin_fmaf(e, vv[u][c].z, acc[c].z);
+      acc[c].w = __builtin_fmaf(e, vv[u][c].w, acc[c].w);
+    }
+  }
+  // lsum: every lane of a team holds its team's sum; fold teams of the wave, then the waves
+#pragma unroll
+  for (int off = 16; off < 64; off <<= 1) lsum += __shfl_xor(lsum, off, 64);
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+#pragma unroll
+    for (int off = 16; off < 64; off <<= 1) {
+      acc[c].x += __shfl_xor(acc[c].x, off, 64);
+      acc[c].y += __shfl_xor(acc[c].y, off, 64);
+      acc[c].z += __shfl_xor(acc[c].z, off, 64);
+      acc[c].w += __shfl_xor(acc[c].w, off, 64);
+    }
+  }
+  __syncthreads();                       // red[] reused
+  if (lane == 0) red[w] = lsum;
+  if ((lane >> 4) == 0) {
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int d = 4 * tl + 64 * c;
+      if (d < hd) *reinterpret_cast<float4*>(part + w * 256 + d) = acc[c];
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    wp[0] = mx;
+    wp[1] = ((red[0] + red[1]) + red[2]) + red[3];
+  }
+  for (int d = threadIdx.x; d < hd; d += 256)
+    wp[2 + d] = ((part[d] + part[256 + d]) + part[512 + d]) + part[768 + d];
+}
+
+__global__ __launch_bounds__(64) void attention_combine_kernel(const float* __restrict__ work, int heads, int hd,
+                                                               int nsp, float* __restrict__ ctx) {
+  __shared__ float f[kAttnMaxSplits];
+  const int h = blockIdx.x, r = blockIdx.y, t = threadIdx.x;
+  const size_t st = (size_t)hd + 2;
+  const float* wp = work + ((size_t)r * heads + h) * nsp * st;
+  // every split's (m, l) loaded in parallel (lane t: splits t, t + 64, ..)
+  float mv[kAttnMaxSplits / 64], lv[kAttnMaxSplits / 64];
+  float M = -INFINITY;
+  int nvis = 0;                          // splits with visible keys: a prefix (the others wrote
+#pragma unroll                           // only m = -inf and l = 0, no values)
+  for (int k = 0; k < kAttnMaxSplits / 64; ++k) {
+    const int sp = t + 64 * k;
+    mv[k] = sp < nsp ? wp[sp * st] : -INFINITY;
+    lv[k] = sp < nsp ? wp[sp * st + 1] : 0.0f;
+    M = fmaxf(M, mv[k]);
+    if (mv[k] != -INFINITY) nvis = sp + 1;
+  }
+  M = wave_max(M);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) nvis = max(nvis, __shfl_xor(nvis, off, 64));
+  float tot = 0.0f;
+#pragma unroll
+  for (int k = 0; k < kAttnMaxSplits / 64; ++k) {
+    const int sp = t + 64 * k;
+    const float fk = mv[k] == -INFINITY ? 0.0f : expf(mv[k] - M);
+    if (sp < nsp) f[sp] = fk;
+    tot = __builtin_fmaf(lv[k], fk, tot);
+  }
+  tot = wave_sum(tot);
+  __syncthreads();
+  const float inv = tot != 0.0f ? 1.0f / tot : 1.0f;
+  float* out = ctx + ((size_t)r * heads + h) * hd;
+  for (int d = t; d < hd; d += 64) {
+    const float* a = wp + 2 + d;
+    float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;    // four independent chains, folded in order
+    int sp = 0;
+    for (; sp + 4 <= nvis; sp += 4) {
+      s0 = __builtin_fmaf(a[sp * st], f[sp], s0);
+      s1 = __builtin_fmaf(a[(sp + 1) * st], f[sp + 1], s1);
+      s2 = __builtin_fmaf(a[(sp + 2) * st], f[sp + 2], s2);
+      s3 = __builtin_fmaf(a[(sp + 3) * st], f[sp + 3], s3);
+    }
+    for (; sp < nvis; ++sp) s0 = __builtin_fmaf(a[sp * st], f[sp], s0);
+    out[d] = (((s0 + s1) + s2) + s3) * inv;
+  }
+}
+
+size_t attention_work_floats(int rows, int heads, int hd, int max_seq) {
+  const size_t nsp = ((size_t)max_seq + kAttnSplitKeys - 1) / kAttnSplitKeys;
+  return (size_t)rows * heads * nsp * (hd + 2);
+}
+
+// Many rows, head size 64 (prefill): f32 MFMA flash attention. A workgroup owns 32 query
+// vectors of one kv head (vector g = row * grp + head-in-group, so a block may cut across
+// rows) and its four waves split the cache into 32-key blocks (wave w takes blocks w, w+4, ..).
+// Per key block, in v_mfma_f32_32x32x2_f32 layout with lane l = (half h = l/32, column l%32):
+//   S^T[key][vec] = K Q^T: A = K[key l%32][dim 32h + s], B = Q[vec l%32][dim 32h + s],
+//     s = 0..31; register i of the result is key 8(i/4) + 4h + i%4 of vector l%32;
+//   online softmax per vector (running max m, rescale of earlier terms by exp(m_old - m_new));
+//   O^T[dim][vec] += V^T P^T: step s takes the key held in result register s, so the B operand
+//     is that register and A = V[that key][dim l%32 + 32 nb].
+// The four waves' (m, sum, O) are combined in LDS in wave order. K and V of the next key block
+// are loaded while the current one is in the MFMAs. Row blocks run longest-first.
+constexpr int kAttnMfmaVecs = 32;
+
+__device__ __forceinline__ int attn_key_of(int i, int h) { return 8 * (i >> 2) + 4 * h + (i & 3); }
+
+__global__ __launch_bounds__(256) void attention_mfma_kernel(const float* __restrict__ q, const float* __restrict__ kc,
+                                                             const float* __restrict__ vc, int rows, int heads,
+                                                             int kv_heads, int max_seq, const int* __restrict__ pos,
+                                                             float* __restrict__ ctx) {
+  constexpr int HD = 64;
+  typedef float f32x16 __attribute__((ext_vector_type(16)));
+  __shared__ __attribute__((aligned(16))) float Os[4][kAttnMfmaVecs][HD + 4];
+  __shared__ float Ms[4][kAttnMfmaVecs], Ls[4][kAttnMfmaVecs];
+  const int grp = heads / kv_heads;
+  const int blk = gridDim.x - 1 - blockIdx.x, kvh = blockIdx.y;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int vl = lane & 31, h = lane >> 5;
+  const int kv_dim = kv_heads * HD;
+  const int p0 = *pos;
+  const int g0 = blk * kAttnMfmaVecs;
+  const int r_last = min((g0 + kAttnMfmaVecs - 1) / grp, rows - 1);
+  const int jmax = min(p0 + r_last, max_seq - 1);
+  const int nkb = jmax / 32 + 1;
+  // this lane's query vector
+  const int g = g0 + vl, r = g / grp, head = kvh * grp + g % grp;
+  const bool valid = r < rows;
+  const int limit = valid ? min(p0 + r, max_seq - 1) : -1;
+  float qb[32];
+  {
+    const float* qr = q + ((size_t)(valid ? r : 0) * heads + (valid ? head : 0)) * HD + 32 * h;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const float4 x = valid ? *reinterpret_cast<const float4*>(qr + 4 * t) : make_float4(0.f, 0.f, 0.f, 0.f);
+      qb[4 * t] = x.x;
+      qb[4 * t + 1] = x.y;
+      qb[4 * t + 2] = x.z;
+      qb[4 * t + 3] = x.w;
+    }
+  }
+  const float scale = 1.0f / sqrtf((float)HD);
+  const float* kb = kc + (size_t)kvh * HD;
+  const float* vb = vc + (size_t)kvh * HD;
+  auto load = [&](int kbi, float (&kd)[32], float (&vd)[2][16]) {
+    const float* kr = kb + (size_t)min(32 * kbi + vl, jmax) * kv_dim + 32 * h;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const float4 x = *reinterpret_cast<const float4*>(kr + 4 * t);
+      kd[4 * t] = x.x;
+      kd[4 * t + 1] = x.y;
+      kd[4 * t + 2] = x.z;
+      kd[4 * t + 3] = x.w;
+    }
+#pragma unroll
+    for (int s = 0; s < 16; ++s) {
+      const float* vr = vb + (size_t)min(32 * kbi + attn_key_of(s, h), jmax) * kv_dim + vl;
+      vd[0][s] = vr[0];
+      vd[1][s] = vr[32];
+    }
+  };
+  float m = -INFINITY, l = 0.0f;
+  f32x16 o0 = {}, o1 = {};
+  auto step = [&](int kbi, const float (&kd)[32], const float (&vd)[2][16]) {
+    f32x16 st = {};
+#pragma unroll
+    for (int s = 0; s < 32; ++s) st = __builtin_amdgcn_mfma_f32_32x32x2f32(kd[s], qb[s], st, 0, 0, 0);
+    float sv[16], mloc = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int j = 32 * kbi + attn_key_of(i, h);
+      sv[i] = j <= limit ? st[i] * scale : -INFINITY;
+      mloc = fmaxf(mloc, sv[i]);
+    }
+    const float mn = fmaxf(m, fmaxf(mloc, __shfl_xor(mloc, 32, 64)));
+    float pv[16];
+    if (mn == -INFINITY) {               // nothing visible yet for this vector
+#pragma unroll
+      for (int i = 0; i < 16; ++i) pv[i] = 0.0f;
+    } else {
+      const float alpha = expf(m - mn);  // m = -inf gives 0
+      float ps = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        pv[i] = expf(sv[i] - mn);
+        ps += pv[i];
+      }
+      l = __builtin_fmaf(l, alpha, ps);
+      o0 *= alpha;
+      o1 *= alpha;
+      m = mn;
+    }
+#pragma unroll
+    for (int s = 0; s < 16; ++s) {
+      o0 = __builtin_amdgcn_mfma_f32_32x32x2f32(vd[0][s], pv[s], o0, 0, 0, 0);
+      o1 = __builtin_amdgcn_mfma_f32_32x32x2f32(vd[1][s], pv[s], o1, 0, 0, 0);
+    }
+  };
+  // two register sets, alternating by hand (a runtime index into them would go to scratch)
+  float kA[32], vA[2][16], kB[32], vB[2][16];
+  if (w < nkb) load(w, kA, vA);
+  for (int kbi = w; kbi < nkb; kbi += 8) {
+    if (kbi + 4 < nkb) load(kbi + 4, kB, vB);
+    step(kbi, kA, vA);
+    if (kbi + 4 >= nkb) break;
+    if (kbi + 8 < nkb) load(kbi + 8, kA, vA);
+    step(kbi + 4, kB, vB);
+  }
+  // wave partials: O^T register i of block nb is dim 32 nb + 8(i/4) + 4h + i%4 of vector vl
+  l += __shfl_xor(l, 32, 64);
+#pragma unroll
+  for (int i = 0; i < 16; i += 4) {
+    const int d = attn_key_of(i, h);
+    *reinterpret_cast<float4*>(&Os[w][vl][d]) = make_float4(o0[i], o0[i + 1], o0[i + 2], o0[i + 3]);
+    *reinterpret_cast<float4*>(&Os[w][vl][32 + d]) = make_float4(o1[i], o1[i + 1], o1[i + 2], o1[i + 3]);
+  }
+  if (h == 0) {
+    Ms[w][vl] = m;
+    Ls[w][vl] = l;
+  }
+  __syncthreads();
+  // combine: thread t -> vector t / 8, dims 8 (t % 8) .. + 7
+  const int v = threadIdx.x >> 3, d0 = 8 * (threadIdx.x & 7);
+  const int gv = g0 + v, rv = gv / grp;
+  if (rv >= rows) return;
+  float M = Ms[0][v];
+#pragma unroll
+  for (int k = 1; k < 4; ++k) M = fmaxf(M, Ms[k][v]);
+  if (M == -INFINITY) return;            // unreachable for a valid vector (key 0 is visible)
+  float f[4], tot = 0.0f;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    f[k] = Ms[k][v] == -INFINITY ? 0.0f : expf(Ms[k][v] - M);
+    tot = __builtin_fmaf(Ls[k][v], f[k], tot);
+  }
+  const float inv = tot != 0.0f ? 1.0f / tot : 1.0f;
+  float outv[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    float a = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) a = __builtin_fmaf(Os[k][v][d0 + e], f[k], a);
+    outv[e] = a * inv;
+  }
+  float* out = ctx + ((size_t)rv * heads + kvh * grp + gv % grp) * HD + d0;
+  *reinterpret_cast<float4*>(out) = make_float4(outv[0], outv[1], outv[2], outv[3]);
+  *reinterpret_cast<float4*>(out + 4) = make_float4(outv[4], outv[5], outv[6], outv[7]);
+}
+
+// q/k/v projection rows (strided; q|k|v may be one fused projection) plus their biases ->
+// rotated q rows (rows x heads x hd, contiguous), rotated k and v appended at cache rows
+// *pos + r (forward.rs:347-363, 437-449). One workgroup per (head of q then k, row); the k
+// workgroups also copy v. Rows landing at or past max_seq are not stored.
+__global__ __launch_bounds__(64) void qkv_rope_append_kernel(const float* __restrict__ qs, int ldq,
+                                                             const float* __restrict__ ks, int ldk,
+                                                             const float* __restrict__ vs, int ldv,
+                                                             const float* __restrict__ bq, const float* __restrict__ bk,
+                                                             const float* __restrict__ bv, int heads, int kv_heads,
+                                                             int hd, float base, const int* __restrict__ pos,
+                                                             float* __restrict__ qout, float* __restrict__ kc,
+                                                             float* __restrict__ vc, int max_seq) {
+  const int hh = blockIdx.x, r = blockIdx.y;
+  const int half = hd >> 1;
+  const int p = *pos + r;
+  const bool is_q = hh < heads;
+  const int kh = hh - heads;
+  if (!is_q && (p < 0 || p >= max_seq)) return;
+  const float* src = is_q ? qs + (size_t)r * ldq + (size_t)hh * hd : ks + (size_t)r * ldk + (size_t)kh * hd;
+  const float* bias = is_q ? (bq ? bq + (size_t)hh * hd : nullptr) : (bk ? bk + (size_t)kh * hd : nullptr);
+  float* dst = is_q ? qout + ((size_t)r * heads + hh) * hd : kc + (size_t)p * kv_heads * hd + (size_t)kh * hd;
+  for (int i = threadIdx.x; i < half; i += 64) {
+    const float f = 1.0f / powf(base, (float)(2 * i) / (float)hd);
+    const float a = (float)p * f;
+    const float c = cosf(a), sn = sinf(a);
+    float x0 = src[i], x1 = src[i + half];
+    if (bias) {
+      x0 += bias[i];
+      x1 += bias[i + half];
+    }
+    dst[i] = x0 * c - x1 * sn;
+    dst[i + half] = x1 * c + x0 * sn;
+  }
+  if (!is_q) {
+    const float* vsrc = vs + (size_t)r * ldv + (size_t)kh * hd;
+    float* vdst = vc + (size_t)p * kv_heads * hd + (size_t)kh * hd;
+    for (int i = threadIdx.x; i < hd; i += 64) vdst[i] = bv ? vsrc[i] + bv[kh * hd + i] : vsrc[i];
+  }
+}
+
+// End of a decode step: the token is the index in the largest of the argmax slots (see
+// argmax_key), the position advances, the token is recorded at its position in hist (when
+// given) and the slots are cleared.
+__global__ void decode_advance_kernel(unsigned long long* best, int* tok, int* pos, int delta, int* hist,
+                                      int hist_len) {
+  if (threadIdx.x != 0) return;
+  unsigned long long k = best[0];
+#pragma unroll
+  for (int i = 1; i < kArgmaxSlots; ++i) k = best[i] > k ? best[i] : k;
+  const int t = (int)(unsigned)(k & 0xffffffffull);
+  const int np = *pos + delta;
+  *tok = t;
+  *pos = np;
+  if (hist && np >= 0 && np < hist_len) hist[np] = t;
+#pragma unroll
+  for (int i = 0; i < kArgmaxSlots; ++i) best[i] = 0ull;
 }
 
 // out[i] = a[i] + b[i % nb]
@@ -188,10 +692,43 @@ hipError_t launch_kv_append(const float* k, const float* v, int rows, int kv_dim
   return hipGetLastError();
 }
 hipError_t launch_attention(const float* q, const float* kc, const float* vc, int rows, int heads, int kv_heads,
-                            int hd, int max_seq, const int* pos, float* ctx, hipStream_t s) {
-  const size_t lds = ((size_t)((max_seq + 3) & ~3) + 4 * (size_t)hd) * sizeof(float);
-  hipLaunchKernelGGL(attention_kernel, dim3((unsigned)heads, (unsigned)rows), dim3(256), lds, s, q, kc, vc, heads,
-                     kv_heads, hd, max_seq, pos, ctx);
+                            int hd, int max_seq, const int* pos, float* work, float* ctx, hipStream_t s) {
+  if (rows >= 8 && hd == 64) {
+    const int grp = heads / kv_heads;
+    const dim3 grid((unsigned)(((size_t)rows * grp + kAttnMfmaVecs - 1) / kAttnMfmaVecs), (unsigned)kv_heads);
+    hipLaunchKernelGGL(attention_mfma_kernel, grid, dim3(256), 0, s, q, kc, vc, rows, heads, kv_heads, max_seq, pos,
+                       ctx);
+    return hipGetLastError();
+  }
+  if (work) {
+    const int nsp = (max_seq + kAttnSplitKeys - 1) / kAttnSplitKeys;
+    const dim3 grid((unsigned)heads, (unsigned)rows, (unsigned)nsp);
+    if (hd <= 64)
+      hipLaunchKernelGGL(attention_split_kernel<1>, grid, dim3(256), 0, s, q, kc, vc, heads, kv_heads, hd, max_seq,
+                         pos, work);
+    else if (hd <= 128)
+      hipLaunchKernelGGL(attention_split_kernel<2>, grid, dim3(256), 0, s, q, kc, vc, heads, kv_heads, hd, max_seq,
+                         pos, work);
+    else
+      hipLaunchKernelGGL(attention_split_kernel<4>, grid, dim3(256), 0, s, q, kc, vc, heads, kv_heads, hd, max_seq,
+                         pos, work);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(attention_combine_kernel, dim3((unsigned)heads, (unsigned)rows), dim3(64), 0, s, work, heads,
+                       hd, nsp, ctx);
+    return hipGetLastError();
+  }
+  const size_t lds = ((size_t)((max_seq + 3) & ~3) + 16 * (size_t)hd) * sizeof(float);
+  const dim3 grid((unsigned)heads, (unsigned)rows);
+  if (hd <= 64)
+    hipLaunchKernelGGL(attention_rows_kernel<1>, grid, dim3(kAttnRowsThreads), lds, s, q, kc, vc, heads, kv_heads, hd,
+                       max_seq, pos, ctx);
+  else if (hd <= 128)
+    hipLaunchKernelGGL(attention_rows_kernel<2>, grid, dim3(kAttnRowsThreads), lds, s, q, kc, vc, heads, kv_heads, hd,
+                       max_seq, pos, ctx);
+  else
+    hipLaunchKernelGGL(attention_rows_kernel<4>, grid, dim3(kAttnRowsThreads), lds, s, q, kc, vc, heads, kv_heads, hd,
+                       max_seq, pos, ctx);
   return hipGetLastError();
 }
 hipError_t launch_add(const float* a, const float* b, size_t n, size_t nb, float* out, hipStream_t s) {
@@ -206,6 +743,19 @@ hipError_t launch_argmax(const float* x, int n, int* idx, hipStream_t s) {
 hipError_t launch_embed(const float* table, int n_vocab, int d, const int* tok, int rows, float* out,
                         hipStream_t s) {
   hipLaunchKernelGGL(embed_kernel, dim3((unsigned)rows), dim3(256), 0, s, table, n_vocab, d, tok, out);
+  return hipGetLastError();
+}
+hipError_t launch_qkv_rope_append(const float* qs, int ldq, const float* ks, int ldk, const float* vs, int ldv,
+                                  const float* bq, const float* bk, const float* bv, int rows, int heads,
+                                  int kv_heads, int hd, float base, const int* pos, float* qout, float* kc,
+                                  float* vc, int max_seq, hipStream_t s) {
+  hipLaunchKernelGGL(qkv_rope_append_kernel, dim3((unsigned)(heads + kv_heads), (unsigned)rows), dim3(64), 0, s, qs,
+                     ldq, ks, ldk, vs, ldv, bq, bk, bv, heads, kv_heads, hd, base, pos, qout, kc, vc, max_seq);
+  return hipGetLastError();
+}
+hipError_t launch_decode_advance(unsigned long long* best, int* tok, int* pos, int delta, int* hist, int hist_len,
+                                 hipStream_t s) {
+  hipLaunchKernelGGL(decode_advance_kernel, dim3(1), dim3(64), 0, s, best, tok, pos, delta, hist, hist_len);
   return hipGetLastError();
 }
 hipError_t launch_pos_add(int* pos, int delta, hipStream_t s) {

@@ -76,6 +76,7 @@ __global__ __launch_bounds__(WAVES * 64) void moe_gemv_kernel(MoeGemvArgs a) {
   float* xl = smem;                      // [NB][KP]
   float* xs16 = smem + NB * KP;          // [NB][KP/16]
   float* red = xs16 + NB * (KP / 16);    // [WAVES][NM][NB][R]
+  float* ssred = red + WAVES * NM * NB * R;   // [WAVES][NB]
 
   const int row = task.row0 + (lane % R);          // weight row inside the expert
   const int tile = row >> 6, rr = row & 63;
@@ -95,8 +96,12 @@ __global__ __launch_bounds__(WAVES * 64) void moe_gemv_kernel(MoeGemvArgs a) {
     }
   }
 
-  // stage the task's activation rows (zero past K and past np)
+  // stage the task's activation rows (zero past K and past np); with an RMS-norm, x * w is
+  // staged, each thread keeps its rows' sums of squares, and 1/rms scales the finished dots
   const int nv = KP / 4;
+  float ss[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) ss[nb] = 0.0f;
   for (int i = threadIdx.x; i < NB * nv; i += WAVES * 64) {
     const int nb = i / nv, k = 4 * (i - nb * nv);
     float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -104,6 +109,14 @@ __global__ __launch_bounds__(WAVES * 64) void moe_gemv_kernel(MoeGemvArgs a) {
       const int p = task.p0 + nb;
       const int xr = a.xrow ? a.xrow[p] : p;
       v = *reinterpret_cast<const float4*>(a.X + (size_t)xr * a.K + k);
+      if (a.norm_w) {
+        float t = __builtin_fmaf(v.x, v.x, __builtin_fmaf(v.y, v.y, __builtin_fmaf(v.z, v.z, v.w * v.w)));
+#pragma unroll
+        for (int q = 0; q < NB; ++q)
+          if (q == nb) ss[q] += t;
+        const float4 w = *reinterpret_cast<const float4*>(a.norm_w + k);
+        v = make_float4(v.x * w.x, v.y * w.y, v.z * w.z, v.w * w.w);
+      }
     }
     reinterpret_cast<float4*>(xl)[i] = v;
   }
@@ -162,16 +175,32 @@ __global__ __launch_bounds__(WAVES * 64) void moe_gemv_kernel(MoeGemvArgs a) {
       for (int off = R; off < 64; off *= 2) v += __shfl_xor(v, off, 64);
       if (lane < R) red[((wave * NM + m) * NB + nb) * R + lane] = v;
     }
+  if (a.norm_w) {
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      float t = ss[nb];
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) t += __shfl_xor(t, off, 64);
+      if (lane == 0) ssred[wave * NB + nb] = t;
+    }
+  }
   __syncthreads();
   if ((int)threadIdx.x < R * NB) {
     const int r = threadIdx.x % R, nb = threadIdx.x / R;
+    float inv = 1.0f;
+    if (a.norm_w) {
+      float t = ssred[nb];
+#pragma unroll
+      for (int w = 1; w < WAVES; ++w) t += ssred[w * NB + nb];
+      inv = 1.0f / sqrtf(t / (float)a.K + a.norm_eps);
+    }
     float v[NM];
 #pragma unroll
     for (int m = 0; m < NM; ++m) {
       float sum = red[((0 * NM + m) * NB + nb) * R + r];
 #pragma unroll
       for (int w = 1; w < WAVES; ++w) sum += red[((w * NM + m) * NB + nb) * R + r];
-      v[m] = sum;
+      v[m] = a.norm_w ? sum * inv : sum;
     }
     const int wrow = task.row0 + r;
     if (nb < task.np && wrow < a.m) {
@@ -185,7 +214,7 @@ template <int T, bool DUAL, int NB>
 static hipError_t launch_moe_gemv_nb(const MoeGemvArgs& a, int ntasks, hipStream_t s) {
   constexpr int R = kMoeGemvRows, W = kMoeGemvWaves;
   const int KP = a.KB * Blk<T>::QK;
-  const size_t lds = ((size_t)NB * KP * 17 / 16 + (size_t)W * (DUAL ? 2 : 1) * NB * R) * sizeof(float);
+  const size_t lds = ((size_t)NB * KP * 17 / 16 + (size_t)W * (DUAL ? 2 : 1) * NB * R + (size_t)W * NB) * sizeof(float);
   hipLaunchKernelGGL((moe_gemv_kernel<T, R, W, NB, DUAL>), dim3((unsigned)ntasks), dim3(W * 64), lds, s, a);
   return hipGetLastError();
 }

@@ -35,9 +35,10 @@ EXPORTS = ("re_init", "re_last_error", "re_version", "re_row_bytes", "re_tiled_b
            "re_qmat_create", "re_qmat_destroy", "re_qmat_rows", "re_qmat_cols", "re_qmat_type",
            "re_qmat_matvec", "re_qmat_matmul", "re_qmat_matvec_dev", "re_qmat_matmul_dev",
            "re_qmat_dequant_dev", "re_dequant", "re_moe_create", "re_moe_destroy", "re_moe_forward",
-           "re_moe_forward_dev", "re_qmat_matvec_add_dev", "re_rmsnorm_dev", "re_rope_dev", "re_kv_append_dev",
+           "re_moe_forward_dev", "re_qmat_matvec_ex_dev", "re_rmsnorm_dev", "re_rope_dev", "re_kv_append_dev",
            "re_attention_dev", "re_add_dev", "re_swiglu_dev", "re_argmax_dev", "re_embed_dev", "re_pos_add_dev",
-           "re_ffn_create", "re_ffn_destroy", "re_ffn_forward_dev")
+           "re_ffn_create", "re_ffn_destroy", "re_ffn_forward_dev", "re_attention_work_bytes",
+           "re_qkv_rope_append_dev", "re_decode_advance_dev")
 
 
 class RehipError(RuntimeError):
@@ -85,11 +86,16 @@ def lib() -> C.CDLL:
         L.re_moe_destroy.restype = None
         L.re_moe_forward.argtypes = [_vp, _vp, _sz, _sz, _vp, _vp, _vp, C.c_int]
         L.re_moe_forward_dev.argtypes = [_vp, _vp, _sz, _sz, _vp, _vp, _vp, C.c_int, _vp]
-        L.re_qmat_matvec_add_dev.argtypes = [_vp, _vp, _vp, _vp, _vp]
+        L.re_qmat_matvec_ex_dev.argtypes = [_vp, _vp, _vp, C.c_float, _vp, _vp, _vp, _vp]
         L.re_rmsnorm_dev.argtypes = [_vp, _vp, _sz, _sz, C.c_float, _vp, _vp]
         L.re_rope_dev.argtypes = [_vp, _sz, _sz, _sz, C.c_float, _vp, C.c_int, _vp]
         L.re_kv_append_dev.argtypes = [_vp, _vp, _sz, _sz, _vp, _vp, _sz, _vp, _vp]
-        L.re_attention_dev.argtypes = [_vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _vp, _vp, _vp]
+        L.re_attention_work_bytes.argtypes = [_sz, _sz, _sz, _sz]
+        L.re_attention_work_bytes.restype = _sz
+        L.re_attention_dev.argtypes = [_vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _vp, _vp, _sz, _vp, _vp]
+        L.re_qkv_rope_append_dev.argtypes = [_vp, _sz, _vp, _sz, _vp, _sz, _vp, _vp, _vp, _sz, _sz, _sz, _sz,
+                                             C.c_float, _vp, _vp, _vp, _vp, _sz, _vp]
+        L.re_decode_advance_dev.argtypes = [_vp, _vp, _vp, C.c_int, _vp, _sz, _vp]
         L.re_add_dev.argtypes = [_vp, _vp, _sz, _sz, _vp, _vp]
         L.re_swiglu_dev.argtypes = [_vp, _vp, _vp, _sz, _vp]
         L.re_argmax_dev.argtypes = [_vp, _sz, _vp, _vp]
@@ -98,7 +104,7 @@ def lib() -> C.CDLL:
         L.re_ffn_create.argtypes = [_vp, _vp, C.POINTER(_vp)]
         L.re_ffn_destroy.argtypes = [_vp]
         L.re_ffn_destroy.restype = None
-        L.re_ffn_forward_dev.argtypes = [_vp, _vp, _vp, _vp]
+        L.re_ffn_forward_dev.argtypes = [_vp, _vp, _vp, C.c_float, _vp, _vp]
         _lib = L
     return _lib
 
@@ -207,10 +213,11 @@ class QMat:
     def matvec_dev(self, x_dev, y_dev, stream=None) -> None:
         _check(lib().re_qmat_matvec_dev(self._h, _dev_ptr(x_dev), _dev_ptr(y_dev), _stream_ptr(stream)))
 
-    def matvec_add_dev(self, x_dev, add_dev, y_dev, stream=None) -> None:
-        """y = W x + add (add may be y itself, or None)."""
-        _check(lib().re_qmat_matvec_add_dev(self._h, _dev_ptr(x_dev), _dev_ptr(add_dev) if add_dev is not None else None,
-                                            _dev_ptr(y_dev), _stream_ptr(stream)))
+    def matvec_ex_dev(self, x_dev, y_dev, norm_w=None, eps=0.0, add=None, best=None, stream=None) -> None:
+        """y = W rmsnorm(x) + add; each piece optional (see re_qmat_matvec_ex_dev). `best` folds the
+        greedy argmax of y into a device uint64 (cleared by decode_advance_dev)."""
+        _check(lib().re_qmat_matvec_ex_dev(self._h, _dev_ptr(x_dev), _p(norm_w), eps, _p(add), _dev_ptr(y_dev),
+                                           _p(best), _stream_ptr(stream)))
 
     def matmul_dev(self, x_dev, rows: int, y_dev, mode: int = MODE_BF16, stream=None) -> None:
         _check(lib().re_qmat_matmul_dev(self._h, _dev_ptr(x_dev), rows, _dev_ptr(y_dev), mode,
@@ -249,9 +256,25 @@ def kv_append_dev(k, v, rows, kv_dim, kcache, vcache, max_seq, pos, stream=None)
                                   _stream_ptr(stream)))
 
 
-def attention_dev(q, kcache, vcache, rows, n_heads, n_kv_heads, head_dim, max_seq, pos, ctx, stream=None):
+def attention_work_bytes(rows, n_heads, head_dim, max_seq) -> int:
+    return int(lib().re_attention_work_bytes(rows, n_heads, head_dim, max_seq))
+
+
+def attention_dev(q, kcache, vcache, rows, n_heads, n_kv_heads, head_dim, max_seq, pos, ctx, work=None,
+                  work_bytes=0, stream=None):
     _check(lib().re_attention_dev(_p(q), _p(kcache), _p(vcache), rows, n_heads, n_kv_heads, head_dim, max_seq,
-                                  _p(pos), _p(ctx), _stream_ptr(stream)))
+                                  _p(pos), _p(work), work_bytes, _p(ctx), _stream_ptr(stream)))
+
+
+def qkv_rope_append_dev(q, ldq, k, ldk, v, ldv, bq, bk, bv, rows, n_heads, n_kv_heads, head_dim, theta, pos, qout,
+                        kcache, vcache, max_seq, stream=None):
+    _check(lib().re_qkv_rope_append_dev(_p(q), ldq, _p(k), ldk, _p(v), ldv, _p(bq), _p(bk), _p(bv), rows, n_heads,
+                                        n_kv_heads, head_dim, theta, _p(pos), _p(qout), _p(kcache), _p(vcache),
+                                        max_seq, _stream_ptr(stream)))
+
+
+def decode_advance_dev(best, tok, pos, delta, hist=None, hist_len=0, stream=None):
+    _check(lib().re_decode_advance_dev(_p(best), _p(tok), _p(pos), delta, _p(hist), hist_len, _stream_ptr(stream)))
 
 
 def add_dev(a, b, n, nb, out, stream=None):
@@ -283,8 +306,9 @@ class Ffn:
         self._h = h
         self._keep = (gate, up)
 
-    def forward_dev(self, x_dev, h_dev, stream=None) -> None:
-        _check(lib().re_ffn_forward_dev(self._h, _dev_ptr(x_dev), _dev_ptr(h_dev), _stream_ptr(stream)))
+    def forward_dev(self, x_dev, h_dev, norm_w=None, eps=0.0, stream=None) -> None:
+        _check(lib().re_ffn_forward_dev(self._h, _dev_ptr(x_dev), _p(norm_w), eps, _dev_ptr(h_dev),
+                                        _stream_ptr(stream)))
 
     def close(self) -> None:
         if self._h:

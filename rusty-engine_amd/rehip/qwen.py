@@ -368,18 +368,22 @@ class DenseDecoder:
 
 class DeviceDecoder:
     """The dense decoder with every step on the GPU (row F1 of the hot-path plan): activations,
-    rotated K/V caches, the position and the sampled token stay in HBM. Each projection is a
-    librehip GEMV (decode) or GEMM (prefill); the q/k/v biases and the residual adds are folded
-    into the GEMV stores; gate and up run as one launch with SwiGLU (`Ffn`). A decode step is
-    captured once as a HIP graph (the position and the token are device integers advanced by
-    the graph itself) and replayed per token, so the host only reads back the token id.
+    rotated K/V caches, the position, the sampled token and the token history stay in HBM.
 
-    Same computation as `DenseDecoder` (runner.rs:205-282, forward.rs:347-586); the attention,
-    RMS-norm, RoPE and argmax are librehip kernels instead of host numpy."""
+    Decode step (captured once as a HIP graph, replayed per token; 7 launches per layer):
+      q|k|v GEMV over one fused q|k|v matrix with the attention RMS-norm in its prologue ->
+      bias + RoPE + K/V-cache append -> key-split attention + combine -> o GEMV with the
+      residual add -> gate/up GEMV pair with the FFN RMS-norm and SwiGLU -> down GEMV with the
+      residual add; then the lm_head GEMV with the output norm and the greedy argmax folded into
+      its stores, and one kernel that takes the token, advances the position and records the
+      token. The host reads back 4 bytes per token (`step`) or nothing until the end (`replay`).
+    Prefill (eager): the same with GEMMs over all prompt rows and MFMA flash attention.
+
+    Same computation as `DenseDecoder` (runner.rs:205-282, forward.rs:347-586)."""
 
     def __init__(self, mb: ModelBytes, max_seq: int, mode: int = MODE_F32, prefill_rows: int = 1024,
                  use_graph: bool = True):
-        from . import Ffn, hip
+        from . import Ffn, attention_work_bytes, hip
         self.mb, self.mode, self.max_seq = mb, mode, max_seq
         self.use_graph = use_graph
         g = self.g = mb.geom
@@ -390,82 +394,85 @@ class DeviceDecoder:
         B = hip.DeviceBuffer
         self.blocks = []
         for b in mb.blocks:
-            q = QMat.from_bytes(mb.attn_type, b.q, d, d)
-            k = QMat.from_bytes(mb.attn_type, b.k, kv, d)
-            v = QMat.from_bytes(mb.attn_type, b.v, kv, d)
-            o = QMat.from_bytes(mb.attn_type, b.o, d, d)
-            gate = QMat.from_bytes(mb.ffn_type, b.gate, g.d_ff, d)
-            up = QMat.from_bytes(mb.ffn_type, b.up, g.d_ff, d)
-            down = QMat.from_bytes(mb.down_type, b.down, d, g.d_ff)
-            self.blocks.append(dict(
-                q=q, k=k, v=v, o=o, gate=gate, up=up, down=down,
-                ffn=Ffn(gate, up),
+            blk = dict(
+                o=QMat.from_bytes(mb.attn_type, b.o, d, d),
+                gate=QMat.from_bytes(mb.ffn_type, b.gate, g.d_ff, d),
+                up=QMat.from_bytes(mb.ffn_type, b.up, g.d_ff, d),
+                down=QMat.from_bytes(mb.down_type, b.down, d, g.d_ff),
                 attn_norm=B.from_array(b.attn_norm), ffn_norm=B.from_array(b.ffn_norm),
                 q_bias=B.from_array(b.q_bias), k_bias=B.from_array(b.k_bias), v_bias=B.from_array(b.v_bias),
-                kc=B(max_seq * kv * 4), vc=B(max_seq * kv * 4)))
+                kc=B(max_seq * kv * 4), vc=B(max_seq * kv * 4))
+            # q, k and v share their input: one fused matrix (rows q | k | v) when they share a type
+            blk["qkv"] = QMat.from_bytes(mb.attn_type, np.concatenate([b.q, b.k, b.v]), d + 2 * kv, d)
+            blk["ffn"] = Ffn(blk["gate"], blk["up"])
+            self.blocks.append(blk)
         self.output = QMat.from_bytes(mb.embed_type, mb.output, mb.n_vocab, d)
         self.output_norm = B.from_array(mb.output_norm)
         self.embed = B.from_array(dequant(mb.embed_type, mb.embed))
         cap = self.cap
         self.x = B(cap * d * 4)
         self.n = B(cap * d * 4)
+        self.qkv = B(cap * (d + 2 * kv) * 4)
         self.qb = B(cap * d * 4)
-        self.kb = B(cap * kv * 4)
-        self.vb = B(cap * kv * 4)
         self.ctx = B(cap * d * 4)
-        self.ob = B(cap * d * 4)
+        self.ob = B(cap * g.d_ff * 4)       # o / down outputs of the prefill
         self.gb = B(cap * g.d_ff * 4)
         self.ub = B(cap * g.d_ff * 4)
         self.hb = B(cap * g.d_ff * 4)
-        self.db = B(cap * d * 4)
         self.logits_buf = B(mb.n_vocab * 4)
+        self.work_bytes = attention_work_bytes(8, g.n_heads, hd, max_seq)
+        self.work = B(self.work_bytes)
         self.pos = B.from_array(np.zeros(1, np.int32))
         self.tok = B.from_array(np.zeros(1, np.int32))
+        self.best = B.from_array(np.zeros(8, np.uint64))         # RE_ARGMAX_SLOTS
+        self.hist = B.from_array(np.zeros(max_seq, np.int32))
         self.toks = B(cap * 4)
         self.stream = hip.Stream()
         self.graph = None
         self.seq_len = 0
 
-    # -- helpers ---------------------------------------------------------------------------
-    def _norm(self, src, w, rows, dst):
-        from . import rmsnorm_dev
-        rmsnorm_dev(src, w, rows, self.g.d_model, self.g.rms_eps, dst, self.stream)
+    # -- pieces ----------------------------------------------------------------------------
+    def _qkv_post(self, blk, rows):
+        from . import qkv_rope_append_dev
+        g, d, kv = self.g, self.g.d_model, self.kv
+        ld = d + 2 * kv
+        qkv_rope_append_dev(self.qkv, ld, _Offset(self.qkv, 4 * d), ld, _Offset(self.qkv, 4 * (d + kv)), ld,
+                            blk["q_bias"], blk["k_bias"], blk["v_bias"], rows, g.n_heads, g.n_kv_heads, g.head_dim,
+                            g.rope_freq_base, self.pos, self.qb, blk["kc"], blk["vc"], self.max_seq, self.stream)
 
-    def _logits_and_token(self, last_row_src):
-        from . import argmax_dev
-        self._norm(last_row_src, self.output_norm, 1, self.n)
-        self.output.matvec_dev(self.n, self.logits_buf, stream=self.stream)
-        argmax_dev(self.logits_buf, self.mb.n_vocab, self.tok, self.stream)
+    def _attention(self, blk, rows):
+        from . import attention_dev
+        g = self.g
+        attention_dev(self.qb, blk["kc"], blk["vc"], rows, g.n_heads, g.n_kv_heads, g.head_dim, self.max_seq,
+                      self.pos, self.ctx, work=self.work if rows < 8 else None,
+                      work_bytes=self.work_bytes if rows < 8 else 0, stream=self.stream)
+
+    def _head_and_advance(self, last_row, delta):
+        from . import decode_advance_dev
+        self.output.matvec_ex_dev(last_row, self.logits_buf, norm_w=self.output_norm, eps=self.g.rms_eps,
+                                  best=self.best, stream=self.stream)
+        decode_advance_dev(self.best, self.tok, self.pos, delta, self.hist, self.max_seq, self.stream)
 
     def _step_body(self):
         """One decode position: token *tok at position *pos -> next token in *tok, *pos + 1."""
-        from . import attention_dev, embed_dev, kv_append_dev, pos_add_dev, rope_dev
-        g, s = self.g, self.stream
-        d, hd = g.d_model, g.head_dim
-        embed_dev(self.embed, self.mb.n_vocab, d, self.tok, 1, self.x, s)
+        from . import embed_dev
+        g, s, eps = self.g, self.stream, self.g.rms_eps
+        embed_dev(self.embed, self.mb.n_vocab, g.d_model, self.tok, 1, self.x, s)
         for blk in self.blocks:
-            self._norm(self.x, blk["attn_norm"], 1, self.n)
-            blk["q"].matvec_add_dev(self.n, blk["q_bias"], self.qb, stream=s)
-            blk["k"].matvec_add_dev(self.n, blk["k_bias"], self.kb, stream=s)
-            blk["v"].matvec_add_dev(self.n, blk["v_bias"], self.vb, stream=s)
-            rope_dev(self.qb, 1, g.n_heads, hd, g.rope_freq_base, self.pos, 0, s)
-            rope_dev(self.kb, 1, g.n_kv_heads, hd, g.rope_freq_base, self.pos, 0, s)
-            kv_append_dev(self.kb, self.vb, 1, self.kv, blk["kc"], blk["vc"], self.max_seq, self.pos, s)
-            attention_dev(self.qb, blk["kc"], blk["vc"], 1, g.n_heads, g.n_kv_heads, hd, self.max_seq, self.pos,
-                          self.ctx, s)
-            blk["o"].matvec_add_dev(self.ctx, self.x, self.x, stream=s)          # residual
-            self._norm(self.x, blk["ffn_norm"], 1, self.n)
-            blk["ffn"].forward_dev(self.n, self.hb, stream=s)
-            blk["down"].matvec_add_dev(self.hb, self.x, self.x, stream=s)        # residual
-        self._logits_and_token(self.x)
-        pos_add_dev(self.pos, 1, s)
+            blk["qkv"].matvec_ex_dev(self.x, self.qkv, norm_w=blk["attn_norm"], eps=eps, stream=s)
+            self._qkv_post(blk, 1)
+            self._attention(blk, 1)
+            blk["o"].matvec_ex_dev(self.ctx, self.x, add=self.x, stream=s)            # residual
+            blk["ffn"].forward_dev(self.x, self.hb, norm_w=blk["ffn_norm"], eps=eps, stream=s)
+            blk["down"].matvec_ex_dev(self.hb, self.x, add=self.x, stream=s)          # residual
+        self._head_and_advance(self.x, 1)
 
     # -- API -------------------------------------------------------------------------------
     def prefill(self, prompt) -> int:
         """Batched prefill of the prompt (runner.rs:236-260); returns the first greedy token."""
-        from . import add_dev, attention_dev, embed_dev, kv_append_dev, pos_add_dev, rope_dev, swiglu_dev
-        g, s = self.g, self.stream
-        d, hd, kv = g.d_model, g.head_dim, self.kv
+        from . import add_dev, embed_dev, rmsnorm_dev, swiglu_dev
+        g, s, m = self.g, self.stream, self.mode
+        d = g.d_model
         prompt = np.asarray(prompt, np.int32)
         rows = prompt.size
         if not (0 < rows <= self.cap and self.seq_len + rows <= self.max_seq):
@@ -474,62 +481,61 @@ class DeviceDecoder:
             raise ValueError("prompt token outside the vocabulary")
         self.toks.upload(prompt)
         embed_dev(self.embed, self.mb.n_vocab, d, self.toks, rows, self.x, s)
-        m = self.mode
         for blk in self.blocks:
-            self._norm(self.x, blk["attn_norm"], rows, self.n)
-            blk["q"].matmul_dev(self.n, rows, self.qb, m, stream=s)
-            blk["k"].matmul_dev(self.n, rows, self.kb, m, stream=s)
-            blk["v"].matmul_dev(self.n, rows, self.vb, m, stream=s)
-            add_dev(self.qb, blk["q_bias"], rows * d, d, self.qb, s)
-            add_dev(self.kb, blk["k_bias"], rows * kv, kv, self.kb, s)
-            add_dev(self.vb, blk["v_bias"], rows * kv, kv, self.vb, s)
-            rope_dev(self.qb, rows, g.n_heads, hd, g.rope_freq_base, self.pos, 0, s)
-            rope_dev(self.kb, rows, g.n_kv_heads, hd, g.rope_freq_base, self.pos, 0, s)
-            kv_append_dev(self.kb, self.vb, rows, kv, blk["kc"], blk["vc"], self.max_seq, self.pos, s)
-            attention_dev(self.qb, blk["kc"], blk["vc"], rows, g.n_heads, g.n_kv_heads, hd, self.max_seq, self.pos,
-                          self.ctx, s)
+            rmsnorm_dev(self.x, blk["attn_norm"], rows, d, g.rms_eps, self.n, s)
+            blk["qkv"].matmul_dev(self.n, rows, self.qkv, m, stream=s)
+            self._qkv_post(blk, rows)
+            self._attention(blk, rows)
             blk["o"].matmul_dev(self.ctx, rows, self.ob, m, stream=s)
             add_dev(self.x, self.ob, rows * d, rows * d, self.x, s)
-            self._norm(self.x, blk["ffn_norm"], rows, self.n)
+            rmsnorm_dev(self.x, blk["ffn_norm"], rows, d, g.rms_eps, self.n, s)
             blk["gate"].matmul_dev(self.n, rows, self.gb, m, stream=s)
             blk["up"].matmul_dev(self.n, rows, self.ub, m, stream=s)
             swiglu_dev(self.gb, self.ub, self.hb, rows * g.d_ff, s)
-            blk["down"].matmul_dev(self.hb, rows, self.db, m, stream=s)
-            add_dev(self.x, self.db, rows * d, rows * d, self.x, s)
-        last = _Offset(self.x, (rows - 1) * d * 4)
-        self._logits_and_token(last)
-        pos_add_dev(self.pos, rows, s)
+            blk["down"].matmul_dev(self.hb, rows, self.ob, m, stream=s)
+            add_dev(self.x, self.ob, rows * d, rows * d, self.x, s)
+        self._head_and_advance(_Offset(self.x, (rows - 1) * d * 4), rows)
         self.seq_len += rows
         self.stream.synchronize()
         return int(self.tok.download(np.int32, 1)[0])
 
+    def _graph(self):
+        from . import hip
+        if self.graph is None:
+            self.graph = hip.Graph(self.stream, self._step_body)
+        return self.graph
+
     def step(self) -> int:
         """Decode the token in *tok at the next position; returns the following greedy token."""
-        from . import hip
         if self.seq_len >= self.max_seq:
             raise ValueError(f"decode past max_seq {self.max_seq}")
         if not self.use_graph:
             self._step_body()
         else:
-            if self.graph is None:
-                self.graph = hip.Graph(self.stream, self._step_body)
-            self.graph.launch()
+            self._graph().launch()
         self.seq_len += 1
         self.stream.synchronize()
         return int(self.tok.download(np.int32, 1)[0])
 
     def replay(self, steps: int) -> None:
         """`steps` decode steps back to back with no host synchronisation in between (the token
-        and position stay on the GPU); waits for the last one."""
-        from . import hip
+        and position stay on the GPU; each token is recorded in the history); waits for the
+        last one."""
         if self.seq_len + steps > self.max_seq:
             raise ValueError(f"decode past max_seq {self.max_seq}")
-        if self.graph is None:
-            self.graph = hip.Graph(self.stream, self._step_body)
         for _ in range(steps):
-            self.graph.launch()
+            if self.use_graph:
+                self._graph().launch()
+            else:
+                self._step_body()
         self.seq_len += steps
         self.stream.synchronize()
+
+    def history(self, start: int, count: int) -> list:
+        """Tokens recorded at positions start .. start + count - 1."""
+        self.stream.synchronize()
+        h = self.hist.download(np.int32, self.max_seq)
+        return [int(t) for t in h[start:start + count]]
 
     def logits(self) -> np.ndarray:
         """The logits of the last position computed (downloaded)."""
@@ -537,10 +543,15 @@ class DeviceDecoder:
         return self.logits_buf.download(np.float32, self.mb.n_vocab)
 
     def generate(self, prompt, max_new: int):
-        out = [self.prefill(prompt)]
-        for _ in range(max_new - 1):
-            out.append(self.step())
-        return out
+        """Prefill, then max_new - 1 graph replays back to back; the tokens come from the
+        device history in one read at the end."""
+        p0 = self.seq_len
+        if p0 + len(prompt) + max_new > self.max_seq:
+            raise ValueError(f"{len(prompt)} + {max_new} tokens from position {p0} exceed max_seq {self.max_seq}")
+        self.prefill(prompt)
+        if max_new > 1:
+            self.replay(max_new - 1)
+        return self.history(p0 + len(prompt), max_new)
 
     def close(self):
         if self.graph is not None:
@@ -548,7 +559,7 @@ class DeviceDecoder:
             self.graph = None
         for blk in self.blocks:
             blk["ffn"].close()
-            for k in ("q", "k", "v", "o", "gate", "up", "down"):
+            for k in ("qkv", "o", "gate", "up", "down"):
                 blk[k].close()
         self.output.close()
         self.stream.destroy()

@@ -66,11 +66,15 @@ def test_kv_append_and_bounds():
     assert not gk[:13].any() and not gv[:13].any()
 
 
+# rows < 8 take the per-(head, row) kernel; rows >= 8 with head_dim 64/128 the query-blocked one
+# (block sizes: 4 rows for 7 heads per kv head, 32 rows for MHA, 1 row for 32 heads per kv head)
 @pytest.mark.parametrize("rows,pos0,nh,nkv,hd", [(1, 0, 14, 2, 64), (1, 300, 14, 2, 64), (6, 0, 14, 2, 64),
-                                                 (5, 40, 4, 4, 32), (33, 7, 8, 1, 128)])
+                                                 (5, 40, 4, 4, 32), (3, 2000, 2, 1, 256), (33, 7, 8, 1, 128),
+                                                 (8, 0, 14, 2, 64), (961, 0, 14, 2, 64), (100, 50, 8, 8, 128),
+                                                 (37, 3, 32, 1, 64), (70, 10, 5, 5, 64), (9, 130, 6, 2, 64)])
 def test_attention(rows, pos0, nh, nkv, hd):
     g = qwen.Geometry(d_model=nh * hd, n_heads=nh, n_kv_heads=nkv)
-    max_seq = 512
+    max_seq = max(512, pos0 + rows + 3)
     rng = np.random.default_rng(rows + pos0 + nh)
     kvd = nkv * hd
     kc = np.zeros((max_seq, kvd), np.float32)
@@ -79,12 +83,85 @@ def test_attention(rows, pos0, nh, nkv, hd):
     kc[:total] = rng.standard_normal((total, kvd))
     vc[:total] = rng.standard_normal((total, kvd))
     q = (rng.standard_normal((rows, nh * hd)) * 2).astype(np.float32)
-    ctx = B(rows * nh * hd * 4)
-    rehip.attention_dev(B.from_array(q), B.from_array(kc), B.from_array(vc), rows, nh, nkv, hd, max_seq,
-                        dev_i32([pos0]), ctx)
-    got = down(ctx, rows * nh * hd).reshape(rows, -1)
     want = qwen.attention(q, kc, vc, g, pos0)
-    np.testing.assert_allclose(got, want, rtol=0, atol=2e-5 * np.abs(want).max())
+    qd, kd, vd, pd = B.from_array(q), B.from_array(kc), B.from_array(vc), dev_i32([pos0])
+    wb = rehip.attention_work_bytes(rows, nh, hd, max_seq)
+    work = B.from_array(np.full(wb // 4, np.nan, np.float32))   # nothing unwritten may be read
+    for use_work in (False, True):                  # few rows: one workgroup per row, or key splits
+        ctx = B(rows * nh * hd * 4)
+        rehip.attention_dev(qd, kd, vd, rows, nh, nkv, hd, max_seq, pd, ctx,
+                            work=work if use_work else None, work_bytes=wb if use_work else 0)
+        got = down(ctx, rows * nh * hd).reshape(rows, -1)
+        np.testing.assert_allclose(got, want, rtol=0, atol=2e-5 * np.abs(want).max())
+    with pytest.raises(rehip.RehipError):
+        rehip.attention_dev(qd, kd, vd, rows, nh, nkv, hd, max_seq, pd, ctx, work=work, work_bytes=wb - 4)
+
+
+def test_attention_split_skips_unwritten_cache_rows():
+    """Cache rows past the visible position hold NaN: neither attention path may read them."""
+    g = qwen.Geometry(d_model=14 * 64, n_heads=14, n_kv_heads=2)
+    max_seq, pos0 = 1000, 300
+    rng = np.random.default_rng(12)
+    kc = np.full((max_seq, 128), np.nan, np.float32)
+    vc = np.full((max_seq, 128), np.nan, np.float32)
+    kc[:pos0 + 9] = rng.standard_normal((pos0 + 9, 128))
+    vc[:pos0 + 9] = rng.standard_normal((pos0 + 9, 128))
+    for rows in (1, 9):
+        q = rng.standard_normal((rows, 14 * 64)).astype(np.float32)
+        want = qwen.attention(q, kc, vc, g, pos0)
+        wb = rehip.attention_work_bytes(rows, 14, 64, max_seq)
+        ctx = B(rows * 14 * 64 * 4)
+        rehip.attention_dev(B.from_array(q), B.from_array(kc), B.from_array(vc), rows, 14, 2, 64, max_seq,
+                            dev_i32([pos0]), ctx, work=B.from_array(np.full(wb // 4, np.nan, np.float32)),
+                            work_bytes=wb)
+        got = down(ctx, rows * 14 * 64).reshape(rows, -1)
+        assert np.isfinite(got).all()
+        np.testing.assert_allclose(got, want, rtol=0, atol=2e-5 * np.abs(want).max())
+
+
+@pytest.mark.parametrize("rows,nh,nkv,hd,pos0,fused", [(1, 14, 2, 64, 37, True), (5, 14, 2, 64, 0, False),
+                                                       (3, 4, 4, 128, 10, True), (2, 2, 1, 256, 7, False)])
+def test_qkv_rope_append(rows, nh, nkv, hd, pos0, fused):
+    rng = np.random.default_rng(rows * 31 + hd)
+    d, kv = nh * hd, nkv * hd
+    max_seq = pos0 + rows + 4
+    qkv = rng.standard_normal((rows, d + 2 * kv)).astype(np.float32)
+    bq, bk, bv = (rng.standard_normal(n).astype(np.float32) for n in (d, kv, kv))
+    kc, vc, qo = B(max_seq * kv * 4), B(max_seq * kv * 4), B(rows * d * 4)
+    kc.zero()
+    vc.zero()
+    if fused:
+        src = B.from_array(qkv)
+        from rehip.qwen import _Offset
+        args = (src, d + 2 * kv, _Offset(src, 4 * d), d + 2 * kv, _Offset(src, 4 * (d + kv)), d + 2 * kv)
+    else:
+        args = (B.from_array(qkv[:, :d]), d, B.from_array(qkv[:, d:d + kv]), kv, B.from_array(qkv[:, d + kv:]), kv)
+    rehip.qkv_rope_append_dev(*args, B.from_array(bq), B.from_array(bk), B.from_array(bv), rows, nh, nkv, hd, 1e6,
+                              dev_i32([pos0]), qo, kc, vc, max_seq)
+    cos, sin = qwen.rope_table(rows, pos0, hd, 1e6)
+    want_q = qwen.rope_rows((qkv[:, :d] + bq).astype(np.float32), nh, hd, cos, sin)
+    want_k = qwen.rope_rows((qkv[:, d:d + kv] + bk).astype(np.float32), nkv, hd, cos, sin)
+    np.testing.assert_allclose(down(qo, rows * d).reshape(rows, d), want_q, rtol=0, atol=5e-4)
+    gk = down(kc, max_seq * kv).reshape(max_seq, kv)
+    gv = down(vc, max_seq * kv).reshape(max_seq, kv)
+    np.testing.assert_allclose(gk[pos0:pos0 + rows], want_k, rtol=0, atol=5e-4)
+    assert np.array_equal(gv[pos0:pos0 + rows], (qkv[:, d + kv:] + bv).astype(np.float32))
+    assert not gk[:pos0].any() and not gv[pos0 + rows:].any()
+
+
+def test_decode_advance():
+    keys = np.zeros(8, np.uint64)
+    keys[5] = (0xC0400000 << 32) | 1234                                     # key of (3.0, 1234)
+    keys[2] = (0xC0000000 << 32) | 4321                                     # key of (2.0, 4321)
+    best = B.from_array(keys)
+    tok, pos, hist = dev_i32([0]), dev_i32([10]), dev_i32(np.full(16, -1))
+    rehip.decode_advance_dev(best, tok, pos, 1, hist, 16)
+    assert int(down(tok, 1, np.int32)[0]) == 1234 and int(down(pos, 1, np.int32)[0]) == 11
+    assert not down(best, 8, np.uint64).any()
+    assert down(hist, 16, np.int32)[11] == 1234
+    before = down(hist, 16, np.int32)
+    rehip.decode_advance_dev(best, tok, pos, 10, hist, 16)                  # past the history: not stored
+    assert int(down(pos, 1, np.int32)[0]) == 21 and np.array_equal(down(hist, 16, np.int32), before)
 
 
 def test_add_and_bias():
@@ -128,28 +205,58 @@ def test_pos_add():
     assert int(down(p, 1, np.int32)[0]) == 969
 
 
+def small_scale_bytes(t, m, n, seed):
+    """Random blocks of a legacy type with a small f16 scale (outputs stay O(1))."""
+    r = np.random.default_rng(seed)
+    bb = {rehip.Q4_0: 18, rehip.Q5_0: 22, rehip.Q8_0: 34}[t]
+    w = r.integers(0, 256, m * rehip.row_bytes(t, n), dtype=np.uint8).reshape(m, -1)
+    w[:, 0::bb] = 0x00
+    w[:, 1::bb] = 0x24
+    return w.reshape(-1)
+
+
 @pytest.mark.parametrize("t,m,n", [(rehip.Q4_K, 896, 896), (rehip.Q6_K, 896, 4864), (rehip.Q8_0, 64, 14336),
-                                   (rehip.Q4_0, 130, 512)])
-def test_matvec_add_is_matvec_plus_add(t, m, n):
-    """The fused add returns the plain GEMV's sum plus `add` exactly, also in place."""
+                                   (rehip.Q4_0, 130, 512), (rehip.Q8_0, 151936 // 8, 896)])
+def test_matvec_ex(t, m, n):
+    """add: the plain GEMV's sum plus `add` exactly, also in place; norm: the GEMV of the
+    RMS-normalised row; best: the last index of the largest output (also on ties)."""
     rng = np.random.default_rng(m + n)
-    w = qwen.conditioned_weight_bytes(rng, t, m, n, 1.0 / np.sqrt(n)) if t in (rehip.Q4_K, rehip.Q6_K, rehip.Q8_0) \
-        else rng.integers(0, 256, m * rehip.row_bytes(t, n), dtype=np.uint8)
-    if t == rehip.Q4_0:
-        w = w.reshape(m, -1)
-        w[:, 0::18] = 0x00
-        w[:, 1::18] = 0x2c                                      # scale bits of a small f16
-        w = w.reshape(-1)
+    if t in (rehip.Q4_K, rehip.Q6_K):
+        w = qwen.conditioned_weight_bytes(rng, t, m, n, 1.0 / np.sqrt(n))
+    else:
+        w = small_scale_bytes(t, m, n, m + n)
+    rb = rehip.row_bytes(t, n)
+    w = w.reshape(m, rb)
+    w[[m // 3, m - 1]] = w[m // 5]                  # identical rows: identical outputs (a tie)
+    w = w.reshape(-1)
     q = rehip.QMat.from_bytes(t, w, m, n)
-    x = rng.standard_normal(n).astype(np.float32)
+    x = (rng.standard_normal(n) * 3).astype(np.float32)
+    nw = rng.standard_normal(n).astype(np.float32)
     add = rng.standard_normal(m).astype(np.float32)
-    xb, yb, ab = B.from_array(x), B(m * 4), B.from_array(add)
+    xb, yb, ab, nb = B.from_array(x), B(m * 4), B.from_array(add), B.from_array(nw)
     q.matvec_dev(xb, yb)
     plain = down(yb, m)
-    q.matvec_add_dev(xb, ab, yb)
+    q.matvec_ex_dev(xb, yb, add=ab)
     assert np.array_equal(down(yb, m), plain + add)
-    q.matvec_add_dev(xb, ab, ab)                                 # y aliases add
+    q.matvec_ex_dev(xb, ab, add=ab)                               # y aliases add
     assert np.array_equal(down(ab, m), plain + add)
+    # norm in the prologue vs an explicit RMS-norm, then the same GEMV
+    q.matvec_ex_dev(xb, yb, norm_w=nb, eps=1e-6)
+    normed = qwen.rmsnorm_rows(x[None, :], nw, 1e-6)[0]
+    q.matvec_dev(B.from_array(normed), ab)
+    ref = down(ab, m)
+    np.testing.assert_allclose(down(yb, m), ref, rtol=0, atol=1e-5 * np.abs(ref).max())
+    # argmax folded into the stores; make row m//5 (and its copies) the maximum
+    best = B.from_array(np.zeros(8, np.uint64))
+    bias = np.zeros(m, np.float32)
+    bias[[m // 5, m // 3, m - 1]] = np.abs(plain).max() + 10
+    q.matvec_ex_dev(xb, yb, add=B.from_array(bias), best=best)
+    y = down(yb, m)
+    key = int(down(best, 8, np.uint64).max())
+    assert key & 0xffffffff == qwen.argmax_last(y) == m - 1
+    best.upload(np.zeros(8, np.uint64))
+    q.matvec_ex_dev(xb, yb, best=best)
+    assert int(down(best, 8, np.uint64).max()) & 0xffffffff == qwen.argmax_last(down(yb, m))
     q.close()
 
 
@@ -175,6 +282,11 @@ def test_ffn_pair(t, inter, hidden):
     got = down(h, inter)
     want = qwen.silu(G.matvec(x)) * U.matvec(x)
     np.testing.assert_allclose(got, want, rtol=0, atol=2e-5 * np.abs(want).max())
+    nw = rng.standard_normal(hidden).astype(np.float32)
+    f.forward_dev(B.from_array(x), h, norm_w=B.from_array(nw), eps=1e-6)
+    xn = qwen.rmsnorm_rows(x[None, :], nw, 1e-6)[0]
+    want = qwen.silu(G.matvec(xn)) * U.matvec(xn)
+    np.testing.assert_allclose(down(h, inter), want, rtol=0, atol=2e-5 * np.abs(want).max())
     f.close()
     G.close()
     U.close()
@@ -205,6 +317,9 @@ def test_device_decoder_tiny_matches_cpu_path(use_graph):
     got = [first] + [dd.step() for _ in range(19)]
     dd.close()
     assert got == want
+    dd = qwen.DeviceDecoder(mb, max_seq=64, prefill_rows=16, use_graph=use_graph)
+    assert dd.generate(prompt, 20) == want            # back-to-back replays, history read at the end
+    dd.close()
     with pytest.raises(ValueError):
         qwen.DeviceDecoder(mb, max_seq=8, prefill_rows=16).prefill(prompt)
 
@@ -215,9 +330,11 @@ def test_device_decoder_qwen_shape_64_steps_match_cpu_path():
     mb = qwen.synth_model(501)
     prompt = np.random.default_rng(502).integers(0, mb.n_vocab, 961)
     want, lg = cpu_tokens(mb, prompt, 64)
-    dd = qwen.DeviceDecoder(mb, max_seq=1024, prefill_rows=961)
+    dd = qwen.DeviceDecoder(mb, max_seq=1040, prefill_rows=961)
     got = [dd.prefill(prompt)]
     assert np.max(np.abs(dd.logits() - lg)) <= 1e-3 * np.max(np.abs(lg))
-    got += [dd.step() for _ in range(63)]
+    got += [dd.step() for _ in range(31)]
+    dd.replay(32)
+    got += dd.history(961 + 32, 32)
     dd.close()
     assert got == want, next(i for i, (a, b) in enumerate(zip(got, want)) if a != b)
