@@ -64,6 +64,12 @@ int re_repack(uint32_t ggml_type, const uint8_t *bytes, size_t nbytes, size_t m,
 /* Upload and repack once. nbytes must equal m * re_row_bytes(type, n). */
 int re_qmat_create(uint32_t ggml_type, const uint8_t *bytes, size_t nbytes, size_t m, size_t n,
                    re_qmat **out);
+/* A stack of `count` same-type, same-shape matrices (nbytes = count * m * row bytes, one after
+ * the other, as ExpertWeights holds experts, moe.rs:349-353); every other entry point works on
+ * matrix 0, re_qmat_matvec_stacked_dev on any range of them in one launch. */
+int re_qmat_create_stacked(uint32_t ggml_type, const uint8_t *bytes, size_t nbytes, size_t m, size_t n,
+                           size_t count, re_qmat **out);
+size_t re_qmat_count(const re_qmat *q);
 void re_qmat_destroy(re_qmat *q);
 size_t re_qmat_rows(const re_qmat *q);   /* m (qmat.rs:62-66) */
 size_t re_qmat_cols(const re_qmat *q);   /* n (qmat.rs:69-73) */
@@ -118,6 +124,12 @@ typedef struct re_ffn re_ffn;
  *             largest slot end as the greedy token (infer.rs:217-223: the last index among equal
  *             maxima). The slots must start at 0 (re_decode_advance_dev clears them).
  * x and norm_w are 16-byte aligned. */
+/* y_b = W_b x_b for the matrices b = first .. first + count - 1 of a stack, in one launch:
+ * x_b = d_x + (b - first) * x_stride (x_stride 0: one shared x), y_b = d_y + (b - first) *
+ * y_stride. Each result is the GEMV of re_qmat_matvec_dev (qmat.rs:80) up to summation order:
+ * the launch shape is planned for the whole stack. */
+int re_qmat_matvec_stacked_dev(re_qmat *q, size_t first, size_t count, const float *d_x, size_t x_stride,
+                               float *d_y, size_t y_stride, void *stream);
 int re_qmat_matvec_ex_dev(re_qmat *q, const float *d_x, const float *d_norm_w, float eps, const float *d_add,
                           float *d_y, unsigned long long *d_best, void *stream);
 /* out[r] = x[r] * (1 / sqrt(mean(x[r]^2) + eps)) * w for rows x d (infer.rs:72-82). */

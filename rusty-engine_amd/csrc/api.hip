@@ -115,7 +115,8 @@ struct Staging {
 
 struct re_qmat {
   MatGeom g{};
-  uint8_t* d_w = nullptr;
+  uint8_t* d_w = nullptr;                 // count matrices, w_stride bytes apart
+  size_t count = 1, w_stride = 0;
   float* d_partial = nullptr;
   int splits = 1, kb_per_split = 1, waves = 4;
   int rows_per_group = 0, groups = 0;   // row-group GEMV launch (0 = split launch)
@@ -152,6 +153,24 @@ size_t env_size(const char* name, size_t dflt) {
 // the fewest of 4/8/16 that leave each lane-group slot at most 2 units (4 for 64-row groups), so
 // a slot's loads are all in flight at once. Longer rows split the row over workgroups (partials
 // + a reduce kernel). Measured on MI355X over the Qwen2.5-0.5B projections in all six types.
+// Row-group shape for `tiles` 64-row tiles (of one matrix, or of a whole stack in one launch)
+// whose rows have `units` 32-quant chunks.
+void rows_shape(size_t tiles, size_t units, int* rows_per_group, int* waves) {
+  int r = 64;
+  for (int c : {64, 16, 8, 4}) {
+    r = c;
+    if (tiles * 64 / (size_t)c >= 512) break;
+  }
+  if (const size_t e = env_size("REHIP_GEMV_ROWS", 0); e == 64 || e == 16 || e == 8 || e == 4) r = (int)e;
+  const size_t per_slot = r == 64 ? 4 : 2;
+  const size_t slots = (units + per_slot - 1) / per_slot;
+  const size_t per_wave = 64 / (size_t)r;
+  const size_t w = (slots + per_wave - 1) / per_wave;
+  *waves = w <= 4 ? 4 : w <= 8 ? 8 : 16;
+  if (const size_t e = env_size("REHIP_GEMV_WAVES", 0); e == 4 || e == 8 || e == 16) *waves = (int)e;
+  *rows_per_group = r;
+}
+
 void plan_gemv(re_qmat* q) {
   const size_t kb = q->g.kb;
   const size_t nch = q->g.qk == 256 ? 8 : 1;
@@ -160,17 +179,7 @@ void plan_gemv(re_qmat* q) {
   q->groups = 0;
   if (q->g.n <= (size_t)kGemvRowsMaxK) {
     int r = 64;
-    for (int c : {64, 16, 8, 4}) {
-      r = c;
-      if (q->g.tiles * 64 / (size_t)c >= 512) break;
-    }
-    if (const size_t e = env_size("REHIP_GEMV_ROWS", 0); e == 64 || e == 16 || e == 8 || e == 4) r = (int)e;
-    const size_t per_slot = r == 64 ? 4 : 2;
-    const size_t slots = (units + per_slot - 1) / per_slot;
-    const size_t per_wave = 64 / (size_t)r;
-    const size_t w = (slots + per_wave - 1) / per_wave;
-    q->waves = w <= 4 ? 4 : w <= 8 ? 8 : 16;
-    if (const size_t e = env_size("REHIP_GEMV_WAVES", 0); e == 4 || e == 8 || e == 16) q->waves = (int)e;
+    rows_shape(q->g.tiles, units, &r, &q->waves);
     q->rows_per_group = r;
     q->groups = (int)(q->g.tiles * 64 / (size_t)r);
     q->splits = 1;
@@ -319,24 +328,31 @@ int re_repack(uint32_t ggml_type, const uint8_t* bytes, size_t nbytes, size_t m,
   return RE_OK;
 }
 
-int re_qmat_create(uint32_t ggml_type, const uint8_t* bytes, size_t nbytes, size_t m, size_t n,
-                   re_qmat** out) {
+int re_qmat_create_stacked(uint32_t ggml_type, const uint8_t* bytes, size_t nbytes, size_t m, size_t n,
+                           size_t count, re_qmat** out) {
   if (!out || !bytes) return fail(RE_ERR_ARG, "null pointer");
   *out = nullptr;
+  if (count == 0 || count > (1u << 20) || nbytes % count)
+    return fail(RE_ERR_SIZE, "%zu bytes do not hold %zu equal matrices", nbytes, count);
   MatGeom g;
-  int rc = check_matrix(ggml_type, nbytes, m, n, &g);
+  int rc = check_matrix(ggml_type, nbytes / count, m, n, &g);
   if (rc) return rc;
   if ((rc = do_init())) return rc;
   re_qmat* q = new (std::nothrow) re_qmat();
   if (!q) return fail(RE_ERR_ARG, "out of memory");
   q->g = g;
+  q->count = count;
+  q->w_stride = (g.bytes + 255) / 256 * 256;
   plan_gemv(q);
   auto cleanup = [&](int code) {
     re_qmat_destroy(q);
     return code;
   };
-  if (hipMalloc(&q->d_w, g.bytes) != hipSuccess) return cleanup(fail(RE_ERR_HIP, "hipMalloc(%zu) failed", g.bytes));
-  if ((rc = upload_tiled(g, bytes, q->d_w))) return cleanup(rc);
+  const size_t total = q->w_stride * count;
+  if (hipMalloc(&q->d_w, total) != hipSuccess) return cleanup(fail(RE_ERR_HIP, "hipMalloc(%zu) failed", total));
+  const size_t one = nbytes / count;
+  for (size_t i = 0; i < count; ++i)
+    if ((rc = upload_tiled(g, bytes + i * one, q->d_w + i * q->w_stride))) return cleanup(rc);
   const size_t m_pad = g.tiles * kTileRows;
   if (q->splits > 1) {
     if (hipMalloc(&q->d_partial, (size_t)q->splits * m_pad * sizeof(float)) != hipSuccess)
@@ -346,6 +362,11 @@ int re_qmat_create(uint32_t ggml_type, const uint8_t* bytes, size_t nbytes, size
     return cleanup(fail(RE_ERR_HIP, "hipStreamCreate failed"));
   *out = q;
   return RE_OK;
+}
+
+int re_qmat_create(uint32_t ggml_type, const uint8_t* bytes, size_t nbytes, size_t m, size_t n,
+                   re_qmat** out) {
+  return re_qmat_create_stacked(ggml_type, bytes, nbytes, m, n, 1, out);
 }
 
 void re_qmat_destroy(re_qmat* q) {
@@ -367,6 +388,64 @@ uint32_t re_qmat_type(const re_qmat* q) { return q ? q->g.type : 0; }
 int re_qmat_matvec_dev(re_qmat* q, const float* d_x, float* d_y, void* stream) {
   if (!q || !d_x || !d_y) return fail(RE_ERR_ARG, "null pointer");
   return gemv_enqueue(q, d_x, d_y, (hipStream_t)stream);
+}
+
+size_t re_qmat_count(const re_qmat* q) { return q ? q->count : 0; }
+
+int re_qmat_matvec_stacked_dev(re_qmat* q, size_t first, size_t count, const float* d_x, size_t x_stride,
+                               float* d_y, size_t y_stride, void* stream) {
+  if (!q || !d_x || !d_y) return fail(RE_ERR_ARG, "null pointer");
+  if (count == 0) return RE_OK;
+  if (first >= q->count || count > q->count - first)
+    return fail(RE_ERR_SIZE, "matrices %zu..%zu of a stack of %zu", first, first + count - 1, q->count);
+  if (x_stride % 4 || x_stride > (1u << 30) || y_stride > (1u << 30) || (x_stride && x_stride < q->g.n) ||
+      y_stride < q->g.m)
+    return fail(RE_ERR_SIZE, "stacked strides x %zu (0 or >= %zu, multiple of 4), y %zu (>= %zu)", x_stride, q->g.n,
+                y_stride, q->g.m);
+  if (!aligned16(d_x)) return fail(RE_ERR_ARG, "x must be 16-byte aligned");
+  const hipStream_t s = (hipStream_t)stream;
+  if (!q->rows_per_group) {                // split launches: one matrix at a time
+    for (size_t b = 0; b < count; ++b) {
+      GemvArgs a{};
+      a.W = q->d_w + (first + b) * q->w_stride;
+      a.x = d_x + b * x_stride;
+      a.y = d_y + b * y_stride;
+      a.partial = q->d_partial;
+      a.m = (int)q->g.m;
+      a.m_pad = (int)(q->g.tiles * kTileRows);
+      a.K = (int)q->g.n;
+      a.KB = (int)q->g.kb;
+      a.tiles = (int)q->g.tiles;
+      a.kb_per_split = q->kb_per_split;
+      a.splits = q->splits;
+      HIP_TRY(launch_gemv(q->g.type, a, q->waves, s));
+    }
+    return RE_OK;
+  }
+  // the launch shape is planned for the whole stack (many matrices: bigger row groups)
+  int rpg = 64, waves = 4;
+  rows_shape(q->g.tiles * count, q->g.kb * (q->g.qk == 256 ? 8 : 1), &rpg, &waves);
+  const size_t groups = q->g.tiles * 64 / (size_t)rpg;
+  if (groups * count > (size_t)INT32_MAX) return fail(RE_ERR_SIZE, "stack too large for one launch");
+  GemvArgs a{};
+  a.W = q->d_w + first * q->w_stride;
+  a.x = d_x;
+  a.y = d_y;
+  a.m = (int)q->g.m;
+  a.m_pad = (int)(q->g.tiles * kTileRows);
+  a.K = (int)q->g.n;
+  a.KB = (int)q->g.kb;
+  a.tiles = (int)q->g.tiles;
+  a.kb_per_split = q->kb_per_split;
+  a.splits = 1;
+  a.rows_per_group = rpg;
+  a.groups = (int)groups;
+  a.batch = (int)count;
+  a.w_stride = q->w_stride;
+  a.x_stride = (int)x_stride;
+  a.y_stride = (int)y_stride;
+  HIP_TRY(launch_gemv(q->g.type, a, waves, s));
+  return RE_OK;
 }
 
 int re_qmat_matvec_ex_dev(re_qmat* q, const float* d_x, const float* d_norm_w, float eps, const float* d_add,

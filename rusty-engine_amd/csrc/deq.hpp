@@ -82,6 +82,21 @@ __device__ __forceinline__ uint32_t bld4(__amdgpu_buffer_rsrc_t r, uint32_t off)
 __device__ __forceinline__ uint32_t bld2(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, 0);
 }
+// Streaming weight loads: the uniform part of the offset in soffset (a scalar register, so no
+// per-lane address arithmetic when the base moves) and the nontemporal cache policy (weights are
+// read once per launch; on MI355X a plain streaming read tops out near 6.2 TB/s and a
+// nontemporal one near 7.0 TB/s).
+constexpr int kLoadNT = 2;   // buffer load aux: nontemporal
+__device__ __forceinline__ uint4 sld16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  const i32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, kLoadNT);
+  return make_uint4((uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]);
+}
+__device__ __forceinline__ uint32_t sld4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, kLoadNT);
+}
+__device__ __forceinline__ uint32_t sld2(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)voff, (int)soff, kLoadNT);
+}
 __device__ __forceinline__ uint32_t ld4(const uint8_t* p) { return *reinterpret_cast<const uint32_t*>(p); }
 __device__ __forceinline__ uint32_t ld2(const uint8_t* p) { return *reinterpret_cast<const uint16_t*>(p); }
 
@@ -105,6 +120,12 @@ template <> struct Blk<T_Q4_0> {
     (void)c;
     r.p[0] = bld16(rs, slab + lane * 16);
     r.t0 = bld2(rs, slab + 1024 + lane * 2);
+    r.t1 = 0;
+  }
+  // whole block through a buffer resource, slab at scalar offset soff
+  __device__ static void sload(__amdgpu_buffer_rsrc_t rs, uint32_t soff, int lane, R& r) {
+    r.p[0] = sld16(rs, lane * 16, soff);
+    r.t0 = sld2(rs, lane * 2, soff + 1024);
     r.t1 = 0;
   }
   __device__ static void decode(const R& r, int c, Run& a, Run& b) {
@@ -144,6 +165,11 @@ template <> struct Blk<T_Q5_0> {
     r.t0 = bld4(rs, slab + 1024 + lane * 4);
     r.t1 = bld2(rs, slab + 1280 + lane * 2);
   }
+  __device__ static void sload(__amdgpu_buffer_rsrc_t rs, uint32_t soff, int lane, R& r) {
+    r.p[0] = sld16(rs, lane * 16, soff);
+    r.t0 = sld4(rs, lane * 4, soff + 1024);
+    r.t1 = sld2(rs, lane * 2, soff + 1280);
+  }
   __device__ static void decode(const R& r, int c, Run& a, Run& b) {
     (void)c;
     const uint32_t w[4] = {r.p[0].x, r.p[0].y, r.p[0].z, r.p[0].w};
@@ -182,6 +208,12 @@ template <> struct Blk<T_Q8_0> {
     r.p[0] = bld16(rs, slab + lane * 16);
     r.p[1] = bld16(rs, slab + 1024 + lane * 16);
     r.t0 = bld2(rs, slab + 2048 + lane * 2);
+    r.t1 = 0;
+  }
+  __device__ static void sload(__amdgpu_buffer_rsrc_t rs, uint32_t soff, int lane, R& r) {
+    r.p[0] = sld16(rs, lane * 16, soff);
+    r.p[1] = sld16(rs, lane * 16, soff + 1024);
+    r.t0 = sld2(rs, lane * 2, soff + 2048);
     r.t1 = 0;
   }
   __device__ static void decode(const R& r, int c, Run& a, Run& b) {
@@ -247,6 +279,17 @@ template <> struct Blk<T_Q4_K> {
     for (int p = 0; p < NP; ++p) r.p[p] = ld16(slab + 1024 * p + lane * 16);
     r.t0 = r.t1 = 0;
   }
+  __device__ static void sload(__amdgpu_buffer_rsrc_t rs, uint32_t soff, int lane, R& r) {
+#pragma unroll
+    for (int p = 0; p < NP; ++p) r.p[p] = sld16(rs, lane * 16, soff + 1024 * p);
+    r.t0 = r.t1 = 0;
+  }
+  // the planes chunks 4H .. 4H + 3 read (head and their four qs planes)
+  template <int H> __device__ static void sload_half(__amdgpu_buffer_rsrc_t rs, uint32_t soff, int lane, R& r) {
+    r.p[0] = sld16(rs, lane * 16, soff);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) r.p[1 + 4 * H + j] = sld16(rs, lane * 16, soff + 1024 * (1 + 4 * H + j));
+  }
   __device__ static void decode(const R& r, int c, Run& a, Run& b) { dec(r.p[0], r.p[1 + c], c, a, b); }
   struct CR { uint4 head, qs; };
   __device__ static void load_chunk(const uint8_t* slab, int lane, int c, CR& r) {
@@ -285,6 +328,18 @@ template <> struct Blk<T_Q5_K> {
 #pragma unroll
     for (int p = 0; p < NP; ++p) r.p[p] = ld16(slab + 1024 * p + lane * 16);
     r.t0 = r.t1 = 0;
+  }
+  __device__ static void sload(__amdgpu_buffer_rsrc_t rs, uint32_t soff, int lane, R& r) {
+#pragma unroll
+    for (int p = 0; p < NP; ++p) r.p[p] = sld16(rs, lane * 16, soff + 1024 * p);
+    r.t0 = r.t1 = 0;
+  }
+  // the planes chunks 4H .. 4H + 3 read (head, both qh planes, their four qs planes)
+  template <int H> __device__ static void sload_half(__amdgpu_buffer_rsrc_t rs, uint32_t soff, int lane, R& r) {
+#pragma unroll
+    for (int p = 0; p < 3; ++p) r.p[p] = sld16(rs, lane * 16, soff + 1024 * p);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) r.p[3 + 4 * H + j] = sld16(rs, lane * 16, soff + 1024 * (3 + 4 * H + j));
   }
   __device__ static void decode(const R& r, int c, Run& a, Run& b) {
     dec(r.p[0], r.p[1 + (c & 1)], r.p[3 + c], c, a, b);
@@ -342,6 +397,21 @@ template <> struct Blk<T_Q6_K> {
     r.t0 = ld2(slab + 1024 * 13 + lane * 2);
     r.t1 = 0;
   }
+  __device__ static void sload(__amdgpu_buffer_rsrc_t rs, uint32_t soff, int lane, R& r) {
+#pragma unroll
+    for (int p = 0; p < NP; ++p) r.p[p] = sld16(rs, lane * 16, soff + 1024 * p);
+    r.t0 = sld2(rs, lane * 2, soff + 1024 * 13);
+    r.t1 = 0;
+  }
+  // the planes chunks 4H .. 4H + 3 read (their ql planes, qh planes 8 + 2H and 9 + 2H, sc, d)
+  template <int H> __device__ static void sload_half(__amdgpu_buffer_rsrc_t rs, uint32_t soff, int lane, R& r) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) r.p[4 * H + j] = sld16(rs, lane * 16, soff + 1024 * (4 * H + j));
+    r.p[8 + 2 * H] = sld16(rs, lane * 16, soff + 1024 * (8 + 2 * H));
+    r.p[9 + 2 * H] = sld16(rs, lane * 16, soff + 1024 * (9 + 2 * H));
+    r.p[12] = sld16(rs, lane * 16, soff + 1024 * 12);
+    r.t0 = sld2(rs, lane * 2, soff + 1024 * 13);
+  }
   __device__ static void decode(const R& r, int c, Run& a, Run& b) {
     dec(r.p[c], r.p[8 + 2 * (c >> 2) + (c & 1)], r.p[12], r.t0, c, a, b);
   }
@@ -388,6 +458,8 @@ __device__ __forceinline__ float run_value_exact(const Run& r, int i) {
 }
 
 typedef __attribute__((__vector_size__(2 * sizeof(float)))) float f32x2_t;
+typedef _Float16 h16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 // Dot of one decoded run (16 quants) with x from LDS: every lane of the wave reads the same
 // address (a broadcast), so 16 activations are four ds_read_b128.
@@ -407,14 +479,20 @@ __device__ __forceinline__ float run_dot(const Run& r, const float* __restrict__
       s = __builtin_fmaf(hi[0], q.z, s);
       s = __builtin_fmaf(hi[1], q.w, s);
     } else {
-      s = __builtin_fmaf(qbyte(r.q, 4 * v + 0), q.x, s);
-      s = __builtin_fmaf(qbyte(r.q, 4 * v + 1), q.y, s);
-      s = __builtin_fmaf(qbyte(r.q, 4 * v + 2), q.z, s);
-      s = __builtin_fmaf(qbyte(r.q, 4 * v + 3), q.w, s);
+      // bytes b -> binary16 1024 + b (0x64 as the high byte: exact), two per v_perm_b32, and the
+      // multiply-add takes the half operand directly (v_fma_mix_f32): 1.5 instructions per quant
+      // instead of a convert and an FMA. The 1024 * sum(x) this adds is taken out below with the
+      // run's sum of x.
+      const h16x2_t p01 = __builtin_bit_cast(h16x2_t, __builtin_amdgcn_perm(0x64646464u, r.q[v], 0x04010400u));
+      const h16x2_t p23 = __builtin_bit_cast(h16x2_t, __builtin_amdgcn_perm(0x64646464u, r.q[v], 0x04030402u));
+      s = __builtin_fmaf((float)p01[0], q.x, s);
+      s = __builtin_fmaf((float)p01[1], q.y, s);
+      s = __builtin_fmaf((float)p23[0], q.z, s);
+      s = __builtin_fmaf((float)p23[1], q.w, s);
     }
   }
-  const float scale = kNibble<T> ? r.scale * 512.0f : r.scale;
-  return __builtin_fmaf(scale, s, -r.offset * xs[r.e >> 4]);
+  if constexpr (kNibble<T>) return __builtin_fmaf(r.scale * 512.0f, s, -r.offset * xs[r.e >> 4]);
+  return __builtin_fmaf(r.scale, s, -__builtin_fmaf(1024.0f, r.scale, r.offset) * xs[r.e >> 4]);
 }
 
 // Sum of one value per thread over a workgroup of WAVES waves: xor tree inside each wave, then

@@ -147,9 +147,13 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_rows_kernel(GemvArgs p) {
   constexpr int S = WAVES * G;           // slots per workgroup
   // LDS: x[KB * QK] (zero past K), xs16[KB * QK / 16], red[WAVES * R], ssred[WAVES]
   extern __shared__ __attribute__((aligned(16))) float smem[];
-  const int per = (p.groups + 7) / 8;
-  const int gi = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
-  if (gi >= p.groups) return;
+  const int nb = p.batch > 1 ? p.batch : 1;
+  const int per = (p.groups * nb + 7) / 8;
+  const int gq = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
+  if (gq >= p.groups * nb) return;
+  const int mb = gq / p.groups, gi = gq - mb * p.groups;     // matrix of the stack, its row group
+  const float* xin = p.x + (size_t)mb * p.x_stride;
+  float* yout = p.y + (size_t)mb * p.y_stride;
   constexpr int GPT = 64 / R;            // row groups per tile
   const int tile = gi / GPT;
   const int lane = threadIdx.x & 63;
@@ -162,7 +166,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_rows_kernel(GemvArgs p) {
   float* red = xs16 + nx / 16;
   float* ssred = red + WAVES * R;
 
-  const uint8_t* tbase = p.W + (size_t)tile * p.KB * B::SLAB;
+  const uint8_t* tbase = p.W + (size_t)mb * p.w_stride + (size_t)tile * p.KB * B::SLAB;
   const int u_end = p.KB * NCH;
   typename B::CR ring[D];
 #pragma unroll
@@ -180,7 +184,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_rows_kernel(GemvArgs p) {
     const int k = 4 * i;
     float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
     if (k < p.K) {
-      v = *reinterpret_cast<const float4*>(p.x + k);
+      v = *reinterpret_cast<const float4*>(xin + k);
       if (p.norm_w) {
         ss = __builtin_fmaf(v.x, v.x, ss);
         ss = __builtin_fmaf(v.y, v.y, ss);
@@ -248,9 +252,165 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_rows_kernel(GemvArgs p) {
       const int row = tile * 64 + rr;
       if (row < p.m) {
         const float y = p.add ? s + p.add[row] : s;
-        p.y[row] = y;
+        yout[row] = y;
         key = argmax_key(y, row);
       }
+    }
+    if (p.best) wave_argmax_fold(key, p.best);
+  }
+}
+
+// Tile GEMV for many tiles (big matrices, stacks of matrices): a workgroup owns one 64-row tile
+// (lane = row) and its waves take the tile's steps in turn (one 256-quant super-block, or four
+// 32-blocks). A step's planes are loaded whole into registers through a buffer
+// resource whose slab offset is a scalar, the next step's loads are in flight while the current
+// one is decoded (two register sets, alternated by hand: no copies, no runtime index), and the
+// weight loads of the first step go out before x is staged. Blocks past the row's end read as
+// zero (resource bound) against zero x, so ragged block counts need no branches. Wave partial
+// sums are folded in wave order (deterministic).
+template <int T> inline constexpr int kTileStepBlocks = Blk<T>::QK == 256 ? 1 : 4;
+
+template <int T, int WAVES, bool HALF>
+__global__ __launch_bounds__(WAVES * 64) void gemv_tile_kernel(GemvArgs p) {
+  using B = Blk<T>;
+  constexpr int NCH = B::NCH;
+  constexpr int G = kTileStepBlocks<T>;            // blocks per step
+  constexpr int SQ = G * B::QK;                    // quants per step
+  // LDS: x[nsteps * SQ] (zero past K), xs16[nsteps * SQ / 16], red[WAVES * 64], ssred[WAVES]
+  extern __shared__ __attribute__((aligned(16))) float smem[];
+  const int nb = p.batch > 1 ? p.batch : 1;
+  const int total = p.tiles * nb;
+  const int per = (total + 7) / 8;
+  const int gq = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
+  if (gq >= total) return;
+  const int mb = gq / p.tiles, tile = gq - mb * p.tiles;
+  const float* xin = p.x + (size_t)mb * p.x_stride;
+  float* yout = p.y + (size_t)mb * p.y_stride;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nsteps = (p.KB + G - 1) / G;
+  const int nx = nsteps * SQ;
+  float* xl = smem;
+  float* xs16 = smem + nx;
+  float* red = xs16 + nx / 16;
+  float* ssred = red + WAVES * 64;
+
+  const uint8_t* tb = p.W + (size_t)mb * p.w_stride + (size_t)tile * p.KB * B::SLAB;
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(tb, (uint32_t)(p.KB * B::SLAB));
+  typename B::R r0[G], r1[G];
+  auto load_step = [&](int st, typename B::R (&r)[G]) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) B::sload(rs, (uint32_t)((st * G + g) * B::SLAB), lane, r[g]);
+  };
+  if (wave < nsteps) {
+    if constexpr (B::NCH == 8 && HALF) B::template sload_half<0>(rs, (uint32_t)(wave * B::SLAB), lane, r0[0]);
+    else load_step(wave, r0);
+  }
+
+  // stage x * norm_w (zero past K) and its per-16 sums; sum of squares per thread
+  float ss = 0.0f;
+  for (int i = threadIdx.x; i < nx / 4; i += WAVES * 64) {
+    const int k = 4 * i;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (k < p.K) {
+      v = *reinterpret_cast<const float4*>(xin + k);
+      if (p.norm_w) {
+        ss = __builtin_fmaf(v.x, v.x, ss);
+        ss = __builtin_fmaf(v.y, v.y, ss);
+        ss = __builtin_fmaf(v.z, v.z, ss);
+        ss = __builtin_fmaf(v.w, v.w, ss);
+        const float4 w = *reinterpret_cast<const float4*>(p.norm_w + k);
+        v = make_float4(v.x * w.x, v.y * w.y, v.z * w.z, v.w * w.w);
+      }
+    }
+    reinterpret_cast<float4*>(xl)[i] = v;
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < nx / 16; i += WAVES * 64) {
+    const float4* q = reinterpret_cast<const float4*>(xl + 16 * i);
+    float t = 0.0f;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) { const float4 u = q[v]; t += u.x; t += u.y; t += u.z; t += u.w; }
+    xs16[i] = t;
+  }
+  __syncthreads();
+
+  float acc = 0.0f;
+  auto step = [&](int st, const typename B::R (&r)[G]) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float* xb = xl + (st * G + g) * B::QK;
+      const float* xs = xs16 + (st * G + g) * (B::QK / 16);
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) {
+        Run a, b;
+        B::decode(r[g], c, a, b);
+        acc += run_dot<T>(a, xb, xs);
+        acc += run_dot<T>(b, xb, xs);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  };
+  if constexpr (B::NCH == 8 && HALF) {
+    // super-blocks: the pipeline runs on half blocks (chunks 0-3 / 4-7), so one block's worth
+    // of registers keeps the next half in flight
+#pragma unroll 1
+    for (int st = wave; st < nsteps; st += WAVES) {
+      const uint32_t so = (uint32_t)(st * B::SLAB);
+      B::template sload_half<1>(rs, so, lane, r1[0]);
+      const float* xb = xl + st * B::QK;
+      const float* xs = xs16 + st * (B::QK / 16);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        Run a, b;
+        B::decode(r0[0], c, a, b);
+        acc += run_dot<T>(a, xb, xs);
+        acc += run_dot<T>(b, xb, xs);
+        __builtin_amdgcn_sched_barrier(0);   // keep each chunk's LDS reads with its math
+      }
+      if (st + WAVES < nsteps) B::template sload_half<0>(rs, (uint32_t)((st + WAVES) * B::SLAB), lane, r0[0]);
+#pragma unroll
+      for (int c = 4; c < 8; ++c) {
+        Run a, b;
+        B::decode(r1[0], c, a, b);
+        acc += run_dot<T>(a, xb, xs);
+        acc += run_dot<T>(b, xb, xs);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  } else {
+    for (int st = wave; st < nsteps; st += 2 * WAVES) {
+      if (st + WAVES < nsteps) load_step(st + WAVES, r1);
+      step(st, r0);
+      if (st + WAVES >= nsteps) break;
+      if (st + 2 * WAVES < nsteps) load_step(st + 2 * WAVES, r0);
+      step(st + WAVES, r1);
+    }
+  }
+
+  red[wave * 64 + lane] = acc;
+  if (p.norm_w) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+    if (lane == 0) ssred[wave] = ss;
+  }
+  __syncthreads();
+  if (wave == 0) {
+    float sum = red[lane];
+#pragma unroll
+    for (int w = 1; w < WAVES; ++w) sum += red[w * 64 + lane];
+    if (p.norm_w) {
+      float t = ssred[0];
+#pragma unroll
+      for (int w = 1; w < WAVES; ++w) t += ssred[w];
+      sum *= 1.0f / sqrtf(t / (float)p.K + p.norm_eps);
+    }
+    const int row = tile * 64 + lane;
+    unsigned long long key = 0;
+    if (row < p.m) {
+      const float y = p.add ? sum + p.add[row] : sum;
+      yout[row] = y;
+      key = argmax_key(y, row);
     }
     if (p.best) wave_argmax_fold(key, p.best);
   }
@@ -299,7 +459,7 @@ __global__ __launch_bounds__(64) void dequant_kernel(const uint8_t* __restrict__
 template <int T, int R>
 static hipError_t launch_rows(const GemvArgs& a, int waves, hipStream_t s) {
   const size_t lds = ((size_t)a.KB * Blk<T>::QK * 17 / 16 + 16 * R + 16) * sizeof(float);
-  const unsigned grid = (unsigned)((a.groups + 7) / 8 * 8);
+  const unsigned grid = (unsigned)(((size_t)a.groups * (a.batch > 1 ? a.batch : 1) + 7) / 8 * 8);
   if (waves == 16) {
     hipLaunchKernelGGL((gemv_rows_kernel<T, R, 16>), dim3(grid), dim3(1024), lds, s, a);
   } else if (waves == 8) {
@@ -311,10 +471,31 @@ static hipError_t launch_rows(const GemvArgs& a, int waves, hipStream_t s) {
 }
 
 template <int T>
+static hipError_t launch_tile(const GemvArgs& a, int waves, hipStream_t s) {
+  constexpr int G = kTileStepBlocks<T>;
+  constexpr int SQ = G * Blk<T>::QK;
+  const size_t nx = (size_t)((a.KB + G - 1) / G) * SQ;
+  const unsigned grid = (unsigned)(((size_t)a.tiles * (a.batch > 1 ? a.batch : 1) + 7) / 8 * 8);
+  const int w = waves >= 8 ? 8 : 4;
+  const size_t lds = (nx + nx / 16 + (size_t)w * 64 + w) * sizeof(float);
+  // super-blocks: half-block pipelining pays once a wave has two or more blocks to stream;
+  // with one block per wave the whole block is loaded before x is staged
+  const bool half = Blk<T>::NCH == 8 && a.KB >= 2 * w;
+  if (w == 8) {
+    if (half) hipLaunchKernelGGL((gemv_tile_kernel<T, 8, true>), dim3(grid), dim3(512), lds, s, a);
+    else hipLaunchKernelGGL((gemv_tile_kernel<T, 8, false>), dim3(grid), dim3(512), lds, s, a);
+  } else {
+    if (half) hipLaunchKernelGGL((gemv_tile_kernel<T, 4, true>), dim3(grid), dim3(256), lds, s, a);
+    else hipLaunchKernelGGL((gemv_tile_kernel<T, 4, false>), dim3(grid), dim3(256), lds, s, a);
+  }
+  return hipGetLastError();
+}
+
+template <int T>
 static hipError_t launch_gemv_t(const GemvArgs& a, int waves, hipStream_t s) {
   if (a.rows_per_group) {
     switch (a.rows_per_group) {
-      case 64: return launch_rows<T, 64>(a, waves, s);
+      case 64: return launch_tile<T>(a, waves, s);
       case 16: return launch_rows<T, 16>(a, waves, s);
       case 8: return launch_rows<T, 8>(a, waves, s);
       case 4: return launch_rows<T, 4>(a, waves, s);

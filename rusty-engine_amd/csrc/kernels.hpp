@@ -20,6 +20,11 @@ struct GemvArgs {
   const float* norm_w;          // nullptr, or x is RMS-normalised first: x * (1/sqrt(mean(x^2)+eps)) * norm_w
   float norm_eps;
   unsigned long long* best;     // nullptr, or kArgmaxSlots slots max-folded with argmax_key(y[r], r)
+  // row-group launch over a stack of same-shape matrices: matrix b at W + b * w_stride reads
+  // x + b * x_stride and writes y + b * y_stride (batch <= 1: one matrix)
+  int batch;
+  size_t w_stride;
+  int x_stride, y_stride;
 };
 
 constexpr int kArgmaxSlots = 8;

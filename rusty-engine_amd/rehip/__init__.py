@@ -38,7 +38,8 @@ EXPORTS = ("re_init", "re_last_error", "re_version", "re_row_bytes", "re_tiled_b
            "re_moe_forward_dev", "re_qmat_matvec_ex_dev", "re_rmsnorm_dev", "re_rope_dev", "re_kv_append_dev",
            "re_attention_dev", "re_add_dev", "re_swiglu_dev", "re_argmax_dev", "re_embed_dev", "re_pos_add_dev",
            "re_ffn_create", "re_ffn_destroy", "re_ffn_forward_dev", "re_attention_work_bytes",
-           "re_qkv_rope_append_dev", "re_decode_advance_dev")
+           "re_qkv_rope_append_dev", "re_decode_advance_dev",
+           "re_qmat_create_stacked", "re_qmat_count", "re_qmat_matvec_stacked_dev")
 
 
 class RehipError(RuntimeError):
@@ -86,6 +87,10 @@ def lib() -> C.CDLL:
         L.re_moe_destroy.restype = None
         L.re_moe_forward.argtypes = [_vp, _vp, _sz, _sz, _vp, _vp, _vp, C.c_int]
         L.re_moe_forward_dev.argtypes = [_vp, _vp, _sz, _sz, _vp, _vp, _vp, C.c_int, _vp]
+        L.re_qmat_create_stacked.argtypes = [C.c_uint32, _vp, _sz, _sz, _sz, _sz, C.POINTER(_vp)]
+        L.re_qmat_count.argtypes = [_vp]
+        L.re_qmat_count.restype = _sz
+        L.re_qmat_matvec_stacked_dev.argtypes = [_vp, _sz, _sz, _vp, _sz, _vp, _sz, _vp]
         L.re_qmat_matvec_ex_dev.argtypes = [_vp, _vp, _vp, C.c_float, _vp, _vp, _vp, _vp]
         L.re_rmsnorm_dev.argtypes = [_vp, _vp, _sz, _sz, C.c_float, _vp, _vp]
         L.re_rope_dev.argtypes = [_vp, _sz, _sz, _sz, C.c_float, _vp, C.c_int, _vp]
@@ -186,6 +191,23 @@ class QMat:
         h = _vp()
         _check(lib().re_qmat_create(ggml_type, src.ctypes.data, src.size, m, n, C.byref(h)))
         return cls(h.value, ggml_type, m, n)
+
+    @classmethod
+    def from_bytes_stacked(cls, ggml_type: int, data, m: int, n: int, count: int) -> "QMat":
+        """`count` matrices of m x n, their GGUF bytes one after the other."""
+        src = _u8(data)
+        h = _vp()
+        _check(lib().re_qmat_create_stacked(ggml_type, src.ctypes.data, src.size, m, n, count, C.byref(h)))
+        return cls(h.value, ggml_type, m, n)
+
+    def count(self) -> int:
+        return lib().re_qmat_count(self._h)
+
+    def matvec_stacked_dev(self, first: int, count: int, x_dev, x_stride: int, y_dev, y_stride: int,
+                           stream=None) -> None:
+        """y_b = W_b x_b for matrices first .. first + count - 1, one launch (strides in floats)."""
+        _check(lib().re_qmat_matvec_stacked_dev(self._h, first, count, _dev_ptr(x_dev), x_stride, _dev_ptr(y_dev),
+                                                y_stride, _stream_ptr(stream)))
 
     def rows(self) -> int:
         return lib().re_qmat_rows(self._h)

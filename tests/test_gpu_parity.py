@@ -170,6 +170,43 @@ def test_gemv_is_deterministic_and_equals_rows1_matmul():
     assert np.array_equal(q.matmul(x, 1, rehip.MODE_BF16), a)
 
 
+@pytest.mark.parametrize("t,m,n,count", [(rehip.Q6_K, 896, 4864, 5), (rehip.Q4_K, 130, 896, 3),
+                                         (rehip.Q8_0, 64, 14336, 2), (rehip.Q5_0, 4864, 896, 2)])
+def test_stacked_gemv_equals_single_launches(t, m, n, count):
+    """One launch over a stack of matrices against the oracle (f32 bound) and one launch per
+    matrix (equal up to summation order: the stack's launch shape is planned for all of it),
+    also with a shared x, a sub-range of the stack and, for K > 12288, the per-matrix split
+    fallback."""
+    rng = np.random.default_rng(m + n + count)
+    ws = [synth.weight_bytes(rng, t, m, n) for _ in range(count)]
+    st = rehip.QMat.from_bytes_stacked(t, np.concatenate(ws), m, n, count)
+    assert st.count() == count
+    singles = [qmat(t, w, m, n) for w in ws]
+    xs = rng.standard_normal((count, n)).astype(np.float32)
+    dx = hip.DeviceBuffer.from_array(xs)
+    dy = hip.DeviceBuffer(count * (m + 3) * 4)
+    st.matvec_stacked_dev(0, count, dx, n, dy, m + 3)
+    hip.synchronize()
+    got = dy.download(np.float32, count * (m + 3)).reshape(count, m + 3)[:, :m]
+    for b in range(count):
+        one = singles[b].matvec(xs[b])
+        np.testing.assert_allclose(got[b], one, rtol=0, atol=1e-5 * np.abs(one).max())
+        err = np.abs(got[b].astype(np.float64) - O.qmat_matvec(t, ws[b], m, n, xs[b]))
+        assert np.all(err <= F32_TOL * O.qmat_absdot(t, ws[b], m, n, xs[b], 1)), b
+    # shared x, matrices 1..count-1
+    st.matvec_stacked_dev(1, count - 1, dx, 0, dy, m)
+    hip.synchronize()
+    got = dy.download(np.float32, (count - 1) * m).reshape(count - 1, m)
+    for b in range(1, count):
+        one = singles[b].matvec(xs[0])
+        np.testing.assert_allclose(got[b - 1], one, rtol=0, atol=1e-5 * np.abs(one).max())
+    with pytest.raises(rehip.RehipError):
+        st.matvec_stacked_dev(1, count, dx, n, dy, m)
+    st.close()
+    for q in singles:
+        q.close()
+
+
 def test_lm_head_gemv_q8_0_full_size():
     rng = np.random.default_rng(305)
     t, m, n = rehip.Q8_0, 151936, 896
