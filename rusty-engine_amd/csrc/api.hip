@@ -167,7 +167,8 @@ void rows_shape(size_t tiles, size_t units, int* rows_per_group, int* waves) {
   const size_t per_wave = 64 / (size_t)r;
   const size_t w = (slots + per_wave - 1) / per_wave;
   *waves = w <= 4 ? 4 : w <= 8 ? 8 : 16;
-  if (const size_t e = env_size("REHIP_GEMV_WAVES", 0); e == 4 || e == 8 || e == 16) *waves = (int)e;
+  if (r == 64) *waves = 4;                   // tile kernel: four waves (two: see below)
+  if (const size_t e = env_size("REHIP_GEMV_WAVES", 0); e == 2 || e == 4 || e == 8 || e == 16) *waves = (int)e;
   *rows_per_group = r;
 }
 

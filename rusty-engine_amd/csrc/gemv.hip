@@ -268,6 +268,15 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_rows_kernel(GemvArgs p) {
 // weight loads of the first step go out before x is staged. Blocks past the row's end read as
 // zero (resource bound) against zero x, so ragged block counts need no branches. Wave partial
 // sums are folded in wave order (deterministic).
+// 0, computed from v so that the compiler cannot move what uses it above the arrival of v (the
+// x reads of a chunk then wait for the chunk's weights instead of all being hoisted to the top
+// of the loop, where their registers would crowd out the weight prefetch)
+__device__ __forceinline__ int after_data(uint32_t v) {
+  int z;
+  asm volatile("v_and_b32 %0, 0, %1" : "=v"(z) : "v"(v));
+  return z;
+}
+
 template <int T> inline constexpr int kTileStepBlocks = Blk<T>::QK == 256 ? 1 : 4;
 
 template <int T, int WAVES, bool HALF>
@@ -345,9 +354,9 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_tile_kernel(GemvArgs p) {
       for (int c = 0; c < NCH; ++c) {
         Run a, b;
         B::decode(r[g], c, a, b);
-        acc += run_dot<T>(a, xb, xs);
-        acc += run_dot<T>(b, xb, xs);
-        __builtin_amdgcn_sched_barrier(0);
+        const int z = after_data(__float_as_uint(acc));
+        acc += run_dot<T>(a, xb + z, xs + z);
+        acc += run_dot<T>(b, xb + z, xs + z);
       }
     }
   };
@@ -364,18 +373,18 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_tile_kernel(GemvArgs p) {
       for (int c = 0; c < 4; ++c) {
         Run a, b;
         B::decode(r0[0], c, a, b);
-        acc += run_dot<T>(a, xb, xs);
-        acc += run_dot<T>(b, xb, xs);
-        __builtin_amdgcn_sched_barrier(0);   // keep each chunk's LDS reads with its math
+        const int z = after_data(__float_as_uint(acc));
+        acc += run_dot<T>(a, xb + z, xs + z);
+        acc += run_dot<T>(b, xb + z, xs + z);
       }
       if (st + WAVES < nsteps) B::template sload_half<0>(rs, (uint32_t)((st + WAVES) * B::SLAB), lane, r0[0]);
 #pragma unroll
       for (int c = 4; c < 8; ++c) {
         Run a, b;
         B::decode(r1[0], c, a, b);
-        acc += run_dot<T>(a, xb, xs);
-        acc += run_dot<T>(b, xb, xs);
-        __builtin_amdgcn_sched_barrier(0);
+        const int z = after_data(__float_as_uint(acc));
+        acc += run_dot<T>(a, xb + z, xs + z);
+        acc += run_dot<T>(b, xb + z, xs + z);
       }
     }
   } else {
@@ -476,7 +485,7 @@ static hipError_t launch_tile(const GemvArgs& a, int waves, hipStream_t s) {
   constexpr int SQ = G * Blk<T>::QK;
   const size_t nx = (size_t)((a.KB + G - 1) / G) * SQ;
   const unsigned grid = (unsigned)(((size_t)a.tiles * (a.batch > 1 ? a.batch : 1) + 7) / 8 * 8);
-  const int w = waves >= 8 ? 8 : 4;
+  const int w = waves >= 8 ? 8 : waves <= 2 ? 2 : 4;
   const size_t lds = (nx + nx / 16 + (size_t)w * 64 + w) * sizeof(float);
   // super-blocks: half-block pipelining pays once a wave has two or more blocks to stream;
   // with one block per wave the whole block is loaded before x is staged
@@ -484,6 +493,9 @@ static hipError_t launch_tile(const GemvArgs& a, int waves, hipStream_t s) {
   if (w == 8) {
     if (half) hipLaunchKernelGGL((gemv_tile_kernel<T, 8, true>), dim3(grid), dim3(512), lds, s, a);
     else hipLaunchKernelGGL((gemv_tile_kernel<T, 8, false>), dim3(grid), dim3(512), lds, s, a);
+  } else if (w == 2) {
+    if (half) hipLaunchKernelGGL((gemv_tile_kernel<T, 2, true>), dim3(grid), dim3(128), lds, s, a);
+    else hipLaunchKernelGGL((gemv_tile_kernel<T, 2, false>), dim3(grid), dim3(128), lds, s, a);
   } else {
     if (half) hipLaunchKernelGGL((gemv_tile_kernel<T, 4, true>), dim3(grid), dim3(256), lds, s, a);
     else hipLaunchKernelGGL((gemv_tile_kernel<T, 4, false>), dim3(grid), dim3(256), lds, s, a);
