@@ -110,6 +110,28 @@ int re_moe_forward_dev(re_moe *e, const float *d_x, size_t tokens, size_t top_k,
                        const uint32_t *ids, const float *weights, float *d_out, int mode,
                        void *stream);
 
+/* ---- MoE layer with the routing on the device (moe.rs:75-125, 360-388): no host round trip --
+ * re_moe_router_logits_dev: logits[t][e] = router_w[e] . x[t] (router_w f32, n_experts x hidden;
+ *   the matvec of moe.rs:367).
+ * re_moe_route_dev: top_k experts per token (ties to the lower expert index, as the reference's
+ *   stable descending sort) and their weights: RE_GATE_SOFTMAX = softmax over the chosen logits
+ *   (top_k, moe.rs:75-93), RE_GATE_SIGMOID = per-expert sigmoid renormalised over the chosen
+ *   (top_k_sigmoid, moe.rs:98-118). n_experts <= 1024. NaN logits rank as -inf.
+ * re_moe_forward_routed_dev: re_moe_forward_dev with device ids/weights (tokens x top_k); the
+ *   grouping by expert and the task lists are built by a kernel; tokens * top_k <= 8192. An id
+ *   outside [0, n_experts) contributes nothing.
+ * re_moe_layer_dev: the three in one stream (scratch for logits/ids/weights is kept by e). */
+#define RE_GATE_SOFTMAX 0
+#define RE_GATE_SIGMOID 1
+int re_moe_router_logits_dev(const float *d_x, const float *d_router_w, size_t tokens, size_t hidden,
+                             size_t n_experts, float *d_logits, void *stream);
+int re_moe_route_dev(const float *d_logits, size_t tokens, size_t n_experts, size_t top_k, int gate,
+                     int *d_ids, float *d_weights, void *stream);
+int re_moe_forward_routed_dev(re_moe *e, const float *d_x, size_t tokens, size_t top_k, const int *d_ids,
+                              const float *d_weights, float *d_out, int mode, void *stream);
+int re_moe_layer_dev(re_moe *e, const float *d_x, size_t tokens, const float *d_router_w, size_t top_k,
+                     int gate, float *d_out, int mode, void *stream);
+
 /* ---- device-resident transformer steps (src/forward.rs, src/infer.rs, src/runner.rs) ------
  * Device pointers, enqueued on `stream`. Positions come from a device int (*d_pos) so that a
  * captured graph serves every decode step; re_pos_add_dev advances it on the stream. */

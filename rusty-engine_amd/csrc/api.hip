@@ -132,6 +132,7 @@ struct re_moe {
   std::mutex mu;
   hipStream_t stream = nullptr;
   Staging sx, sout, sg, su, sh, syp, smeta;
+  Staging dmeta, droute;                  // device-routed path: plan + task lists; logits, ids, weights
   // pinned host staging of the per-call routing metadata, reused once its last upload is done
   void* hmeta = nullptr;
   size_t hmeta_cap = 0;
@@ -565,6 +566,8 @@ int re_moe_create(uint32_t gate_type, const uint8_t* gate, size_t gate_bytes, ui
 
 void re_moe_destroy(re_moe* e) {
   if (!e) return;
+  e->dmeta.release();
+  e->droute.release();
   if (e->stream) (void)hipStreamSynchronize(e->stream);
   if (e->d_gate) (void)hipFree(e->d_gate);
   if (e->d_up) (void)hipFree(e->d_up);
@@ -575,6 +578,192 @@ void re_moe_destroy(re_moe* e) {
   if (e->hmeta) (void)hipHostFree(e->hmeta);
   if (e->stream) (void)hipStreamDestroy(e->stream);
   delete e;
+}
+
+// ---- MoE with the routing on the device (row F3: no host round trip) ------------------------
+int re_moe_route_dev(const float* d_logits, size_t tokens, size_t n_experts, size_t top_k, int gate, int* d_ids,
+                     float* d_weights, void* stream) {
+  if (!d_logits || !d_ids || !d_weights) return fail(RE_ERR_ARG, "null pointer");
+  if (tokens == 0) return RE_OK;
+  if (n_experts == 0 || n_experts > 1024 || top_k == 0 || top_k > n_experts || tokens > (1u << 24))
+    return fail(RE_ERR_SIZE, "route: %zu experts (<= 1024), top_k %zu, %zu tokens", n_experts, top_k, tokens);
+  if (gate != RE_GATE_SOFTMAX && gate != RE_GATE_SIGMOID) return fail(RE_ERR_ARG, "unknown gate %d", gate);
+  HIP_TRY(launch_moe_route(d_logits, (int)tokens, (int)n_experts, (int)top_k, gate, d_ids, d_weights,
+                           (hipStream_t)stream));
+  return RE_OK;
+}
+
+int re_moe_router_logits_dev(const float* d_x, const float* d_router_w, size_t tokens, size_t hidden,
+                             size_t n_experts, float* d_logits, void* stream) {
+  if (!d_x || !d_router_w || !d_logits) return fail(RE_ERR_ARG, "null pointer");
+  if (tokens == 0) return RE_OK;
+  if (hidden == 0 || hidden > 16384 || n_experts == 0 || n_experts > 65535 * 4 || tokens > 65535)
+    return fail(RE_ERR_SIZE, "router: %zu tokens x %zu hidden, %zu experts", tokens, hidden, n_experts);
+  HIP_TRY(launch_moe_router_logits(d_x, d_router_w, (int)tokens, (int)hidden, (int)n_experts, d_logits,
+                                   (hipStream_t)stream));
+  return RE_OK;
+}
+
+int re_moe_forward_routed_dev(re_moe* e, const float* d_x, size_t tokens, size_t top_k, const int* d_ids,
+                              const float* d_weights, float* d_out, int mode, void* stream) {
+  if (!e) return fail(RE_ERR_ARG, "null moe");
+  if (mode != RE_MODE_BF16 && mode != RE_MODE_F32) return fail(RE_ERR_ARG, "unknown mode %d", mode);
+  if (tokens == 0) return RE_OK;
+  if (!d_x || !d_out || !d_ids || !d_weights || top_k == 0) return fail(RE_ERR_ARG, "null pointer or top_k = 0");
+  const size_t pairs = tokens * top_k;
+  if (pairs > (size_t)kMoeMaxDevicePairs || e->n_experts > 1024)
+    return fail(RE_ERR_SIZE, "device routing takes <= %d (token, expert) pairs and <= 1024 experts",
+                kMoeMaxDevicePairs);
+  if (tokens * e->hidden * sizeof(float) >= (1ull << 31) || e->gg.bytes * e->n_experts >= (1ull << 31) ||
+      e->gd.bytes * e->n_experts >= (1ull << 31) || pairs * e->inter * sizeof(float) >= (1ull << 31))
+    return fail(RE_ERR_SIZE, "MoE operands must stay below 2 GiB");
+  hipStream_t s = (hipStream_t)stream;
+  // the grouping runs on the device, so the path is chosen from the batch size alone: the
+  // grouped GEMV while an expert would get few rows on average (pairs <= 2 x experts)
+  const bool gemv = pairs <= 2 * e->n_experts;
+  MoePlanShape sh{};
+  sh.pairs = (int)pairs;
+  sh.k = (int)top_k;
+  sh.n_experts = (int)e->n_experts;
+  sh.gemv = gemv;
+  sh.chunk = gemv ? (tokens == 1 ? 1 : kMoeGemvBatch) : kMoeTile;
+  if (gemv) {
+    sh.rows_gu = kMoeGemvRows;
+    sh.tiles_gu = (int)((e->inter + kMoeGemvRows - 1) / kMoeGemvRows);
+    sh.tiles_d = (int)((e->hidden + kMoeGemvRows - 1) / kMoeGemvRows);
+  } else {
+    sh.rows_gu = kMoeTile;
+    sh.tiles_gu = (int)((e->inter + kMoeTile - 1) / kMoeTile);
+    sh.tiles_d = (int)((e->hidden + kMoeTile - 1) / kMoeTile);
+  }
+  const int max_chunks = (int)((pairs + sh.chunk - 1) / sh.chunk + std::min(pairs, e->n_experts));
+  sh.max_gu = max_chunks * sh.tiles_gu;
+  sh.max_d = max_chunks * sh.tiles_d;
+  int rc;
+  const size_t act = pairs * e->inter * sizeof(float);
+  if ((rc = e->dmeta.ensure(moe_meta_bytes(sh))) || (rc = e->sh.ensure(act)) ||
+      (rc = e->syp.ensure(pairs * e->hidden * sizeof(float))))
+    return rc;
+  const bool dual = gemv && e->gg.type == e->gu.type;
+  if (!dual && ((rc = e->sg.ensure(act)) || (rc = e->su.ensure(act)))) return rc;
+  int* dm = (int*)e->dmeta.p;
+  HIP_TRY(launch_moe_plan(d_ids, sh, dm, s));
+  const int* xrow = dm;
+  const int* pos = dm + pairs;
+  const int* ntasks = dm + 2 * pairs;
+  const uint8_t* tasks = (const uint8_t*)(dm + 2 * pairs + 4);
+  if (gemv) {
+    const MoeGemvTask* tg = (const MoeGemvTask*)tasks;
+    MoeGemvArgs g{};
+    g.max_rows = sh.chunk;
+    g.X = d_x;
+    g.xrow = xrow;
+    g.tasks = tg;
+    g.ntasks = ntasks;
+    g.m = (int)e->inter;
+    g.K = (int)e->hidden;
+    g.KB = (int)e->gg.kb;
+    g.ldy = (int)e->inter;
+    g.w_stride = e->gg.bytes;
+    if (dual) {
+      g.W0 = e->d_gate;
+      g.W1 = e->d_up;
+      g.Y = (float*)e->sh.p;
+      HIP_TRY(launch_moe_gemv(e->gg.type, true, g, sh.max_gu, s));
+    } else {
+      g.W0 = e->d_gate;
+      g.Y = (float*)e->sg.p;
+      HIP_TRY(launch_moe_gemv(e->gg.type, false, g, sh.max_gu, s));
+      g.W0 = e->d_up;
+      g.w_stride = e->gu.bytes;
+      g.KB = (int)e->gu.kb;
+      g.Y = (float*)e->su.p;
+      HIP_TRY(launch_moe_gemv(e->gu.type, false, g, sh.max_gu, s));
+      HIP_TRY(launch_swiglu((const float*)e->sg.p, (const float*)e->su.p, (float*)e->sh.p, pairs * e->inter, s));
+    }
+    MoeGemvArgs d{};
+    d.max_rows = sh.chunk;
+    d.W0 = e->d_down;
+    d.w_stride = e->gd.bytes;
+    d.X = (const float*)e->sh.p;
+    d.xrow = nullptr;
+    d.Y = (float*)e->syp.p;
+    d.tasks = tg + sh.max_gu;
+    d.ntasks = ntasks + 1;
+    d.m = (int)e->hidden;
+    d.K = (int)e->inter;
+    d.KB = (int)e->gd.kb;
+    d.ldy = (int)e->hidden;
+    HIP_TRY(launch_moe_gemv(e->gd.type, false, d, sh.max_d, s));
+  } else {
+    const GemmTask* tg = (const GemmTask*)tasks;
+    GemmArgs a{};
+    a.X = d_x;
+    a.x_bytes = (uint32_t)(tokens * e->hidden * sizeof(float));
+    a.splits = 1;
+    a.steps_per_split = 1 << 30;
+    a.tasks = tg;
+    a.ntasks = ntasks;
+    a.xrow = xrow;
+    a.m = (int)e->inter;
+    a.K = (int)e->hidden;
+    a.KB = (int)e->gg.kb;
+    a.tiles = (int)e->gg.tiles;
+    a.ldy = (int)e->inter;
+    a.w_stride = e->gg.bytes;
+    a.w_bytes = (uint32_t)(e->gg.bytes * e->n_experts);
+    a.W = e->d_gate;
+    a.Y = (float*)e->sg.p;
+    const int kg_gu = gemm_kgroups(GemmTile::k64x64, mode, (long)sh.max_gu, (int)((e->hidden + kGemmBK - 1) / kGemmBK));
+    const int kg_d = gemm_kgroups(GemmTile::k64x64, mode, (long)sh.max_d, (int)((e->inter + kGemmBK - 1) / kGemmBK));
+    HIP_TRY(launch_gemm(e->gg.type, mode, a, sh.max_gu, GemmTile::k64x64, kg_gu, s));
+    a.W = e->d_up;
+    a.w_stride = e->gu.bytes;
+    a.w_bytes = (uint32_t)(e->gu.bytes * e->n_experts);
+    a.KB = (int)e->gu.kb;
+    a.tiles = (int)e->gu.tiles;
+    a.Y = (float*)e->su.p;
+    HIP_TRY(launch_gemm(e->gu.type, mode, a, sh.max_gu, GemmTile::k64x64, kg_gu, s));
+    HIP_TRY(launch_swiglu((const float*)e->sg.p, (const float*)e->su.p, (float*)e->sh.p, pairs * e->inter, s));
+    GemmArgs d{};
+    d.X = (const float*)e->sh.p;
+    d.x_bytes = (uint32_t)act;
+    d.splits = 1;
+    d.steps_per_split = 1 << 30;
+    d.tasks = tg + sh.max_gu;
+    d.ntasks = ntasks + 1;
+    d.xrow = nullptr;
+    d.m = (int)e->hidden;
+    d.K = (int)e->inter;
+    d.KB = (int)e->gd.kb;
+    d.tiles = (int)e->gd.tiles;
+    d.ldy = (int)e->hidden;
+    d.w_stride = e->gd.bytes;
+    d.w_bytes = (uint32_t)(e->gd.bytes * e->n_experts);
+    d.W = e->d_down;
+    d.Y = (float*)e->syp.p;
+    HIP_TRY(launch_gemm(e->gd.type, mode, d, sh.max_d, GemmTile::k64x64, kg_d, s));
+  }
+  HIP_TRY(launch_combine((const float*)e->syp.p, pos, d_weights, d_out, (int)tokens, (int)top_k, (int)e->hidden, s));
+  return RE_OK;
+}
+
+int re_moe_layer_dev(re_moe* e, const float* d_x, size_t tokens, const float* d_router_w, size_t top_k, int gate,
+                     float* d_out, int mode, void* stream) {
+  if (!e || !d_x || !d_router_w || !d_out) return fail(RE_ERR_ARG, "null pointer");
+  if (tokens == 0) return RE_OK;
+  if (tokens > 65535) return fail(RE_ERR_SIZE, "%zu tokens", tokens);
+  const size_t E = e->n_experts;
+  const size_t logit_bytes = (tokens * E * sizeof(float) + 255) / 256 * 256;
+  const size_t id_bytes = (tokens * top_k * sizeof(int) + 255) / 256 * 256;
+  int rc;
+  if ((rc = e->droute.ensure(logit_bytes + 2 * id_bytes))) return rc;
+  float* logits = (float*)e->droute.p;
+  int* ids = (int*)((uint8_t*)e->droute.p + logit_bytes);
+  float* w = (float*)((uint8_t*)e->droute.p + logit_bytes + id_bytes);
+  if ((rc = re_moe_router_logits_dev(d_x, d_router_w, tokens, e->hidden, E, logits, stream))) return rc;
+  if ((rc = re_moe_route_dev(logits, tokens, E, top_k, gate, ids, w, stream))) return rc;
+  return re_moe_forward_routed_dev(e, d_x, tokens, top_k, ids, w, d_out, mode, stream);
 }
 
 int re_moe_forward_dev(re_moe* e, const float* d_x, size_t tokens, size_t top_k, const uint32_t* ids,

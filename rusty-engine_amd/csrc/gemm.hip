@@ -146,6 +146,7 @@ __global__ __launch_bounds__(WM* WN * 64 * KG) void gemm_kernel(GemmArgs p) {
   int mtile, r0, rn, split = 0;
   uint32_t wbase = 0;
   if constexpr (GROUPED) {
+    if (p.ntasks && (int)blockIdx.x >= *p.ntasks) return;   // grid sized for the most tasks
     const GemmTask t = p.tasks[blockIdx.x];
     mtile = t.mtile;
     r0 = t.r0;

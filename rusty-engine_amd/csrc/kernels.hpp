@@ -94,6 +94,7 @@ struct GemmArgs {
   float* partial;          // splits > 1: splits * N * ldy floats, summed by a second kernel
   const GemmTask* tasks;   // grouped launch: one task per workgroup (nullptr = dense grid)
   const int* xrow;         // grouped: X row of gathered row p (nullptr = p itself)
+  const int* ntasks;       // grouped: nullptr, or the task count on the device (larger grids exit early)
 };
 
 struct GemmPlan {
@@ -129,6 +130,7 @@ struct MoeGemvArgs {
   int max_rows;               // largest np over the tasks
   const float* norm_w;        // nullptr, or each X row is RMS-normalised first (as GemvArgs)
   float norm_eps;
+  const int* ntasks;          // nullptr, or the task count on the device (larger grids exit early)
 };
 constexpr int kMoeGemvRows = 16;   // weight rows per task
 constexpr int kMoeGemvWaves = 4;
@@ -159,6 +161,27 @@ hipError_t launch_embed(const float* table, int n_vocab, int d, const int* tok, 
 hipError_t launch_pos_add(int* pos, int delta, hipStream_t s);
 
 // MoE helpers
+// Device-side routing (moe.rs:75-125): top-k experts per token, gate 0 = softmax over the chosen
+// logits, 1 = per-expert sigmoid renormalised over the chosen
+hipError_t launch_moe_route(const float* logits, int tokens, int n_experts, int k, int gate, int* ids,
+                            float* weights, hipStream_t s);
+// logits[t][e] = router_w[e] . x[t] (f32)
+hipError_t launch_moe_router_logits(const float* x, const float* router_w, int tokens, int hidden, int n_experts,
+                                    float* logits, hipStream_t s);
+// Device-side grouping of tokens * k (token, slot) pairs by expert (pair order kept inside an
+// expert) and the task lists of the grouped launches. meta layout (ints): xrow[P] | pos[P] |
+// ntasks[2] | pad | tasks_gu[max_gu] | tasks_d[max_d]; chunk = rows per task (kMoeGemvBatch or 1
+// for the GEMV tasks, kMoeTile for GEMM tasks); rows_gu / rows_d = weight rows per task
+// (kMoeGemvRows or kMoeTile); gemv selects MoeGemvTask or GemmTask records.
+constexpr int kMoeMaxDevicePairs = 8192;
+struct MoePlanShape {
+  int pairs, k, n_experts, chunk, gemv;
+  int tiles_gu, tiles_d;        // weight-row tasks per chunk (ceil(inter/rows), ceil(hidden/rows))
+  int rows_gu;                  // weight rows per task (16 for GEMV tasks; GEMM tasks name a tile)
+  int max_gu, max_d;            // capacity of the task lists
+};
+size_t moe_meta_bytes(const MoePlanShape& sh);
+hipError_t launch_moe_plan(const int* ids, const MoePlanShape& sh, void* meta, hipStream_t s);
 hipError_t launch_swiglu(const float* g, const float* u, float* h, size_t n, hipStream_t s);
 hipError_t launch_combine(const float* yp, const int* pos, const float* w, float* out, int tokens,
                           int k, int hidden, hipStream_t s);

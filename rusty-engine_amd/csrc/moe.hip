@@ -32,9 +32,240 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
   float o = 0.0f;
   for (int j = 0; j < k; ++j) {
     const int p = pos[t * k + j];
+    if (p < 0) continue;                  // expert id out of range (device routing input)
     o = __fadd_rn(o, __fmul_rn(w[t * k + j], yp[(size_t)p * hidden + c]));
   }
   out[(size_t)t * hidden + c] = o;
+}
+
+// ---- device-side routing and grouping (no host round trip) --------------------------------
+
+// Router scores of one token: one wave per token; lane l holds experts l, l + 64, ...
+// Selection repeats a wave-wide argmax k times, ties to the lower expert index, which is the
+// order the reference's stable descending sort gives (moe.rs:75-93, 98-118). NaN scores are
+// treated as -inf (the reference's partial_cmp leaves their order unspecified).
+constexpr int kRouteMaxExperts = 1024;
+
+__global__ __launch_bounds__(64) void moe_route_kernel(const float* __restrict__ logits, int n_experts, int k,
+                                                       int gate, int* __restrict__ ids,
+                                                       float* __restrict__ weights) {
+  constexpr int EPL = kRouteMaxExperts / 64;
+  __shared__ float topv[kRouteMaxExperts];
+  __shared__ int topi[kRouteMaxExperts];
+  const int t = blockIdx.x, lane = threadIdx.x;
+  const float* row = logits + (size_t)t * n_experts;
+  float v[EPL];
+  bool taken[EPL];
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) {
+    const int e = lane + 64 * j;
+    float x = -INFINITY;
+    if (e < n_experts) {
+      x = row[e];
+      if (gate == 1) x = 1.0f / (1.0f + expf(-x));     // sigmoid (moe.rs:43-46)
+      if (x != x) x = -INFINITY;
+    }
+    v[j] = x;
+    taken[j] = e >= n_experts;
+  }
+  for (int r = 0; r < k; ++r) {
+    float bv = -INFINITY;
+    int be = 0x7fffffff;
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) {
+      const int e = lane + 64 * j;
+      if (!taken[j] && (v[j] > bv || (v[j] == bv && e < be))) { bv = v[j]; be = e; }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      const float ov = __shfl_xor(bv, off, 64);
+      const int oe = __shfl_xor(be, off, 64);
+      if (ov > bv || (ov == bv && oe < be)) { bv = ov; be = oe; }
+    }
+#pragma unroll
+    for (int j = 0; j < EPL; ++j)
+      if (lane + 64 * j == be) taken[j] = true;
+    if (lane == 0) { topv[r] = bv; topi[r] = be; }
+  }
+  __syncthreads();
+  if (lane != 0) return;
+  if (gate == 1) {
+    // weights = sig / sum of the chosen sigs, summed in order (moe.rs:108-117)
+    float ws = 0.0f;
+    for (int r = 0; r < k; ++r) ws += topv[r];
+    for (int r = 0; r < k; ++r) {
+      ids[t * k + r] = topi[r];
+      weights[t * k + r] = ws == 0.0f ? 0.0f : topv[r] / ws;
+    }
+  } else {
+    // softmax over the chosen logits (moe.rs:53-72): max, exp(v - max), sequential sum, divide
+    float mx = -INFINITY;
+    for (int r = 0; r < k; ++r) mx = fmaxf(mx, topv[r]);
+    float sum = 0.0f;
+    for (int r = 0; r < k; ++r) {
+      topv[r] = expf(topv[r] - mx);
+      sum += topv[r];
+    }
+    for (int r = 0; r < k; ++r) {
+      ids[t * k + r] = topi[r];
+      weights[t * k + r] = sum != 0.0f ? topv[r] / sum : topv[r];
+    }
+  }
+}
+
+// logits[t][e] = router_w[e] . x[t] (the f32 matvec of moe.rs:367): x[t] staged in LDS, one wave
+// per expert; lanes take every 64th element, then a fixed xor tree.
+__global__ __launch_bounds__(256) void moe_router_logits_kernel(const float* __restrict__ x,
+                                                                const float* __restrict__ w, int hidden,
+                                                                int n_experts, float* __restrict__ logits) {
+  extern __shared__ float xs[];
+  const int t = blockIdx.y;
+  const float* xr = x + (size_t)t * hidden;
+  for (int i = threadIdx.x; i < hidden; i += 256) xs[i] = xr[i];
+  __syncthreads();
+  const int lane = threadIdx.x & 63;
+  const int e = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (e >= n_experts) return;
+  const float* wr = w + (size_t)e * hidden;
+  float a = 0.0f;
+  for (int i = lane; i < hidden; i += 64) a = __builtin_fmaf(wr[i], xs[i], a);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) a += __shfl_xor(a, off, 64);
+  if (lane == 0) logits[(size_t)t * n_experts + e] = a;
+}
+
+// Grouping on the device, one 1024-thread workgroup: keys (expert << 13 | pair) are sorted by a
+// bitonic network in LDS (pair order inside an expert: the host grouping's order), then
+// xrow[slot] = pair / k and pos[pair] = slot; per-expert counts and starts give the chunks
+// (runs of `chunk` gathered rows) and the task lists, laid out exactly as the host planner lays
+// them out (expert, then chunk, then weight-row task). Pairs with an expert id out of range get
+// pos = -1 and no task (the combine skips them).
+__device__ __forceinline__ int* meta_xrow(void* m) { return (int*)m; }
+
+__global__ __launch_bounds__(1024) void moe_plan_kernel(const int* __restrict__ ids, MoePlanShape sh,
+                                                        int* __restrict__ meta) {
+  __shared__ uint32_t key[kMoeMaxDevicePairs];
+  __shared__ int cnt[kRouteMaxExperts], start[kRouteMaxExperts], cstart[kRouteMaxExperts + 1];
+  const int P = sh.pairs, E = sh.n_experts, tid = threadIdx.x;
+  int* xrow = meta;
+  int* pos = meta + P;
+  int* ntasks = meta + 2 * P;
+  uint8_t* tasks = (uint8_t*)(meta + 2 * P + 4);
+  int n2 = 1;
+  while (n2 < P) n2 <<= 1;
+  for (int e = tid; e < E; e += 1024) cnt[e] = 0;
+  __syncthreads();
+  for (int p = tid; p < n2; p += 1024) {
+    uint32_t kk = 0xffffffffu;
+    if (p < P) {
+      const int e = ids[p];
+      if (e >= 0 && e < E) {
+        kk = ((uint32_t)e << 13) | (uint32_t)p;
+        atomicAdd(&cnt[e], 1);
+      } else {
+        pos[p] = -1;
+      }
+    }
+    key[p] = kk;
+  }
+  __syncthreads();
+  // bitonic sort, ascending
+  for (int size = 2; size <= n2; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int i = tid; i < n2 / 2; i += 1024) {
+        const int lo = 2 * i - (i & (stride - 1));
+        const int hi = lo + stride;
+        const bool up = (lo & size) == 0;
+        const uint32_t a = key[lo], b = key[hi];
+        if ((a > b) == up) { key[lo] = b; key[hi] = a; }
+      }
+      __syncthreads();
+    }
+  }
+  if (tid == 0) {
+    int acc = 0, cacc = 0;
+    for (int e = 0; e < E; ++e) {
+      start[e] = acc;
+      acc += cnt[e];
+      cstart[e] = cacc;
+      cacc += (cnt[e] + sh.chunk - 1) / sh.chunk;
+    }
+    cstart[E] = cacc;
+    ntasks[0] = min(cacc * sh.tiles_gu, sh.max_gu);   // the capacities bound every count
+    ntasks[1] = min(cacc * sh.tiles_d, sh.max_d);
+  }
+  __syncthreads();
+  for (int i = tid; i < P; i += 1024) {
+    const uint32_t kk = key[i];
+    if (kk == 0xffffffffu) continue;
+    const int p = (int)(kk & 0x1fffu);
+    xrow[i] = p / sh.k;
+    pos[p] = i;
+  }
+  const int nch = cstart[E];
+  const int n_gu = min(nch * sh.tiles_gu, sh.max_gu), n_d = min(nch * sh.tiles_d, sh.max_d);
+  auto chunk_of = [&](int c, int& e, int& r0, int& rn) {
+    int lo = 0, hi = E - 1;                  // last expert with cstart <= c
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (cstart[mid] <= c) lo = mid; else hi = mid - 1;
+    }
+    e = lo;
+    const int r = (c - cstart[e]) * sh.chunk;
+    r0 = start[e] + r;
+    rn = min(sh.chunk, cnt[e] - r);
+  };
+  if (sh.gemv) {
+    MoeGemvTask* tg = (MoeGemvTask*)tasks;
+    MoeGemvTask* td = tg + sh.max_gu;
+    for (int t = tid; t < n_gu; t += 1024) {
+      int e, r0, rn;
+      chunk_of(t / sh.tiles_gu, e, r0, rn);
+      tg[t] = {e, (t % sh.tiles_gu) * sh.rows_gu, r0, rn};
+    }
+    for (int t = tid; t < n_d; t += 1024) {
+      int e, r0, rn;
+      chunk_of(t / sh.tiles_d, e, r0, rn);
+      td[t] = {e, (t % sh.tiles_d) * sh.rows_gu, r0, rn};
+    }
+  } else {
+    GemmTask* tg = (GemmTask*)tasks;
+    GemmTask* td = tg + sh.max_gu;
+    for (int t = tid; t < n_gu; t += 1024) {
+      int e, r0, rn;
+      chunk_of(t / sh.tiles_gu, e, r0, rn);
+      tg[t] = {e, t % sh.tiles_gu, r0, rn};
+    }
+    for (int t = tid; t < n_d; t += 1024) {
+      int e, r0, rn;
+      chunk_of(t / sh.tiles_d, e, r0, rn);
+      td[t] = {e, t % sh.tiles_d, r0, rn};
+    }
+  }
+}
+
+size_t moe_meta_bytes(const MoePlanShape& sh) {
+  const size_t rec = sh.gemv ? sizeof(MoeGemvTask) : sizeof(GemmTask);
+  return (size_t)(2 * sh.pairs + 4) * sizeof(int) + (size_t)(sh.max_gu + sh.max_d) * rec;
+}
+
+hipError_t launch_moe_route(const float* logits, int tokens, int n_experts, int k, int gate, int* ids,
+                            float* weights, hipStream_t s) {
+  hipLaunchKernelGGL(moe_route_kernel, dim3((unsigned)tokens), dim3(64), 0, s, logits, n_experts, k, gate, ids,
+                     weights);
+  return hipGetLastError();
+}
+
+hipError_t launch_moe_router_logits(const float* x, const float* router_w, int tokens, int hidden, int n_experts,
+                                    float* logits, hipStream_t s) {
+  hipLaunchKernelGGL(moe_router_logits_kernel, dim3((unsigned)((n_experts + 3) / 4), (unsigned)tokens), dim3(256),
+                     (size_t)hidden * sizeof(float), s, x, router_w, hidden, n_experts, logits);
+  return hipGetLastError();
+}
+
+hipError_t launch_moe_plan(const int* ids, const MoePlanShape& sh, void* meta, hipStream_t s) {
+  hipLaunchKernelGGL(moe_plan_kernel, dim3(1), dim3(1024), 0, s, ids, sh, (int*)meta);
+  return hipGetLastError();
 }
 
 hipError_t launch_swiglu(const float* g, const float* u, float* h, size_t n, hipStream_t s) {
@@ -69,6 +300,7 @@ __global__ __launch_bounds__(WAVES * 64) void moe_gemv_kernel(MoeGemvArgs a) {
   constexpr int S = WAVES * G;
   constexpr int NM = DUAL ? 2 : 1;
   extern __shared__ __attribute__((aligned(16))) float smem[];
+  if (a.ntasks && (int)blockIdx.x >= *a.ntasks) return;   // grid sized for the most tasks
   const MoeGemvTask task = a.tasks[blockIdx.x];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);

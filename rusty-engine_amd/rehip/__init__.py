@@ -39,7 +39,8 @@ EXPORTS = ("re_init", "re_last_error", "re_version", "re_row_bytes", "re_tiled_b
            "re_attention_dev", "re_add_dev", "re_swiglu_dev", "re_argmax_dev", "re_embed_dev", "re_pos_add_dev",
            "re_ffn_create", "re_ffn_destroy", "re_ffn_forward_dev", "re_attention_work_bytes",
            "re_qkv_rope_append_dev", "re_decode_advance_dev",
-           "re_qmat_create_stacked", "re_qmat_count", "re_qmat_matvec_stacked_dev")
+           "re_qmat_create_stacked", "re_qmat_count", "re_qmat_matvec_stacked_dev", "re_moe_router_logits_dev",
+           "re_moe_route_dev", "re_moe_forward_routed_dev", "re_moe_layer_dev")
 
 
 class RehipError(RuntimeError):
@@ -87,6 +88,10 @@ def lib() -> C.CDLL:
         L.re_moe_destroy.restype = None
         L.re_moe_forward.argtypes = [_vp, _vp, _sz, _sz, _vp, _vp, _vp, C.c_int]
         L.re_moe_forward_dev.argtypes = [_vp, _vp, _sz, _sz, _vp, _vp, _vp, C.c_int, _vp]
+        L.re_moe_router_logits_dev.argtypes = [_vp, _vp, _sz, _sz, _sz, _vp, _vp]
+        L.re_moe_route_dev.argtypes = [_vp, _sz, _sz, _sz, C.c_int, _vp, _vp, _vp]
+        L.re_moe_forward_routed_dev.argtypes = [_vp, _vp, _sz, _sz, _vp, _vp, _vp, C.c_int, _vp]
+        L.re_moe_layer_dev.argtypes = [_vp, _vp, _sz, _vp, _sz, C.c_int, _vp, C.c_int, _vp]
         L.re_qmat_create_stacked.argtypes = [C.c_uint32, _vp, _sz, _sz, _sz, _sz, C.POINTER(_vp)]
         L.re_qmat_count.argtypes = [_vp]
         L.re_qmat_count.restype = _sz
@@ -278,6 +283,19 @@ def kv_append_dev(k, v, rows, kv_dim, kcache, vcache, max_seq, pos, stream=None)
                                   _stream_ptr(stream)))
 
 
+GATE_SOFTMAX, GATE_SIGMOID = 0, 1
+
+
+def moe_router_logits_dev(x, router_w, tokens, hidden, n_experts, logits, stream=None):
+    _check(lib().re_moe_router_logits_dev(_p(x), _p(router_w), tokens, hidden, n_experts, _p(logits),
+                                          _stream_ptr(stream)))
+
+
+def moe_route_dev(logits, tokens, n_experts, top_k, gate, ids, weights, stream=None):
+    _check(lib().re_moe_route_dev(_p(logits), tokens, n_experts, top_k, gate, _p(ids), _p(weights),
+                                  _stream_ptr(stream)))
+
+
 def attention_work_bytes(rows, n_heads, head_dim, max_seq) -> int:
     return int(lib().re_attention_work_bytes(rows, n_heads, head_dim, max_seq))
 
@@ -371,6 +389,17 @@ class MoeExperts:
         wv = _f32(weights)
         _check(lib().re_moe_forward_dev(self._h, _dev_ptr(x_dev), tokens, top_k, idv.ctypes.data,
                                         wv.ctypes.data, _dev_ptr(out_dev), mode, _stream_ptr(stream)))
+
+    def forward_routed_dev(self, x_dev, tokens, top_k, ids_dev, weights_dev, out_dev, mode=MODE_BF16,
+                           stream=None) -> None:
+        """Expert FFN with device-resident routing (ids int32, weights f32: tokens x top_k)."""
+        _check(lib().re_moe_forward_routed_dev(self._h, _dev_ptr(x_dev), tokens, top_k, _dev_ptr(ids_dev),
+                                               _dev_ptr(weights_dev), _dev_ptr(out_dev), mode, _stream_ptr(stream)))
+
+    def layer_dev(self, x_dev, tokens, router_w_dev, top_k, gate, out_dev, mode=MODE_BF16, stream=None) -> None:
+        """Router logits, top-k routing and the expert FFN, all on the device (moe.rs:360-388)."""
+        _check(lib().re_moe_layer_dev(self._h, _dev_ptr(x_dev), tokens, _dev_ptr(router_w_dev), top_k, gate,
+                                      _dev_ptr(out_dev), mode, _stream_ptr(stream)))
 
     def close(self) -> None:
         if self._h:

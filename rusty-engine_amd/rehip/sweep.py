@@ -117,6 +117,30 @@ def time_moe(tokens: int, mode: int, reps: int, seed: int = 401):
         moe.forward_dev(dx, tokens, k, ids, wts, dy, mode, stream=s)
     s.synchronize()
     us = (_time.perf_counter() - t0) / reps * 1e6
+    # the same FFN with the routing on the device (ids/weights resident), and the whole layer
+    # (f32 router matvec + top-k + FFN), each as a replayed graph of `reps` calls
+    did = hip.DeviceBuffer.from_array(np.asarray(ids, np.int32))
+    dw = hip.DeviceBuffer.from_array(np.asarray(wts, np.float32))
+    rw = hip.DeviceBuffer.from_array((np.random.default_rng(seed + 3).standard_normal((E, H)) / np.sqrt(H))
+                                     .astype(np.float32))
+    e0, e1 = hip.Event(), hip.Event()
+
+    def graph_us(fn):
+        fn()
+        s.synchronize()
+        g = hip.Graph(s, lambda: [fn() for _ in range(reps)])
+        g.launch()
+        s.synchronize()
+        e0.record(s)
+        g.launch()
+        e1.record(s)
+        e1.synchronize()
+        g.destroy()
+        return e0.elapsed_ms(e1) * 1e3 / reps
+
+    us_routed = graph_us(lambda: moe.forward_routed_dev(dx, tokens, k, did, dw, dy, mode, stream=s))
+    from . import GATE_SOFTMAX
+    us_layer = graph_us(lambda: moe.layer_dev(dx, tokens, rw, k, GATE_SOFTMAX, dy, mode, stream=s))
     moe.close()
     s.destroy()
     hit = len(np.unique(ids))
@@ -125,7 +149,9 @@ def time_moe(tokens: int, mode: int, reps: int, seed: int = 401):
     flop = 2.0 * tokens * k * 3 * H * I
     return {"tokens": tokens, "pairs": tokens * k, "experts_hit": int(hit), "mode": "f32" if mode == 1 else "bf16",
             "us": us, "bytes": int(nbytes), "gbs": nbytes / (us * 1e-6) / 1e9,
-            "frac_hbm": nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, "tflops": flop / (us * 1e-6) / 1e12}
+            "frac_hbm": nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, "tflops": flop / (us * 1e-6) / 1e12,
+            "us_device_routed": us_routed, "gbs_device_routed": nbytes / (us_routed * 1e-6) / 1e9,
+            "us_layer_device": us_layer}
 
 
 def time_decode(prompt_len: int, steps: int, mode: int, seed: int = 501, use_graph: bool = True):
@@ -198,7 +224,9 @@ def main(argv=None) -> int:
                 rows.append(r)
                 print(f"MoE T={tokens:4d} pairs={r['pairs']:5d} experts={r['experts_hit']:3d} {r['mode']:4s} "
                       f"{r['us']:9.1f} us {r['gbs']:8.1f} GB/s ({100 * r['frac_hbm']:5.1f}% of HBM) "
-                      f"{r['tflops']:7.2f} TFLOP/s", flush=True)
+                      f"{r['tflops']:7.2f} TFLOP/s | device-routed {r['us_device_routed']:8.1f} us "
+                      f"{r['gbs_device_routed']:8.1f} GB/s ({100 * r['gbs_device_routed'] / HBM_PEAK_GBS:5.1f}%) "
+                      f"| layer incl. router {r['us_layer_device']:8.1f} us", flush=True)
         if args.json:
             with open(args.json, "w") as f:
                 json.dump(rows, f, indent=1)

@@ -1,0 +1,145 @@
+"""MoE layer with the routing on the device (row F3): router logits, top-k routing and the
+expert grouping run as kernels, so a layer needs no host round trip.
+
+Bars: the chosen expert ids equal the oracle router's (moe.rs:75-118, restated in the oracle)
+exactly, including ties (lower index first); routing weights agree to f32 rounding of expf
+(parity of libm exp is unpinned: 1e-6 relative); the device-routed expert FFN equals the
+host-routed one (re_moe_forward_dev) bit for bit when both take the same path, and the full
+layer matches the oracle's f64-free restatement within the MoE bars (f32 1e-4, bf16 1e-2
+relative to norm)."""
+import numpy as np
+import pytest
+
+import oracle as O
+import rehip
+from rehip import hip, synth
+
+pytestmark = pytest.mark.gpu
+B = hip.DeviceBuffer
+
+
+def down(buf, n, dtype=np.float32):
+    hip.synchronize()
+    return buf.download(dtype, n)
+
+
+@pytest.mark.parametrize("T,E,k", [(1, 128, 8), (37, 128, 8), (5, 16, 4), (3, 1000, 16), (2, 8, 8)])
+@pytest.mark.parametrize("gate", [rehip.GATE_SOFTMAX, rehip.GATE_SIGMOID])
+def test_route_matches_oracle_router(T, E, k, gate):
+    rng = np.random.default_rng(T * 31 + E + gate)
+    logits = rng.standard_normal((T, E)).astype(np.float32)
+    logits[0, 3] = logits[0, 7] = logits[0].max() + 1        # a tie at the top: index 3 first
+    if T > 1:
+        logits[1, :] = 0.25                                  # all equal: experts 0..k-1 in order
+    ids, w = B(T * k * 4), B(T * k * 4)
+    rehip.moe_route_dev(B.from_array(logits), T, E, k, gate, ids, w)
+    gi = down(ids, T * k, np.int32).reshape(T, k)
+    gw = down(w, T * k).reshape(T, k)
+    for t in range(T):
+        oi, ow = (O.top_k if gate == rehip.GATE_SOFTMAX else O.top_k_sigmoid)(logits[t], k)
+        assert np.array_equal(gi[t], np.asarray(oi, np.int32)), t
+        np.testing.assert_allclose(gw[t], ow, rtol=1e-6, atol=1e-7)
+    assert list(gi[0, :2]) == [3, 7]
+
+
+def test_router_logits_matvec():
+    rng = np.random.default_rng(3)
+    T, H, E = 7, 2048, 128
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    w = (rng.standard_normal((E, H)) / 45).astype(np.float32)
+    out = B(T * E * 4)
+    rehip.moe_router_logits_dev(B.from_array(x), B.from_array(w), T, H, E, out)
+    got = down(out, T * E).reshape(T, E)
+    want = x.astype(np.float64) @ w.astype(np.float64).T
+    bound = 2.0 ** -20 * (np.abs(x).astype(np.float64) @ np.abs(w).astype(np.float64).T)
+    assert np.all(np.abs(got - want) <= bound)
+
+
+def moe_case(seed, E, hidden, inter, T, k, gt=rehip.Q4_K, dt=rehip.Q6_K):
+    rng = np.random.default_rng(seed)
+    gate = np.concatenate([synth.weight_bytes(rng, gt, inter, hidden) for _ in range(E)])
+    up = np.concatenate([synth.weight_bytes(rng, gt, inter, hidden) for _ in range(E)])
+    down_ = np.concatenate([synth.weight_bytes(rng, dt, hidden, inter) for _ in range(E)])
+    x = synth.activations(rng, T, hidden)
+    logits = rng.standard_normal((T, E)).astype(np.float32)
+    return gate, up, down_, x, logits
+
+
+@pytest.mark.parametrize("T,E,k", [(1, 16, 4), (5, 16, 4), (40, 16, 4), (3, 128, 8), (300, 32, 4)])
+def test_forward_routed_equals_host_routed(T, E, k):
+    """Device grouping/tasks vs the host planner: the same kernels over the same rows, so the
+    outputs are identical whenever both pick the same path (GEMV for few rows per expert,
+    grouped GEMM otherwise)."""
+    hidden, inter = 512, 256
+    gate, up, down_, x, logits = moe_case(900 + T + E, E, hidden, inter, T, k)
+    ids = np.zeros((T, k), np.int32)
+    wts = np.zeros((T, k), np.float32)
+    for t in range(T):
+        ids[t], wts[t] = O.top_k(logits[t], k)
+    moe = rehip.MoeExperts(rehip.Q4_K, gate, rehip.Q4_K, up, rehip.Q6_K, down_, E, hidden, inter)
+    xd = B.from_array(x)
+    idd, wd = B.from_array(ids.reshape(-1)), B.from_array(wts.reshape(-1))
+    pairs = T * k
+    touched = len(set(ids.reshape(-1).tolist()))
+    same_path = (pairs <= 4 * touched) == (pairs <= 2 * E)
+    want_oracle = O.moe_ffn(rehip.Q4_K, gate, rehip.Q4_K, up, rehip.Q6_K, down_, E, hidden, inter, x, T, k,
+                            ids.reshape(-1).astype(np.uint32), wts.reshape(-1))
+    for mode, tol in [(rehip.MODE_F32, 1e-4), (rehip.MODE_BF16, 1e-2)]:
+        out = B(T * hidden * 4)
+        moe.forward_routed_dev(xd, T, k, idd, wd, out, mode)
+        got = down(out, T * hidden)
+        host = moe.forward(x, T, k, ids.reshape(-1).astype(np.uint32), wts.reshape(-1), mode)
+        if same_path:
+            assert np.array_equal(got, host), mode
+        rel = np.linalg.norm(got - want_oracle) / np.linalg.norm(want_oracle)
+        assert rel <= tol, (mode, rel)
+    moe.close()
+
+
+def test_forward_routed_skips_out_of_range_ids():
+    E, hidden, inter, T, k = 8, 256, 128, 3, 2
+    gate, up, down_, x, logits = moe_case(77, E, hidden, inter, T, k)
+    ids = np.array([[1, 9], [2, 3], [-1, 4]], np.int32)
+    wts = np.full((T, k), 0.5, np.float32)
+    moe = rehip.MoeExperts(rehip.Q4_K, gate, rehip.Q4_K, up, rehip.Q6_K, down_, E, hidden, inter)
+    out = B(T * hidden * 4)
+    moe.forward_routed_dev(B.from_array(x), T, k, B.from_array(ids.reshape(-1)), B.from_array(wts.reshape(-1)), out,
+                           rehip.MODE_F32)
+    got = down(out, T * hidden).reshape(T, hidden)
+    # only the valid pairs: as if the invalid ones had weight 0 (routed to any expert)
+    ids_ok = np.where((ids >= 0) & (ids < E), ids, 0).astype(np.uint32)
+    w_ok = np.where((ids >= 0) & (ids < E), wts, 0.0).astype(np.float32)
+    want = O.moe_ffn(rehip.Q4_K, gate, rehip.Q4_K, up, rehip.Q6_K, down_, E, hidden, inter, x, T, k,
+                     ids_ok.reshape(-1), w_ok.reshape(-1)).reshape(T, hidden)
+    np.testing.assert_allclose(got, want, rtol=0, atol=1e-4 * np.abs(want).max())
+    moe.close()
+
+
+@pytest.mark.parametrize("T", [1, 32])
+@pytest.mark.parametrize("gate", [rehip.GATE_SOFTMAX, rehip.GATE_SIGMOID])
+def test_moe_layer_qwen3_shape(T, gate):
+    """Qwen3-30B-A3B-like layer: hidden 2048, 128 experts, top-8, Q4_K gate/up, Q6_K down; the
+    router weights are f32 (moe.rs:367). Against the oracle router on the same f32 logits and
+    the oracle FFN."""
+    E, hidden, inter, k = 128, 2048, 768, 8
+    gate_b, up, down_, x, _ = moe_case(4000 + T, E, hidden, inter, T, k)
+    rng = np.random.default_rng(4100 + T)
+    rw = (rng.standard_normal((E, hidden)) / np.sqrt(hidden)).astype(np.float32)
+    moe = rehip.MoeExperts(rehip.Q4_K, gate_b, rehip.Q4_K, up, rehip.Q6_K, down_, E, hidden, inter)
+    out = B(T * hidden * 4)
+    xd, rwd = B.from_array(x), B.from_array(rw)
+    logits = B(T * E * 4)
+    rehip.moe_router_logits_dev(xd, rwd, T, hidden, E, logits)
+    lg = down(logits, T * E).reshape(T, E)
+    ids = np.zeros((T, k), np.uint32)
+    wts = np.zeros((T, k), np.float32)
+    for t in range(T):
+        ids[t], wts[t] = (O.top_k if gate == rehip.GATE_SOFTMAX else O.top_k_sigmoid)(lg[t], k)
+    want = O.moe_ffn(rehip.Q4_K, gate_b, rehip.Q4_K, up, rehip.Q6_K, down_, E, hidden, inter, x, T, k,
+                     ids.reshape(-1), wts.reshape(-1))
+    for mode, tol in [(rehip.MODE_F32, 1e-4), (rehip.MODE_BF16, 1e-2)]:
+        moe.layer_dev(xd, T, rwd, k, gate, out, mode)
+        got = down(out, T * hidden)
+        rel = np.linalg.norm(got - want) / np.linalg.norm(want)
+        assert rel <= tol, (mode, rel)
+    moe.close()
