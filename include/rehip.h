@@ -211,6 +211,46 @@ void re_ffn_destroy(re_ffn *f);
 /* d_norm_w: NULL, or x is RMS-normalised first (the FFN norm, forward.rs:479). */
 int re_ffn_forward_dev(re_ffn *f, const float *d_x, const float *d_norm_w, float eps, float *d_h, void *stream);
 
+/* ---- GGUF model files (src/gguf.rs:17-392, src/loader.rs:17-130) ----
+ * re_gguf_open maps the file read-only and parses its header: magic "GGUF", version 2 (u32
+ * counts) or 3 (u64 counts), metadata of every value kind (nested arrays included), up to 8 dims
+ * per tensor, data start = header end rounded up to general.alignment (U32 or U64; default 32).
+ * Parse failures return RE_ERR_ARG with "gguf parse error at <offset>: <message>" (gguf.rs:60-70).
+ * Strings and tensor data returned below point into the mapping and live until re_gguf_close. */
+typedef struct re_gguf re_gguf;
+int re_gguf_open(const char *path, re_gguf **out);               /* MmapModel::open (loader.rs:30-50) */
+void re_gguf_close(re_gguf *g);
+uint32_t re_gguf_version(const re_gguf *g);
+size_t re_gguf_kv_count(const re_gguf *g);
+size_t re_gguf_tensor_count(const re_gguf *g);
+uint64_t re_gguf_alignment(const re_gguf *g);                  /* GgufFile::alignment (gguf.rs:143-150) */
+size_t re_gguf_data_offset(const re_gguf *g);                  /* header end, before alignment */
+size_t re_gguf_data_start(const re_gguf *g);                   /* aligned_start (loader.rs:17-21) */
+/* i-th metadata key (NUL-terminated copy) and its value kind (0 U8 .. 12 F64, gguf.rs:274-312). */
+int re_gguf_kv(const re_gguf *g, size_t i, const char **key, uint32_t *kind);
+/* First value under `key` (gguf.rs:139-141): integers and Bool widened to int64, F32/F64 to
+ * double, strings as (pointer, length) without a NUL, arrays as element kind and count. */
+int re_gguf_get_int(const re_gguf *g, const char *key, int64_t *v);
+int re_gguf_get_float(const re_gguf *g, const char *key, double *v);
+int re_gguf_get_str(const re_gguf *g, const char *key, const char **s, size_t *len);
+int re_gguf_get_array(const re_gguf *g, const char *key, uint32_t *elem_kind, uint64_t *count);
+/* Tensor i: name, ggml type, dims (dims[0..7], zero past n_dims) and byte offset past data start. */
+int re_gguf_tensor_info(const re_gguf *g, size_t i, const char **name, uint32_t *type, uint32_t *n_dims,
+                        uint64_t *dims, uint64_t *offset);
+int re_gguf_find_tensor(const re_gguf *g, const char *name, size_t *index);
+/* MmapModel::tensor_bytes (loader.rs:95-101): [data_start + offset, + nbytes) of the mapping,
+ * nbytes from the type and element count (quant.rs:75-101); RE_ERR_TYPE for an unsized type or
+ * a count that is not whole blocks, RE_ERR_SIZE when the range leaves the file. */
+int re_gguf_tensor_data(const re_gguf *g, size_t i, const uint8_t **data, size_t *nbytes);
+/* QMat::from_model (qmat.rs:310-330): W[m x n] from the tensor with dims [n, m] (or [n, m, count]:
+ * a stacked QMat of count matrices). The mapped bytes are copied to the device unchanged and
+ * repacked there. Errors: "QMat: tensor '<name>' missing" / "... bytes out of bounds". */
+int re_qmat_from_gguf(const re_gguf *g, const char *name, size_t m, size_t n, re_qmat **out);
+/* One MoE layer's stacked experts (model.rs:372-389): gate and up tensors with dims
+ * [hidden, inter, n_experts], down with [inter, hidden, n_experts]. */
+int re_moe_from_gguf(const re_gguf *g, const char *gate, const char *up, const char *down, size_t n_experts,
+                     size_t hidden, size_t inter, re_moe **out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -35,6 +35,21 @@ int fail(int code, const char* fmt, ...) {
     if (e_ != hipSuccess) return fail(RE_ERR_HIP, "%s: %s", #expr, hipGetErrorString(e_)); \
   } while (0)
 
+}  // namespace
+
+namespace rehip {
+// error reporting for the other translation units of the library (gguf.cpp)
+int report_error(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof g_err, fmt, ap);
+  va_end(ap);
+  return code;
+}
+}  // namespace rehip
+
+namespace {
+
 const char* type_name(uint32_t t) {
   switch (t) {
     case T_Q4_0: return "Q4_0";
@@ -202,15 +217,84 @@ void plan_gemv(re_qmat* q) {
   if (const size_t w = env_size("REHIP_GEMV_WAVES", 0); w == 4 || w == 8 || w == 16) q->waves = (int)w;
 }
 
-int upload_tiled(const MatGeom& g, const uint8_t* bytes, uint8_t* d_dst) {
-  std::vector<uint8_t> tiled;
-  try {
-    tiled.resize(g.bytes);
-  } catch (const std::bad_alloc&) {
-    return fail(RE_ERR_ARG, "host out of memory for %zu-byte repack", g.bytes);
+// Uploads `count` matrices stored as GGUF row-major blocks (back to back in host memory, e.g. a
+// mapped file) into the tiled layout at d_dst (dst_stride bytes apart). The bytes move as they
+// are, in chunks of up to 32 MiB (whole matrices, or whole 64-row tiles of one large matrix),
+// into one of two device staging buffers on a copy stream (the runtime's pageable-copy path: it
+// measured at twice the rate of a host memcpy into pinned staging followed by a DMA); the repack
+// kernel permutes each chunk on a second stream while the next chunk is copied into the other
+// buffer. The staging buffers (2 x 32 MiB of device memory) and the two streams are made on a
+// device's first upload and kept until the process ends; uploads serialize on them.
+constexpr size_t kUploadChunk = 32u << 20;
+constexpr int kMaxDevices = 64;
+
+struct Uploader {
+  hipStream_t cs = nullptr, ks = nullptr;            // copies, repack kernels
+  hipEvent_t copied[2] = {nullptr, nullptr}, done[2] = {nullptr, nullptr};
+  void* d[2] = {nullptr, nullptr};
+  bool ready = false;
+  int setup() {
+    if (ready) return RE_OK;
+    if (!cs) HIP_TRY(hipStreamCreateWithFlags(&cs, hipStreamNonBlocking));
+    if (!ks) HIP_TRY(hipStreamCreateWithFlags(&ks, hipStreamNonBlocking));
+    for (int b = 0; b < 2; ++b) {
+      if (!copied[b]) HIP_TRY(hipEventCreateWithFlags(&copied[b], hipEventDisableTiming));
+      if (!done[b]) HIP_TRY(hipEventCreateWithFlags(&done[b], hipEventDisableTiming));
+      if (!d[b]) HIP_TRY(hipMalloc(&d[b], kUploadChunk));
+    }
+    ready = true;
+    return RE_OK;
   }
-  repack_host(g, bytes, tiled.data());
-  HIP_TRY(hipMemcpy(d_dst, tiled.data(), g.bytes, hipMemcpyHostToDevice));
+};
+std::mutex g_up_mu;
+Uploader g_up[kMaxDevices];
+
+int upload_tiled(const MatGeom& g, const uint8_t* src, size_t count, uint8_t* d_dst, size_t dst_stride) {
+  const size_t row_bytes = g.kb * (size_t)g.bb;
+  const size_t mat_src = g.m * row_bytes;
+  const size_t tile_src = row_bytes * kTileRows;
+  if (tile_src > kUploadChunk)
+    return fail(RE_ERR_SIZE, "64-row tile of %zu bytes exceeds the upload staging (%zu)", tile_src, kUploadChunk);
+  // whole matrices per chunk when they fit, else whole tiles of one matrix
+  const size_t mats_per_chunk = mat_src <= kUploadChunk ? std::min(count, kUploadChunk / mat_src) : 1;
+  const size_t tiles_per_chunk = mat_src <= kUploadChunk ? g.tiles : kUploadChunk / tile_src;
+  if (mats_per_chunk * g.tiles * g.kb > (size_t)INT32_MAX) return fail(RE_ERR_SIZE, "repack grid too large");
+  int dev = 0;
+  HIP_TRY(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kMaxDevices) return fail(RE_ERR_ARG, "device %d out of range", dev);
+  std::lock_guard<std::mutex> lk(g_up_mu);
+  Uploader& u = g_up[dev];
+  int rc = u.setup();
+  if (rc) return rc;
+  auto drain = [&](hipError_t e) {
+    (void)hipStreamSynchronize(u.cs);
+    (void)hipStreamSynchronize(u.ks);
+    return fail(RE_ERR_HIP, "upload: %s", hipGetErrorString(e));
+  };
+  size_t it = 0;
+  for (size_t i0 = 0; i0 < count; i0 += mats_per_chunk) {
+    const size_t nm = std::min(mats_per_chunk, count - i0);
+    for (size_t t0 = 0; t0 < g.tiles; t0 += tiles_per_chunk, ++it) {
+      const size_t nt = std::min(tiles_per_chunk, g.tiles - t0);
+      const size_t row0 = t0 * kTileRows;
+      const size_t rows = std::min(g.m - row0, nt * kTileRows);
+      const size_t bytes = nm > 1 ? nm * mat_src : rows * row_bytes;
+      const int b = (int)(it & 1);
+      hipError_t e = hipSuccess;
+      if (it >= 2) e = hipEventSynchronize(u.done[b]);   // the repack of chunk it - 2 has left d[b]
+      if (e == hipSuccess)
+        e = hipMemcpyAsync(u.d[b], src + i0 * mat_src + row0 * row_bytes, bytes, hipMemcpyHostToDevice, u.cs);
+      if (e == hipSuccess) e = hipEventRecord(u.copied[b], u.cs);
+      if (e == hipSuccess) e = hipStreamWaitEvent(u.ks, u.copied[b], 0);
+      if (e == hipSuccess)
+        e = launch_repack(g.type, (const uint8_t*)u.d[b], d_dst + i0 * dst_stride + t0 * g.kb * g.slab_bytes,
+                          nm > 1 ? (int)g.m : (int)rows, (int)g.kb, (int)nt, (int)nm, mat_src, dst_stride, u.ks);
+      if (e == hipSuccess) e = hipEventRecord(u.done[b], u.ks);
+      if (e != hipSuccess) return drain(e);
+    }
+  }
+  hipError_t e = hipStreamSynchronize(u.ks);
+  if (e != hipSuccess) return drain(e);
   return RE_OK;
 }
 
@@ -352,9 +436,7 @@ int re_qmat_create_stacked(uint32_t ggml_type, const uint8_t* bytes, size_t nbyt
   };
   const size_t total = q->w_stride * count;
   if (hipMalloc(&q->d_w, total) != hipSuccess) return cleanup(fail(RE_ERR_HIP, "hipMalloc(%zu) failed", total));
-  const size_t one = nbytes / count;
-  for (size_t i = 0; i < count; ++i)
-    if ((rc = upload_tiled(g, bytes + i * one, q->d_w + i * q->w_stride))) return cleanup(rc);
+  if ((rc = upload_tiled(g, bytes, count, q->d_w, q->w_stride))) return cleanup(rc);
   const size_t m_pad = g.tiles * kTileRows;
   if (q->splits > 1) {
     if (hipMalloc(&q->d_partial, (size_t)q->splits * m_pad * sizeof(float)) != hipSuccess)
@@ -553,8 +635,7 @@ int re_moe_create(uint32_t gate_type, const uint8_t* gate, size_t gate_bytes, ui
   for (auto& pt : parts) {
     if (hipMalloc(pt.dst, pt.g->bytes * n_experts) != hipSuccess)
       return cleanup(fail(RE_ERR_HIP, "hipMalloc(%zu) failed", pt.g->bytes * n_experts));
-    for (size_t x = 0; x < n_experts; ++x)
-      if ((rc = upload_tiled(*pt.g, pt.src + x * pt.slice, *pt.dst + x * pt.g->bytes))) return cleanup(rc);
+    if ((rc = upload_tiled(*pt.g, pt.src, n_experts, *pt.dst, pt.g->bytes))) return cleanup(rc);
   }
   if (hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking) != hipSuccess)
     return cleanup(fail(RE_ERR_HIP, "hipStreamCreate failed"));

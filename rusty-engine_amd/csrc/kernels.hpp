@@ -64,6 +64,10 @@ constexpr int kGemvRowsMaxK = 12288;
 hipError_t launch_gemv(uint32_t type, const GemvArgs& a, int waves, hipStream_t s);
 hipError_t launch_dequant(uint32_t type, const uint8_t* W, float* out, int m, int n, int KB, int tiles,
                           hipStream_t s);
+// GGUF row-major blocks -> tiled slabs (repack.hip): `mats` matrices of m rows x kb blocks,
+// mat_src bytes apart at src (device) and dst_stride bytes apart at dst, `tiles` tiles each
+hipError_t launch_repack(uint32_t type, const uint8_t* src, uint8_t* dst, int m, int kb, int tiles, int mats,
+                         size_t mat_src, size_t dst_stride, hipStream_t s);
 
 // GEMM: K steps of 128 elements.
 constexpr int kGemmBK = 128;

@@ -40,7 +40,11 @@ EXPORTS = ("re_init", "re_last_error", "re_version", "re_row_bytes", "re_tiled_b
            "re_ffn_create", "re_ffn_destroy", "re_ffn_forward_dev", "re_attention_work_bytes",
            "re_qkv_rope_append_dev", "re_decode_advance_dev",
            "re_qmat_create_stacked", "re_qmat_count", "re_qmat_matvec_stacked_dev", "re_moe_router_logits_dev",
-           "re_moe_route_dev", "re_moe_forward_routed_dev", "re_moe_layer_dev")
+           "re_moe_route_dev", "re_moe_forward_routed_dev", "re_moe_layer_dev",
+           "re_gguf_open", "re_gguf_close", "re_gguf_version", "re_gguf_kv_count", "re_gguf_tensor_count",
+           "re_gguf_alignment", "re_gguf_data_offset", "re_gguf_data_start", "re_gguf_kv", "re_gguf_get_int",
+           "re_gguf_get_float", "re_gguf_get_str", "re_gguf_get_array", "re_gguf_tensor_info",
+           "re_gguf_find_tensor", "re_gguf_tensor_data", "re_qmat_from_gguf", "re_moe_from_gguf")
 
 
 class RehipError(RuntimeError):
@@ -115,6 +119,24 @@ def lib() -> C.CDLL:
         L.re_ffn_destroy.argtypes = [_vp]
         L.re_ffn_destroy.restype = None
         L.re_ffn_forward_dev.argtypes = [_vp, _vp, _vp, C.c_float, _vp, _vp]
+        L.re_gguf_open.argtypes = [C.c_char_p, C.POINTER(_vp)]
+        L.re_gguf_close.argtypes = [_vp]
+        L.re_gguf_close.restype = None
+        for f, r in (("re_gguf_version", C.c_uint32), ("re_gguf_kv_count", _sz), ("re_gguf_tensor_count", _sz),
+                     ("re_gguf_alignment", C.c_uint64), ("re_gguf_data_offset", _sz), ("re_gguf_data_start", _sz)):
+            getattr(L, f).argtypes = [_vp]
+            getattr(L, f).restype = r
+        L.re_gguf_kv.argtypes = [_vp, _sz, C.POINTER(C.c_char_p), C.POINTER(C.c_uint32)]
+        L.re_gguf_get_int.argtypes = [_vp, C.c_char_p, C.POINTER(C.c_int64)]
+        L.re_gguf_get_float.argtypes = [_vp, C.c_char_p, C.POINTER(C.c_double)]
+        L.re_gguf_get_str.argtypes = [_vp, C.c_char_p, C.POINTER(_vp), C.POINTER(_sz)]
+        L.re_gguf_get_array.argtypes = [_vp, C.c_char_p, C.POINTER(C.c_uint32), C.POINTER(C.c_uint64)]
+        L.re_gguf_tensor_info.argtypes = [_vp, _sz, C.POINTER(C.c_char_p), C.POINTER(C.c_uint32),
+                                          C.POINTER(C.c_uint32), C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]
+        L.re_gguf_find_tensor.argtypes = [_vp, C.c_char_p, C.POINTER(_sz)]
+        L.re_gguf_tensor_data.argtypes = [_vp, _sz, C.POINTER(_vp), C.POINTER(_sz)]
+        L.re_qmat_from_gguf.argtypes = [_vp, C.c_char_p, _sz, _sz, C.POINTER(_vp)]
+        L.re_moe_from_gguf.argtypes = [_vp, C.c_char_p, C.c_char_p, C.c_char_p, _sz, _sz, _sz, C.POINTER(_vp)]
         _lib = L
     return _lib
 
@@ -204,6 +226,15 @@ class QMat:
         h = _vp()
         _check(lib().re_qmat_create_stacked(ggml_type, src.ctypes.data, src.size, m, n, count, C.byref(h)))
         return cls(h.value, ggml_type, m, n)
+
+    @classmethod
+    def from_gguf(cls, model: "Gguf", name: str, m: int, n: int) -> "QMat":
+        """QMat::from_model (qmat.rs:310-330): tensor `name` (dims [n, m], or [n, m, count] for a
+        stack) straight from the mapped file to the device, repacked there."""
+        h = _vp()
+        _check(lib().re_qmat_from_gguf(model._h, name.encode(), m, n, C.byref(h)))
+        t = model.tensor(name)
+        return cls(h.value, t.ggml_type, m, n)
 
     def count(self) -> int:
         return lib().re_qmat_count(self._h)
@@ -365,6 +396,19 @@ class Ffn:
 class MoeExperts:
     """All experts of one MoE layer resident on the GPU (gate/up inter x hidden, down hidden x inter)."""
 
+    @classmethod
+    def from_gguf(cls, model: "Gguf", gate: str, up: str, down: str, n_experts: int, hidden: int,
+                  inter: int) -> "MoeExperts":
+        """The layer's stacked expert tensors (ffn_{gate,up,down}_exps, model.rs:372-389) uploaded
+        from the mapped file and repacked on the device."""
+        h = _vp()
+        _check(lib().re_moe_from_gguf(model._h, gate.encode(), up.encode(), down.encode(), n_experts, hidden, inter,
+                                      C.byref(h)))
+        self = cls.__new__(cls)
+        self._h = h
+        self.n_experts, self.hidden, self.inter = n_experts, hidden, inter
+        return self
+
     def __init__(self, gate_type, gate, up_type, up, down_type, down, n_experts, hidden, inter):
         g, u, d = _u8(gate), _u8(up), _u8(down)
         h = _vp()
@@ -405,6 +449,124 @@ class MoeExperts:
         if self._h:
             lib().re_moe_destroy(self._h)
             self._h = C.c_void_p(0)
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+# ---- GGUF files (src/gguf.rs, src/loader.rs) ----------------------------------------------------
+GGUF_VALUE_KINDS = ("U8", "I8", "U16", "I16", "U32", "I32", "F32", "Bool", "Str", "Array", "U64", "I64", "F64")
+
+
+class TensorEntry:
+    """One row of the tensor-info table (gguf.rs TensorEntry): name, dims, ggml type, byte offset."""
+
+    def __init__(self, name: str, dims: list, ggml_type: int, offset: int):
+        self.name, self.dims, self.ggml_type, self.offset = name, dims, ggml_type, offset
+
+    def numel(self) -> int:
+        n = 1
+        for d in self.dims:
+            n *= d
+        return n
+
+    def __repr__(self) -> str:
+        return f"TensorEntry({self.name!r}, dims={self.dims}, type={self.ggml_type}, offset={self.offset})"
+
+
+class Gguf:
+    """A GGUF model file mapped read-only (MmapModel, loader.rs:25-130) with its parsed header
+    (GgufFile, gguf.rs:120-160). Tensor bytes are views into the mapping; they stay valid while
+    this object is open."""
+
+    def __init__(self, path):
+        h = _vp()
+        _check(lib().re_gguf_open(os.fsencode(path), C.byref(h)))
+        self._h = h
+        L = lib()
+        self.version = L.re_gguf_version(h)
+        self.n_kv = L.re_gguf_kv_count(h)
+        self.n_tensors = L.re_gguf_tensor_count(h)
+        self.data_offset = L.re_gguf_data_offset(h)
+        self.data_start = L.re_gguf_data_start(h)
+        self.tensors = [self._info(i) for i in range(self.n_tensors)]
+        self._by_name = {}
+        for t in self.tensors:
+            self._by_name.setdefault(t.name, t)
+
+    def _info(self, i: int) -> TensorEntry:
+        name, ty, nd = C.c_char_p(), C.c_uint32(), C.c_uint32()
+        dims, off = (C.c_uint64 * 8)(), C.c_uint64()
+        _check(lib().re_gguf_tensor_info(self._h, i, C.byref(name), C.byref(ty), C.byref(nd), dims, C.byref(off)))
+        return TensorEntry(name.value.decode("utf-8", "replace"), [int(dims[d]) for d in range(nd.value)],
+                           ty.value, off.value)
+
+    def alignment(self) -> int:
+        return lib().re_gguf_alignment(self._h)
+
+    def keys(self) -> list:
+        out = []
+        for i in range(self.n_kv):
+            k, kind = C.c_char_p(), C.c_uint32()
+            _check(lib().re_gguf_kv(self._h, i, C.byref(k), C.byref(kind)))
+            out.append((k.value.decode("utf-8", "replace"), GGUF_VALUE_KINDS[kind.value]))
+        return out
+
+    def get(self, key: str):
+        """The first value under `key`: int, float, str, or ("Array", element kind, count);
+        None when absent (gguf.rs:139-141)."""
+        kinds = dict(self.keys())
+        kind = kinds.get(key)
+        if kind is None:
+            return None
+        L, k = lib(), key.encode()
+        if kind == "Str":
+            p, n = _vp(), _sz()
+            _check(L.re_gguf_get_str(self._h, k, C.byref(p), C.byref(n)))
+            return C.string_at(p.value, n.value).decode("utf-8", "replace") if n.value else ""
+        if kind in ("F32", "F64"):
+            v = C.c_double()
+            _check(L.re_gguf_get_float(self._h, k, C.byref(v)))
+            return v.value
+        if kind == "Array":
+            ek, cnt = C.c_uint32(), C.c_uint64()
+            _check(L.re_gguf_get_array(self._h, k, C.byref(ek), C.byref(cnt)))
+            return ("Array", GGUF_VALUE_KINDS[ek.value], cnt.value)
+        v = C.c_int64()
+        _check(L.re_gguf_get_int(self._h, k, C.byref(v)))
+        return bool(v.value) if kind == "Bool" else v.value
+
+    def tensor(self, name: str) -> TensorEntry:
+        t = self._by_name.get(name)
+        if t is None:
+            raise RehipError(RE_ERR_ARG, f"tensor '{name}' not found")
+        return t
+
+    def tensor_bytes(self, name: str) -> np.ndarray:
+        """Read-only uint8 view of the tensor's bytes in the mapping (loader.rs:95-101)."""
+        i = _sz()
+        _check(lib().re_gguf_find_tensor(self._h, name.encode(), C.byref(i)))
+        p, n = _vp(), _sz()
+        _check(lib().re_gguf_tensor_data(self._h, i.value, C.byref(p), C.byref(n)))
+        if n.value == 0:
+            return np.empty(0, np.uint8)
+        a = np.ctypeslib.as_array((C.c_uint8 * n.value).from_address(p.value))
+        a.flags.writeable = False
+        return a
+
+    def close(self) -> None:
+        if self._h:
+            lib().re_gguf_close(self._h)
+            self._h = _vp(0)
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
 
     def __del__(self):
         try:

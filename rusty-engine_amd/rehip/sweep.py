@@ -192,6 +192,95 @@ def time_decode(prompt_len: int, steps: int, mode: int, seed: int = 501, use_gra
             "step_us_device": 1e6 * (t3 - t2) / steps, "step_us_readback": 1e6 * (t4 - t3) / (steps - 1)}
 
 
+def time_load(layers: int, workdir: str, seed: int = 601, variant_env=None):
+    """GGUF ingest: a file of `layers` Qwen3-30B-A3B-shaped MoE layers (128 experts, hidden 2048,
+    inter 768; Q4_K gate/up, Q6_K down: 309 MB a layer) is written, mapped and uploaded expert
+    stack by expert stack (map -> pinned chunk -> device -> repack kernel). The file is in the page
+    cache (just written), so this is the map-to-HBM rate, not a disk read; each pass maps the file
+    afresh and pays its page faults. Beside it: a plain
+    pageable hipMemcpy of the same bytes (the bus rate the upload is bound by) and the host repack
+    (the same permutation on one CPU core)."""
+    import os
+    import time
+
+    from . import MoeExperts, Gguf, Q4_K, Q6_K, repack
+    from . import gguf_writer as W
+    variant_env = variant_env or {}
+    E, hidden, inter = 128, 2048, 768
+    rng = np.random.default_rng(seed)
+    per = {Q4_K: inter * hidden // 256 * 144 * E, Q6_K: hidden * inter // 256 * 210 * E}
+    gu = rng.integers(0, 256, per[Q4_K], dtype=np.uint8).tobytes()
+    dn = rng.integers(0, 256, per[Q6_K], dtype=np.uint8).tobytes()
+    tensors = []
+    for layer in range(layers):
+        p = f"blk.{layer}."
+        tensors += [(p + "ffn_gate_exps.weight", [hidden, inter, E], Q4_K, gu),
+                    (p + "ffn_up_exps.weight", [hidden, inter, E], Q4_K, gu),
+                    (p + "ffn_down_exps.weight", [inter, hidden, E], Q6_K, dn)]
+    path = os.path.join(workdir, "load_bench.gguf")
+    with open(path, "wb") as f:
+        f.write(W.write([("general.architecture", W.STR, "qwen3moe")], tensors))
+    total = layers * (2 * len(gu) + len(dn))
+    print(f"load: wrote {total / 1e9:.2f} GB of expert tensors", flush=True)
+    t0 = time.perf_counter()
+    g = Gguf(path)
+    t1 = time.perf_counter()
+    g.close()
+
+    def upload_all():
+        # a fresh mapping each time: its pages fault in as the upload touches them
+        ta = time.perf_counter()
+        g = Gguf(path)
+        moes = []
+        for layer in range(layers):
+            p = f"blk.{layer}."
+            moes.append(MoeExperts.from_gguf(g, p + "ffn_gate_exps.weight", p + "ffn_up_exps.weight",
+                                             p + "ffn_down_exps.weight", E, hidden, inter))
+        tb = time.perf_counter()
+        for m in moes:
+            m.close()
+        g.close()
+        return tb - ta
+
+    variants = {}
+    for name, env in variant_env.items():
+        old = {k: os.environ.get(k) for k in env}
+        os.environ.update(env)
+        variants[name] = total / upload_all() / 1e9
+        for k, v in old.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+        print(f"load: {name} {variants[name]:.2f} GB/s", flush=True)
+    t2 = time.perf_counter()
+    up_s = upload_all()
+    buf = hip.DeviceBuffer(len(gu))
+    src = np.frombuffer(gu, np.uint8)
+    buf.upload(src)
+    t3 = time.perf_counter()
+    for _ in range(3):
+        buf.upload(src)
+    t4 = time.perf_counter()
+    g = Gguf(path)
+    view = g.tensor_bytes("blk.0.ffn_gate_exps.weight")
+    t7 = time.perf_counter()
+    buf.upload(view)                             # pageable copy straight from a fresh mapping
+    t8 = time.perf_counter()
+    del view
+    g.close()
+    buf.free()
+    one = gu[: per[Q4_K] // E]
+    t5 = time.perf_counter()
+    repack(Q4_K, one, inter, hidden)
+    t6 = time.perf_counter()
+    os.remove(path)
+    return {"layers": layers, "bytes": total, "open_ms": 1e3 * (t1 - t0), "upload_s": up_s,
+            "gbs": total / up_s / 1e9, "variants": variants, "memcpy_pageable_gbs": 3 * len(gu) / (t4 - t3) / 1e9,
+            "memcpy_from_map_gbs": len(gu) / (t8 - t7) / 1e9,
+            "host_repack_gbs": len(one) / (t6 - t5) / 1e9}
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--types", default="Q4_0,Q5_0,Q8_0,Q4_K,Q5_K,Q6_K")
@@ -206,8 +295,25 @@ def main(argv=None) -> int:
     ap.add_argument("--prompt", type=int, default=961, help="decoder prompt length")
     ap.add_argument("--steps", type=int, default=128, help="decoder steps")
     ap.add_argument("--no-graph", action="store_true", help="decoder steps launched eagerly")
+    ap.add_argument("--load", type=int, default=0, help="time GGUF ingest of this many MoE layers instead")
+    ap.add_argument("--workdir", default="/tmp", help="where --load writes its GGUF file")
+    ap.add_argument("--load-variants", default="", help="name:ENV=v,ENV=v;... upload settings timed first")
     args = ap.parse_args(argv)
     init()
+    if args.load:
+        venv = {}
+        for spec in filter(None, args.load_variants.split(";")):
+            name, _, kv = spec.partition(":")
+            venv[name] = dict(item.split("=", 1) for item in kv.split(",") if item)
+        r = time_load(args.load, args.workdir, variant_env=venv)
+        print(f"load {r['layers']} layers {r['bytes'] / 1e9:.2f} GB: open {r['open_ms']:.2f} ms, map -> HBM "
+              f"{r['upload_s']:.3f} s = {r['gbs']:.2f} GB/s | pageable hipMemcpy {r['memcpy_pageable_gbs']:.2f} GB/s "
+              f"(from a fresh mapping {r['memcpy_from_map_gbs']:.2f} GB/s) | host repack (1 core) "
+              f"{r['host_repack_gbs']:.2f} GB/s", flush=True)
+        if args.json:
+            with open(args.json, "w") as f:
+                json.dump(r, f, indent=1)
+        return 0
     if args.decode:
         for mode in [{"bf16": 0, "f32": 1}[v] for v in args.modes.split(",") if v]:
             r = time_decode(args.prompt, args.steps, mode, use_graph=not args.no_graph)
