@@ -211,6 +211,21 @@ void re_ffn_destroy(re_ffn *f);
 /* d_norm_w: NULL, or x is RMS-normalised first (the FFN norm, forward.rs:479). */
 int re_ffn_forward_dev(re_ffn *f, const float *d_x, const float *d_norm_w, float eps, float *d_h, void *stream);
 
+/* ---- int8 activations (src/kernel.rs:70-166) ------------------------------------------
+ * re_quantize_q8_act[_dev]: Q8Activation::from_f32 (kernel.rs:88-105) of `rows` activation rows
+ * of n values (n a multiple of 32): scales rows x n/32 f32 (d = max|x|/127 per block) and qs
+ * rows x n i8 (round half away from zero of x/d, clamped to [-127, 127]), each row laid out like
+ * one Q8Activation. The _dev form needs x and qs 16-byte aligned. Bit-identical to the reference.
+ * re_qmat_matmul_i8[_dev]: matvec_q8_0_i8 / matmul_q8_0_i8 (kernel.rs:145-166) of a Q8_0 QMat
+ * against such rows: y (rows x m) = per block the exact i32 dot of weight and activation i8,
+ * folded as s += ((f32)isum * dw) * dx in block order; bit-identical to dot_q8_0_i8
+ * (kernel.rs:123-142). RE_ERR_TYPE for a matrix that is not Q8_0. */
+int re_quantize_q8_act(const float *x, size_t rows, size_t n, float *scales, int8_t *qs);
+int re_quantize_q8_act_dev(const float *d_x, size_t rows, size_t n, float *d_scales, int8_t *d_qs, void *stream);
+int re_qmat_matmul_i8(re_qmat *q, const float *scales, const int8_t *qs, size_t rows, float *y);
+int re_qmat_matmul_i8_dev(re_qmat *q, const float *d_scales, const int8_t *d_qs, size_t rows, float *d_y,
+                          void *stream);
+
 /* ---- GGUF model files (src/gguf.rs:17-392, src/loader.rs:17-130) ----
  * re_gguf_open maps the file read-only and parses its header: magic "GGUF", version 2 (u32
  * counts) or 3 (u64 counts), metadata of every value kind (nested arrays included), up to 8 dims

@@ -66,6 +66,10 @@ def lib():
         L.orc_dequant.argtypes = [C.c_uint32, C.c_void_p, _sz, C.c_void_p, C.POINTER(_sz)]
         L.orc_quantize_q8_0.argtypes = [_f32p, _sz, _u8p]
         L.orc_quantize_q4_0.argtypes = [_f32p, _sz, _u8p]
+        L.orc_quantize_q8_act.argtypes = [_f32p, _sz, _f32p, C.c_void_p]
+        L.orc_dot_q8_0_i8.argtypes = [_u8p, _sz, _f32p, C.c_void_p]
+        L.orc_dot_q8_0_i8.restype = C.c_float
+        L.orc_matmul_q8_0_i8.argtypes = [_u8p, _sz, _sz, _f32p, C.c_void_p, _sz, _f32p]
         L.orc_dot.argtypes = [C.c_uint32, _u8p, _sz, _f32p]
         L.orc_dot.restype = C.c_float
         L.orc_matvec.argtypes = [C.c_uint32, _u8p, _sz, _sz, _f32p, _f32p]
@@ -166,6 +170,33 @@ def quantize_q4_0(src) -> np.ndarray:
     out = np.empty(s.size // 32 * 18, np.uint8)
     _check(lib().orc_quantize_q4_0(s, s.size, out))
     return out
+
+
+def quantize_q8_act(x):
+    """Q8Activation::from_f32 (kernel.rs:88-105): (scales f32[n/32], qs i8[n])."""
+    s = _f32(x)
+    scales = np.empty(max(s.size // 32, 1), np.float32)
+    qs = np.empty(max(s.size, 1), np.int8)
+    _check(lib().orc_quantize_q8_act(s, s.size, scales, qs.ctypes.data))
+    return scales[: s.size // 32], qs[: s.size]
+
+
+def dot_q8_0_i8(row, scales, qs) -> float:
+    """dot_q8_0_i8 (kernel.rs:123-142) over whole Q8_0 blocks."""
+    r = _u8(row)
+    sc = _f32(scales)
+    q = np.ascontiguousarray(qs, np.int8).reshape(-1)
+    return float(lib().orc_dot_q8_0_i8(r, r.size // 34, sc, q.ctypes.data))
+
+
+def matmul_q8_0_i8(w, m: int, n: int, scales, qs, rows: int) -> np.ndarray:
+    """matvec/matmul_q8_0_i8 (kernel.rs:145-166): rows x m."""
+    ww = _u8(w)
+    sc = _f32(scales)
+    q = np.ascontiguousarray(qs, np.int8).reshape(-1)
+    out = np.empty(max(rows * m, 1), np.float32)
+    _check(lib().orc_matmul_q8_0_i8(ww, m, n, sc, q.ctypes.data, rows, out))
+    return out[: rows * m]
 
 
 # ---- kernel.rs ----------------------------------------------------------------------------

@@ -167,6 +167,57 @@ int orc_quantize_q4_0(const float *src, size_t n, uint8_t *out) {
     return ORC_OK;
 }
 
+/* ---- src/kernel.rs:70-166: int8 activations and the integer Q8_0 dot -------------- */
+/* Q8Activation::from_f32 (kernel.rs:88-105): per 32-value block d = max|x| / 127 (the f32::max
+ * fold from 0, so NaN inputs never win), inv = 1/d or 0 when d == 0, q = x*inv rounded half away
+ * from zero and clamped to [-127, 127]; a NaN product becomes 0 (Rust's saturating `as i8`). */
+int orc_quantize_q8_act(const float *x, size_t n, float *scales, int8_t *qs) {
+    if (n % 32) return fail(ORC_ERR_SIZE, "Q8Activation::from_f32: length %zu not a multiple of 32", n);
+    for (size_t b = 0; b < n / 32; ++b) {
+        const float *blk = x + 32 * b;
+        float amax = 0.0f;
+        for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(blk[j]));
+        const float d = amax / 127.0f;
+        const float inv = d > 0.0f ? 1.0f / d : 0.0f;
+        for (int j = 0; j < 32; ++j) {
+            float r = roundf(blk[j] * inv);
+            if (isnan(r)) r = 0.0f;
+            r = fminf(fmaxf(r, -127.0f), 127.0f);
+            qs[32 * b + j] = (int8_t)r;
+        }
+        scales[b] = d;
+    }
+    return ORC_OK;
+}
+
+/* dot_q8_0_i8 (kernel.rs:123-142): per block the exact i32 sum of w_i * q_i, then
+ * s += (isum as f32) * dw * dx evaluated left to right, blocks in order from s = 0. */
+float orc_dot_q8_0_i8(const uint8_t *a, size_t nb, const float *scales, const int8_t *qs) {
+    float s = 0.0f;
+    for (size_t k = 0; k < nb; ++k) {
+        const uint8_t *blk = a + 34 * k;
+        const float dw = orc_f16_to_f32((uint16_t)(blk[0] | (blk[1] << 8)));
+        int32_t isum = 0;
+        for (int j = 0; j < 32; ++j) isum += (int32_t)(int8_t)blk[2 + j] * (int32_t)qs[32 * k + j];
+        float t = (float)isum * dw;
+        t = t * scales[k];
+        s = s + t;
+    }
+    return s;
+}
+
+/* matvec_q8_0_i8 / matmul_q8_0_i8 (kernel.rs:145-166): row by row; activation row r holds
+ * scales[r*nb ..] and qs[r*n ..]; out is rows x m. */
+int orc_matmul_q8_0_i8(const uint8_t *w, size_t m, size_t n, const float *scales, const int8_t *qs,
+                       size_t rows, float *out) {
+    if (n % 32) return fail(ORC_ERR_SIZE, "matvec_q8_0_i8: n = %zu not a multiple of 32", n);
+    const size_t nb = n / 32, row_bytes = nb * 34;
+    for (size_t r = 0; r < rows; ++r)
+        for (size_t i = 0; i < m; ++i)
+            out[r * m + i] = orc_dot_q8_0_i8(w + i * row_bytes, nb, scales + r * nb, qs + r * n);
+    return ORC_OK;
+}
+
 /* ---- scalar fused dots: kernel.rs:17-46, 171-191, 283-322 ------------------------- */
 static float seq_sum_products(const float *a, const float *b, size_t n) {
     float s = -0.0f;

@@ -47,6 +47,15 @@ int orc_dequant(uint32_t t, const uint8_t *data, size_t len, float *out, size_t 
 int orc_quantize_q8_0(const float *src, size_t n, uint8_t *out);
 int orc_quantize_q4_0(const float *src, size_t n, uint8_t *out);
 
+/* ---- src/kernel.rs:70-166: int8 activations (Q8Activation) and the integer Q8_0 dot ---- */
+/* Q8Activation::from_f32: scales[n/32] (f32), qs[n] (i8); n a multiple of 32 */
+int orc_quantize_q8_act(const float *x, size_t n, float *scales, int8_t *qs);
+/* dot_q8_0_i8 over nb whole Q8_0 blocks */
+float orc_dot_q8_0_i8(const uint8_t *a, size_t nb, const float *scales, const int8_t *qs);
+/* matvec/matmul_q8_0_i8: W m x n Q8_0, activation rows (scales rows x n/32, qs rows x n) */
+int orc_matmul_q8_0_i8(const uint8_t *w, size_t m, size_t n, const float *scales, const int8_t *qs,
+                       size_t rows, float *out);
+
 /* ---- src/kernel.rs scalar fused dots and GEMV -------------------------------------- */
 /* dot over `nb` whole blocks of type t against x[nb*QK] (kernel.rs:17-46, 171-191, 283-322) */
 float orc_dot(uint32_t t, const uint8_t *row, size_t nb, const float *x);

@@ -568,6 +568,76 @@ int re_qmat_matmul(re_qmat* q, const float* x, size_t rows, float* y, int mode) 
   return RE_OK;
 }
 
+// ---- int8 activations (kernel.rs:70-166) -------------------------------------------------
+int re_quantize_q8_act_dev(const float* d_x, size_t rows, size_t n, float* d_scales, int8_t* d_qs, void* stream) {
+  if (rows == 0) return RE_OK;
+  if (!d_x || !d_scales || !d_qs) return fail(RE_ERR_ARG, "null pointer");
+  if (n == 0 || n % 32) return fail(RE_ERR_SIZE, "Q8Activation::from_f32: length %zu not a multiple of 32", n);
+  if (rows > (1u << 24) || n > (1u << 24) || rows * (n / 32) > (size_t)INT32_MAX * 256)
+    return fail(RE_ERR_SIZE, "activation %zu x %zu too large", rows, n);
+  if (!aligned16(d_x) || !aligned16(d_qs)) return fail(RE_ERR_ARG, "x and qs must be 16-byte aligned");
+  HIP_TRY(launch_quantize_q8_act(d_x, (int)rows, (int)n, d_scales, d_qs, (hipStream_t)stream));
+  return RE_OK;
+}
+
+int re_quantize_q8_act(const float* x, size_t rows, size_t n, float* scales, int8_t* qs) {
+  if (rows == 0) return RE_OK;
+  if (!x || !scales || !qs) return fail(RE_ERR_ARG, "null pointer");
+  if (n == 0 || n % 32) return fail(RE_ERR_SIZE, "Q8Activation::from_f32: length %zu not a multiple of 32", n);
+  int rc = do_init();
+  if (rc) return rc;
+  const size_t xb = rows * n * sizeof(float), sb = rows * (n / 32) * sizeof(float), qb = rows * n;
+  void* d = nullptr;
+  HIP_TRY(hipMalloc(&d, xb + sb + qb + 512));
+  uint8_t* base = (uint8_t*)d;
+  float* dx = (float*)base;
+  float* ds = (float*)(base + (xb + 255) / 256 * 256);
+  int8_t* dq = (int8_t*)(base + (xb + 255) / 256 * 256 + (sb + 255) / 256 * 256);
+  hipError_t e = hipMemcpy(dx, x, xb, hipMemcpyHostToDevice);
+  if (e == hipSuccess) rc = re_quantize_q8_act_dev(dx, rows, n, ds, dq, nullptr);
+  if (e == hipSuccess && !rc) e = hipMemcpy(scales, ds, sb, hipMemcpyDeviceToHost);
+  if (e == hipSuccess && !rc) e = hipMemcpy(qs, dq, qb, hipMemcpyDeviceToHost);
+  (void)hipFree(d);
+  if (e != hipSuccess) return fail(RE_ERR_HIP, "quantize copy: %s", hipGetErrorString(e));
+  return rc;
+}
+
+int re_qmat_matmul_i8_dev(re_qmat* q, const float* d_scales, const int8_t* d_qs, size_t rows, float* d_y,
+                          void* stream) {
+  if (!q) return fail(RE_ERR_ARG, "null pointer");
+  if (q->g.type != T_Q8_0)
+    return fail(RE_ERR_TYPE, "the int8 activation path needs Q8_0 weights, this matrix is %s", type_name(q->g.type));
+  if (q->count != 1) return fail(RE_ERR_ARG, "stacked matrix: use one matrix per call");
+  if (rows == 0) return RE_OK;
+  if (!d_scales || !d_qs || !d_y) return fail(RE_ERR_ARG, "null pointer");
+  if (rows > 65535u * 32u) return fail(RE_ERR_SIZE, "%zu activation rows (at most %u)", rows, 65535u * 32u);
+  if (!aligned16(d_qs)) return fail(RE_ERR_ARG, "qs must be 16-byte aligned");
+  HIP_TRY(launch_q8_i8_gemm(q->d_w, (int)q->g.tiles, d_scales, d_qs, d_y, (int)q->g.m, (int)q->g.n, (int)rows,
+                            (hipStream_t)stream));
+  return RE_OK;
+}
+
+int re_qmat_matmul_i8(re_qmat* q, const float* scales, const int8_t* qs, size_t rows, float* y) {
+  if (!q || (rows && (!scales || !qs || !y))) return fail(RE_ERR_ARG, "null pointer");
+  if (q->g.type != T_Q8_0)
+    return fail(RE_ERR_TYPE, "the int8 activation path needs Q8_0 weights, this matrix is %s", type_name(q->g.type));
+  if (rows == 0) return RE_OK;
+  std::lock_guard<std::mutex> lk(q->mu);
+  const size_t qb = rows * q->g.n, sb = rows * (q->g.n / 32) * sizeof(float), yb = rows * q->g.m * sizeof(float);
+  const size_t qoff = (sb + 255) / 256 * 256;
+  int rc;
+  if ((rc = q->sx.ensure(qoff + qb)) || (rc = q->sy.ensure(yb))) return rc;
+  uint8_t* base = (uint8_t*)q->sx.p;
+  HIP_TRY(hipMemcpyAsync(base, scales, sb, hipMemcpyHostToDevice, q->stream));
+  HIP_TRY(hipMemcpyAsync(base + qoff, qs, qb, hipMemcpyHostToDevice, q->stream));
+  if ((rc = re_qmat_matmul_i8_dev(q, (const float*)base, (const int8_t*)(base + qoff), rows, (float*)q->sy.p,
+                                  q->stream)))
+    return rc;
+  HIP_TRY(hipMemcpyAsync(y, q->sy.p, yb, hipMemcpyDeviceToHost, q->stream));
+  HIP_TRY(hipStreamSynchronize(q->stream));
+  return RE_OK;
+}
+
 int re_qmat_dequant_dev(re_qmat* q, float* d_out, void* stream) {
   if (!q || !d_out) return fail(RE_ERR_ARG, "null pointer");
   HIP_TRY(launch_dequant(q->g.type, q->d_w, d_out, (int)q->g.m, (int)q->g.n, (int)q->g.kb, (int)q->g.tiles,

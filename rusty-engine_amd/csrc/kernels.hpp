@@ -64,6 +64,12 @@ constexpr int kGemvRowsMaxK = 12288;
 hipError_t launch_gemv(uint32_t type, const GemvArgs& a, int waves, hipStream_t s);
 hipError_t launch_dequant(uint32_t type, const uint8_t* W, float* out, int m, int n, int KB, int tiles,
                           hipStream_t s);
+// Int8 activations (i8.hip): Q8Activation::from_f32 of rows x n f32 (n % 32 == 0, x 16-byte
+// aligned) into scales (rows x n/32) and qs (rows x n, 16-byte aligned); and the Q8_0 x i8 GEMM
+// over tiled Q8_0 weights, y rows x m.
+hipError_t launch_quantize_q8_act(const float* x, int rows, int n, float* scales, int8_t* qs, hipStream_t s);
+hipError_t launch_q8_i8_gemm(const uint8_t* W, int tiles, const float* xs, const int8_t* xq, float* y, int m, int n,
+                             int rows, hipStream_t s);
 // GGUF row-major blocks -> tiled slabs (repack.hip): `mats` matrices of m rows x kb blocks,
 // mat_src bytes apart at src (device) and dst_stride bytes apart at dst, `tiles` tiles each
 hipError_t launch_repack(uint32_t type, const uint8_t* src, uint8_t* dst, int m, int kb, int tiles, int mats,

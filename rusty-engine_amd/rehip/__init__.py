@@ -44,7 +44,8 @@ EXPORTS = ("re_init", "re_last_error", "re_version", "re_row_bytes", "re_tiled_b
            "re_gguf_open", "re_gguf_close", "re_gguf_version", "re_gguf_kv_count", "re_gguf_tensor_count",
            "re_gguf_alignment", "re_gguf_data_offset", "re_gguf_data_start", "re_gguf_kv", "re_gguf_get_int",
            "re_gguf_get_float", "re_gguf_get_str", "re_gguf_get_array", "re_gguf_tensor_info",
-           "re_gguf_find_tensor", "re_gguf_tensor_data", "re_qmat_from_gguf", "re_moe_from_gguf")
+           "re_gguf_find_tensor", "re_gguf_tensor_data", "re_qmat_from_gguf", "re_moe_from_gguf",
+           "re_quantize_q8_act", "re_quantize_q8_act_dev", "re_qmat_matmul_i8", "re_qmat_matmul_i8_dev")
 
 
 class RehipError(RuntimeError):
@@ -136,6 +137,10 @@ def lib() -> C.CDLL:
         L.re_gguf_find_tensor.argtypes = [_vp, C.c_char_p, C.POINTER(_sz)]
         L.re_gguf_tensor_data.argtypes = [_vp, _sz, C.POINTER(_vp), C.POINTER(_sz)]
         L.re_qmat_from_gguf.argtypes = [_vp, C.c_char_p, _sz, _sz, C.POINTER(_vp)]
+        L.re_quantize_q8_act.argtypes = [_vp, _sz, _sz, _vp, _vp]
+        L.re_quantize_q8_act_dev.argtypes = [_vp, _sz, _sz, _vp, _vp, _vp]
+        L.re_qmat_matmul_i8.argtypes = [_vp, _vp, _vp, _sz, _vp]
+        L.re_qmat_matmul_i8_dev.argtypes = [_vp, _vp, _vp, _sz, _vp, _vp]
         L.re_moe_from_gguf.argtypes = [_vp, C.c_char_p, C.c_char_p, C.c_char_p, _sz, _sz, _sz, C.POINTER(_vp)]
         _lib = L
     return _lib
@@ -280,6 +285,21 @@ class QMat:
     def matmul_dev(self, x_dev, rows: int, y_dev, mode: int = MODE_BF16, stream=None) -> None:
         _check(lib().re_qmat_matmul_dev(self._h, _dev_ptr(x_dev), rows, _dev_ptr(y_dev), mode,
                                         _stream_ptr(stream)))
+
+    def matmul_i8(self, scales, qs, rows: int) -> np.ndarray:
+        """matvec/matmul_q8_0_i8 (kernel.rs:145-166) of a Q8_0 matrix against quantized activation
+        rows (scales rows x n/32 f32, qs rows x n int8, as quantize_q8_act returns them)."""
+        sc = _f32(scales)
+        q = np.ascontiguousarray(qs, np.int8).reshape(-1)
+        if sc.size != rows * (self.n // 32) or q.size != rows * self.n:
+            raise RehipError(RE_ERR_SIZE, f"matmul_i8: want {rows} rows of {self.n} quantized values")
+        y = np.empty(max(rows * self.m, 1), np.float32)
+        _check(lib().re_qmat_matmul_i8(self._h, sc.ctypes.data, q.ctypes.data, rows, y.ctypes.data))
+        return y[:rows * self.m]
+
+    def matmul_i8_dev(self, scales_dev, qs_dev, rows: int, y_dev, stream=None) -> None:
+        _check(lib().re_qmat_matmul_i8_dev(self._h, _dev_ptr(scales_dev), _dev_ptr(qs_dev), rows, _dev_ptr(y_dev),
+                                           _stream_ptr(stream)))
 
     def dequant_dev(self, out_dev, stream=None) -> None:
         _check(lib().re_qmat_dequant_dev(self._h, _dev_ptr(out_dev), _stream_ptr(stream)))
@@ -455,6 +475,23 @@ class MoeExperts:
             self.close()
         except Exception:
             pass
+
+
+# ---- int8 activations (src/kernel.rs:70-166) ---------------------------------------------------
+def quantize_q8_act(x, rows: int = 1):
+    """Q8Activation::from_f32 on the GPU for `rows` rows of n values: (scales f32 rows x n/32,
+    qs int8 rows x n)."""
+    xv = _f32(x)
+    n = xv.size // max(rows, 1)
+    sc = np.empty(max(rows * (n // 32), 1), np.float32)
+    qs = np.empty(max(rows * n, 1), np.int8)
+    _check(lib().re_quantize_q8_act(xv.ctypes.data, rows, n, sc.ctypes.data, qs.ctypes.data))
+    return sc[: rows * (n // 32)], qs[: rows * n]
+
+
+def quantize_q8_act_dev(x_dev, rows: int, n: int, scales_dev, qs_dev, stream=None) -> None:
+    _check(lib().re_quantize_q8_act_dev(_dev_ptr(x_dev), rows, n, _dev_ptr(scales_dev), _dev_ptr(qs_dev),
+                                        _stream_ptr(stream)))
 
 
 # ---- GGUF files (src/gguf.rs, src/loader.rs) ----------------------------------------------------

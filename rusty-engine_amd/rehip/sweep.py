@@ -21,6 +21,7 @@ from . import hip, synth
 PROJECTIONS = [("tiny", 64, 32), ("q", 896, 896), ("o", 896, 896), ("k", 128, 896), ("v", 128, 896),
                ("gate", 4864, 896), ("up", 4864, 896), ("down", 896, 4864), ("lm_head", 151936, 896)]
 HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0
 
 
 def algorithmic_bytes(t: int, m: int, k: int) -> int:
@@ -88,6 +89,45 @@ def time_gemm(t: int, m: int, k: int, n: int, mode: int, launches: int, seed: in
     peak = F32_PEAK_TFLOPS if mode == 1 else BF16_PEAK_TFLOPS
     return {"m": m, "k": k, "n": n, "mode": "f32" if mode == 1 else "bf16", "us": us, "tflops": tf,
             "frac_peak": tf / peak, "gbs": algorithmic_bytes(t, m, k) / (us * 1e-6) / 1e9}
+
+
+def time_i8(m: int, k: int, n: int, launches: int, seed: int = 701):
+    """Int8 activation path (kernel.rs:70-166): Q8_0 W[m x k] times n quantized activation rows,
+    one launch of the i8 MFMA GEMM each (the quantize kernel timed apart), against the bf16 and
+    f32 GEMMs on the same weights. Ops = 2 n m k."""
+    from . import MODE_BF16, MODE_F32, Q8_0, quantize_q8_act_dev
+    rng = np.random.default_rng(seed)
+    w = synth.weight_bytes(rng, Q8_0, m, k)
+    x = synth.activations(rng, n, k)
+    q = QMat.from_bytes(Q8_0, w, m, k)
+    dx = hip.DeviceBuffer.from_array(x)
+    ds, dq, dy = hip.DeviceBuffer(n * (k // 32) * 4), hip.DeviceBuffer(n * k), hip.DeviceBuffer(n * m * 4)
+    s = hip.Stream()
+
+    def timed(body):
+        body()
+        s.synchronize()
+        g = hip.Graph(s, lambda: [body() for _ in range(launches)])
+        g.launch()
+        s.synchronize()
+        e0, e1 = hip.Event(), hip.Event()
+        e0.record(s)
+        g.launch()
+        e1.record(s)
+        e1.synchronize()
+        g.destroy()
+        return e0.elapsed_ms(e1) * 1e3 / launches
+
+    us_q = timed(lambda: quantize_q8_act_dev(dx, n, k, ds, dq, stream=s))
+    us_i8 = timed(lambda: q.matmul_i8_dev(ds, dq, n, dy, stream=s))
+    us_bf16 = timed(lambda: q.matmul_dev(dx, n, dy, MODE_BF16, stream=s))
+    us_f32 = timed(lambda: q.matmul_dev(dx, n, dy, MODE_F32, stream=s))
+    q.close()
+    s.destroy()
+    ops = 2.0 * n * m * k
+    return {"m": m, "k": k, "n": n, "us_quantize": us_q, "us_i8": us_i8, "tops_i8": ops / (us_i8 * 1e-6) / 1e12,
+            "frac_int8_peak": ops / (us_i8 * 1e-6) / 1e12 / INT8_PEAK_TOPS, "us_bf16": us_bf16, "us_f32": us_f32,
+            "gbs_i8": algorithmic_bytes(Q8_0, m, k) / (us_i8 * 1e-6) / 1e9}
 
 
 MOE = {"n_experts": 128, "hidden": 2048, "inter": 768, "top_k": 8}
@@ -295,11 +335,25 @@ def main(argv=None) -> int:
     ap.add_argument("--prompt", type=int, default=961, help="decoder prompt length")
     ap.add_argument("--steps", type=int, default=128, help="decoder steps")
     ap.add_argument("--no-graph", action="store_true", help="decoder steps launched eagerly")
+    ap.add_argument("--i8", action="store_true", help="time the int8 activation GEMM instead")
     ap.add_argument("--load", type=int, default=0, help="time GGUF ingest of this many MoE layers instead")
     ap.add_argument("--workdir", default="/tmp", help="where --load writes its GGUF file")
     ap.add_argument("--load-variants", default="", help="name:ENV=v,ENV=v;... upload settings timed first")
     args = ap.parse_args(argv)
     init()
+    if args.i8:
+        rows = []
+        for m, k in ((4864, 896), (896, 4864)):
+            for n in (int(v) for v in args.rows.split(",") if v):
+                r = time_i8(m, k, n, launches=50 if n > 64 else 200)
+                rows.append(r)
+                print(f"i8 Q8_0 {m}x{k} N={n:4d}: quantize {r['us_quantize']:7.2f} us | i8 GEMM {r['us_i8']:8.2f} us "
+                      f"{r['tops_i8']:7.1f} TOP/s ({100 * r['frac_int8_peak']:4.1f}% of int8) "
+                      f"{r['gbs_i8']:7.1f} GB/s | bf16 {r['us_bf16']:8.2f} us | f32 {r['us_f32']:8.2f} us", flush=True)
+        if args.json:
+            with open(args.json, "w") as f:
+                json.dump(rows, f, indent=1)
+        return 0
     if args.load:
         venv = {}
         for spec in filter(None, args.load_variants.split(";")):
