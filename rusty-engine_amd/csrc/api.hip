@@ -1188,6 +1188,26 @@ int re_attention_dev(const float* d_q, const float* d_kcache, const float* d_vca
   return RE_OK;
 }
 
+int re_attention_decode_dev(const float* d_q, const float* d_k, const float* d_v, const float* d_bq, const float* d_bk,
+                            const float* d_bv, size_t n_heads, size_t n_kv_heads, size_t head_dim, float theta,
+                            const int* d_pos, float* d_kcache, float* d_vcache, size_t max_seq, float* d_work,
+                            size_t work_bytes, float* d_ctx, void* stream) {
+  if (!d_q || !d_k || !d_v || !d_pos || !d_kcache || !d_vcache || !d_work || !d_ctx)
+    return fail(RE_ERR_ARG, "null pointer");
+  if (n_heads == 0 || n_kv_heads == 0 || n_heads % n_kv_heads || head_dim == 0 || head_dim % 4 || head_dim > 256 ||
+      max_seq == 0 || max_seq > 32768 || n_heads > 65535)
+    return fail(RE_ERR_SIZE, "attention shape heads %zu/%zu head_dim %zu max_seq %zu", n_heads, n_kv_heads, head_dim,
+                max_seq);
+  if (!aligned16(d_kcache) || !aligned16(d_vcache) || !aligned16(d_ctx))
+    return fail(RE_ERR_ARG, "caches and ctx must be 16-byte aligned");
+  if (work_bytes < re_attention_work_bytes(1, n_heads, head_dim, max_seq))
+    return fail(RE_ERR_SIZE, "attention workspace of %zu bytes, need %zu", work_bytes,
+                re_attention_work_bytes(1, n_heads, head_dim, max_seq));
+  HIP_TRY(launch_attention_decode(d_q, d_k, d_v, d_bq, d_bk, d_bv, (int)n_heads, (int)n_kv_heads, (int)head_dim, theta,
+                                  d_pos, d_kcache, d_vcache, (int)max_seq, d_work, d_ctx, (hipStream_t)stream));
+  return RE_OK;
+}
+
 int re_qkv_rope_append_dev(const float* d_q, size_t ldq, const float* d_k, size_t ldk, const float* d_v, size_t ldv,
                            const float* d_bq, const float* d_bk, const float* d_bv, size_t rows, size_t n_heads,
                            size_t n_kv_heads, size_t head_dim, float theta, const int* d_pos, float* d_qout,

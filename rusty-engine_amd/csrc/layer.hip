@@ -238,11 +238,37 @@ __global__ __launch_bounds__(kAttnRowsThreads) void attention_rows_kernel(
 constexpr int kAttnSplitKeys = 128;      // 16 teams x 8 keys
 constexpr int kAttnMaxSplits = 256;      // 32768 cache rows
 
-template <int NC>
-__global__ __launch_bounds__(256) void attention_split_kernel(const float* __restrict__ q, const float* __restrict__ kc,
-                                                              const float* __restrict__ vc, int heads, int kv_heads,
+// One decode row's q|k|v epilogue folded into the key-split attention (attention_decode): the
+// projection outputs are raw (no bias, not rotated); each workgroup rotates its q head itself,
+// and the split holding the new key position rotates k and biases v for its kv head, uses them
+// for that key, and (the first q head of the kv group only) appends them to the caches. No other
+// split reads that cache row in this launch, so there is no ordering between workgroups.
+struct DecodeQkv {
+  const float* ks;      // raw k of the row (kv_heads x hd), ks/vs strided like q
+  const float* vs;
+  const float* bq;      // biases or null
+  const float* bk;
+  const float* bv;
+  float base;           // RoPE theta
+  float* kc_out;        // caches, written at row *pos
+  float* vc_out;
+};
+
+// NeoX rotation of the pair (x0, x1) = (x[i], x[i + hd/2]) at position p (infer.rs:90-139); shared
+// by qkv_rope_append_kernel and the folded decode epilogue, so both give the same bits
+__device__ __forceinline__ void rope_pair(float x0, float x1, int i, int hd, int p, float base, float& o0, float& o1) {
+  const float f = 1.0f / powf(base, (float)(2 * i) / (float)hd);
+  const float a = (float)p * f;
+  const float c = cosf(a), sn = sinf(a);
+  o0 = x0 * c - x1 * sn;
+  o1 = x1 * c + x0 * sn;
+}
+
+template <int NC, bool QKV>   // kc / vc are not __restrict__: with QKV the new row is stored through dq
+__global__ __launch_bounds__(256) void attention_split_kernel(const float* __restrict__ q, const float* kc,
+                                                              const float* vc, int heads, int kv_heads,
                                                               int hd, int max_seq, const int* __restrict__ pos,
-                                                              float* __restrict__ work) {
+                                                              float* __restrict__ work, DecodeQkv dq) {
   constexpr int U = 8;
   __shared__ float sc[kAttnSplitKeys];
   __shared__ float red[4];
@@ -250,7 +276,8 @@ __global__ __launch_bounds__(256) void attention_split_kernel(const float* __res
   const int h = blockIdx.x, r = blockIdx.y, sp = blockIdx.z, nsp = gridDim.z;
   const int kvh = h / (heads / kv_heads);
   const int kv_dim = kv_heads * hd;
-  const int L = min(max(*pos + r + 1, 1), max_seq);
+  const int p0 = *pos;
+  const int L = min(max(p0 + r + 1, 1), max_seq);
   const int j0 = sp * kAttnSplitKeys;
   float* wp = work + (((size_t)r * heads + h) * nsp + sp) * (hd + 2);
   if (j0 >= L) {                         // nothing visible in this split
@@ -260,17 +287,38 @@ __global__ __launch_bounds__(256) void attention_split_kernel(const float* __res
   const int jn = min(kAttnSplitKeys, L - j0);
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int team = 4 * w + (lane >> 4), tl = lane & 15;
-  const float* qh = q + ((size_t)r * heads + h) * hd;
-  float4 qv[NC];
-#pragma unroll
-  for (int c = 0; c < NC; ++c) {
-    const int d = 4 * tl + 64 * c;
-    qv[c] = d < hd ? *reinterpret_cast<const float4*>(qh + d) : make_float4(0.f, 0.f, 0.f, 0.f);
-  }
   const float scale = 1.0f / sqrtf((float)hd);
   const float* kbase = kc + (size_t)kvh * hd;
   const float* vbase = vc + (size_t)kvh * hd;
-  // keys j0 + 16 u + team, u < U: all loads of K and V issued up front (V lands under the scores)
+  // QKV: the split holding key p0 (< max_seq) also builds the new key and value. Thread t < hd/2
+  // takes rotation pair t of q (and of k), thread t < hd element t of v; their inputs are loaded
+  // before the K/V rows so that the epilogue waits for them alone.
+  const bool has_new = QKV && p0 >= 0 && p0 < max_seq && p0 >= j0 && p0 < j0 + jn;
+  const int half = hd >> 1, t = threadIdx.x;
+  float qx0 = 0.0f, qx1 = 0.0f, kx0 = 0.0f, kx1 = 0.0f, vx = 0.0f;
+  if constexpr (QKV) {
+    if (t < half) {
+      const float* qr = q + (size_t)h * hd;
+      qx0 = qr[t];
+      qx1 = qr[t + half];
+      if (dq.bq) {
+        qx0 += dq.bq[(size_t)h * hd + t];
+        qx1 += dq.bq[(size_t)h * hd + t + half];
+      }
+      if (has_new) {
+        const float* kr = dq.ks + (size_t)kvh * hd;
+        kx0 = kr[t];
+        kx1 = kr[t + half];
+        if (dq.bk) {
+          kx0 += dq.bk[(size_t)kvh * hd + t];
+          kx1 += dq.bk[(size_t)kvh * hd + t + half];
+        }
+      }
+    }
+    if (has_new && t < hd) vx = dq.bv ? dq.vs[(size_t)kvh * hd + t] + dq.bv[(size_t)kvh * hd + t] : dq.vs[(size_t)kvh * hd + t];
+  }
+  // keys j0 + 16 u + team, u < U: all loads of K and V issued up front (V lands under the scores;
+  // with QKV the new key's row, not yet written, is replaced after the epilogue)
   float4 kv[U][NC], vv[U][NC];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
@@ -288,6 +336,43 @@ __global__ __launch_bounds__(256) void attention_split_kernel(const float* __res
     for (int c = 0; c < NC; ++c) {
       const int d = 4 * tl + 64 * c;
       vv[u][c] = d < hd ? *reinterpret_cast<const float4*>(vbase + row + d) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  }
+  // QKV: rotated q in part[0..hd), the new key and value in part[256..256+hd), part[512..512+hd)
+  if constexpr (QKV) {
+    if (t < half) {
+      rope_pair(qx0, qx1, t, hd, p0, dq.base, part[t], part[t + half]);
+      if (has_new) rope_pair(kx0, kx1, t, hd, p0, dq.base, part[256 + t], part[256 + t + half]);
+    }
+    if (has_new && t < hd) part[512 + t] = vx;
+    __syncthreads();
+    if (has_new && h % (heads / kv_heads) == 0) {
+      for (int i = threadIdx.x; i < hd; i += 256) {
+        dq.kc_out[(size_t)p0 * kv_dim + (size_t)kvh * hd + i] = part[256 + i];
+        dq.vc_out[(size_t)p0 * kv_dim + (size_t)kvh * hd + i] = part[512 + i];
+      }
+    }
+  }
+  const float* qh = QKV ? part : q + ((size_t)r * heads + h) * hd;
+  float4 qv[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int d = 4 * tl + 64 * c;
+    qv[c] = d < hd ? *reinterpret_cast<const float4*>(qh + d) : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  if (has_new) {                         // the new key is the split's last: from LDS, not the cache
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (j0 + min(16 * u + team, jn - 1) == p0) {
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          const int d = 4 * tl + 64 * c;
+          if (d < hd) {
+            kv[u][c] = *reinterpret_cast<const float4*>(part + 256 + d);
+            vv[u][c] = *reinterpret_cast<const float4*>(part + 512 + d);
+          }
+        }
+      }
     }
   }
   float mx = -INFINITY;
@@ -594,16 +679,12 @@ __global__ __launch_bounds__(64) void qkv_rope_append_kernel(const float* __rest
   const float* bias = is_q ? (bq ? bq + (size_t)hh * hd : nullptr) : (bk ? bk + (size_t)kh * hd : nullptr);
   float* dst = is_q ? qout + ((size_t)r * heads + hh) * hd : kc + (size_t)p * kv_heads * hd + (size_t)kh * hd;
   for (int i = threadIdx.x; i < half; i += 64) {
-    const float f = 1.0f / powf(base, (float)(2 * i) / (float)hd);
-    const float a = (float)p * f;
-    const float c = cosf(a), sn = sinf(a);
     float x0 = src[i], x1 = src[i + half];
     if (bias) {
       x0 += bias[i];
       x1 += bias[i + half];
     }
-    dst[i] = x0 * c - x1 * sn;
-    dst[i + half] = x1 * c + x0 * sn;
+    rope_pair(x0, x1, i, hd, p, base, dst[i], dst[i + half]);
   }
   if (!is_q) {
     const float* vsrc = vs + (size_t)r * ldv + (size_t)kh * hd;
@@ -703,15 +784,16 @@ hipError_t launch_attention(const float* q, const float* kc, const float* vc, in
   if (work) {
     const int nsp = (max_seq + kAttnSplitKeys - 1) / kAttnSplitKeys;
     const dim3 grid((unsigned)heads, (unsigned)rows, (unsigned)nsp);
+    const DecodeQkv none{};
     if (hd <= 64)
-      hipLaunchKernelGGL(attention_split_kernel<1>, grid, dim3(256), 0, s, q, kc, vc, heads, kv_heads, hd, max_seq,
-                         pos, work);
+      hipLaunchKernelGGL((attention_split_kernel<1, false>), grid, dim3(256), 0, s, q, kc, vc, heads, kv_heads, hd,
+                         max_seq, pos, work, none);
     else if (hd <= 128)
-      hipLaunchKernelGGL(attention_split_kernel<2>, grid, dim3(256), 0, s, q, kc, vc, heads, kv_heads, hd, max_seq,
-                         pos, work);
+      hipLaunchKernelGGL((attention_split_kernel<2, false>), grid, dim3(256), 0, s, q, kc, vc, heads, kv_heads, hd,
+                         max_seq, pos, work, none);
     else
-      hipLaunchKernelGGL(attention_split_kernel<4>, grid, dim3(256), 0, s, q, kc, vc, heads, kv_heads, hd, max_seq,
-                         pos, work);
+      hipLaunchKernelGGL((attention_split_kernel<4, false>), grid, dim3(256), 0, s, q, kc, vc, heads, kv_heads, hd,
+                         max_seq, pos, work, none);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(attention_combine_kernel, dim3((unsigned)heads, (unsigned)rows), dim3(64), 0, s, work, heads,
@@ -731,6 +813,27 @@ hipError_t launch_attention(const float* q, const float* kc, const float* vc, in
                        max_seq, pos, ctx);
   return hipGetLastError();
 }
+hipError_t launch_attention_decode(const float* q, const float* k, const float* v, const float* bq, const float* bk,
+                                   const float* bv, int heads, int kv_heads, int hd, float base, const int* pos,
+                                   float* kc, float* vc, int max_seq, float* work, float* ctx, hipStream_t s) {
+  const int nsp = (max_seq + kAttnSplitKeys - 1) / kAttnSplitKeys;
+  const dim3 grid((unsigned)heads, 1u, (unsigned)nsp);
+  const DecodeQkv dq{k, v, bq, bk, bv, base, kc, vc};
+  if (hd <= 64)
+    hipLaunchKernelGGL((attention_split_kernel<1, true>), grid, dim3(256), 0, s, q, kc, vc, heads, kv_heads, hd,
+                       max_seq, pos, work, dq);
+  else if (hd <= 128)
+    hipLaunchKernelGGL((attention_split_kernel<2, true>), grid, dim3(256), 0, s, q, kc, vc, heads, kv_heads, hd,
+                       max_seq, pos, work, dq);
+  else
+    hipLaunchKernelGGL((attention_split_kernel<4, true>), grid, dim3(256), 0, s, q, kc, vc, heads, kv_heads, hd,
+                       max_seq, pos, work, dq);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(attention_combine_kernel, dim3((unsigned)heads, 1u), dim3(64), 0, s, work, heads, hd, nsp, ctx);
+  return hipGetLastError();
+}
+
 hipError_t launch_add(const float* a, const float* b, size_t n, size_t nb, float* out, hipStream_t s) {
   if (n == 0) return hipSuccess;
   hipLaunchKernelGGL(add_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a, b, n, nb, out);

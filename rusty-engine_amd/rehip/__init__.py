@@ -45,7 +45,8 @@ EXPORTS = ("re_init", "re_last_error", "re_version", "re_row_bytes", "re_tiled_b
            "re_gguf_alignment", "re_gguf_data_offset", "re_gguf_data_start", "re_gguf_kv", "re_gguf_get_int",
            "re_gguf_get_float", "re_gguf_get_str", "re_gguf_get_array", "re_gguf_tensor_info",
            "re_gguf_find_tensor", "re_gguf_tensor_data", "re_qmat_from_gguf", "re_moe_from_gguf",
-           "re_quantize_q8_act", "re_quantize_q8_act_dev", "re_qmat_matmul_i8", "re_qmat_matmul_i8_dev")
+           "re_quantize_q8_act", "re_quantize_q8_act_dev", "re_qmat_matmul_i8", "re_qmat_matmul_i8_dev",
+           "re_attention_decode_dev")
 
 
 class RehipError(RuntimeError):
@@ -137,6 +138,8 @@ def lib() -> C.CDLL:
         L.re_gguf_find_tensor.argtypes = [_vp, C.c_char_p, C.POINTER(_sz)]
         L.re_gguf_tensor_data.argtypes = [_vp, _sz, C.POINTER(_vp), C.POINTER(_sz)]
         L.re_qmat_from_gguf.argtypes = [_vp, C.c_char_p, _sz, _sz, C.POINTER(_vp)]
+        L.re_attention_decode_dev.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, C.c_float, _vp, _vp, _vp,
+                                              _sz, _vp, _sz, _vp, _vp]
         L.re_quantize_q8_act.argtypes = [_vp, _sz, _sz, _vp, _vp]
         L.re_quantize_q8_act_dev.argtypes = [_vp, _sz, _sz, _vp, _vp, _vp]
         L.re_qmat_matmul_i8.argtypes = [_vp, _vp, _vp, _sz, _vp]
@@ -362,6 +365,15 @@ def qkv_rope_append_dev(q, ldq, k, ldk, v, ldv, bq, bk, bv, rows, n_heads, n_kv_
     _check(lib().re_qkv_rope_append_dev(_p(q), ldq, _p(k), ldk, _p(v), ldv, _p(bq), _p(bk), _p(bv), rows, n_heads,
                                         n_kv_heads, head_dim, theta, _p(pos), _p(qout), _p(kcache), _p(vcache),
                                         max_seq, _stream_ptr(stream)))
+
+
+def attention_decode_dev(q, k, v, bq, bk, bv, n_heads, n_kv_heads, head_dim, theta, pos, kcache, vcache, max_seq,
+                         work, work_bytes, ctx, stream=None):
+    """One decode row: q/k/v bias + RoPE + cache append folded into the key-split attention
+    (re_attention_decode_dev)."""
+    _check(lib().re_attention_decode_dev(_p(q), _p(k), _p(v), _p(bq), _p(bk), _p(bv), n_heads, n_kv_heads, head_dim,
+                                         theta, _p(pos), _p(kcache), _p(vcache), max_seq, _p(work), work_bytes,
+                                         _p(ctx), _stream_ptr(stream)))
 
 
 def decode_advance_dev(best, tok, pos, delta, hist=None, hist_len=0, stream=None):

@@ -440,6 +440,15 @@ class DeviceDecoder:
                             blk["q_bias"], blk["k_bias"], blk["v_bias"], rows, g.n_heads, g.n_kv_heads, g.head_dim,
                             g.rope_freq_base, self.pos, self.qb, blk["kc"], blk["vc"], self.max_seq, self.stream)
 
+    def _decode_attention(self, blk):
+        """One decode row: q|k|v epilogue and attention in one call (two kernels)."""
+        from . import attention_decode_dev
+        g, d, kv = self.g, self.g.d_model, self.kv
+        attention_decode_dev(self.qkv, _Offset(self.qkv, 4 * d), _Offset(self.qkv, 4 * (d + kv)), blk["q_bias"],
+                             blk["k_bias"], blk["v_bias"], g.n_heads, g.n_kv_heads, g.head_dim, g.rope_freq_base,
+                             self.pos, blk["kc"], blk["vc"], self.max_seq, self.work, self.work_bytes, self.ctx,
+                             self.stream)
+
     def _attention(self, blk, rows):
         from . import attention_dev
         g = self.g
@@ -460,8 +469,7 @@ class DeviceDecoder:
         embed_dev(self.embed, self.mb.n_vocab, g.d_model, self.tok, 1, self.x, s)
         for blk in self.blocks:
             blk["qkv"].matvec_ex_dev(self.x, self.qkv, norm_w=blk["attn_norm"], eps=eps, stream=s)
-            self._qkv_post(blk, 1)
-            self._attention(blk, 1)
+            self._decode_attention(blk)
             blk["o"].matvec_ex_dev(self.ctx, self.x, add=self.x, stream=s)            # residual
             blk["ffn"].forward_dev(self.x, self.hb, norm_w=blk["ffn_norm"], eps=eps, stream=s)
             blk["down"].matvec_ex_dev(self.hb, self.x, add=self.x, stream=s)          # residual

@@ -341,3 +341,49 @@ def test_device_decoder_qwen_shape_64_steps_match_cpu_path():
     got += dd.history(961 + 32, 32)
     dd.close()
     assert got == want, next(i for i, (a, b) in enumerate(zip(got, want)) if a != b)
+
+
+@pytest.mark.parametrize("nh,nkv,hd,pos0,bias", [(14, 2, 64, 0, True), (14, 2, 64, 37, True), (14, 2, 64, 127, False),
+                                                 (14, 2, 64, 128, True), (4, 4, 128, 300, True),
+                                                 (2, 1, 256, 511, True), (14, 2, 64, 512, True)])
+def test_attention_decode_equals_epilogue_then_attention(nh, nkv, hd, pos0, bias):
+    """re_attention_decode_dev (q|k|v epilogue folded into the split attention) against
+    re_qkv_rope_append_dev + re_attention_dev on the same raw projection row: identical context
+    and caches, including the split boundary (position 128), the last cache row and a position
+    past the cache (nothing stored, the old keys attended)."""
+    max_seq = 512
+    rng = np.random.default_rng(pos0 + nh)
+    kvd = nkv * hd
+    kc0 = np.zeros((max_seq, kvd), np.float32)
+    vc0 = np.zeros((max_seq, kvd), np.float32)
+    n_old = min(pos0, max_seq)
+    kc0[:n_old] = rng.standard_normal((n_old, kvd))
+    vc0[:n_old] = rng.standard_normal((n_old, kvd))
+    qkv = rng.standard_normal(nh * hd + 2 * kvd).astype(np.float32)
+    bq = (0.1 * rng.standard_normal(nh * hd)).astype(np.float32) if bias else None
+    bk = (0.1 * rng.standard_normal(kvd)).astype(np.float32) if bias else None
+    bv = (0.1 * rng.standard_normal(kvd)).astype(np.float32) if bias else None
+    dq = B.from_array(qkv)
+    kd, vd = nh * hd * 4, (nh * hd + kvd) * 4
+    bqd, bkd, bvd = [B.from_array(b) if b is not None else None for b in (bq, bk, bv)]
+    pd = dev_i32([pos0])
+    wb = rehip.attention_work_bytes(1, nh, hd, max_seq)
+    theta = 10000.0
+    # reference path: epilogue kernel, then attention
+    kc_a, vc_a = B.from_array(kc0), B.from_array(vc0)
+    qb, ctx_a = B(nh * hd * 4), B(nh * hd * 4)
+    ld = nh * hd + 2 * kvd
+    rehip.qkv_rope_append_dev(dq, ld, qwen._Offset(dq, kd), ld, qwen._Offset(dq, vd), ld, bqd, bkd, bvd, 1, nh, nkv, hd, theta, pd,
+                              qb, kc_a, vc_a, max_seq)
+    rehip.attention_dev(qb, kc_a, vc_a, 1, nh, nkv, hd, max_seq, pd, ctx_a,
+                        work=B.from_array(np.full(wb // 4, np.nan, np.float32)), work_bytes=wb)
+    # folded path
+    kc_b, vc_b = B.from_array(kc0), B.from_array(vc0)
+    ctx_b = B(nh * hd * 4)
+    rehip.attention_decode_dev(dq, qwen._Offset(dq, kd), qwen._Offset(dq, vd), bqd, bkd, bvd, nh, nkv, hd, theta, pd, kc_b, vc_b,
+                               max_seq, B.from_array(np.full(wb // 4, np.nan, np.float32)), wb, ctx_b)
+    a, b = down(ctx_a, nh * hd), down(ctx_b, nh * hd)
+    assert np.isfinite(b).all()
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    assert np.array_equal(down(kc_a, max_seq * kvd), down(kc_b, max_seq * kvd))
+    assert np.array_equal(down(vc_a, max_seq * kvd), down(vc_b, max_seq * kvd))
