@@ -158,6 +158,124 @@ __global__ __launch_bounds__(128) void q8_i8_gemm_kernel(const uint8_t* __restri
   }
 }
 
+constexpr int kSegWaves = 4;    // K segments (one per wave) of one output tile
+constexpr int kSegBlocks = 4;   // blocks per wave per round
+
+// Long rows over few output tiles: one 32 x 32 output tile per workgroup of kSegWaves waves. A
+// round covers kSegWaves * kSegBlocks consecutive blocks; wave w takes kSegBlocks of them and
+// computes their terms ((f32)isum * dw) * dx in parallel with the other waves (one i8 MFMA per
+// block, as q8_i8_gemm_kernel), then the running sums (16 per lane) pass from wave to wave
+// through LDS, each wave adding its terms in block order: the same fold, in the same order, as
+// one lane walking all blocks, with only the adds serial. The next round's operands load during
+// the folds (keeping two rounds in flight measured no faster: the compiler's wait counts then
+// drain every outstanding load at the round's first MFMA).
+__global__ __launch_bounds__(64 * kSegWaves) void q8_i8_gemm_seg_kernel(const uint8_t* __restrict__ W,
+                                                                         const float* __restrict__ xs,
+                                                                         const int8_t* __restrict__ xq,
+                                                                         float* __restrict__ y, int m, int n,
+                                                                         int rows) {
+#pragma clang fp contract(off)
+  constexpr int S = kSegWaves, KBs = kSegBlocks, RB = S * KBs;
+  static_assert(kI8Chunk % RB == 0, "scale chunks hold whole rounds");
+  extern __shared__ __align__(16) float dxs_flat[];   // min(nb, kI8Chunk) x 32 scales
+  float (*dxs)[32] = reinterpret_cast<float (*)[32]>(dxs_flat);
+  __shared__ float sbuf[16][64];          // running sums, [result register][lane]
+  const int nb = n >> 5;
+  const int grp = blockIdx.x;             // 32 weight rows: tile grp/2, rows 32 (grp%2) ..
+  const int tile = grp >> 1;
+  const int r0 = blockIdx.y * 32;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int h = lane >> 5, c = lane & 31;
+  const int trow = (grp & 1) * 32 + c;
+  const uint8_t* wb = W + (size_t)tile * nb * (64 * 34) + h * (64 * 16) + trow * 16;
+  const uint8_t* wd = W + (size_t)tile * nb * (64 * 34) + 2 * (64 * 16) + trow * 2;
+  const int8_t* arow = xq + (size_t)min(r0 + c, rows - 1) * n + 16 * h;
+  const int rounds = (nb + RB - 1) / RB;
+  v4i A[KBs], Bw[KBs];
+  uint32_t D[KBs];
+  auto load = [&](int rr, v4i (&a)[KBs], v4i (&b)[KBs], uint32_t (&d)[KBs]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < KBs; ++j) {
+      const int kb = min(rr * RB + wave * KBs + j, nb - 1);
+      a[j] = *reinterpret_cast<const v4i*>(arow + (size_t)kb * 32);
+      b[j] = *reinterpret_cast<const v4i*>(wb + (size_t)kb * (64 * 34));
+      d[j] = *reinterpret_cast<const uint16_t*>(wd + (size_t)kb * (64 * 34));
+    }
+  };
+  load(0, A, Bw, D);
+  float s[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) s[i] = 0.0f;
+  auto round = [&](int rr, v4i (&a)[KBs], v4i (&b)[KBs], uint32_t (&d)[KBs]) __attribute__((always_inline)) {
+    const int b0 = rr * RB;
+    const int kc0 = b0 / kI8Chunk * kI8Chunk;     // first block of the staged scale chunk
+    if (b0 == kc0) {
+      // scales of 32 activation rows x the chunk's blocks -> dxs[block][row], 8 loads in flight
+      const int kc = min(kI8Chunk, nb - kc0);
+      __syncthreads();                    // the previous chunk's readers are done
+      for (int e0 = threadIdx.x; e0 < kc * 32; e0 += 64 * S * 8) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int e = e0 + 64 * S * u;
+          const int t = e / kc, k = e - t * kc;
+          v[u] = e < kc * 32 ? xs[(size_t)min(r0 + t, rows - 1) * nb + kc0 + k] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int e = e0 + 64 * S * u;
+          const int t = e / kc, k = e - t * kc;
+          if (e < kc * 32) dxs[k][t] = v[u];
+        }
+      }
+      __syncthreads();
+    }
+    float tm[KBs][16];
+#pragma unroll
+    for (int j = 0; j < KBs; ++j) {
+      const v16i acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[j], b[j], v16i{}, 0, 0, 0);
+      const float dw = f16_bits_to_f32(d[j]);
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int kl = min(b0 + wave * KBs + j, nb - 1) - kc0;   // clamped blocks are not folded
+        const float4 dx = *reinterpret_cast<const float4*>(&dxs[kl][8 * g + 4 * h]);
+        const float dxv[4] = {dx.x, dx.y, dx.z, dx.w};
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) tm[j][4 * g + jj] = ((float)acc[4 * g + jj] * dw) * dxv[jj];
+      }
+    }
+    if (rr + 1 < rounds) load(rr + 1, a, b, d);   // the next round's operands load during the folds
+    // ordered fold: waves 0 .. S-1 in turn, each continuing the running sums of the one before
+    for (int w = 0; w < S; ++w) {
+      if (wave == w) {
+        if (rr > 0 || w > 0) {
+#pragma unroll
+          for (int i = 0; i < 16; ++i) s[i] = sbuf[i][lane];
+        }
+#pragma unroll
+        for (int j = 0; j < KBs; ++j) {
+          if (b0 + w * KBs + j < nb) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) s[i] = s[i] + tm[j][i];
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) sbuf[i][lane] = s[i];
+      }
+      __syncthreads();
+    }
+  };
+  for (int rr = 0; rr < rounds; ++rr) round(rr, A, Bw, D);
+  if (wave != 0) return;
+  const int wr = tile * 64 + trow;
+  if (wr >= m) return;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int r = r0 + 8 * (i >> 2) + 4 * h + (i & 3);
+    if (r < rows) y[(size_t)r * m + wr] = sbuf[i][lane];
+  }
+}
+
 constexpr int kI8GemvRows = 16;       // weight rows per workgroup
 constexpr int kI8GemvMaxBlocks = 960; // 16 x (nb + 1) f32 terms in LDS, at most 61.5 KB (n <= 30720)
 
@@ -220,9 +338,16 @@ hipError_t launch_q8_i8_gemm(const uint8_t* W, int tiles, const float* xs, const
                        y, m, n);
     return hipGetLastError();
   }
+  const unsigned rgroups = (unsigned)((rows + 31) / 32);
+  // long rows over few output tiles: split each tile's fold over the waves of a workgroup
+  if ((n >> 5) >= 64 && (size_t)tiles * 2 * rgroups < 512) {
+    const size_t lds = (size_t)min(n >> 5, kI8Chunk) * 32 * sizeof(float);
+    hipLaunchKernelGGL(q8_i8_gemm_seg_kernel, dim3((unsigned)tiles * 2, rgroups), dim3(64 * kSegWaves), lds, s, W,
+                       xs, xq, y, m, n, rows);
+    return hipGetLastError();
+  }
   const size_t lds = (size_t)min(n >> 5, kI8Chunk) * 32 * sizeof(float);
-  hipLaunchKernelGGL(q8_i8_gemm_kernel, dim3((unsigned)tiles, (unsigned)((rows + 31) / 32)), dim3(128), lds, s, W, xs,
-                     xq, y, m, n, rows);
+  hipLaunchKernelGGL(q8_i8_gemm_kernel, dim3((unsigned)tiles, rgroups), dim3(128), lds, s, W, xs, xq, y, m, n, rows);
   return hipGetLastError();
 }
 

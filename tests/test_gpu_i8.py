@@ -69,8 +69,12 @@ def test_reference_fixture_matvec_and_matmul():
     q.close()
 
 
+# rows >= 64 blocks over few output tiles take the K-segmented kernel (the fold handed from wave
+# to wave): (130, 2048, 33), (64, 2080, 5) with a one-block last round, (896, 4864, 7), and
+# (64, 9600, 3) whose 300 blocks of scales are staged in two chunks
 @pytest.mark.parametrize("m,n,rows", [(64, 32, 1), (130, 256, 1), (130, 256, 33), (256, 896, 961),
-                                      (4864, 896, 1), (896, 4864, 7)])
+                                      (4864, 896, 1), (896, 4864, 7), (130, 2048, 33), (64, 2080, 5),
+                                      (64, 9600, 3)])
 def test_matmul_i8_bit_exact(m, n, rows):
     rng = np.random.default_rng(m + n + rows)
     w = synth.weight_bytes(rng, rehip.Q8_0, m, n)
