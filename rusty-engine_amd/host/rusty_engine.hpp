@@ -7,6 +7,9 @@
 //   q.rows(), q.cols()                         src/qmat.rs:62-73
 //   top_k / top_k_sigmoid / route / silu       src/moe.rs:44-125 (host router)
 //   moe_layer_forward(...)                     src/moe.rs:360-388, experts on the GPU
+//   MmapModel::open(path), header(), tensor_bytes(name)   src/loader.rs:25-130, src/gguf.rs:120-170
+//   QMat::from_model(model, name, m, n)        src/qmat.rs:310-330 (bytes go to the GPU from the map)
+//   Q8Activation::from_f32(x), q.matvec_i8 / matmul_i8   src/kernel.rs:70-166 (int8 activations)
 // Failures surface as EngineError (src/core.rs:56-68) thrown with librehip's message; the
 // reference panics on unknown types at call time, this layer throws at construction.
 #pragma once
@@ -18,6 +21,7 @@
 #include <numeric>
 #include <stdexcept>
 #include <string>
+#include <utility>
 #include <vector>
 
 #include "../../include/rehip.h"
@@ -35,9 +39,116 @@ inline void check(int rc) {
 
 enum class Precision { Bf16Mfma = RE_MODE_BF16, F32Strict = RE_MODE_F32 };
 
+// ---- GGUF model files (src/gguf.rs, src/loader.rs) -----------------------------------------
+// One row of the tensor-info table (gguf.rs TensorEntry).
+struct TensorEntry {
+  std::string name;
+  std::vector<uint64_t> dims;
+  uint32_t ggml_type = 0;
+  uint64_t offset = 0;
+  uint64_t numel() const {
+    uint64_t n = 1;
+    for (uint64_t d : dims) n *= d;
+    return n;
+  }
+};
+
+// The parsed header (GgufFile, gguf.rs:126-170): version, metadata accessors, tensor table.
+class GgufHeader {
+ public:
+  explicit GgufHeader(const re_gguf* g) : g_(g) {
+    const size_t nt = re_gguf_tensor_count(g);
+    tensors.reserve(nt);
+    for (size_t i = 0; i < nt; ++i) {
+      const char* name = nullptr;
+      uint32_t type = 0, nd = 0;
+      uint64_t dims[8], off = 0;
+      check(re_gguf_tensor_info(g, i, &name, &type, &nd, dims, &off));
+      tensors.push_back(TensorEntry{name, std::vector<uint64_t>(dims, dims + nd), type, off});
+    }
+  }
+  uint32_t version() const { return re_gguf_version(g_); }
+  size_t n_kv() const { return re_gguf_kv_count(g_); }
+  uint64_t alignment() const { return re_gguf_alignment(g_); }
+  size_t data_offset() const { return re_gguf_data_offset(g_); }
+  // metadata by key; EngineError when absent or of another kind
+  int64_t get_int(const std::string& key) const {
+    int64_t v = 0;
+    check(re_gguf_get_int(g_, key.c_str(), &v));
+    return v;
+  }
+  double get_float(const std::string& key) const {
+    double v = 0;
+    check(re_gguf_get_float(g_, key.c_str(), &v));
+    return v;
+  }
+  std::string get_str(const std::string& key) const {
+    const char* p = nullptr;
+    size_t n = 0;
+    check(re_gguf_get_str(g_, key.c_str(), &p, &n));
+    return std::string(p, n);
+  }
+  std::vector<TensorEntry> tensors;
+
+ private:
+  const re_gguf* g_;
+};
+
+// A GGUF file mapped read-only (MmapModel, loader.rs:25-130). Tensor bytes are views into the
+// mapping and stay valid while the model lives.
+class MmapModel {
+ public:
+  static MmapModel open(const std::string& path) {
+    re_gguf* g = nullptr;
+    check(re_gguf_open(path.c_str(), &g));
+    return MmapModel(g);
+  }
+  const GgufHeader& header() const { return *header_; }
+  size_t data_start() const { return re_gguf_data_start(g_.get()); }
+  // [data_start + offset, + nbytes) of a named tensor (loader.rs:95-101)
+  std::pair<const uint8_t*, size_t> tensor_bytes(const std::string& name) const {
+    size_t i = 0;
+    check(re_gguf_find_tensor(g_.get(), name.c_str(), &i));
+    const uint8_t* p = nullptr;
+    size_t n = 0;
+    check(re_gguf_tensor_data(g_.get(), i, &p, &n));
+    return {p, n};
+  }
+  const re_gguf* raw() const { return g_.get(); }
+
+ private:
+  explicit MmapModel(re_gguf* g) : g_(g, re_gguf_close), header_(std::make_shared<GgufHeader>(g)) {}
+  std::shared_ptr<re_gguf> g_;
+  std::shared_ptr<GgufHeader> header_;
+};
+
+// ---- int8 activations (src/kernel.rs:70-166) ------------------------------------------------
+// One activation row quantized per 32 values: f32 scale d = max|x| / 127 and i8 values
+// round(x / d) (Q8Activation::from_f32, kernel.rs:88-105), computed on the GPU, bit-identical.
+struct Q8Activation {
+  std::vector<float> scales;
+  std::vector<int8_t> qs;
+  static Q8Activation from_f32(const std::vector<float>& x) {
+    if (x.size() % 32) throw EngineError(RE_ERR_SIZE, "Q8Activation::from_f32: length must be a multiple of 32");
+    Q8Activation a;
+    a.scales.resize(x.size() / 32);
+    a.qs.resize(x.size());
+    if (!x.empty()) check(re_quantize_q8_act(x.data(), 1, x.size(), a.scales.data(), a.qs.data()));
+    return a;
+  }
+  size_t blocks() const { return scales.size(); }
+};
+
 // A GPU-resident quantized weight matrix W[m x n] (the Quant variant of QMat, qmat.rs:30-42).
 class QMat {
  public:
+  // tensor `name` of a mapped model, dims [n, m]; EngineError when missing or out of bounds
+  static QMat from_model(const MmapModel& model, const std::string& name, size_t m, size_t n) {
+    re_qmat* h = nullptr;
+    check(re_qmat_from_gguf(model.raw(), name.c_str(), m, n, &h));
+    return QMat(h);
+  }
+
   static QMat from_bytes(uint32_t ggml_type, const std::vector<uint8_t>& bytes, size_t m, size_t n) {
     re_qmat* h = nullptr;
     check(re_qmat_create(ggml_type, bytes.data(), bytes.size(), m, n, &h));
@@ -62,6 +173,25 @@ class QMat {
     if (x.size() != nrows * cols()) throw EngineError(RE_ERR_SIZE, "matmul: X rows x n mismatch");
     std::vector<float> y(nrows * rows());
     check(re_qmat_matmul(h_.get(), x.data(), nrows, y.data(), static_cast<int>(prec)));
+    return y;
+  }
+
+  // matvec_q8_0_i8 / matmul_q8_0_i8 (kernel.rs:145-166): Q8_0 weights times quantized rows,
+  // bit-identical to the reference's integer dot
+  std::vector<float> matvec_i8(const Q8Activation& x) const { return matmul_i8(std::vector<Q8Activation>{x}); }
+  std::vector<float> matmul_i8(const std::vector<Q8Activation>& xs) const {
+    const size_t n = cols(), nrows = xs.size();
+    std::vector<float> sc, y(nrows * rows());
+    std::vector<int8_t> qs;
+    sc.reserve(nrows * n / 32);
+    qs.reserve(nrows * n);
+    for (const auto& a : xs) {
+      if (a.qs.size() != n || a.scales.size() != n / 32)
+        throw EngineError(RE_ERR_SIZE, "matmul_i8: activation length mismatch");
+      sc.insert(sc.end(), a.scales.begin(), a.scales.end());
+      qs.insert(qs.end(), a.qs.begin(), a.qs.end());
+    }
+    if (nrows) check(re_qmat_matmul_i8(h_.get(), sc.data(), qs.data(), nrows, y.data()));
     return y;
   }
 

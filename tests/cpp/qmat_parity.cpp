@@ -1,5 +1,6 @@
 // C++ parity tests of the host-side mirror (rusty_engine.hpp) on the GPU, written like the
-// reference's own unit tests (src/qmat.rs:333-399, src/kernel.rs:2080-2584, src/moe.rs:624-801).
+// reference's own unit tests (src/qmat.rs:333-399, src/kernel.rs:2080-2584, src/moe.rs:624-801,
+// src/gguf.rs:1063-1312).
 // The CPU oracle (oracle/oracle.h) is the checker. Exit status 0 = all passed.
 #include <cmath>
 #include <cstdio>
@@ -190,6 +191,135 @@ static void test_moe_layer_routes_to_best_expert() {  // moe.rs:784-796
   }
 }
 
+// ---- GGUF (gguf.rs:1063-1312, loader.rs:245-270) --------------------------------------------
+static void put_u32(std::vector<uint8_t>& b, uint32_t v) { for (int i = 0; i < 4; ++i) b.push_back((v >> (8 * i)) & 0xFF); }
+static void put_u64(std::vector<uint8_t>& b, uint64_t v) { for (int i = 0; i < 8; ++i) b.push_back((v >> (8 * i)) & 0xFF); }
+static void put_str(std::vector<uint8_t>& b, const std::string& s) {
+  put_u64(b, s.size());
+  b.insert(b.end(), s.begin(), s.end());
+}
+
+static std::string write_file(const std::string& name, const std::vector<uint8_t>& bytes) {
+  const std::string path = std::string("/tmp/") + name;
+  FILE* f = std::fopen(path.c_str(), "wb");
+  std::fwrite(bytes.data(), 1, bytes.size(), f);
+  std::fclose(f);
+  return path;
+}
+
+static void test_gguf_header_fixture() {  // gguf.rs:1085-1145, synth_gguf
+  std::printf("gguf_parses_header_kv_and_tensor_info\n");
+  std::vector<uint8_t> b = {'G', 'G', 'U', 'F'};
+  put_u32(b, 3);
+  put_u64(b, 1);
+  put_u64(b, 3);
+  put_str(b, "general.architecture");
+  put_u32(b, 8);
+  put_str(b, "qwen2moe");
+  put_str(b, "general.block_count");
+  put_u32(b, 4);
+  put_u32(b, 48);
+  put_str(b, "tokenizer.ggml.tokens");
+  put_u32(b, 9);
+  put_u32(b, 8);
+  put_u64(b, 2);
+  put_str(b, "a");
+  put_str(b, "b");
+  put_str(b, "blk.0.ffn_gate_exps.weight");
+  put_u32(b, 3);
+  put_u64(b, 2048);
+  put_u64(b, 512);
+  put_u64(b, 64);
+  put_u32(b, 12);
+  put_u64(b, 0);
+  const auto m = MmapModel::open(write_file("re_fixture.gguf", b));
+  const auto& h = m.header();
+  CHECK(h.version() == 3 && h.tensors.size() == 1 && h.n_kv() == 3, "counts");
+  CHECK(h.data_offset() == b.size(), "data offset %zu", h.data_offset());
+  CHECK(h.get_str("general.architecture") == "qwen2moe", "architecture");
+  CHECK(h.get_int("general.block_count") == 48, "block count");
+  CHECK(h.alignment() == 32, "default alignment");
+  const auto& t = h.tensors[0];
+  CHECK(t.name == "blk.0.ffn_gate_exps.weight" && t.dims == std::vector<uint64_t>({2048, 512, 64}) &&
+            t.ggml_type == 12 && t.offset == 0,
+        "tensor entry");
+  bool threw = false;
+  try {
+    m.tensor_bytes("blk.0.ffn_gate_exps.weight");     // header only: the bytes are past the end
+  } catch (const EngineError& e) {
+    threw = e.code == RE_ERR_SIZE;
+  }
+  CHECK(threw, "tensor bytes out of bounds");
+  std::vector<uint8_t> bad = b;
+  bad[4] = 1;                                            // version 1
+  threw = false;
+  try {
+    MmapModel::open(write_file("re_bad.gguf", bad));
+  } catch (const EngineError& e) {
+    threw = std::string(e.what()).find("unsupported GGUF version 1") != std::string::npos;
+  }
+  CHECK(threw, "version 1 rejected");
+}
+
+static void test_qmat_from_model_equals_from_bytes() {  // qmat.rs:310-330
+  std::printf("qmat_from_model_equals_from_bytes\n");
+  std::mt19937 g(5);
+  const size_t m = 200, n = 512;
+  const auto w = random_blocks(g, ORC_Q4_K, m, n);
+  std::vector<uint8_t> b = {'G', 'G', 'U', 'F'};
+  put_u32(b, 3);
+  put_u64(b, 1);
+  put_u64(b, 0);
+  put_str(b, "blk.0.ffn_up.weight");
+  put_u32(b, 2);
+  put_u64(b, n);
+  put_u64(b, m);
+  put_u32(b, ORC_Q4_K);
+  put_u64(b, 0);
+  while (b.size() % 32) b.push_back(0);
+  b.insert(b.end(), w.begin(), w.end());
+  const auto model = MmapModel::open(write_file("re_model.gguf", b));
+  const auto bytes = model.tensor_bytes("blk.0.ffn_up.weight");
+  CHECK(bytes.second == w.size() && std::memcmp(bytes.first, w.data(), w.size()) == 0, "mapped bytes");
+  const QMat a = QMat::from_model(model, "blk.0.ffn_up.weight", m, n), c = QMat::from_bytes(ORC_Q4_K, w, m, n);
+  const auto x = randn(g, n);
+  CHECK(a.matvec(x) == c.matvec(x), "from_model and from_bytes give the same bits");
+  bool threw = false;
+  try {
+    QMat::from_model(model, "nope", m, n);
+  } catch (const EngineError& e) {
+    threw = std::string(e.what()) == "QMat: tensor 'nope' missing";
+  }
+  CHECK(threw, "missing tensor message");
+}
+
+// ---- int8 activations (kernel.rs:2210-2326) ---------------------------------------------------
+static void test_q8_activation_and_i8_matmul() {
+  std::printf("q8_activation_and_i8_matmul_match_oracle\n");
+  std::mt19937 g(9);
+  const size_t m = 300, n = 1024, rows = 3;
+  const auto w = random_blocks(g, ORC_Q8_0, m, n);
+  const QMat q = QMat::from_bytes(ORC_Q8_0, w, m, n);
+  std::vector<Q8Activation> xs;
+  for (size_t r = 0; r < rows; ++r) {
+    auto x = randn(g, n);
+    for (size_t i = 0; i < n; ++i) x[i] *= (float)(r + 1) * 3.0f;
+    const Q8Activation a = Q8Activation::from_f32(x);
+    std::vector<float> sc(n / 32);
+    std::vector<int8_t> qs(n);
+    orc_quantize_q8_act(x.data(), n, sc.data(), qs.data());
+    CHECK(std::memcmp(sc.data(), a.scales.data(), sc.size() * 4) == 0 && qs == a.qs, "quantize row %zu", r);
+    xs.push_back(a);
+  }
+  const auto y = q.matmul_i8(xs);
+  for (size_t r = 0; r < rows; ++r) {
+    std::vector<float> want(m);
+    orc_matmul_q8_0_i8(w.data(), m, n, xs[r].scales.data(), xs[r].qs.data(), 1, want.data());
+    CHECK(std::memcmp(want.data(), y.data() + r * m, m * 4) == 0, "i8 matmul row %zu bit-identical", r);
+  }
+  CHECK(q.matvec_i8(xs[1]) == std::vector<float>(y.begin() + m, y.begin() + 2 * m), "matvec_i8 == matmul_i8 row");
+}
+
 int main() {
   try {
     check(re_init());
@@ -199,6 +329,9 @@ int main() {
     test_every_type_against_oracle();
     test_router_matches_oracle();
     test_moe_layer_routes_to_best_expert();
+    test_gguf_header_fixture();
+    test_qmat_from_model_equals_from_bytes();
+    test_q8_activation_and_i8_matmul();
   } catch (const EngineError& e) {
     std::printf("EngineError %d: %s\n", e.code, e.what());
     return 2;
