@@ -5,7 +5,7 @@
  *   QMat::matvec  src/qmat.rs:80     -> re_qmat_matvec
  *   QMat::matmul  src/qmat.rs:169    -> re_qmat_matmul
  *   QMat::from_bytes / from_model    -> re_qmat_create   (src/qmat.rs:52-59, 312-330)
- *   quant::dequant src/quant.rs:363  -> re_dequant        (bit-exact, quant types)
+ *   quant::dequant src/quant.rs:363  -> re_dequant        (bit-exact, quant and float types)
  *   moe expert FFN + combine          -> re_moe_forward    (src/moe.rs:288-300, 360-388)
  *
  * Conventions (from the reference):
@@ -61,7 +61,10 @@ int re_repack(uint32_t ggml_type, const uint8_t *bytes, size_t nbytes, size_t m,
               uint8_t *out, size_t out_len);
 
 /* ---- QMat (src/qmat.rs:30-42) ---------------------------------------------------------- */
-/* Upload and repack once. nbytes must equal m * re_row_bytes(type, n). */
+/* Upload and repack once. nbytes must equal m * re_row_bytes(type, n). F32 (0), F16 (1) and
+ * BF16 (30) bytes are QMat::F32 / the no-fused-kernel arms (qmat.rs:45-49, 128-151): kept
+ * row-major, nbytes = m * n * element size, f32 products in every mode; they do not stack and
+ * take neither the norm/argmax epilogues of re_qmat_matvec_ex_dev nor re_ffn_create. */
 int re_qmat_create(uint32_t ggml_type, const uint8_t *bytes, size_t nbytes, size_t m, size_t n,
                    re_qmat **out);
 /* A stack of `count` same-type, same-shape matrices (nbytes = count * m * row bytes, one after
@@ -89,7 +92,8 @@ int re_qmat_matmul_dev(re_qmat *q, const float *d_x, size_t rows, float *d_y, in
 int re_qmat_dequant_dev(re_qmat *q, float *d_out, void *stream);
 
 /* Flat-stream dequant on the GPU (quant::dequant, src/quant.rs:363-453) for the six quant
- * types: out receives nbytes / block_bytes * QK floats. Same length errors as the reference. */
+ * types and F32/F16/BF16: out receives nbytes / block_bytes * QK floats (nbytes / element size
+ * for the float types). Same length errors as the reference. */
 int re_dequant(uint32_t ggml_type, const uint8_t *bytes, size_t nbytes, float *out, size_t out_len);
 
 /* ---- MoE expert FFN (src/moe.rs:288-300, 360-388) ------------------------------------- */

@@ -430,11 +430,27 @@ int orc_matmul_blocks(uint32_t t, const uint8_t *w, size_t m, size_t n, const fl
     return ORC_OK;
 }
 
+/* QMat::F32 and QMat::Quant over F16/BF16 carry no fused kernel: the whole matrix widens
+ * through quant::dequant (quant.rs:365-397) and each output is moe::matvec's sequential
+ * sum of products (moe.rs:271-277, qmat.rs:132, 146-151, 277-283). One element per block. */
+static void dq_f32(const uint8_t *b, float *o) { *o = bits_f32(rd32(b)); }
+static void dq_f16(const uint8_t *b, float *o) { *o = orc_f16_to_f32(rd16(b)); }
+static void dq_bf16(const uint8_t *b, float *o) { *o = bits_f32((uint32_t)rd16(b) << 16); }
+
+static int dense_geom(uint32_t t, size_t *qk, size_t *bb, dq_fn *dq) {
+    switch (t) {
+    case 0: *qk = 1; *bb = 4; *dq = dq_f32; return 1;
+    case 1: *qk = 1; *bb = 2; *dq = dq_f16; return 1;
+    case 30: *qk = 1; *bb = 2; *dq = dq_bf16; return 1;
+    default: return 0;
+    }
+}
+
 /* ---- QMat-level semantics with padded rows ---------------------------------------- */
 int orc_qmat_row_bytes(uint32_t t, size_t n, size_t *row_bytes) {
     size_t qk = 0, bb = 0;
     dq_fn dq;
-    int rc = quant_geom(t, &qk, &bb, &dq);
+    int rc = dense_geom(t, &qk, &bb, &dq) ? ORC_OK : quant_geom(t, &qk, &bb, &dq);
     if (rc) return rc;
     *row_bytes = (n + qk - 1) / qk * bb;
     return ORC_OK;
@@ -442,7 +458,7 @@ int orc_qmat_row_bytes(uint32_t t, size_t n, size_t *row_bytes) {
 
 static int qmat_check(uint32_t t, size_t nbytes, size_t m, size_t n, size_t *qk, size_t *bb,
                       dq_fn *dq, size_t *rb) {
-    int rc = quant_geom(t, qk, bb, dq);
+    int rc = dense_geom(t, qk, bb, dq) ? ORC_OK : quant_geom(t, qk, bb, dq);
     if (rc) return rc;
     if (n == 0) return fail(ORC_ERR_SIZE, "QMat: n must be > 0");
     *rb = (n + *qk - 1) / *qk * *bb;
@@ -457,7 +473,7 @@ int orc_qmat_matvec(uint32_t t, const uint8_t *w, size_t nbytes, size_t m, size_
     dq_fn dq;
     int rc = qmat_check(t, nbytes, m, n, &qk, &bb, &dq, &rb);
     if (rc) return rc;
-    if (n % qk == 0) return orc_matvec(t, w, m, n, x, out);
+    if (qk > 1 && n % qk == 0) return orc_matvec(t, w, m, n, x, out);
     size_t nb = rb / bb;
     float *row = (float *)malloc(nb * qk * sizeof(float));
     if (!row) return fail(ORC_ERR_ARG, "out of memory");
@@ -475,7 +491,7 @@ int orc_qmat_matmul(uint32_t t, const uint8_t *w, size_t nbytes, size_t m, size_
     dq_fn dq;
     int rc = qmat_check(t, nbytes, m, n, &qk, &bb, &dq, &rb);
     if (rc) return rc;
-    if (n % qk == 0) return orc_matmul(t, w, m, n, x, rows, out);
+    if (qk > 1 && n % qk == 0) return orc_matmul(t, w, m, n, x, rows, out);
     for (size_t i = 0; i < rows; ++i) {
         rc = orc_qmat_matvec(t, w, nbytes, m, n, x + i * n, out + i * m);
         if (rc) return rc;

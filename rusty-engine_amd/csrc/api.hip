@@ -58,6 +58,9 @@ const char* type_name(uint32_t t) {
     case T_Q4_K: return "Q4_K";
     case T_Q5_K: return "Q5_K";
     case T_Q6_K: return "Q6_K";
+    case 0: return "F32";
+    case 1: return "F16";
+    case 30: return "BF16";
     default: return "?";
   }
 }
@@ -129,7 +132,8 @@ struct Staging {
 }  // namespace
 
 struct re_qmat {
-  MatGeom g{};
+  MatGeom g{};                            // dense types: only type, m and n are set
+  bool dense = false;                     // F32 / F16 / BF16 weights, row-major as stored (no tiles)
   uint8_t* d_w = nullptr;                 // count matrices, w_stride bytes apart
   size_t count = 1, w_stride = 0;
   float* d_partial = nullptr;
@@ -420,10 +424,43 @@ int re_repack(uint32_t ggml_type, const uint8_t* bytes, size_t nbytes, size_t m,
   return RE_OK;
 }
 
+// QMat::F32 and the float arms of the fallback (qmat.rs:128-151): the row-major elements as stored
+int create_dense(uint32_t ggml_type, const uint8_t* bytes, size_t nbytes, size_t m, size_t n, re_qmat** out) {
+  if (m == 0 || n == 0) return fail(RE_ERR_SIZE, "empty matrix %zu x %zu", m, n);
+  if (m > (1u << 30) || n > (1u << 30)) return fail(RE_ERR_SIZE, "matrix %zu x %zu too large", m, n);
+  const size_t want = m * n * dense_elem_bytes(ggml_type);
+  if (nbytes != want)
+    return fail(RE_ERR_SIZE, "%s weight %zu x %zu needs %zu bytes, got %zu", type_name(ggml_type), m, n, want, nbytes);
+  int rc = do_init();
+  if (rc) return rc;
+  re_qmat* q = new (std::nothrow) re_qmat();
+  if (!q) return fail(RE_ERR_ARG, "out of memory");
+  q->dense = true;
+  q->g.type = ggml_type;
+  q->g.m = m;
+  q->g.n = n;
+  q->count = 1;
+  if (hipMalloc(&q->d_w, nbytes) != hipSuccess) {
+    re_qmat_destroy(q);
+    return fail(RE_ERR_HIP, "hipMalloc(%zu) failed", nbytes);
+  }
+  if (hipMemcpy(q->d_w, bytes, nbytes, hipMemcpyHostToDevice) != hipSuccess ||
+      hipStreamCreateWithFlags(&q->stream, hipStreamNonBlocking) != hipSuccess) {
+    re_qmat_destroy(q);
+    return fail(RE_ERR_HIP, "dense weight upload failed");
+  }
+  *out = q;
+  return RE_OK;
+}
+
 int re_qmat_create_stacked(uint32_t ggml_type, const uint8_t* bytes, size_t nbytes, size_t m, size_t n,
                            size_t count, re_qmat** out) {
   if (!out || !bytes) return fail(RE_ERR_ARG, "null pointer");
   *out = nullptr;
+  if (dense_type(ggml_type)) {
+    if (count != 1) return fail(RE_ERR_TYPE, "%s weights are not stacked", type_name(ggml_type));
+    return create_dense(ggml_type, bytes, nbytes, m, n, out);
+  }
   if (count == 0 || count > (1u << 20) || nbytes % count)
     return fail(RE_ERR_SIZE, "%zu bytes do not hold %zu equal matrices", nbytes, count);
   MatGeom g;
@@ -477,6 +514,10 @@ uint32_t re_qmat_type(const re_qmat* q) { return q ? q->g.type : 0; }
 
 int re_qmat_matvec_dev(re_qmat* q, const float* d_x, float* d_y, void* stream) {
   if (!q || !d_x || !d_y) return fail(RE_ERR_ARG, "null pointer");
+  if (q->dense) {
+    HIP_TRY(launch_dense_gemm(q->g.type, q->d_w, d_x, d_y, (int)q->g.m, (int)q->g.n, 1, nullptr, (hipStream_t)stream));
+    return RE_OK;
+  }
   return gemv_enqueue(q, d_x, d_y, (hipStream_t)stream);
 }
 
@@ -486,6 +527,7 @@ int re_qmat_matvec_stacked_dev(re_qmat* q, size_t first, size_t count, const flo
                                float* d_y, size_t y_stride, void* stream) {
   if (!q || !d_x || !d_y) return fail(RE_ERR_ARG, "null pointer");
   if (count == 0) return RE_OK;
+  if (q->dense) return fail(RE_ERR_TYPE, "%s weights are not stacked", type_name(q->g.type));
   if (first >= q->count || count > q->count - first)
     return fail(RE_ERR_SIZE, "matrices %zu..%zu of a stack of %zu", first, first + count - 1, q->count);
   if (x_stride % 4 || x_stride > (1u << 30) || y_stride > (1u << 30) || (x_stride && x_stride < q->g.n) ||
@@ -542,6 +584,12 @@ int re_qmat_matvec_ex_dev(re_qmat* q, const float* d_x, const float* d_norm_w, f
                           float* d_y, unsigned long long* d_best, void* stream) {
   if (!q || !d_x || !d_y) return fail(RE_ERR_ARG, "null pointer");
   if (d_norm_w && !(eps >= 0.0f)) return fail(RE_ERR_ARG, "norm eps must be >= 0");
+  if (q->dense) {
+    if (d_norm_w || d_best)
+      return fail(RE_ERR_TYPE, "%s weights take the plain product and the residual add only", type_name(q->g.type));
+    HIP_TRY(launch_dense_gemm(q->g.type, q->d_w, d_x, d_y, (int)q->g.m, (int)q->g.n, 1, d_add, (hipStream_t)stream));
+    return RE_OK;
+  }
   return gemv_enqueue(q, d_x, d_y, (hipStream_t)stream, d_add, d_norm_w, eps, d_best);
 }
 
@@ -550,6 +598,12 @@ int re_qmat_matmul_dev(re_qmat* q, const float* d_x, size_t rows, float* d_y, in
   if (mode != RE_MODE_BF16 && mode != RE_MODE_F32) return fail(RE_ERR_ARG, "unknown mode %d", mode);
   if (rows == 0) return RE_OK;
   if (rows > (1u << 24)) return fail(RE_ERR_SIZE, "rows = %zu too large", rows);
+  if (q->dense) {                        // f32 products in either mode (the reference's f32 matvec)
+    if (rows > 65535u * 4u) return fail(RE_ERR_SIZE, "rows = %zu too large for dense weights", rows);
+    HIP_TRY(launch_dense_gemm(q->g.type, q->d_w, d_x, d_y, (int)q->g.m, (int)q->g.n, (int)rows, nullptr,
+                              (hipStream_t)stream));
+    return RE_OK;
+  }
   if (rows == 1) return gemv_enqueue(q, d_x, d_y, (hipStream_t)stream);
   return gemm_enqueue(q, d_x, rows, d_y, mode, (hipStream_t)stream);
 }
@@ -646,12 +700,36 @@ int re_qmat_matmul_i8(re_qmat* q, const float* scales, const int8_t* qs, size_t 
 
 int re_qmat_dequant_dev(re_qmat* q, float* d_out, void* stream) {
   if (!q || !d_out) return fail(RE_ERR_ARG, "null pointer");
+  if (q->dense) {
+    HIP_TRY(launch_dense_to_f32(q->g.type, q->d_w, d_out, q->g.m * q->g.n, (hipStream_t)stream));
+    return RE_OK;
+  }
   HIP_TRY(launch_dequant(q->g.type, q->d_w, d_out, (int)q->g.m, (int)q->g.n, (int)q->g.kb, (int)q->g.tiles,
                          (hipStream_t)stream));
   return RE_OK;
 }
 
 int re_dequant(uint32_t ggml_type, const uint8_t* bytes, size_t nbytes, float* out, size_t out_len) {
+  if (dense_type(ggml_type)) {            // F32 / F16 / BF16 widen element by element (quant.rs:365-392)
+    const size_t es = dense_elem_bytes(ggml_type);
+    if (nbytes % es)
+      return fail(RE_ERR_SIZE, "%s data len %zu not a multiple of %zu", type_name(ggml_type), nbytes, es);
+    const size_t count = nbytes / es;
+    if (out_len != count) return fail(RE_ERR_SIZE, "out needs %zu floats, got %zu", count, out_len);
+    if (count == 0) return RE_OK;
+    if (!bytes || !out) return fail(RE_ERR_ARG, "null pointer");
+    int rc = do_init();
+    if (rc) return rc;
+    void* d = nullptr;
+    const size_t src_off = (count * sizeof(float) + 255) / 256 * 256;
+    HIP_TRY(hipMalloc(&d, src_off + nbytes));
+    hipError_t e = hipMemcpy((uint8_t*)d + src_off, bytes, nbytes, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = launch_dense_to_f32(ggml_type, (uint8_t*)d + src_off, (float*)d, count, nullptr);
+    if (e == hipSuccess) e = hipMemcpy(out, d, count * sizeof(float), hipMemcpyDeviceToHost);
+    (void)hipFree(d);
+    if (e != hipSuccess) return fail(RE_ERR_HIP, "dequant: %s", hipGetErrorString(e));
+    return RE_OK;
+  }
   const TypeInfo* ti = type_info(ggml_type);
   if (!ti) return fail(RE_ERR_TYPE, "no scalar dequant for ggml type %u", ggml_type);
   if (nbytes % ti->bb)
@@ -1274,6 +1352,7 @@ int re_pos_add_dev(int* d_pos, int delta, void* stream) {
 int re_ffn_create(re_qmat* gate, re_qmat* up, re_ffn** out) {
   if (!gate || !up || !out) return fail(RE_ERR_ARG, "null pointer");
   *out = nullptr;
+  if (gate->dense || up->dense) return fail(RE_ERR_TYPE, "ffn: quantized gate and up only");
   if (gate->g.type != up->g.type || gate->g.m != up->g.m || gate->g.n != up->g.n)
     return fail(RE_ERR_SIZE, "ffn: gate and up must share type and shape");
   if (gate->g.n > (size_t)kGemvRowsMaxK) return fail(RE_ERR_SIZE, "ffn: rows longer than %d", kGemvRowsMaxK);

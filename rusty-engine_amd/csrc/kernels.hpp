@@ -64,6 +64,13 @@ constexpr int kGemvRowsMaxK = 12288;
 hipError_t launch_gemv(uint32_t type, const GemvArgs& a, int waves, hipStream_t s);
 hipError_t launch_dequant(uint32_t type, const uint8_t* W, float* out, int m, int n, int KB, int tiles,
                           hipStream_t s);
+// Dense F32 / F16 / BF16 weights (dense.hip): row-major as stored, m x n elements
+bool dense_type(uint32_t type);                  // ggml types 0, 1, 30
+size_t dense_elem_bytes(uint32_t type);
+// Y (rows x m) = X (rows x n) W^T (+ add[r] per output row when given)
+hipError_t launch_dense_gemm(uint32_t type, const void* W, const float* x, float* y, int m, int n, int rows,
+                             const float* add, hipStream_t s);
+hipError_t launch_dense_to_f32(uint32_t type, const void* src, float* dst, size_t count, hipStream_t s);
 // Int8 activations (i8.hip): Q8Activation::from_f32 of rows x n f32 (n % 32 == 0, x 16-byte
 // aligned) into scales (rows x n/32) and qs (rows x n, 16-byte aligned); and the Q8_0 x i8 GEMM
 // over tiled Q8_0 weights, y rows x m.

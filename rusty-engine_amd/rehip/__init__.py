@@ -26,6 +26,11 @@ QUANT_TYPES = (Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K)
 GEOM = {Q4_0: (32, 18), Q5_0: (32, 22), Q8_0: (32, 34), Q4_K: (256, 144), Q5_K: (256, 176),
         Q6_K: (256, 210)}
 TYPE_NAMES = {Q4_0: "Q4_0", Q5_0: "Q5_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K"}
+# Unquantized weights (QMat::F32 and the Quant arms without a fused kernel, src/qmat.rs:31-41):
+# element size in bytes.
+F32, F16, BF16 = 0, 1, 30
+DENSE_TYPES = {F32: 4, F16: 2, BF16: 2}
+TYPE_NAMES.update({F32: "F32", F16: "F16", BF16: "BF16"})
 
 RE_OK, RE_ERR_TYPE, RE_ERR_SIZE, RE_ERR_ARG, RE_ERR_HIP, RE_ERR_NODEV = 0, 1, 2, 3, 4, 5
 MODE_BF16, MODE_F32 = 0, 1
@@ -195,8 +200,8 @@ def repack(ggml_type: int, data, m: int, n: int) -> np.ndarray:
 def dequant(ggml_type: int, data) -> np.ndarray:
     """GPU dequant of a flat block stream (quant::dequant, src/quant.rs:363)."""
     src = _u8(data)
-    qk, bb = GEOM.get(ggml_type, (1, 1))
-    n = src.size // bb * qk if ggml_type in GEOM else 0
+    qk, bb = GEOM.get(ggml_type, (1, DENSE_TYPES.get(ggml_type, 1)))
+    n = src.size // bb * qk if ggml_type in GEOM or ggml_type in DENSE_TYPES else 0
     out = np.empty(max(n, 1), np.float32)
     _check(lib().re_dequant(ggml_type, src.ctypes.data, src.size, out.ctypes.data, n))
     return out[:n]
@@ -214,7 +219,8 @@ def _stream_ptr(stream) -> int | None:
 
 
 class QMat:
-    """GPU-resident quantized matrix W[m x n] (src/qmat.rs:30-42, Quant variant)."""
+    """GPU-resident weight matrix W[m x n] (src/qmat.rs:30-42): quant blocks in the tiled layout,
+    or F32/F16/BF16 elements row-major."""
 
     def __init__(self, handle: int, ggml_type: int, m: int, n: int):
         self._h = C.c_void_p(handle)
@@ -226,6 +232,14 @@ class QMat:
         h = _vp()
         _check(lib().re_qmat_create(ggml_type, src.ctypes.data, src.size, m, n, C.byref(h)))
         return cls(h.value, ggml_type, m, n)
+
+    @classmethod
+    def from_f32(cls, data, m: int, n: int) -> "QMat":
+        """QMat::from_f32 (qmat.rs:45-49): a row-major f32 matrix, products in f32."""
+        w = np.ascontiguousarray(data, np.float32).reshape(-1)
+        if w.size != m * n:
+            raise ValueError("QMat::from_f32: shape mismatch")
+        return cls.from_bytes(F32, w.view(np.uint8), m, n)
 
     @classmethod
     def from_bytes_stacked(cls, ggml_type: int, data, m: int, n: int, count: int) -> "QMat":
