@@ -438,8 +438,8 @@ static hipError_t launch_shape(const GemmArgs& a, int ntasks, hipStream_t s) {
   }
 }
 
-// tile x K-group instances: dense 64x64 (KG 1/2) and 128x128 (1) in both modes, 128x256 and
-// 256x128 (1) in bf16; grouped (MoE) 64x64 (KG 1/2) in both modes.
+// tile x K-group instances: dense 64x64 (KG 1/2) in both modes, 128x128, 128x256 and 256x128
+// (KG 1) in bf16; grouped (MoE) 64x64 (KG 1/2) in both modes.
 template <int T, bool F32>
 static hipError_t launch_t(const GemmArgs& a, int ntasks, GemmTile tile, int kg, hipStream_t s) {
   if (a.tasks) {
@@ -455,6 +455,9 @@ static hipError_t launch_t(const GemmArgs& a, int ntasks, GemmTile tile, int kg,
     case GemmTile::k256x128:
       if constexpr (F32) return hipErrorInvalidValue;
       else return kg != 1 ? hipErrorInvalidValue : launch_shape<T, F32, 256, 128, 4, 2, 1, false>(a, ntasks, s);
+    case GemmTile::k128x128:
+      if constexpr (F32) return hipErrorInvalidValue;
+      else return kg != 1 ? hipErrorInvalidValue : launch_shape<T, F32, 128, 128, 2, 2, 1, false>(a, ntasks, s);
     default:
       if (kg == 1) return launch_shape<T, F32, 64, 64, 2, 2, 1, false>(a, ntasks, s);
       if (kg == 2) return launch_shape<T, F32, 64, 64, 2, 2, 2, false>(a, ntasks, s);
@@ -496,8 +499,9 @@ GemmPlan plan_gemm(int m, int n, int K, int mode) {
       pl.splits = (int)std::max<long>(1, splits);
     }
   } else if (t128 >= 200) {
-    pl.tile = GemmTile::k128x128;
-    pl.kgroups = gemm_kgroups(pl.tile, mode, t128, steps);
+    // many tiles already: 64 x 64 with one K-group (the 128 x 128 bf16 tile measured slower)
+    pl.tile = GemmTile::k64x64;
+    pl.kgroups = 1;
   } else {
     pl.tile = GemmTile::k64x64;
     pl.kgroups = gemm_kgroups(pl.tile, mode, t64, steps);
