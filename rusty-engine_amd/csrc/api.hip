@@ -890,6 +890,7 @@ int re_moe_forward_routed_dev(re_moe* e, const float* d_x, size_t tokens, size_t
   if (gemv) {
     const MoeGemvTask* tg = (const MoeGemvTask*)tasks;
     MoeGemvArgs g{};
+    g.rows_per_task = kMoeGemvRows;
     g.max_rows = sh.chunk;
     g.X = d_x;
     g.xrow = xrow;
@@ -917,6 +918,7 @@ int re_moe_forward_routed_dev(re_moe* e, const float* d_x, size_t tokens, size_t
       HIP_TRY(launch_swiglu((const float*)e->sg.p, (const float*)e->su.p, (float*)e->sh.p, pairs * e->inter, s));
     }
     MoeGemvArgs d{};
+    d.rows_per_task = kMoeGemvRows;
     d.max_rows = sh.chunk;
     d.W0 = e->d_down;
     d.w_stride = e->gd.bytes;
@@ -1094,6 +1096,7 @@ int re_moe_forward_dev(re_moe* e, const float* d_x, size_t tokens, size_t top_k,
     int max_rows = 0;
     for (size_t x = 0; x < e->n_experts; ++x) max_rows = std::max(max_rows, std::min(count[x], kMoeGemvBatch));
     MoeGemvArgs g{};
+    g.rows_per_task = kMoeGemvRows;
     g.max_rows = max_rows;
     g.X = d_x;
     g.xrow = (const int*)dm;
@@ -1120,6 +1123,7 @@ int re_moe_forward_dev(re_moe* e, const float* d_x, size_t tokens, size_t top_k,
       HIP_TRY(launch_swiglu((const float*)e->sg.p, (const float*)e->su.p, (float*)e->sh.p, pairs * e->inter, s));
     }
     MoeGemvArgs d{};
+    d.rows_per_task = kMoeGemvRows;
     d.max_rows = max_rows;
     d.W0 = e->d_down;
     d.w_stride = e->gd.bytes;
@@ -1357,7 +1361,7 @@ int re_ffn_create(re_qmat* gate, re_qmat* up, re_ffn** out) {
     return fail(RE_ERR_SIZE, "ffn: gate and up must share type and shape");
   if (gate->g.n > (size_t)kGemvRowsMaxK) return fail(RE_ERR_SIZE, "ffn: rows longer than %d", kGemvRowsMaxK);
   std::vector<MoeGemvTask> t;
-  for (size_t row = 0; row < gate->g.m; row += kMoeGemvRows) t.push_back({0, (int)row, 0, 1});
+  for (size_t row = 0; row < gate->g.m; row += kFfnGemvRows) t.push_back({0, (int)row, 0, 1});
   re_ffn* f = new (std::nothrow) re_ffn();
   if (!f) return fail(RE_ERR_ARG, "out of memory");
   f->gate = gate;
@@ -1385,6 +1389,7 @@ int re_ffn_forward_dev(re_ffn* f, const float* d_x, const float* d_norm_w, float
   if (!f || !d_x || !d_h) return fail(RE_ERR_ARG, "null pointer");
   if (!aligned16(d_x) || !aligned16(d_norm_w)) return fail(RE_ERR_ARG, "x and norm weights must be 16-byte aligned");
   MoeGemvArgs g{};
+  g.rows_per_task = kFfnGemvRows;
   g.norm_w = d_norm_w;
   g.norm_eps = eps;
   g.W0 = f->gate->d_w;

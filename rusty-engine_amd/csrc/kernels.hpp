@@ -148,8 +148,13 @@ struct MoeGemvArgs {
   const float* norm_w;        // nullptr, or each X row is RMS-normalised first (as GemvArgs)
   float norm_eps;
   const int* ntasks;          // nullptr, or the task count on the device (larger grids exit early)
+  int rows_per_task;          // kMoeGemvRows, or kFfnGemvRows (single-row dual launches only)
 };
-constexpr int kMoeGemvRows = 16;   // weight rows per task
+// weight rows per expert task: with 16, staging the task's activation rows costs as many bytes
+// as its weights; 64 leaves too few tasks
+constexpr int kMoeGemvRows = 32;
+// weight rows per task of the one-row gate/up pair (re_ffn): more, smaller tasks suit decode
+constexpr int kFfnGemvRows = 16;
 constexpr int kMoeGemvWaves = 4;
 constexpr int kMoeGemvBatch = 4;   // gathered rows per task
 // dual: gate and up (W0, W1) with SwiGLU output; else one matrix

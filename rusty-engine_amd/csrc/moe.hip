@@ -256,8 +256,70 @@ hipError_t launch_moe_route(const float* logits, int tokens, int n_experts, int 
   return hipGetLastError();
 }
 
+// Tiled form for hidden % 4 == 0 and 16-byte aligned rows: a workgroup computes 8 experts x TT
+// tokens (two experts per wave); lane l takes the float4 at k = 4 l + 256 i of every row, so the
+// router rows are read once per token tile and the token rows once per 8 experts. Each of the
+// 2 TT sums is folded over the wave by a fixed xor tree.
+template <int TT>
+__global__ __launch_bounds__(256) void moe_router_tile_kernel(const float* __restrict__ x,
+                                                              const float* __restrict__ w, int hidden,
+                                                              int n_experts, int tokens,
+                                                              float* __restrict__ logits) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int e0 = blockIdx.x * 8 + 2 * wave, t0 = blockIdx.y * TT;
+  if (e0 >= n_experts) return;           // no workgroup barrier below
+  const bool e1ok = e0 + 1 < n_experts;
+  const float4* w0 = reinterpret_cast<const float4*>(w + (size_t)e0 * hidden);
+  const float4* w1 = reinterpret_cast<const float4*>(w + (size_t)(e1ok ? e0 + 1 : e0) * hidden);
+  const float4* xr[TT];
+#pragma unroll
+  for (int t = 0; t < TT; ++t)
+    xr[t] = reinterpret_cast<const float4*>(x + (size_t)min(t0 + t, tokens - 1) * hidden);
+  float acc[2][TT];
+#pragma unroll
+  for (int t = 0; t < TT; ++t) acc[0][t] = acc[1][t] = 0.0f;
+  const int nv = hidden / 4;
+  for (int v = lane; v < nv; v += 64) {
+    const float4 a = w0[v], b = w1[v];
+#pragma unroll
+    for (int t = 0; t < TT; ++t) {
+      const float4 q = xr[t][v];
+      acc[0][t] = __builtin_fmaf(a.w, q.w, __builtin_fmaf(a.z, q.z, __builtin_fmaf(a.y, q.y, __builtin_fmaf(a.x, q.x, acc[0][t]))));
+      acc[1][t] = __builtin_fmaf(b.w, q.w, __builtin_fmaf(b.z, q.z, __builtin_fmaf(b.y, q.y, __builtin_fmaf(b.x, q.x, acc[1][t]))));
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int t = 0; t < TT; ++t) {
+      float v = acc[j][t];
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+      acc[j][t] = v;
+    }
+  if (lane == 0) {
+#pragma unroll
+    for (int t = 0; t < TT; ++t) {
+      if (t0 + t >= tokens) break;
+      logits[(size_t)(t0 + t) * n_experts + e0] = acc[0][t];
+      if (e1ok) logits[(size_t)(t0 + t) * n_experts + e0 + 1] = acc[1][t];
+    }
+  }
+}
+
 hipError_t launch_moe_router_logits(const float* x, const float* router_w, int tokens, int hidden, int n_experts,
                                     float* logits, hipStream_t s) {
+  const bool tiled = hidden % 4 == 0 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)router_w & 15) == 0;
+  if (tiled) {
+    const unsigned ge = (unsigned)((n_experts + 7) / 8);
+    if (tokens < 8)
+      hipLaunchKernelGGL(moe_router_tile_kernel<1>, dim3(ge, (unsigned)tokens), dim3(256), 0, s, x, router_w, hidden,
+                         n_experts, tokens, logits);
+    else
+      hipLaunchKernelGGL(moe_router_tile_kernel<8>, dim3(ge, (unsigned)((tokens + 7) / 8)), dim3(256), 0, s, x,
+                         router_w, hidden, n_experts, tokens, logits);
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL(moe_router_logits_kernel, dim3((unsigned)((n_experts + 3) / 4), (unsigned)tokens), dim3(256),
                      (size_t)hidden * sizeof(float), s, x, router_w, hidden, n_experts, logits);
   return hipGetLastError();
@@ -442,9 +504,9 @@ __global__ __launch_bounds__(WAVES * 64) void moe_gemv_kernel(MoeGemvArgs a) {
   }
 }
 
-template <int T, bool DUAL, int NB>
+template <int T, bool DUAL, int NB, int R = kMoeGemvRows>
 static hipError_t launch_moe_gemv_nb(const MoeGemvArgs& a, int ntasks, hipStream_t s) {
-  constexpr int R = kMoeGemvRows, W = kMoeGemvWaves;
+  constexpr int W = kMoeGemvWaves;
   const int KP = a.KB * Blk<T>::QK;
   const size_t lds = ((size_t)NB * KP * 17 / 16 + (size_t)W * (DUAL ? 2 : 1) * NB * R + (size_t)W * NB) * sizeof(float);
   hipLaunchKernelGGL((moe_gemv_kernel<T, R, W, NB, DUAL>), dim3((unsigned)ntasks), dim3(W * 64), lds, s, a);
@@ -454,6 +516,13 @@ static hipError_t launch_moe_gemv_nb(const MoeGemvArgs& a, int ntasks, hipStream
 // tasks of at most one gathered row use the single-row instance (no idle activation slots)
 template <int T, bool DUAL>
 static hipError_t launch_moe_gemv_t(const MoeGemvArgs& a, int ntasks, hipStream_t s) {
+  if (a.rows_per_task == kFfnGemvRows) {
+    if constexpr (DUAL) {
+      if (a.max_rows <= 1) return launch_moe_gemv_nb<T, true, 1, kFfnGemvRows>(a, ntasks, s);
+    }
+    return hipErrorInvalidValue;
+  }
+  if (a.rows_per_task != kMoeGemvRows) return hipErrorInvalidValue;
   return a.max_rows <= 1 ? launch_moe_gemv_nb<T, DUAL, 1>(a, ntasks, s)
                          : launch_moe_gemv_nb<T, DUAL, kMoeGemvBatch>(a, ntasks, s);
 }

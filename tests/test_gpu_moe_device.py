@@ -42,9 +42,11 @@ def test_route_matches_oracle_router(T, E, k, gate):
     assert list(gi[0, :2]) == [3, 7]
 
 
-def test_router_logits_matvec():
-    rng = np.random.default_rng(3)
-    T, H, E = 7, 2048, 128
+@pytest.mark.parametrize("T,H,E", [(7, 2048, 128), (37, 2048, 61), (512, 1024, 128), (9, 2046, 20)])
+def test_router_logits_matvec(T, H, E):
+    # the tiled kernel (one and eight tokens per workgroup, a partial expert group) and the
+    # per-expert kernel (rows not a whole number of float4)
+    rng = np.random.default_rng(3 + T)
     x = rng.standard_normal((T, H)).astype(np.float32)
     w = (rng.standard_normal((E, H)) / 45).astype(np.float32)
     out = B(T * E * 4)
