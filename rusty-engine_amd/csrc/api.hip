@@ -151,6 +151,7 @@ struct re_moe {
   std::mutex mu;
   hipStream_t stream = nullptr;
   Staging sx, sout, sg, su, sh, syp, smeta;
+  Staging sxb;                            // bf16 copy of the activation rows (grouped GEMM path)
   Staging dmeta, droute;                  // device-routed path: plan + task lists; logits, ids, weights
   // pinned host staging of the per-call routing metadata, reused once its last upload is done
   void* hmeta = nullptr;
@@ -165,6 +166,16 @@ namespace {
 size_t env_size(const char* name, size_t dflt) {
   const char* v = std::getenv(name);
   return (v && *v) ? (size_t)std::strtoull(v, nullptr, 10) : dflt;
+}
+
+bool aligned16(const void* p);
+
+// bf16 mode of the grouped MoE GEMMs: the activation rows are rounded to bf16 once and SwiGLU
+// writes h as bf16 -- the rounding each GEMM tile would apply while staging them -- so the
+// tiles stage half the bytes and convert nothing (identical results). REHIP_MOE_XB=0 turns it off.
+bool moe_bf16_acts(const re_moe* e, const float* d_x, int mode) {
+  return mode == RE_MODE_BF16 && e->hidden % 8 == 0 && e->inter % 8 == 0 && aligned16(d_x) &&
+         env_size("REHIP_MOE_XB", 1) != 0;
 }
 
 // GEMV launch shape. Work units are 32-quant chunks (KB * chunks-per-block per row).
@@ -807,7 +818,7 @@ void re_moe_destroy(re_moe* e) {
   if (e->d_gate) (void)hipFree(e->d_gate);
   if (e->d_up) (void)hipFree(e->d_up);
   if (e->d_down) (void)hipFree(e->d_down);
-  for (Staging* s : {&e->sx, &e->sout, &e->sg, &e->su, &e->sh, &e->syp, &e->smeta}) s->release();
+  for (Staging* s : {&e->sx, &e->sout, &e->sg, &e->su, &e->sh, &e->syp, &e->smeta, &e->sxb}) s->release();
   if (e->meta_ev) (void)hipEventSynchronize(e->meta_ev);
   if (e->meta_ev) (void)hipEventDestroy(e->meta_ev);
   if (e->hmeta) (void)hipHostFree(e->hmeta);
@@ -951,6 +962,14 @@ int re_moe_forward_routed_dev(re_moe* e, const float* d_x, size_t tokens, size_t
     a.w_bytes = (uint32_t)(e->gg.bytes * e->n_experts);
     a.W = e->d_gate;
     a.Y = (float*)e->sg.p;
+    const bool xb = moe_bf16_acts(e, d_x, mode);
+    if (xb) {
+      if ((rc = e->sxb.ensure(tokens * e->hidden * 2))) return rc;
+      HIP_TRY(launch_x_to_bf16(d_x, e->sxb.p, tokens * e->hidden, s));
+      a.X = e->sxb.p;
+      a.x_bytes = (uint32_t)(tokens * e->hidden * 2);
+      a.x_bf16 = 1;
+    }
     const int kg_gu = gemm_kgroups(GemmTile::k64x64, mode, (long)sh.max_gu, (int)((e->hidden + kGemmBK - 1) / kGemmBK));
     const int kg_d = gemm_kgroups(GemmTile::k64x64, mode, (long)sh.max_d, (int)((e->inter + kGemmBK - 1) / kGemmBK));
     HIP_TRY(launch_gemm(e->gg.type, mode, a, sh.max_gu, GemmTile::k64x64, kg_gu, s));
@@ -961,10 +980,12 @@ int re_moe_forward_routed_dev(re_moe* e, const float* d_x, size_t tokens, size_t
     a.tiles = (int)e->gu.tiles;
     a.Y = (float*)e->su.p;
     HIP_TRY(launch_gemm(e->gu.type, mode, a, sh.max_gu, GemmTile::k64x64, kg_gu, s));
-    HIP_TRY(launch_swiglu((const float*)e->sg.p, (const float*)e->su.p, (float*)e->sh.p, pairs * e->inter, s));
+    if (xb) HIP_TRY(launch_swiglu_bf16((const float*)e->sg.p, (const float*)e->su.p, e->sh.p, pairs * e->inter, s));
+    else HIP_TRY(launch_swiglu((const float*)e->sg.p, (const float*)e->su.p, (float*)e->sh.p, pairs * e->inter, s));
     GemmArgs d{};
-    d.X = (const float*)e->sh.p;
-    d.x_bytes = (uint32_t)act;
+    d.X = e->sh.p;
+    d.x_bytes = (uint32_t)(xb ? act / 2 : act);
+    d.x_bf16 = xb;
     d.splits = 1;
     d.steps_per_split = 1 << 30;
     d.tasks = tg + sh.max_gu;
@@ -1157,6 +1178,14 @@ int re_moe_forward_dev(re_moe* e, const float* d_x, size_t tokens, size_t top_k,
     const int kg_d = gemm_kgroups(GemmTile::k64x64, mode, (long)n_d, (int)((e->inter + kGemmBK - 1) / kGemmBK));
     if ((rc = e->sg.ensure(act)) || (rc = e->su.ensure(act))) return rc;
     a.Y = (float*)e->sg.p;
+    const bool xb = moe_bf16_acts(e, d_x, mode);
+    if (xb) {
+      if ((rc = e->sxb.ensure(tokens * e->hidden * 2))) return rc;
+      HIP_TRY(launch_x_to_bf16(d_x, e->sxb.p, tokens * e->hidden, s));
+      a.X = e->sxb.p;
+      a.x_bytes = (uint32_t)(tokens * e->hidden * 2);
+      a.x_bf16 = 1;
+    }
     HIP_TRY(launch_gemm(e->gg.type, mode, a, (int)n_gu, GemmTile::k64x64, kg_gu, s));
     a.W = e->d_up;
     a.w_bytes = (uint32_t)(e->gu.bytes * e->n_experts);
@@ -1165,13 +1194,15 @@ int re_moe_forward_dev(re_moe* e, const float* d_x, size_t tokens, size_t top_k,
     a.tiles = (int)e->gu.tiles;
     a.Y = (float*)e->su.p;
     HIP_TRY(launch_gemm(e->gu.type, mode, a, (int)n_gu, GemmTile::k64x64, kg_gu, s));
-    HIP_TRY(launch_swiglu((const float*)e->sg.p, (const float*)e->su.p, (float*)e->sh.p, pairs * e->inter, s));
+    if (xb) HIP_TRY(launch_swiglu_bf16((const float*)e->sg.p, (const float*)e->su.p, e->sh.p, pairs * e->inter, s));
+    else HIP_TRY(launch_swiglu((const float*)e->sg.p, (const float*)e->su.p, (float*)e->sh.p, pairs * e->inter, s));
     GemmArgs d{};
     d.W = e->d_down;
     d.w_bytes = (uint32_t)(e->gd.bytes * e->n_experts);
     d.w_stride = e->gd.bytes;
-    d.X = (const float*)e->sh.p;
-    d.x_bytes = (uint32_t)(pairs * e->inter * sizeof(float));
+    d.X = e->sh.p;
+    d.x_bytes = (uint32_t)(pairs * e->inter * (xb ? 2 : sizeof(float)));
+    d.x_bf16 = xb;
     d.splits = 1;
     d.steps_per_split = 1 << 30;
     d.Y = (float*)e->syp.p;

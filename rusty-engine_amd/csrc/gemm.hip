@@ -29,6 +29,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "deq.hpp"
 #include "kernels.hpp"
@@ -119,16 +120,19 @@ __device__ __forceinline__ typename DecX<F32>::T cvt_x(float4 v) {
 
 constexpr uint32_t kOob = 0x80000000u;   // a byte offset past every buffer: the load returns 0
 
-template <int T, bool F32, bool GROUPED, int BM, int BN, int WM, int WN, int KG>
+template <int T, bool F32, bool GROUPED, int BM, int BN, int WM, int WN, int KG, bool XB = false>
 __global__ __launch_bounds__(WM* WN * 64 * KG) void gemm_kernel(GemmArgs p) {
   using B = Blk<T>;
   using E = typename Elem<F32>::T;
+  static_assert(!XB || !F32, "bf16 activations feed the bf16 mode only");
   constexpr int GT = WM * WN * 64;                 // threads of one K-group
   constexpr int BK = kGemmBK;
   constexpr int LD = BK + Elem<F32>::PAD;          // LDS row stride (elements)
   constexpr int WJOBS = BM * 4 / GT;               // (row, chunk) jobs per thread per step
-  constexpr int XV = BN * BK / 4 / GT;             // 16-byte X loads per thread per step
-  constexpr int XR = GT / 32;                      // X rows covered by one pass of a group
+  constexpr int XE = XB ? 8 : 4;                   // X elements per 16-byte load
+  constexpr uint32_t XS = XB ? 2 : 4;              // bytes per X element
+  constexpr int XV = BN * BK / XE / GT;            // 16-byte X loads per thread per step
+  constexpr int XR = GT / (BK / XE);               // X rows covered by one pass of a group
   constexpr int TM = BM / WM / 32, TN = BN / WN / 32;
   constexpr int STAGE = (BM + BN) * LD;            // LDS elements of one group
   static_assert(WJOBS >= 1 && XV >= 1 && TM >= 1 && TN >= 1, "tile shape");
@@ -188,24 +192,24 @@ __global__ __launch_bounds__(WM* WN * 64 * KG) void gemm_kernel(GemmArgs p) {
   // activation rows this thread stages: rows XR*jj + tid/32, k offset 4*(tid%32). Dense launches
   // address row r0 + XR*jj + tid/32 as one per-thread offset plus a scalar jj*XR*K*4 (rows past
   // N lie past the end of X and read zeros); grouped launches gather rows through xrow.
-  const int xk = 4 * (tid & 31);
+  const int xk = XE * (tid % (BK / XE));
   constexpr int XOFFS = GROUPED ? XV : 1;
   uint32_t xoff[XOFFS];
   if constexpr (GROUPED) {
 #pragma unroll
     for (int jj = 0; jj < XV; ++jj) {
-      const int rl = XR * jj + (tid >> 5);
+      const int rl = XR * jj + tid / (BK / XE);
       uint32_t o = kOob;
       if (rl < rn) {
         const int row = p.xrow ? p.xrow[r0 + rl] : r0 + rl;
-        o = (uint32_t)row * (uint32_t)p.K * 4u + (uint32_t)xk * 4u;
+        o = (uint32_t)row * (uint32_t)p.K * XS + (uint32_t)xk * XS;
       }
       xoff[jj] = o;
     }
   } else {
-    xoff[0] = (uint32_t)(r0 + (tid >> 5)) * (uint32_t)p.K * 4u + (uint32_t)xk * 4u;
+    xoff[0] = (uint32_t)(r0 + tid / (BK / XE)) * (uint32_t)p.K * XS + (uint32_t)xk * XS;
   }
-  const uint32_t xrow_step = (uint32_t)XR * (uint32_t)p.K * 4u;   // bytes between a thread's rows
+  const uint32_t xrow_step = (uint32_t)XR * (uint32_t)p.K * XS;   // bytes between a thread's rows
   // weight jobs: row rl = j % BM of tile (BM/64)*mtile + rl/64, chunk c = j / BM
   uint32_t wrow[WJOBS];
   int wc[WJOBS];
@@ -231,19 +235,30 @@ __global__ __launch_bounds__(WM* WN * 64 * KG) void gemm_kernel(GemmArgs p) {
       B::bload_chunk(wr, slab, tl, cc, raw[rep]);
     }
   };
-  auto load_x = [&](int s, float4 (&xv)[XV]) {
+  auto load_x = [&](int s, i32x4_t (&xv)[XV]) {
     const bool in = s < s_end && s * BK + xk < p.K;
 #pragma unroll
     for (int jj = 0; jj < XV; ++jj) {
       i32x4_t v;
       if constexpr (GROUPED) {
-        const uint32_t o = in ? xoff[jj] + (uint32_t)(s * BK) * 4u : kOob;
+        const uint32_t o = in ? xoff[jj] + (uint32_t)(s * BK) * XS : kOob;
         v = __builtin_amdgcn_raw_buffer_load_b128(xr, (int)o, 0, 0);
       } else {
-        const uint32_t o = in ? xoff[0] + (uint32_t)(s * BK) * 4u : kOob;
+        const uint32_t o = in ? xoff[0] + (uint32_t)(s * BK) * XS : kOob;
         v = __builtin_amdgcn_raw_buffer_load_b128(xr, (int)o, (int)(jj * xrow_step), 0);
       }
-      xv[jj] = make_float4(__int_as_float(v[0]), __int_as_float(v[1]), __int_as_float(v[2]), __int_as_float(v[3]));
+      xv[jj] = v;
+    }
+  };
+  // staged X element pack: bf16 activations are stored as loaded; f32 ones are rounded (bf16
+  // mode, RNE) or kept (f32 mode)
+  using XD = std::conditional_t<XB, bf16x8_t, typename DecX<F32>::T>;
+  auto cvt = [&](const i32x4_t& v) -> XD {
+    if constexpr (XB) {
+      return __builtin_bit_cast(bf16x8_t, v);
+    } else {
+      return cvt_x<F32>(make_float4(__int_as_float(v[0]), __int_as_float(v[1]), __int_as_float(v[2]),
+                                    __int_as_float(v[3])));
     }
   };
   auto decode = [&](int s, const typename B::CR (&raw)[WJOBS], DecChunk<F32> (&dec)[WJOBS]) {
@@ -261,18 +276,17 @@ __global__ __launch_bounds__(WM* WN * 64 * KG) void gemm_kernel(GemmArgs p) {
       dec[rep].eb = kl + b.e;
     }
   };
-  auto write_lds = [&](const DecChunk<F32> (&dec)[WJOBS], const typename DecX<F32>::T (&xd)[XV]) {
+  auto write_lds = [&](const DecChunk<F32> (&dec)[WJOBS], const XD (&xd)[XV]) {
 #pragma unroll
     for (int rep = 0; rep < WJOBS; ++rep) store_dec<F32>(Ws + ((tid + GT * rep) % BM) * LD, dec[rep]);
 #pragma unroll
-    for (int jj = 0; jj < XV; ++jj)
-      *reinterpret_cast<typename DecX<F32>::T*>(Xs + (XR * jj + (tid >> 5)) * LD + xk) = xd[jj];
+    for (int jj = 0; jj < XV; ++jj) *reinterpret_cast<XD*>(Xs + (XR * jj + tid / (BK / XE)) * LD + xk) = xd[jj];
   };
 
   typename B::CR rawA[WJOBS], rawB[WJOBS];
   DecChunk<F32> dec[WJOBS];
-  float4 xraw[XV];
-  typename DecX<F32>::T xdec[XV];
+  i32x4_t xraw[XV];
+  XD xdec[XV];
 
   // prologue: step s0 into LDS, raw chunks of s0 + KG in flight
   load_w(s0, rawA);
@@ -280,7 +294,7 @@ __global__ __launch_bounds__(WM* WN * 64 * KG) void gemm_kernel(GemmArgs p) {
   load_w(s0 + KG, rawB);
   decode(s0, rawA, dec);
 #pragma unroll
-  for (int jj = 0; jj < XV; ++jj) xdec[jj] = cvt_x<F32>(xraw[jj]);
+  for (int jj = 0; jj < XV; ++jj) xdec[jj] = cvt(xraw[jj]);
   write_lds(dec, xdec);
 #pragma unroll
   for (int rep = 0; rep < WJOBS; ++rep) rawA[rep] = rawB[rep];
@@ -333,7 +347,7 @@ __global__ __launch_bounds__(WM* WN * 64 * KG) void gemm_kernel(GemmArgs p) {
       }
     }
 #pragma unroll
-    for (int jj = 0; jj < XV; ++jj) xdec[jj] = cvt_x<F32>(xraw[jj]);
+    for (int jj = 0; jj < XV; ++jj) xdec[jj] = cvt(xraw[jj]);
     __syncthreads();                      // every wave is done reading step s
     write_lds(dec, xdec);                 // step s + KG (zeros past the end)
     __syncthreads();
@@ -419,10 +433,30 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(const float* __restric
   y[i] = s;
 }
 
+// x[i] -> bf16 with round to nearest even (the rounding the bf16-mode GEMM applies to f32 X), 8
+// elements (two 16-byte loads, one store) per thread
+__global__ __launch_bounds__(256) void x_to_bf16_kernel(const float4* __restrict__ x, bf16x8_t* __restrict__ xb,
+                                                        size_t n8) {
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n8; i += (size_t)gridDim.x * 256) {
+    const float4 a = x[2 * i], b = x[2 * i + 1];
+    bf16x8_t o;
+    o[0] = (__bf16)a.x; o[1] = (__bf16)a.y; o[2] = (__bf16)a.z; o[3] = (__bf16)a.w;
+    o[4] = (__bf16)b.x; o[5] = (__bf16)b.y; o[6] = (__bf16)b.z; o[7] = (__bf16)b.w;
+    xb[i] = o;
+  }
+}
+
 template <int T, bool F32, int BM, int BN, int WM, int WN, int KG, bool GROUPED>
 static hipError_t launch_shape(const GemmArgs& a, int ntasks, hipStream_t s) {
   constexpr int NT = WM * WN * 64 * KG;
   if constexpr (GROUPED) {
+    if constexpr (!F32) {
+      if (a.x_bf16) {
+        hipLaunchKernelGGL((gemm_kernel<T, false, true, BM, BN, WM, WN, KG, true>), dim3((unsigned)ntasks), dim3(NT),
+                           0, s, a);
+        return hipGetLastError();
+      }
+    }
     hipLaunchKernelGGL((gemm_kernel<T, F32, true, BM, BN, WM, WN, KG>), dim3((unsigned)ntasks), dim3(NT), 0, s, a);
     return hipGetLastError();
   } else {
@@ -442,6 +476,7 @@ static hipError_t launch_shape(const GemmArgs& a, int ntasks, hipStream_t s) {
 // (KG 1) in bf16; grouped (MoE) 64x64 (KG 1/2) in both modes.
 template <int T, bool F32>
 static hipError_t launch_t(const GemmArgs& a, int ntasks, GemmTile tile, int kg, hipStream_t s) {
+  if (a.x_bf16 && (F32 || !a.tasks)) return hipErrorInvalidValue;   // bf16 X: grouped bf16 launches
   if (a.tasks) {
     if (tile != GemmTile::k64x64) return hipErrorInvalidValue;
     if (kg == 1) return launch_shape<T, F32, 64, 64, 2, 2, 1, true>(a, ntasks, s);
@@ -518,6 +553,15 @@ GemmPlan plan_gemm(int m, int n, int K, int mode) {
   pl.steps_per_split = (steps + pl.splits - 1) / pl.splits;
   pl.splits = (steps + pl.steps_per_split - 1) / pl.steps_per_split;
   return pl;
+}
+
+hipError_t launch_x_to_bf16(const float* x, void* xb, size_t n, hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  if (n % 8) return hipErrorInvalidValue;
+  const size_t n8 = n / 8;
+  const unsigned grid = (unsigned)std::min<size_t>((n8 + 255) / 256, 4096);
+  hipLaunchKernelGGL(x_to_bf16_kernel, dim3(grid), dim3(256), 0, s, (const float4*)x, (bf16x8_t*)xb, n8);
+  return hipGetLastError();
 }
 
 hipError_t launch_gemm(uint32_t type, int mode, const GemmArgs& a, int ntasks, GemmTile tile, int kgroups,

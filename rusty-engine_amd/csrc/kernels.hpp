@@ -100,8 +100,9 @@ struct GemmArgs {
   const uint8_t* W;        // tiled slabs (expert 0)
   uint32_t w_bytes;        // bytes readable from W (all experts); < 2 GiB
   size_t w_stride;         // bytes between experts
-  const float* X;          // activations, row-major, K floats per row
+  const void* X;           // activations, row-major, K floats per row (K bf16 when x_bf16)
   uint32_t x_bytes;        // bytes readable from X; < 2 GiB
+  int x_bf16;              // grouped bf16-mode launch: X already rounded to bf16
   float* Y;                // output, row stride ldy
   int m, K, KB, tiles;     // weight geometry (per expert)
   int N;                   // activation rows (dense launch)
@@ -127,6 +128,8 @@ GemmPlan plan_gemm(int m, int n, int K, int mode);
 int gemm_kgroups(GemmTile tile, int mode, long workgroups, int steps);
 hipError_t launch_gemm(uint32_t type, int mode, const GemmArgs& a, int ntasks, GemmTile tile, int kgroups,
                        hipStream_t s);
+// xb[i] = bf16(x[i]), round to nearest even; n a multiple of 8, both buffers 16-byte aligned
+hipError_t launch_x_to_bf16(const float* x, void* xb, size_t n, hipStream_t s);
 
 // Grouped expert GEMV (few gathered rows per expert): one task per workgroup
 struct MoeGemvTask {
@@ -210,6 +213,7 @@ struct MoePlanShape {
 size_t moe_meta_bytes(const MoePlanShape& sh);
 hipError_t launch_moe_plan(const int* ids, const MoePlanShape& sh, void* meta, hipStream_t s);
 hipError_t launch_swiglu(const float* g, const float* u, float* h, size_t n, hipStream_t s);
+hipError_t launch_swiglu_bf16(const float* g, const float* u, void* h, size_t n, hipStream_t s);
 hipError_t launch_combine(const float* yp, const int* pos, const float* w, float* out, int tokens,
                           int k, int hidden, hipStream_t s);
 

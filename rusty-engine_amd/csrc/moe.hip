@@ -330,6 +330,20 @@ hipError_t launch_moe_plan(const int* ids, const MoePlanShape& sh, void* meta, h
   return hipGetLastError();
 }
 
+// the same h rounded to bf16 (RNE), for a bf16-mode GEMM that consumes it
+__global__ __launch_bounds__(256) void swiglu_bf16_kernel(const float* __restrict__ g, const float* __restrict__ u,
+                                                          __bf16* __restrict__ h, size_t n) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  h[i] = (__bf16)silu_mul(g[i], u[i]);
+}
+
+hipError_t launch_swiglu_bf16(const float* g, const float* u, void* h, size_t n, hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(swiglu_bf16_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, g, u, (__bf16*)h, n);
+  return hipGetLastError();
+}
+
 hipError_t launch_swiglu(const float* g, const float* u, float* h, size_t n, hipStream_t s) {
   if (n == 0) return hipSuccess;
   hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, g, u, h, n);

@@ -67,6 +67,36 @@ def moe_case(seed, E, hidden, inter, T, k, gt=rehip.Q4_K, dt=rehip.Q6_K):
     return gate, up, down_, x, logits
 
 
+@pytest.mark.parametrize("T,E,k,gt,dt", [(64, 16, 4, rehip.Q4_K, rehip.Q6_K), (300, 32, 4, rehip.Q4_K, rehip.Q6_K),
+                                         (200, 8, 2, rehip.Q8_0, rehip.Q5_0)])
+def test_grouped_gemm_bf16_activations_bit_identical(T, E, k, gt, dt, monkeypatch):
+    """bf16 mode of the grouped expert GEMMs: activation rows rounded to bf16 up front and h
+    written as bf16 by SwiGLU (REHIP_MOE_XB=1, the default) give the same bits as rounding each
+    tile while staging it (0), host- and device-routed."""
+    hidden, inter = 512, 256
+    gate, up, down_, x, logits = moe_case(950 + T + E, E, hidden, inter, T, k, gt, dt)
+    ids = np.zeros((T, k), np.int32)
+    wts = np.zeros((T, k), np.float32)
+    for t in range(T):
+        ids[t], wts[t] = O.top_k(logits[t], k)
+    moe = rehip.MoeExperts(gt, gate, gt, up, dt, down_, E, hidden, inter)
+    xd = B.from_array(x)
+    idd, wd = B.from_array(ids.reshape(-1)), B.from_array(wts.reshape(-1))
+    res = {}
+    for xb in ("0", "1"):
+        monkeypatch.setenv("REHIP_MOE_XB", xb)
+        out = B(T * hidden * 4)
+        moe.forward_routed_dev(xd, T, k, idd, wd, out, rehip.MODE_BF16)
+        res[xb] = (down(out, T * hidden),
+                   moe.forward(x, T, k, ids.reshape(-1).astype(np.uint32), wts.reshape(-1), rehip.MODE_BF16))
+    assert np.array_equal(res["0"][0], res["1"][0])
+    assert np.array_equal(res["0"][1], res["1"][1])
+    want = O.moe_ffn(gt, gate, gt, up, dt, down_, E, hidden, inter, x, T, k,
+                     ids.reshape(-1).astype(np.uint32), wts.reshape(-1))
+    assert np.linalg.norm(res["1"][1] - want) / np.linalg.norm(want) <= 1e-2
+    moe.close()
+
+
 @pytest.mark.parametrize("T,E,k", [(1, 16, 4), (5, 16, 4), (40, 16, 4), (3, 128, 8), (300, 32, 4)])
 def test_forward_routed_equals_host_routed(T, E, k):
     """Device grouping/tasks vs the host planner: the same kernels over the same rows, so the
