@@ -351,9 +351,9 @@ int gemm_enqueue(re_qmat* q, const float* d_x, size_t rows, float* d_y, int mode
   if (xbytes >= (1ull << 31) || q->g.bytes >= (1ull << 31))
     return fail(RE_ERR_SIZE, "GEMM operands must stay below 2 GiB (X %zu B, W %zu B)", xbytes, q->g.bytes);
   GemmPlan pl = plan_gemm((int)q->g.m, (int)rows, (int)q->g.n, mode);
-  // tuning knobs: REHIP_GEMM_TILE (1 64x64, 2 128x128, 3 128x256, 4 256x128), REHIP_GEMM_KG,
+  // tuning knobs: REHIP_GEMM_TILE (1 64x64, 2 128x128, 3 128x256, 4 256x128, 5 128x192), REHIP_GEMM_KG,
   // REHIP_GEMM_SPLITS; a combination the library does not build fails at launch
-  if (const size_t t = env_size("REHIP_GEMM_TILE", 0); t >= 1 && t <= 4) {
+  if (const size_t t = env_size("REHIP_GEMM_TILE", 0); t >= 1 && t <= 5) {
     pl.tile = (GemmTile)(t - 1);
     pl.kgroups = (int)env_size("REHIP_GEMM_KG", 1);
     const int steps = (int)((q->g.n + kGemmBK - 1) / kGemmBK);

@@ -86,7 +86,7 @@ hipError_t launch_repack(uint32_t type, const uint8_t* src, uint8_t* dst, int m,
 constexpr int kGemmBK = 128;
 constexpr int kMoeTile = 64;   // tile of the grouped (MoE) launches (64 x 64, four waves)
 
-enum class GemmTile { k64x64, k128x128, k128x256, k256x128 };
+enum class GemmTile { k64x64, k128x128, k128x256, k256x128, k128x192 };
 
 // Work item of a grouped launch (MoE): one tile of one expert.
 struct GemmTask {

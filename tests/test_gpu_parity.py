@@ -241,7 +241,7 @@ def test_gemm_parity_both_modes(t, m, n, rows):
 
 @pytest.mark.parametrize("t", rehip.QUANT_TYPES)
 @pytest.mark.parametrize("tile,kg,splits", [(1, 1, 1), (1, 2, 1), (2, 1, 1), (3, 1, 1), (4, 1, 1), (3, 1, 2),
-                                            (4, 1, 3), (1, 2, 3)])
+                                            (4, 1, 3), (1, 2, 3), (5, 1, 1), (5, 1, 3)])
 def test_gemm_forced_tiles(t, tile, kg, splits, monkeypatch):
     # every tile / K-group / K-split instance in bf16 mode on a ragged shape: 300 weight rows (a
     # partial 128- and 256-row tile), 500 activation rows, K = 1280 (5 super-blocks)
