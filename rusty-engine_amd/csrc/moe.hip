@@ -182,17 +182,35 @@ __global__ __launch_bounds__(1024) void moe_plan_kernel(const int* __restrict__ 
       __syncthreads();
     }
   }
-  if (tid == 0) {
-    int acc = 0, cacc = 0;
-    for (int e = 0; e < E; ++e) {
-      start[e] = acc;
-      acc += cnt[e];
-      cstart[e] = cacc;
-      cacc += (cnt[e] + sh.chunk - 1) / sh.chunk;
+  // row starts and chunk starts per expert: an exclusive scan over the block, one expert per
+  // thread (E <= 1024): wave scans, then the wave totals in order
+  __shared__ int wsum[2][16];
+  {
+    const int lane = tid & 63, w = tid >> 6;
+    const int c = tid < E ? cnt[tid] : 0;
+    const int ch = tid < E ? (c + sh.chunk - 1) / sh.chunk : 0;
+    int sc = c, sch = ch;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int a = __shfl_up(sc, off, 64), b = __shfl_up(sch, off, 64);
+      if (lane >= off) { sc += a; sch += b; }
     }
-    cstart[E] = cacc;
-    ntasks[0] = min(cacc * sh.tiles_gu, sh.max_gu);   // the capacities bound every count
-    ntasks[1] = min(cacc * sh.tiles_d, sh.max_d);
+    if (lane == 63) { wsum[0][w] = sc; wsum[1][w] = sch; }
+    __syncthreads();
+    int base = 0, cbase = 0, ctot = 0;
+    for (int j = 0; j < 16; ++j) {
+      if (j < w) { base += wsum[0][j]; cbase += wsum[1][j]; }
+      ctot += wsum[1][j];
+    }
+    if (tid < E) {
+      start[tid] = base + sc - c;
+      cstart[tid] = cbase + sch - ch;
+    }
+    if (tid == 0) {
+      cstart[E] = ctot;
+      ntasks[0] = min(ctot * sh.tiles_gu, sh.max_gu);   // the capacities bound every count
+      ntasks[1] = min(ctot * sh.tiles_d, sh.max_d);
+    }
   }
   __syncthreads();
   for (int i = tid; i < P; i += 1024) {
@@ -215,31 +233,20 @@ __global__ __launch_bounds__(1024) void moe_plan_kernel(const int* __restrict__ 
     r0 = start[e] + r;
     rn = min(sh.chunk, cnt[e] - r);
   };
-  if (sh.gemv) {
-    MoeGemvTask* tg = (MoeGemvTask*)tasks;
-    MoeGemvTask* td = tg + sh.max_gu;
-    for (int t = tid; t < n_gu; t += 1024) {
-      int e, r0, rn;
-      chunk_of(t / sh.tiles_gu, e, r0, rn);
-      tg[t] = {e, (t % sh.tiles_gu) * sh.rows_gu, r0, rn};
-    }
-    for (int t = tid; t < n_d; t += 1024) {
-      int e, r0, rn;
-      chunk_of(t / sh.tiles_d, e, r0, rn);
-      td[t] = {e, (t % sh.tiles_d) * sh.rows_gu, r0, rn};
-    }
-  } else {
-    GemmTask* tg = (GemmTask*)tasks;
-    GemmTask* td = tg + sh.max_gu;
-    for (int t = tid; t < n_gu; t += 1024) {
-      int e, r0, rn;
-      chunk_of(t / sh.tiles_gu, e, r0, rn);
-      tg[t] = {e, t % sh.tiles_gu, r0, rn};
-    }
-    for (int t = tid; t < n_d; t += 1024) {
-      int e, r0, rn;
-      chunk_of(t / sh.tiles_d, e, r0, rn);
-      td[t] = {e, t % sh.tiles_d, r0, rn};
+  // one thread per chunk: its expert once, then its weight-row tasks (task t = chunk * tiles + tile)
+  for (int c = tid; c < nch; c += 1024) {
+    int e, r0, rn;
+    chunk_of(c, e, r0, rn);
+    if (sh.gemv) {
+      MoeGemvTask* tg = (MoeGemvTask*)tasks;
+      MoeGemvTask* td = tg + sh.max_gu;
+      for (int j = 0, t = c * sh.tiles_gu; j < sh.tiles_gu && t < n_gu; ++j, ++t) tg[t] = {e, j * sh.rows_gu, r0, rn};
+      for (int j = 0, t = c * sh.tiles_d; j < sh.tiles_d && t < n_d; ++j, ++t) td[t] = {e, j * sh.rows_gu, r0, rn};
+    } else {
+      GemmTask* tg = (GemmTask*)tasks;
+      GemmTask* td = tg + sh.max_gu;
+      for (int j = 0, t = c * sh.tiles_gu; j < sh.tiles_gu && t < n_gu; ++j, ++t) tg[t] = {e, j, r0, rn};
+      for (int j = 0, t = c * sh.tiles_d; j < sh.tiles_d && t < n_d; ++j, ++t) td[t] = {e, j, r0, rn};
     }
   }
 }
