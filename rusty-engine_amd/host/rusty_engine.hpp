@@ -139,9 +139,17 @@ struct Q8Activation {
   size_t blocks() const { return scales.size(); }
 };
 
-// A GPU-resident quantized weight matrix W[m x n] (the Quant variant of QMat, qmat.rs:30-42).
+// A GPU-resident weight matrix W[m x n] (qmat.rs:30-42): quant blocks, or F32/F16/BF16 elements.
 class QMat {
  public:
+  // QMat::from_f32 (qmat.rs:45-49): a row-major f32 matrix; products in f32
+  static QMat from_f32(const std::vector<float>& data, size_t m, size_t n) {
+    if (data.size() != m * n) throw EngineError(RE_ERR_SIZE, "QMat::from_f32: shape mismatch");
+    re_qmat* h = nullptr;
+    check(re_qmat_create(0, reinterpret_cast<const uint8_t*>(data.data()), data.size() * sizeof(float), m, n, &h));
+    return QMat(h);
+  }
+
   // tensor `name` of a mapped model, dims [n, m]; EngineError when missing or out of bounds
   static QMat from_model(const MmapModel& model, const std::string& name, size_t m, size_t n) {
     re_qmat* h = nullptr;

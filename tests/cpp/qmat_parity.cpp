@@ -129,6 +129,22 @@ static void test_every_type_against_oracle() {
   }
 }
 
+static void test_from_f32_matches_plain_matvec() {  // qmat.rs:337-345
+  std::printf("from_f32_matches_plain_matvec\n");
+  std::vector<float> data(12);
+  for (int i = 0; i < 12; ++i) data[i] = (float)i * 0.25f - 1.0f;
+  const QMat qm = QMat::from_f32(data, 3, 4);
+  const std::vector<float> x = {1.0f, -2.0f, 0.5f, 3.0f};
+  std::vector<float> want(3);
+  for (int r = 0; r < 3; ++r) {           // moe::matvec: sequential sum from -0.0 (moe.rs:271-277)
+    float acc = -0.0f;
+    for (int k = 0; k < 4; ++k) acc += data[r * 4 + k] * x[k];
+    want[r] = acc;
+  }
+  CHECK(qm.matvec(x) == want, "f32 weights: exact sums match the plain matvec");
+  CHECK(qm.rows() == 3 && qm.cols() == 4 && qm.ggml_type() == 0, "shape and type");
+}
+
 static void test_unknown_type_is_an_error() {  // kernel.rs:2006, 2027 panic -> EngineError
   std::printf("unknown_type_is_an_error\n");
   bool threw = false;
@@ -331,6 +347,7 @@ int main() {
     test_moe_layer_routes_to_best_expert();
     test_gguf_header_fixture();
     test_qmat_from_model_equals_from_bytes();
+    test_from_f32_matches_plain_matvec();
     test_q8_activation_and_i8_matmul();
   } catch (const EngineError& e) {
     std::printf("EngineError %d: %s\n", e.code, e.what());
