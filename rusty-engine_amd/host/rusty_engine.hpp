@@ -6,7 +6,8 @@
 //   q.matmul(x, rows) -> Y[rows x m]           src/qmat.rs:169
 //   q.rows(), q.cols()                         src/qmat.rs:62-73
 //   top_k / top_k_sigmoid / route / silu       src/moe.rs:44-125 (host router)
-//   moe_layer_forward(...)                     src/moe.rs:360-388, experts on the GPU
+//   moe_layer_forward(..., shared)             src/moe.rs:360-388, experts on the GPU, optional shared expert
+//   combine(routed, weights, shared)           src/moe.rs:306-345
 //   MmapModel::open(path), header(), tensor_bytes(name)   src/loader.rs:25-130, src/gguf.rs:120-170
 //   QMat::from_model(model, name, m, n)        src/qmat.rs:310-330 (bytes go to the GPU from the map)
 //   Q8Activation::from_f32(x), q.matvec_i8 / matmul_i8   src/kernel.rs:70-166 (int8 activations)
@@ -312,9 +313,33 @@ class MoeExperts {
 // One MoE FFN layer on `tokens` hidden vectors (moe.rs:360-388): router logits on the host
 // (router_w is n_experts x hidden f32, `matvec` of moe.rs:271-277), route, then the routed
 // experts' SwiGLU FFNs and the weighted combine in routing order on the GPU.
+// combine (moe.rs:306-345): out = sum over k, in order, of routed[k] * weights[k], then + shared
+// verbatim; the reference's shape errors
+inline std::vector<float> combine(const std::vector<std::vector<float>>& routed, const std::vector<float>& weights,
+                                  const std::vector<float>* shared = nullptr) {
+  if (routed.size() != weights.size())
+    throw EngineError(RE_ERR_SIZE, "combine: " + std::to_string(routed.size()) + " outputs vs " +
+                                       std::to_string(weights.size()) + " weights");
+  const size_t dim = !routed.empty() ? routed[0].size() : (shared ? shared->size() : 0);
+  for (const auto& r : routed)
+    if (r.size() != dim) throw EngineError(RE_ERR_SIZE, "combine: ragged routed outputs");
+  if (shared && shared->size() != dim)
+    throw EngineError(RE_ERR_SIZE,
+                      "combine: shared dim " + std::to_string(shared->size()) + " != " + std::to_string(dim));
+  std::vector<float> out(dim, 0.0f);
+  for (size_t k = 0; k < routed.size(); ++k)
+    for (size_t i = 0; i < dim; ++i) out[i] += routed[k][i] * weights[k];
+  if (shared)
+    for (size_t i = 0; i < dim; ++i) out[i] += (*shared)[i];
+  return out;
+}
+
+// `shared`: an optional shared expert (a one-expert MoeExperts) whose FFN output is added
+// verbatim after the routed sum (moe.rs:380-385)
 inline std::vector<float> moe_layer_forward(const std::vector<float>& hidden, size_t tokens,
                                             const std::vector<float>& router_w, const MoeExperts& experts,
-                                            RouterConfig cfg, Precision prec = Precision::Bf16Mfma) {
+                                            RouterConfig cfg, Precision prec = Precision::Bf16Mfma,
+                                            const MoeExperts* shared = nullptr) {
   const size_t d = experts.hidden(), e = experts.n_experts();
   if (hidden.size() != tokens * d || router_w.size() != e * d)
     throw EngineError(RE_ERR_SIZE, "moe_layer_forward: shape mismatch");
@@ -334,7 +359,16 @@ inline std::vector<float> moe_layer_forward(const std::vector<float>& hidden, si
       w[t * k + j] = chosen[j].weight;
     }
   }
-  return experts.forward(hidden, tokens, k, ids, w, prec);
+  std::vector<float> out = experts.forward(hidden, tokens, k, ids, w, prec);
+  if (shared) {
+    if (shared->n_experts() != 1 || shared->hidden() != d)
+      throw EngineError(RE_ERR_SIZE, "moe_layer_forward: the shared expert must be one expert of the same width");
+    // weight 1 through the routed combine gives the expert's output itself (0 + 1 * v)
+    const std::vector<float> so =
+        shared->forward(hidden, tokens, 1, std::vector<uint32_t>(tokens, 0), std::vector<float>(tokens, 1.0f), prec);
+    for (size_t i = 0; i < out.size(); ++i) out[i] += so[i];
+  }
+  return out;
 }
 
 }  // namespace rusty_engine

@@ -207,6 +207,44 @@ static void test_moe_layer_routes_to_best_expert() {  // moe.rs:784-796
   }
 }
 
+static void test_moe_layer_adds_shared_expert() {  // moe.rs:788-801
+  std::printf("moe_layer_adds_shared_expert\n");
+  auto ident = q8_identity(1);
+  std::vector<uint8_t> two = ident;
+  two.insert(two.end(), ident.begin(), ident.end());
+  MoeExperts ex(ORC_Q8_0, two, ORC_Q8_0, two, ORC_Q8_0, two, 2, 32, 32);
+  MoeExperts shared(ORC_Q8_0, ident, ORC_Q8_0, ident, ORC_Q8_0, ident, 1, 32, 32);
+  std::vector<float> router_w(2 * 32, 0.0f);
+  router_w[0] = 10.0f;  // expert 0 wins (sigmoid, top-1: weight 1)
+  std::vector<float> h(32, 0.0f);
+  h[0] = 1.0f;
+  for (Precision p : {Precision::F32Strict, Precision::Bf16Mfma}) {
+    const auto out = moe_layer_forward(h, 1, router_w, ex, RouterConfig{Gate::Sigmoid, 1}, p, &shared);
+    CHECK(std::fabs(out[0] - 2.0f * silu(1.0f)) < 1e-2f, "out[0] = %g", out[0]);
+    float rest = 0;
+    for (int i = 1; i < 32; ++i) rest += std::fabs(out[i]);
+    CHECK(rest < 1e-5f, "off-diagonal %g", rest);
+  }
+}
+
+static void test_combine_routed_plus_shared() {  // moe.rs:749-765
+  std::printf("combine_routed_plus_shared\n");
+  const std::vector<std::vector<float>> routed = {{1.0f, 2.0f}, {3.0f, 4.0f}};
+  const std::vector<float> w = {0.5f, 0.5f}, sh = {1.0f, 1.0f};
+  CHECK(combine(routed, w, &sh) == std::vector<float>({3.0f, 4.0f}), "0.5*[1,2] + 0.5*[3,4] + [1,1]");
+  CHECK(combine(routed, w) == std::vector<float>({2.0f, 3.0f}), "no shared expert");
+  bool threw = false;
+  try { (void)combine({{1.0f, 2.0f}}, {0.5f, 0.5f}); } catch (const EngineError& e) {
+    threw = std::string(e.what()) == "combine: 1 outputs vs 2 weights";
+  }
+  CHECK(threw, "outputs vs weights count");
+  threw = false;
+  try { (void)combine({{1.0f}, {2.0f, 3.0f}}, {0.5f, 0.5f}); } catch (const EngineError& e) {
+    threw = std::string(e.what()) == "combine: ragged routed outputs";
+  }
+  CHECK(threw, "ragged outputs");
+}
+
 // ---- GGUF (gguf.rs:1063-1312, loader.rs:245-270) --------------------------------------------
 static void put_u32(std::vector<uint8_t>& b, uint32_t v) { for (int i = 0; i < 4; ++i) b.push_back((v >> (8 * i)) & 0xFF); }
 static void put_u64(std::vector<uint8_t>& b, uint64_t v) { for (int i = 0; i < 8; ++i) b.push_back((v >> (8 * i)) & 0xFF); }
@@ -345,6 +383,8 @@ int main() {
     test_every_type_against_oracle();
     test_router_matches_oracle();
     test_moe_layer_routes_to_best_expert();
+    test_moe_layer_adds_shared_expert();
+    test_combine_routed_plus_shared();
     test_gguf_header_fixture();
     test_qmat_from_model_equals_from_bytes();
     test_from_f32_matches_plain_matvec();
