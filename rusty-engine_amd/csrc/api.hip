@@ -972,16 +972,26 @@ int re_moe_forward_routed_dev(re_moe* e, const float* d_x, size_t tokens, size_t
     }
     const int kg_gu = gemm_kgroups(GemmTile::k64x64, mode, (long)sh.max_gu, (int)((e->hidden + kGemmBK - 1) / kGemmBK));
     const int kg_d = gemm_kgroups(GemmTile::k64x64, mode, (long)sh.max_d, (int)((e->inter + kGemmBK - 1) / kGemmBK));
-    HIP_TRY(launch_gemm(e->gg.type, mode, a, sh.max_gu, GemmTile::k64x64, kg_gu, s));
-    a.W = e->d_up;
-    a.w_stride = e->gu.bytes;
-    a.w_bytes = (uint32_t)(e->gu.bytes * e->n_experts);
-    a.KB = (int)e->gu.kb;
-    a.tiles = (int)e->gu.tiles;
-    a.Y = (float*)e->su.p;
-    HIP_TRY(launch_gemm(e->gu.type, mode, a, sh.max_gu, GemmTile::k64x64, kg_gu, s));
-    if (xb) HIP_TRY(launch_swiglu_bf16((const float*)e->sg.p, (const float*)e->su.p, e->sh.p, pairs * e->inter, s));
-    else HIP_TRY(launch_swiglu((const float*)e->sg.p, (const float*)e->su.p, (float*)e->sh.p, pairs * e->inter, s));
+    // bf16 activations and one gate/up type: one launch decodes both tiles against one staging of
+    // the rows and writes h = silu(gate) * up as bf16 (the same values as the separate GEMMs and
+    // SwiGLU below). REHIP_MOE_PAIR=0 turns it off.
+    const bool pair = xb && e->gg.type == e->gu.type && kg_gu == 1 && env_size("REHIP_MOE_PAIR", 1) != 0;
+    if (pair) {
+      a.W2 = e->d_up;
+      a.Y = (float*)e->sh.p;
+      HIP_TRY(launch_gemm(e->gg.type, mode, a, sh.max_gu, GemmTile::k64x64, 1, s));
+    } else {
+      HIP_TRY(launch_gemm(e->gg.type, mode, a, sh.max_gu, GemmTile::k64x64, kg_gu, s));
+      a.W = e->d_up;
+      a.w_stride = e->gu.bytes;
+      a.w_bytes = (uint32_t)(e->gu.bytes * e->n_experts);
+      a.KB = (int)e->gu.kb;
+      a.tiles = (int)e->gu.tiles;
+      a.Y = (float*)e->su.p;
+      HIP_TRY(launch_gemm(e->gu.type, mode, a, sh.max_gu, GemmTile::k64x64, kg_gu, s));
+      if (xb) HIP_TRY(launch_swiglu_bf16((const float*)e->sg.p, (const float*)e->su.p, e->sh.p, pairs * e->inter, s));
+      else HIP_TRY(launch_swiglu((const float*)e->sg.p, (const float*)e->su.p, (float*)e->sh.p, pairs * e->inter, s));
+    }
     GemmArgs d{};
     d.X = e->sh.p;
     d.x_bytes = (uint32_t)(xb ? act / 2 : act);
@@ -1186,16 +1196,26 @@ int re_moe_forward_dev(re_moe* e, const float* d_x, size_t tokens, size_t top_k,
       a.x_bytes = (uint32_t)(tokens * e->hidden * 2);
       a.x_bf16 = 1;
     }
-    HIP_TRY(launch_gemm(e->gg.type, mode, a, (int)n_gu, GemmTile::k64x64, kg_gu, s));
-    a.W = e->d_up;
-    a.w_bytes = (uint32_t)(e->gu.bytes * e->n_experts);
-    a.w_stride = e->gu.bytes;
-    a.KB = (int)e->gu.kb;
-    a.tiles = (int)e->gu.tiles;
-    a.Y = (float*)e->su.p;
-    HIP_TRY(launch_gemm(e->gu.type, mode, a, (int)n_gu, GemmTile::k64x64, kg_gu, s));
-    if (xb) HIP_TRY(launch_swiglu_bf16((const float*)e->sg.p, (const float*)e->su.p, e->sh.p, pairs * e->inter, s));
-    else HIP_TRY(launch_swiglu((const float*)e->sg.p, (const float*)e->su.p, (float*)e->sh.p, pairs * e->inter, s));
+    // bf16 activations and one gate/up type: one launch decodes both tiles against one staging of
+    // the rows and writes h = silu(gate) * up as bf16 (the same values as the separate GEMMs and
+    // SwiGLU below). REHIP_MOE_PAIR=0 turns it off.
+    const bool pair = xb && e->gg.type == e->gu.type && kg_gu == 1 && env_size("REHIP_MOE_PAIR", 1) != 0;
+    if (pair) {
+      a.W2 = e->d_up;
+      a.Y = (float*)e->sh.p;
+      HIP_TRY(launch_gemm(e->gg.type, mode, a, (int)n_gu, GemmTile::k64x64, 1, s));
+    } else {
+      HIP_TRY(launch_gemm(e->gg.type, mode, a, (int)n_gu, GemmTile::k64x64, kg_gu, s));
+      a.W = e->d_up;
+      a.w_bytes = (uint32_t)(e->gu.bytes * e->n_experts);
+      a.w_stride = e->gu.bytes;
+      a.KB = (int)e->gu.kb;
+      a.tiles = (int)e->gu.tiles;
+      a.Y = (float*)e->su.p;
+      HIP_TRY(launch_gemm(e->gu.type, mode, a, (int)n_gu, GemmTile::k64x64, kg_gu, s));
+      if (xb) HIP_TRY(launch_swiglu_bf16((const float*)e->sg.p, (const float*)e->su.p, e->sh.p, pairs * e->inter, s));
+      else HIP_TRY(launch_swiglu((const float*)e->sg.p, (const float*)e->su.p, (float*)e->sh.p, pairs * e->inter, s));
+    }
     GemmArgs d{};
     d.W = e->d_down;
     d.w_bytes = (uint32_t)(e->gd.bytes * e->n_experts);

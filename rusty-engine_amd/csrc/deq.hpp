@@ -510,4 +510,11 @@ __device__ __forceinline__ float wg_sum(float v, float* red) {
   return s;
 }
 
+// silu(x) * u with silu(x) = x * (1 / (1 + exp(-x))), each step rounded (moe.rs:44-51, 280-283);
+// shared by the SwiGLU kernel, the expert GEMV and the fused gate/up GEMM epilogue
+__device__ __forceinline__ float silu_mul(float x, float u) {
+  const float sig = __frcp_rn(__fadd_rn(1.0f, expf(-x)));
+  return __fmul_rn(__fmul_rn(x, sig), u);
+}
+
 }  // namespace rehip

@@ -120,11 +120,13 @@ __device__ __forceinline__ typename DecX<F32>::T cvt_x(float4 v) {
 
 constexpr uint32_t kOob = 0x80000000u;   // a byte offset past every buffer: the load returns 0
 
-template <int T, bool F32, bool GROUPED, int BM, int BN, int WM, int WN, int KG, bool XB = false>
+template <int T, bool F32, bool GROUPED, int BM, int BN, int WM, int WN, int KG, bool XB = false, bool DUAL = false>
 __global__ __launch_bounds__(WM* WN * 64 * KG) void gemm_kernel(GemmArgs p) {
   using B = Blk<T>;
   using E = typename Elem<F32>::T;
   static_assert(!XB || !F32, "bf16 activations feed the bf16 mode only");
+  static_assert(!DUAL || (GROUPED && XB && KG == 1), "gate/up pairs: grouped bf16 launches, one K-group");
+  constexpr int NW = DUAL ? 2 : 1;                 // weight tiles per step (gate, up)
   constexpr int GT = WM * WN * 64;                 // threads of one K-group
   constexpr int BK = kGemmBK;
   constexpr int LD = BK + Elem<F32>::PAD;          // LDS row stride (elements)
@@ -134,7 +136,7 @@ __global__ __launch_bounds__(WM* WN * 64 * KG) void gemm_kernel(GemmArgs p) {
   constexpr int XV = BN * BK / XE / GT;            // 16-byte X loads per thread per step
   constexpr int XR = GT / (BK / XE);               // X rows covered by one pass of a group
   constexpr int TM = BM / WM / 32, TN = BN / WN / 32;
-  constexpr int STAGE = (BM + BN) * LD;            // LDS elements of one group
+  constexpr int STAGE = (NW * BM + BN) * LD;       // LDS elements of one group
   static_assert(WJOBS >= 1 && XV >= 1 && TM >= 1 && TN >= 1, "tile shape");
   static_assert((KG - 1) * BM * BN * 4 <= KG * STAGE * (int)sizeof(E), "K-group partials fit in LDS");
   __shared__ __attribute__((aligned(16))) E smem[KG * STAGE];
@@ -145,7 +147,8 @@ __global__ __launch_bounds__(WM* WN * 64 * KG) void gemm_kernel(GemmArgs p) {
   const int wave = tid >> 6;                       // wave inside the K-group
   const int wm = wave / WN, wn = wave % WN;
   E* const Ws = smem + grp * STAGE;
-  E* const Xs = Ws + BM * LD;
+  E* const Ws2 = Ws + BM * LD;                     // up tile (pairs only)
+  E* const Xs = Ws + NW * BM * LD;
 
   int mtile, r0, rn, split = 0;
   uint32_t wbase = 0;
@@ -179,15 +182,24 @@ __global__ __launch_bounds__(WM* WN * 64 * KG) void gemm_kernel(GemmArgs p) {
   const int s0 = s_begin + grp;
 
   const __amdgpu_buffer_rsrc_t wr = make_rsrc(p.W, p.w_bytes);
+  const __amdgpu_buffer_rsrc_t wr2 = make_rsrc(DUAL ? p.W2 : p.W, p.w_bytes);
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(p.X, p.x_bytes);
 
-  f32x16_t acc[TM][TN];
+  f32x16_t acc[TM][TN], acc2[DUAL ? TM : 1][DUAL ? TN : 1];   // acc2: the up tile of a pair
 #pragma unroll
   for (int i = 0; i < TM; ++i)
 #pragma unroll
     for (int j = 0; j < TN; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+  if constexpr (DUAL) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc2[i][j][r] = 0.0f;
+  }
 
   // activation rows this thread stages: rows XR*jj + tid/32, k offset 4*(tid%32). Dense launches
   // address row r0 + XR*jj + tid/32 as one per-thread offset plus a scalar jj*XR*K*4 (rows past
@@ -222,7 +234,7 @@ __global__ __launch_bounds__(WM* WN * 64 * KG) void gemm_kernel(GemmArgs p) {
     wrow[rep] = tile < p.tiles ? wbase + (uint32_t)tile * (uint32_t)p.KB * (uint32_t)B::SLAB : kOob;
   }
 
-  auto load_w = [&](int s, typename B::CR (&raw)[WJOBS]) {
+  auto load_w = [&](int s, typename B::CR (&raw)[WJOBS], const __amdgpu_buffer_rsrc_t& rsrc) {
     const bool in = s < s_end;
 #pragma unroll
     for (int rep = 0; rep < WJOBS; ++rep) {
@@ -232,7 +244,7 @@ __global__ __launch_bounds__(WM* WN * 64 * KG) void gemm_kernel(GemmArgs p) {
       if constexpr (B::QK == 32) { kb = 4 * s + wc[rep]; cc = 0; }
       else { kb = s >> 1; cc = 4 * (s & 1) + wc[rep]; }
       const uint32_t slab = (in && kb < p.KB) ? wrow[rep] + (uint32_t)kb * (uint32_t)B::SLAB : kOob;
-      B::bload_chunk(wr, slab, tl, cc, raw[rep]);
+      B::bload_chunk(rsrc, slab, tl, cc, raw[rep]);
     }
   };
   auto load_x = [&](int s, i32x4_t (&xv)[XV]) {
@@ -276,42 +288,63 @@ __global__ __launch_bounds__(WM* WN * 64 * KG) void gemm_kernel(GemmArgs p) {
       dec[rep].eb = kl + b.e;
     }
   };
-  auto write_lds = [&](const DecChunk<F32> (&dec)[WJOBS], const XD (&xd)[XV]) {
+  auto write_lds = [&](const DecChunk<F32> (&dec)[WJOBS], const DecChunk<F32> (&dec2)[WJOBS], const XD (&xd)[XV]) {
 #pragma unroll
     for (int rep = 0; rep < WJOBS; ++rep) store_dec<F32>(Ws + ((tid + GT * rep) % BM) * LD, dec[rep]);
+    if constexpr (DUAL) {
+#pragma unroll
+      for (int rep = 0; rep < WJOBS; ++rep) store_dec<F32>(Ws2 + ((tid + GT * rep) % BM) * LD, dec2[rep]);
+    }
 #pragma unroll
     for (int jj = 0; jj < XV; ++jj) *reinterpret_cast<XD*>(Xs + (XR * jj + tid / (BK / XE)) * LD + xk) = xd[jj];
   };
 
   typename B::CR rawA[WJOBS], rawB[WJOBS];
   DecChunk<F32> dec[WJOBS];
+  // up tile of a gate/up pair (unused otherwise)
+  typename B::CR rawA2[WJOBS], rawB2[WJOBS];
+  DecChunk<F32> dec2[WJOBS];
   i32x4_t xraw[XV];
   XD xdec[XV];
 
   // prologue: step s0 into LDS, raw chunks of s0 + KG in flight
-  load_w(s0, rawA);
+  load_w(s0, rawA, wr);
+  if constexpr (DUAL) load_w(s0, rawA2, wr2);
   load_x(s0, xraw);
-  load_w(s0 + KG, rawB);
+  load_w(s0 + KG, rawB, wr);
+  if constexpr (DUAL) load_w(s0 + KG, rawB2, wr2);
   decode(s0, rawA, dec);
+  if constexpr (DUAL) decode(s0, rawA2, dec2);
 #pragma unroll
   for (int jj = 0; jj < XV; ++jj) xdec[jj] = cvt(xraw[jj]);
-  write_lds(dec, xdec);
+  write_lds(dec, dec2, xdec);
 #pragma unroll
   for (int rep = 0; rep < WJOBS; ++rep) rawA[rep] = rawB[rep];
+  if constexpr (DUAL) {
+#pragma unroll
+    for (int rep = 0; rep < WJOBS; ++rep) rawA2[rep] = rawB2[rep];
+  }
   __syncthreads();
 
   for (int it = 0; it < iters; ++it) {
     const int s = s0 + KG * it;
     load_x(s + KG, xraw);
-    load_w(s + 2 * KG, rawB);
+    load_w(s + 2 * KG, rawB, wr);
+    if constexpr (DUAL) load_w(s + 2 * KG, rawB2, wr2);
     decode(s + KG, rawA, dec);             // VALU under the MFMAs below
+    if constexpr (DUAL) decode(s + KG, rawA2, dec2);
     if constexpr (!F32) {
       // operands of k-slice kk+1 are read from LDS while the MFMAs of slice kk run
       const E* wsrc = Ws + (BM / WM * wm + (lane & 31)) * LD + 8 * (lane >> 5);
+      const E* wsrc2 = wsrc + BM * LD;     // the up tile's same row and slice (pairs only)
       const E* xsrc = Xs + (BN / WN * wn + (lane & 31)) * LD + 8 * (lane >> 5);
-      bf16x8_t av[2][TM], bv[2][TN];
+      bf16x8_t av[2][TM], bv[2][TN], av2[2][DUAL ? TM : 1];
 #pragma unroll
       for (int i = 0; i < TM; ++i) av[0][i] = *reinterpret_cast<const bf16x8_t*>(wsrc + 32 * i * LD);
+      if constexpr (DUAL) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i) av2[0][i] = *reinterpret_cast<const bf16x8_t*>(wsrc2 + 32 * i * LD);
+      }
 #pragma unroll
       for (int j = 0; j < TN; ++j) bv[0][j] = *reinterpret_cast<const bf16x8_t*>(xsrc + 32 * j * LD);
 #pragma unroll
@@ -321,6 +354,11 @@ __global__ __launch_bounds__(WM* WN * 64 * KG) void gemm_kernel(GemmArgs p) {
 #pragma unroll
           for (int i = 0; i < TM; ++i)
             av[nxt][i] = *reinterpret_cast<const bf16x8_t*>(wsrc + 32 * i * LD + 16 * (kk + 1));
+          if constexpr (DUAL) {
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+              av2[nxt][i] = *reinterpret_cast<const bf16x8_t*>(wsrc2 + 32 * i * LD + 16 * (kk + 1));
+          }
 #pragma unroll
           for (int j = 0; j < TN; ++j)
             bv[nxt][j] = *reinterpret_cast<const bf16x8_t*>(xsrc + 32 * j * LD + 16 * (kk + 1));
@@ -330,6 +368,13 @@ __global__ __launch_bounds__(WM* WN * 64 * KG) void gemm_kernel(GemmArgs p) {
 #pragma unroll
           for (int j = 0; j < TN; ++j)
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[cur][i], bv[cur][j], acc[i][j], 0, 0, 0);
+        if constexpr (DUAL) {
+#pragma unroll
+          for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+              acc2[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av2[cur][i], bv[cur][j], acc2[i][j], 0, 0, 0);
+        }
       }
     } else {
 #pragma unroll 8
@@ -349,10 +394,23 @@ __global__ __launch_bounds__(WM* WN * 64 * KG) void gemm_kernel(GemmArgs p) {
 #pragma unroll
     for (int jj = 0; jj < XV; ++jj) xdec[jj] = cvt(xraw[jj]);
     __syncthreads();                      // every wave is done reading step s
-    write_lds(dec, xdec);                 // step s + KG (zeros past the end)
+    write_lds(dec, dec2, xdec);           // step s + KG (zeros past the end)
     __syncthreads();
 #pragma unroll
     for (int rep = 0; rep < WJOBS; ++rep) rawA[rep] = rawB[rep];
+    if constexpr (DUAL) {
+#pragma unroll
+      for (int rep = 0; rep < WJOBS; ++rep) rawA2[rep] = rawB2[rep];
+    }
+  }
+  if constexpr (DUAL) {
+    // h = silu(gate) * up, elementwise on the finished accumulators
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = silu_mul(acc[i][j][r], acc2[i][j][r]);
   }
 
   if constexpr (KG > 1) {
@@ -407,6 +465,22 @@ __global__ __launch_bounds__(WM* WN * 64 * KG) void gemm_kernel(GemmArgs p) {
       for (int t = 0; t < 4; ++t) {
         const int xr = 8 * t + xr8;
         const float4 v = *reinterpret_cast<const float4*>(scr + xr * SROW + c4);
+        if constexpr (DUAL) {
+          if (xl0 + xr < rn) {
+            __bf16* hrow = reinterpret_cast<__bf16*>(p.Y) + (size_t)(r0 + xl0 + xr) * p.ldy;
+            const float vv[4] = {v.x, v.y, v.z, v.w};
+            if (wr + 3 < p.m) {
+              bf16x4_t o;
+              o[0] = (__bf16)v.x; o[1] = (__bf16)v.y; o[2] = (__bf16)v.z; o[3] = (__bf16)v.w;
+              *reinterpret_cast<bf16x4_t*>(hrow + wr) = o;
+            } else {
+#pragma unroll
+              for (int e = 0; e < 3; ++e)
+                if (wr + e < p.m) hrow[wr + e] = (__bf16)vv[e];
+            }
+          }
+          continue;
+        }
         if (xl0 + xr < rn) {
           float* yrow = Y + (size_t)(r0 + xl0 + xr) * p.ldy;
           if (wr + 3 < p.m) {
@@ -451,6 +525,16 @@ static hipError_t launch_shape(const GemmArgs& a, int ntasks, hipStream_t s) {
   constexpr int NT = WM * WN * 64 * KG;
   if constexpr (GROUPED) {
     if constexpr (!F32) {
+      if (a.W2) {
+        if constexpr (KG == 1) {
+          if (!a.x_bf16) return hipErrorInvalidValue;
+          hipLaunchKernelGGL((gemm_kernel<T, false, true, BM, BN, WM, WN, 1, true, true>), dim3((unsigned)ntasks),
+                             dim3(NT), 0, s, a);
+          return hipGetLastError();
+        } else {
+          return hipErrorInvalidValue;
+        }
+      }
       if (a.x_bf16) {
         hipLaunchKernelGGL((gemm_kernel<T, false, true, BM, BN, WM, WN, KG, true>), dim3((unsigned)ntasks), dim3(NT),
                            0, s, a);
@@ -476,7 +560,7 @@ static hipError_t launch_shape(const GemmArgs& a, int ntasks, hipStream_t s) {
 // 256x128 (KG 1) in bf16; grouped (MoE) 64x64 (KG 1/2) in both modes.
 template <int T, bool F32>
 static hipError_t launch_t(const GemmArgs& a, int ntasks, GemmTile tile, int kg, hipStream_t s) {
-  if (a.x_bf16 && (F32 || !a.tasks)) return hipErrorInvalidValue;   // bf16 X: grouped bf16 launches
+  if ((a.x_bf16 || a.W2) && (F32 || !a.tasks)) return hipErrorInvalidValue;   // grouped bf16 launches only
   if (a.tasks) {
     if (tile != GemmTile::k64x64) return hipErrorInvalidValue;
     if (kg == 1) return launch_shape<T, F32, 64, 64, 2, 2, 1, true>(a, ntasks, s);

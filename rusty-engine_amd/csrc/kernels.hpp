@@ -103,6 +103,8 @@ struct GemmArgs {
   const void* X;           // activations, row-major, K floats per row (K bf16 when x_bf16)
   uint32_t x_bytes;        // bytes readable from X; < 2 GiB
   int x_bf16;              // grouped bf16-mode launch: X already rounded to bf16
+  const uint8_t* W2;       // grouped bf16 launch with bf16 X: up weights beside W (gate), same geometry;
+                           // the tile writes silu(gate) * up as bf16 (ldy elements per row)
   float* Y;                // output, row stride ldy
   int m, K, KB, tiles;     // weight geometry (per expert)
   int N;                   // activation rows (dense launch)

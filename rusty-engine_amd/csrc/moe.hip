@@ -8,10 +8,6 @@
 
 namespace rehip {
 
-__device__ __forceinline__ float silu_mul(float x, float u) {
-  const float sig = __frcp_rn(__fadd_rn(1.0f, expf(-x)));
-  return __fmul_rn(__fmul_rn(x, sig), u);
-}
 
 // h = silu(g) * u, silu(x) = x * (1 / (1 + exp(-x)))  (moe.rs:44-51, 280-283)
 __global__ __launch_bounds__(256) void swiglu_kernel(const float* __restrict__ g, const float* __restrict__ u,
