@@ -147,6 +147,27 @@ def test_forward_routed_skips_out_of_range_ids():
     moe.close()
 
 
+@pytest.mark.parametrize("T,E,k", [(1, 32, 4), (5, 32, 8), (40, 16, 4), (129, 32, 8), (300, 64, 4)])
+@pytest.mark.parametrize("gate", [rehip.GATE_SOFTMAX, rehip.GATE_SIGMOID])
+def test_moe_layer_equals_route_then_forward(T, E, k, gate):
+    """The layer entry point equals router logits -> route -> forward_routed run as separate
+    calls, bit for bit."""
+    hidden, inter = 512, 256
+    gate_b, up, down_, x, _ = moe_case(5000 + T + E + gate, E, hidden, inter, T, k)
+    rw = (np.random.default_rng(5100 + T).standard_normal((E, hidden)) / np.sqrt(hidden)).astype(np.float32)
+    moe = rehip.MoeExperts(rehip.Q4_K, gate_b, rehip.Q4_K, up, rehip.Q6_K, down_, E, hidden, inter)
+    xd, rwd = B.from_array(x), B.from_array(rw)
+    logits, ids, w = B(T * E * 4), B(T * k * 4), B(T * k * 4)
+    for mode in (rehip.MODE_F32, rehip.MODE_BF16):
+        a, b = B(T * hidden * 4), B(T * hidden * 4)
+        moe.layer_dev(xd, T, rwd, k, gate, a, mode)
+        rehip.moe_router_logits_dev(xd, rwd, T, hidden, E, logits)
+        rehip.moe_route_dev(logits, T, E, k, gate, ids, w)
+        moe.forward_routed_dev(xd, T, k, ids, w, b, mode)
+        assert np.array_equal(down(a, T * hidden), down(b, T * hidden)), mode
+    moe.close()
+
+
 @pytest.mark.parametrize("T", [1, 32])
 @pytest.mark.parametrize("gate", [rehip.GATE_SOFTMAX, rehip.GATE_SIGMOID])
 def test_moe_layer_qwen3_shape(T, gate):
