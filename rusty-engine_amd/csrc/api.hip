@@ -170,6 +170,15 @@ size_t env_size(const char* name, size_t dflt) {
 
 bool aligned16(const void* p);
 
+}  // namespace
+
+int rehip::moe_gemv_rows_down() {
+  const size_t r = env_size("REHIP_MOE_DROWS", 0);
+  return r == 32 || r == 64 ? (int)r : 64;   // down (K = inter, short rows): 64 measured faster
+}
+
+namespace {
+
 // bf16 mode of the grouped MoE GEMMs: the activation rows are rounded to bf16 once and SwiGLU
 // writes h as bf16 -- the rounding each GEMM tile would apply while staging them -- so the
 // tiles stage half the bytes and convert nothing (identical results). REHIP_MOE_XB=0 turns it off.
@@ -874,11 +883,13 @@ int re_moe_forward_routed_dev(re_moe* e, const float* d_x, size_t tokens, size_t
   sh.gemv = gemv;
   sh.chunk = gemv ? (tokens == 1 ? 1 : kMoeGemvBatch) : kMoeTile;
   if (gemv) {
+    const int rd = moe_gemv_rows_down();
     sh.rows_gu = kMoeGemvRows;
+    sh.rows_d = rd;
     sh.tiles_gu = (int)((e->inter + kMoeGemvRows - 1) / kMoeGemvRows);
-    sh.tiles_d = (int)((e->hidden + kMoeGemvRows - 1) / kMoeGemvRows);
+    sh.tiles_d = (int)((e->hidden + rd - 1) / rd);
   } else {
-    sh.rows_gu = kMoeTile;
+    sh.rows_gu = sh.rows_d = kMoeTile;
     sh.tiles_gu = (int)((e->inter + kMoeTile - 1) / kMoeTile);
     sh.tiles_d = (int)((e->hidden + kMoeTile - 1) / kMoeTile);
   }
@@ -929,7 +940,7 @@ int re_moe_forward_routed_dev(re_moe* e, const float* d_x, size_t tokens, size_t
       HIP_TRY(launch_swiglu((const float*)e->sg.p, (const float*)e->su.p, (float*)e->sh.p, pairs * e->inter, s));
     }
     MoeGemvArgs d{};
-    d.rows_per_task = kMoeGemvRows;
+    d.rows_per_task = moe_gemv_rows_down();
     d.max_rows = sh.chunk;
     d.W0 = e->d_down;
     d.w_stride = e->gd.bytes;
@@ -1073,7 +1084,8 @@ int re_moe_forward_dev(re_moe* e, const float* d_x, size_t tokens, size_t top_k,
       for (int r = 0; r < count[x]; r += kMoeGemvBatch) {
         const int np = std::min(kMoeGemvBatch, count[x] - r);
         for (size_t row = 0; row < e->inter; row += kMoeGemvRows) v_gu.push_back({(int)x, (int)row, start[x] + r, np});
-        for (size_t row = 0; row < e->hidden; row += kMoeGemvRows) v_d.push_back({(int)x, (int)row, start[x] + r, np});
+        for (size_t row = 0; row < e->hidden; row += (size_t)moe_gemv_rows_down())
+          v_d.push_back({(int)x, (int)row, start[x] + r, np});
       }
   } else {
     const int mt_gu = (int)((e->inter + kMoeTile - 1) / kMoeTile), mt_d = (int)((e->hidden + kMoeTile - 1) / kMoeTile);
@@ -1154,7 +1166,7 @@ int re_moe_forward_dev(re_moe* e, const float* d_x, size_t tokens, size_t top_k,
       HIP_TRY(launch_swiglu((const float*)e->sg.p, (const float*)e->su.p, (float*)e->sh.p, pairs * e->inter, s));
     }
     MoeGemvArgs d{};
-    d.rows_per_task = kMoeGemvRows;
+    d.rows_per_task = moe_gemv_rows_down();
     d.max_rows = max_rows;
     d.W0 = e->d_down;
     d.w_stride = e->gd.bytes;

@@ -158,6 +158,9 @@ struct MoeGemvArgs {
 // weight rows per expert task: with 16, staging the task's activation rows costs as many bytes
 // as its weights; 64 leaves too few tasks
 constexpr int kMoeGemvRows = 32;
+// weight rows per down-projection GEMV task: 64 (its rows are short, K = inter), or
+// REHIP_MOE_DROWS = 32 / 64
+int moe_gemv_rows_down();
 // weight rows per task of the one-row gate/up pair (re_ffn): more, smaller tasks suit decode
 constexpr int kFfnGemvRows = 16;
 constexpr int kMoeGemvWaves = 4;
@@ -209,7 +212,7 @@ constexpr int kMoeMaxDevicePairs = 8192;
 struct MoePlanShape {
   int pairs, k, n_experts, chunk, gemv;
   int tiles_gu, tiles_d;        // weight-row tasks per chunk (ceil(inter/rows), ceil(hidden/rows))
-  int rows_gu;                  // weight rows per task (16 for GEMV tasks; GEMM tasks name a tile)
+  int rows_gu, rows_d;          // weight rows per GEMV task (gate/up, down); GEMM tasks name a tile
   int max_gu, max_d;            // capacity of the task lists
 };
 size_t moe_meta_bytes(const MoePlanShape& sh);

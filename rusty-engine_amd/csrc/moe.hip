@@ -237,7 +237,7 @@ __global__ __launch_bounds__(1024) void moe_plan_kernel(const int* __restrict__ 
       MoeGemvTask* tg = (MoeGemvTask*)tasks;
       MoeGemvTask* td = tg + sh.max_gu;
       for (int j = 0, t = c * sh.tiles_gu; j < sh.tiles_gu && t < n_gu; ++j, ++t) tg[t] = {e, j * sh.rows_gu, r0, rn};
-      for (int j = 0, t = c * sh.tiles_d; j < sh.tiles_d && t < n_d; ++j, ++t) td[t] = {e, j * sh.rows_gu, r0, rn};
+      for (int j = 0, t = c * sh.tiles_d; j < sh.tiles_d && t < n_d; ++j, ++t) td[t] = {e, j * sh.rows_d, r0, rn};
     } else {
       GemmTask* tg = (GemmTask*)tasks;
       GemmTask* td = tg + sh.max_gu;
@@ -536,6 +536,13 @@ static hipError_t launch_moe_gemv_t(const MoeGemvArgs& a, int ntasks, hipStream_
   if (a.rows_per_task == kFfnGemvRows) {
     if constexpr (DUAL) {
       if (a.max_rows <= 1) return launch_moe_gemv_nb<T, true, 1, kFfnGemvRows>(a, ntasks, s);
+    }
+    return hipErrorInvalidValue;
+  }
+  if (a.rows_per_task == 64) {
+    if constexpr (!DUAL) {
+      return a.max_rows <= 1 ? launch_moe_gemv_nb<T, false, 1, 64>(a, ntasks, s)
+                             : launch_moe_gemv_nb<T, false, kMoeGemvBatch, 64>(a, ntasks, s);
     }
     return hipErrorInvalidValue;
   }
