@@ -71,8 +71,9 @@ def moe_case(seed, E, hidden, inter, T, k, gt=rehip.Q4_K, dt=rehip.Q6_K):
                                          (200, 8, 2, rehip.Q8_0, rehip.Q5_0)])
 def test_grouped_gemm_bf16_activations_bit_identical(T, E, k, gt, dt, monkeypatch):
     """bf16 mode of the grouped expert GEMMs: activation rows rounded to bf16 up front and h
-    written as bf16 by SwiGLU (REHIP_MOE_XB=1, the default) give the same bits as rounding each
-    tile while staging it (0), host- and device-routed."""
+    written as bf16 by SwiGLU (REHIP_MOE_XB=1, the default), with gate and up as two launches
+    or as one fused launch (REHIP_MOE_PAIR), give the same bits as rounding each tile while
+    staging it (REHIP_MOE_XB=0), host- and device-routed."""
     hidden, inter = 512, 256
     gate, up, down_, x, logits = moe_case(950 + T + E, E, hidden, inter, T, k, gt, dt)
     ids = np.zeros((T, k), np.int32)
@@ -83,14 +84,18 @@ def test_grouped_gemm_bf16_activations_bit_identical(T, E, k, gt, dt, monkeypatc
     xd = B.from_array(x)
     idd, wd = B.from_array(ids.reshape(-1)), B.from_array(wts.reshape(-1))
     res = {}
-    for xb in ("0", "1"):
+    # f32 rows staged per tile; bf16 rows with gate and up apart; bf16 rows with the fused pair
+    for xb, pair in (("0", "0"), ("1", "0"), ("1", "1")):
         monkeypatch.setenv("REHIP_MOE_XB", xb)
+        monkeypatch.setenv("REHIP_MOE_PAIR", pair)
         out = B(T * hidden * 4)
         moe.forward_routed_dev(xd, T, k, idd, wd, out, rehip.MODE_BF16)
-        res[xb] = (down(out, T * hidden),
-                   moe.forward(x, T, k, ids.reshape(-1).astype(np.uint32), wts.reshape(-1), rehip.MODE_BF16))
-    assert np.array_equal(res["0"][0], res["1"][0])
-    assert np.array_equal(res["0"][1], res["1"][1])
+        res[xb + pair] = (down(out, T * hidden),
+                          moe.forward(x, T, k, ids.reshape(-1).astype(np.uint32), wts.reshape(-1), rehip.MODE_BF16))
+    for key in ("10", "11"):
+        assert np.array_equal(res["00"][0], res[key][0]), key
+        assert np.array_equal(res["00"][1], res[key][1]), key
+    res["1"] = res["11"]
     want = O.moe_ffn(gt, gate, gt, up, dt, down_, E, hidden, inter, x, T, k,
                      ids.reshape(-1).astype(np.uint32), wts.reshape(-1))
     assert np.linalg.norm(res["1"][1] - want) / np.linalg.norm(want) <= 1e-2
