@@ -172,6 +172,13 @@ bool aligned16(const void* p);
 
 }  // namespace
 
+// weight rows per gate/up task of a one-token call (gate and up of one type): 16, twice the
+// workgroups of 32 for the few experts one token hits (REHIP_MOE_GUROWS1 = 16 / 32)
+static int moe_gemv_rows_gu1() {
+  const size_t r = env_size("REHIP_MOE_GUROWS1", 0);
+  return r == 16 || r == 32 ? (int)r : kFfnGemvRows;
+}
+
 int rehip::moe_gemv_rows_down() {
   const size_t r = env_size("REHIP_MOE_DROWS", 0);
   return r == 32 || r == 64 ? (int)r : 64;   // down (K = inter, short rows): 64 measured faster
@@ -884,9 +891,10 @@ int re_moe_forward_routed_dev(re_moe* e, const float* d_x, size_t tokens, size_t
   sh.chunk = gemv ? (tokens == 1 ? 1 : kMoeGemvBatch) : kMoeTile;
   if (gemv) {
     const int rd = moe_gemv_rows_down();
-    sh.rows_gu = kMoeGemvRows;
+    const int rgu = tokens == 1 && e->gg.type == e->gu.type ? moe_gemv_rows_gu1() : kMoeGemvRows;
+    sh.rows_gu = rgu;
     sh.rows_d = rd;
-    sh.tiles_gu = (int)((e->inter + kMoeGemvRows - 1) / kMoeGemvRows);
+    sh.tiles_gu = (int)((e->inter + rgu - 1) / rgu);
     sh.tiles_d = (int)((e->hidden + rd - 1) / rd);
   } else {
     sh.rows_gu = sh.rows_d = kMoeTile;
@@ -912,7 +920,7 @@ int re_moe_forward_routed_dev(re_moe* e, const float* d_x, size_t tokens, size_t
   if (gemv) {
     const MoeGemvTask* tg = (const MoeGemvTask*)tasks;
     MoeGemvArgs g{};
-    g.rows_per_task = kMoeGemvRows;
+    g.rows_per_task = sh.rows_gu;
     g.max_rows = sh.chunk;
     g.X = d_x;
     g.xrow = xrow;
@@ -1077,13 +1085,14 @@ int re_moe_forward_dev(re_moe* e, const float* d_x, size_t tokens, size_t top_k,
   // Few rows per expert (decode-sized batches): grouped GEMV tasks that read each weight once
   // per kMoeGemvBatch rows. Otherwise MFMA tiles of kMoeTile gathered rows.
   const bool gemv = pairs <= (size_t)kMoeGemvBatch * touched;
+  const int rgu = tokens == 1 && e->gg.type == e->gu.type ? moe_gemv_rows_gu1() : kMoeGemvRows;
   std::vector<MoeGemvTask> v_gu, v_d;
   std::vector<GemmTask> t_gu, t_d;
   if (gemv) {
     for (size_t x = 0; x < e->n_experts; ++x)
       for (int r = 0; r < count[x]; r += kMoeGemvBatch) {
         const int np = std::min(kMoeGemvBatch, count[x] - r);
-        for (size_t row = 0; row < e->inter; row += kMoeGemvRows) v_gu.push_back({(int)x, (int)row, start[x] + r, np});
+        for (size_t row = 0; row < e->inter; row += (size_t)rgu) v_gu.push_back({(int)x, (int)row, start[x] + r, np});
         for (size_t row = 0; row < e->hidden; row += (size_t)moe_gemv_rows_down())
           v_d.push_back({(int)x, (int)row, start[x] + r, np});
       }
@@ -1139,7 +1148,7 @@ int re_moe_forward_dev(re_moe* e, const float* d_x, size_t tokens, size_t top_k,
     int max_rows = 0;
     for (size_t x = 0; x < e->n_experts; ++x) max_rows = std::max(max_rows, std::min(count[x], kMoeGemvBatch));
     MoeGemvArgs g{};
-    g.rows_per_task = kMoeGemvRows;
+    g.rows_per_task = rgu;
     g.max_rows = max_rows;
     g.X = d_x;
     g.xrow = (const int*)dm;
