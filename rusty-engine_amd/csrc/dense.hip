@@ -83,11 +83,16 @@ hipError_t launch_dense_t(const void* W, const float* x, float* y, int m, int n,
                           hipStream_t s) {
   using S = typename DenseElem<T>::S;
   const unsigned gx = (unsigned)((m + 3) / 4);
+  // 1, 4 or 16 activation rows per workgroup: W is read once per row group, and every output keeps
+  // the same per-lane order and fold whatever the group
   if (rows == 1)
     hipLaunchKernelGGL((dense_gemm_kernel<T, 1>), dim3(gx, 1u), dim3(256), 0, s, (const S*)W, x, y, m, n, rows, add);
-  else
+  else if (rows < 16)
     hipLaunchKernelGGL((dense_gemm_kernel<T, 4>), dim3(gx, (unsigned)((rows + 3) / 4)), dim3(256), 0, s, (const S*)W,
                        x, y, m, n, rows, add);
+  else
+    hipLaunchKernelGGL((dense_gemm_kernel<T, 16>), dim3(gx, (unsigned)((rows + 15) / 16)), dim3(256), 0, s,
+                       (const S*)W, x, y, m, n, rows, add);
   return hipGetLastError();
 }
 

@@ -77,8 +77,10 @@ def test_dense_matvec_matmul(t, m, n):
         for mode in (rehip.MODE_F32, rehip.MODE_BF16):     # f32 products in either mode
             y = q.matmul(xs, rows, mode)
             _check_product(y, t, raw, m, n, xs, rows)
-        # a row's output does not depend on the rows beside it
+        # a row's output does not depend on the rows beside it, nor on the row-group size
+        # (1, 4 or 16 rows per workgroup)
         assert np.array_equal(q.matmul(xs[:1], 1, rehip.MODE_F32), q.matvec(xs[0]))
+        assert np.array_equal(q.matmul(xs[:2], 2, rehip.MODE_F32), q.matmul(xs, rows, rehip.MODE_F32)[:2 * m])
     q.close()
 
 
