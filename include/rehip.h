@@ -156,6 +156,16 @@ typedef struct re_ffn re_ffn;
  * the launch shape is planned for the whole stack. */
 int re_qmat_matvec_stacked_dev(re_qmat *q, size_t first, size_t count, const float *d_x, size_t x_stride,
                                float *d_y, size_t y_stride, void *stream);
+/* Launch shape the GEMV of re_qmat_matvec_dev (count = 1) or of a re_qmat_matvec_stacked_dev call
+ * over `count` matrices would use, for tests and profiles (no counterpart in the reference, whose
+ * GEMV has one shape): kernel RE_GEMV_TILE (one 64-row tile per workgroup), RE_GEMV_ROWS (row
+ * groups of 4/8/16 rows), RE_GEMV_SPLIT (rows split over workgroups + a reduce) or RE_GEMV_DENSE
+ * (F32/F16/BF16 weights); waves per workgroup; half = 1 when super-blocks stream half blocks. */
+#define RE_GEMV_SPLIT 0
+#define RE_GEMV_ROWS 1
+#define RE_GEMV_TILE 2
+#define RE_GEMV_DENSE 3
+int re_qmat_gemv_plan(const re_qmat *q, size_t count, int *kernel, int *rows_per_group, int *waves, int *half);
 int re_qmat_matvec_ex_dev(re_qmat *q, const float *d_x, const float *d_norm_w, float eps, const float *d_add,
                           float *d_y, unsigned long long *d_best, void *stream);
 /* out[r] = x[r] * (1 / sqrt(mean(x[r]^2) + eps)) * w for rows x d (infer.rs:72-82). */

@@ -194,6 +194,18 @@ bool moe_bf16_acts(const re_moe* e, const float* d_x, int mode) {
          env_size("REHIP_MOE_XB", 1) != 0;
 }
 
+// The grouped expert GEMV stages each task's activation rows (kMoeGemvBatch rows of K floats
+// plus their per-16 sums) and the wave partials in LDS; when a projection's rows are too long for
+// that, the grouped GEMM tasks (fixed LDS per tile) serve every batch size.
+bool moe_gemv_fits(const re_moe* e) {
+  auto lds = [](size_t kp) {
+    return (kMoeGemvBatch * kp * 17 / 16 + (size_t)kMoeGemvWaves * 2 * kMoeGemvBatch * 64 +
+            (size_t)kMoeGemvWaves * kMoeGemvBatch) * sizeof(float);
+  };
+  return lds(e->gg.kb * e->gg.qk) <= kMaxLdsBytes && lds(e->gu.kb * e->gu.qk) <= kMaxLdsBytes &&
+         lds(e->gd.kb * e->gd.qk) <= kMaxLdsBytes;
+}
+
 // GEMV launch shape. Work units are 32-quant chunks (KB * chunks-per-block per row).
 // Rows up to kGemvRowsMaxK long use the row-group kernel: the rows per workgroup are the largest
 // of 64/16/8/4 that still give >= 512 workgroups (two per CU), and the waves per workgroup are
@@ -607,6 +619,36 @@ int re_qmat_matvec_stacked_dev(re_qmat* q, size_t first, size_t count, const flo
   return RE_OK;
 }
 
+int re_qmat_gemv_plan(const re_qmat* q, size_t count, int* kernel, int* rows_per_group, int* waves, int* half) {
+  if (!q || !kernel || !rows_per_group || !waves || !half) return fail(RE_ERR_ARG, "null pointer");
+  if (count == 0 || count > q->count) return fail(RE_ERR_SIZE, "%zu matrices of a stack of %zu", count, q->count);
+  *half = 0;
+  if (q->dense) {
+    *kernel = RE_GEMV_DENSE;
+    *rows_per_group = 1;
+    *waves = 1;
+    return RE_OK;
+  }
+  if (!q->rows_per_group) {
+    *kernel = RE_GEMV_SPLIT;
+    *rows_per_group = 64;
+    *waves = gemv_rows_waves(q->waves);
+    return RE_OK;
+  }
+  int r = q->rows_per_group, w = q->waves;
+  if (count > 1) rows_shape(q->g.tiles * count, q->g.kb * (q->g.qk == 256 ? 8 : 1), q->g.qk == 256 ? 8 : 1, &r, &w);
+  *rows_per_group = r;
+  if (r == 64) {
+    *kernel = RE_GEMV_TILE;
+    *waves = gemv_tile_waves(w);
+    *half = gemv_tile_half(q->g.qk, (int)q->g.kb, *waves) ? 1 : 0;
+  } else {
+    *kernel = RE_GEMV_ROWS;
+    *waves = gemv_rows_waves(w);
+  }
+  return RE_OK;
+}
+
 int re_qmat_matvec_ex_dev(re_qmat* q, const float* d_x, const float* d_norm_w, float eps, const float* d_add,
                           float* d_y, unsigned long long* d_best, void* stream) {
   if (!q || !d_x || !d_y) return fail(RE_ERR_ARG, "null pointer");
@@ -877,12 +919,13 @@ int re_moe_forward_routed_dev(re_moe* e, const float* d_x, size_t tokens, size_t
     return fail(RE_ERR_SIZE, "device routing takes <= %d (token, expert) pairs and <= 1024 experts",
                 kMoeMaxDevicePairs);
   if (tokens * e->hidden * sizeof(float) >= (1ull << 31) || e->gg.bytes * e->n_experts >= (1ull << 31) ||
-      e->gd.bytes * e->n_experts >= (1ull << 31) || pairs * e->inter * sizeof(float) >= (1ull << 31))
+      e->gu.bytes * e->n_experts >= (1ull << 31) || e->gd.bytes * e->n_experts >= (1ull << 31) ||
+      pairs * e->inter * sizeof(float) >= (1ull << 31))
     return fail(RE_ERR_SIZE, "MoE operands must stay below 2 GiB");
   hipStream_t s = (hipStream_t)stream;
   // the grouping runs on the device, so the path is chosen from the batch size alone: the
   // grouped GEMV while an expert would get few rows on average (pairs <= 2 x experts)
-  const bool gemv = pairs <= 2 * e->n_experts;
+  const bool gemv = pairs <= 2 * e->n_experts && moe_gemv_fits(e);
   MoePlanShape sh{};
   sh.pairs = (int)pairs;
   sh.k = (int)top_k;
@@ -1079,13 +1122,17 @@ int re_moe_forward_dev(re_moe* e, const float* d_x, size_t tokens, size_t top_k,
     pos[p] = at;
   }
   if (tokens * e->hidden * sizeof(float) >= (1ull << 31) || e->gg.bytes * e->n_experts >= (1ull << 31) ||
-      e->gd.bytes * e->n_experts >= (1ull << 31) || pairs * e->inter * sizeof(float) >= (1ull << 31))
+      e->gu.bytes * e->n_experts >= (1ull << 31) || e->gd.bytes * e->n_experts >= (1ull << 31) ||
+      pairs * e->inter * sizeof(float) >= (1ull << 31))
     return fail(RE_ERR_SIZE, "MoE operands must stay below 2 GiB");
 
   // Few rows per expert (decode-sized batches): grouped GEMV tasks that read each weight once
   // per kMoeGemvBatch rows. Otherwise MFMA tiles of kMoeTile gathered rows.
-  const bool gemv = pairs <= (size_t)kMoeGemvBatch * touched;
-  const int rgu = tokens == 1 && e->gg.type == e->gu.type ? moe_gemv_rows_gu1() : kMoeGemvRows;
+  const bool gemv = pairs <= (size_t)kMoeGemvBatch * touched && moe_gemv_fits(e);
+  int max_rows = 0;
+  for (size_t x = 0; x < e->n_experts; ++x) max_rows = std::max(max_rows, std::min(count[x], kMoeGemvBatch));
+  // 16-row gate/up tasks exist for single-row tasks only (a repeated expert id gives 2+ rows)
+  const int rgu = tokens == 1 && max_rows <= 1 && e->gg.type == e->gu.type ? moe_gemv_rows_gu1() : kMoeGemvRows;
   std::vector<MoeGemvTask> v_gu, v_d;
   std::vector<GemmTask> t_gu, t_d;
   if (gemv) {
@@ -1145,8 +1192,6 @@ int re_moe_forward_dev(re_moe* e, const float* d_x, size_t tokens, size_t top_k,
   e->meta_pending = true;
 
   if (gemv) {
-    int max_rows = 0;
-    for (size_t x = 0; x < e->n_experts; ++x) max_rows = std::max(max_rows, std::min(count[x], kMoeGemvBatch));
     MoeGemvArgs g{};
     g.rows_per_task = rgu;
     g.max_rows = max_rows;

@@ -485,11 +485,11 @@ static hipError_t launch_tile(const GemvArgs& a, int waves, hipStream_t s) {
   constexpr int SQ = G * Blk<T>::QK;
   const size_t nx = (size_t)((a.KB + G - 1) / G) * SQ;
   const unsigned grid = (unsigned)(((size_t)a.tiles * (a.batch > 1 ? a.batch : 1) + 7) / 8 * 8);
-  const int w = waves >= 8 ? 8 : waves <= 2 ? 2 : 4;
+  const int w = gemv_tile_waves(waves);
   const size_t lds = (nx + nx / 16 + (size_t)w * 64 + w) * sizeof(float);
   // super-blocks: half-block pipelining pays once a wave has two or more blocks to stream;
   // with one block per wave the whole block is loaded before x is staged
-  const bool half = Blk<T>::NCH == 8 && a.KB >= 2 * w;
+  const bool half = gemv_tile_half(Blk<T>::QK, a.KB, w);
   if (w == 8) {
     if (half) hipLaunchKernelGGL((gemv_tile_kernel<T, 8, true>), dim3(grid), dim3(512), lds, s, a);
     else hipLaunchKernelGGL((gemv_tile_kernel<T, 8, false>), dim3(grid), dim3(512), lds, s, a);

@@ -56,9 +56,19 @@ __device__ __forceinline__ unsigned long long argmax_key(float v, int i) {
   return ((unsigned long long)b << 32) | (unsigned)i;
 }
 
+// LDS one workgroup may use on gfx950 (160 KiB per CU)
+constexpr size_t kMaxLdsBytes = 160u * 1024u;
+
 // longest row (elements) a GEMV workgroup stages in LDS: x, its per-16 sums and the wave
 // partials stay under 64 KiB of dynamic LDS
 constexpr int kGemvRowsMaxK = 12288;
+
+// Effective shape of a GEMV launch. The tile kernel (64 rows per workgroup) runs 2, 4 or 8
+// waves; super-block types stream half blocks once each wave has two or more blocks. The
+// row-group kernels run 4, 8 or 16 waves.
+inline int gemv_tile_waves(int waves) { return waves >= 8 ? 8 : waves <= 2 ? 2 : 4; }
+inline bool gemv_tile_half(int qk, int kb, int tile_waves) { return qk == 256 && kb >= 2 * tile_waves; }
+inline int gemv_rows_waves(int waves) { return waves == 16 ? 16 : waves == 8 ? 8 : 4; }
 
 // waves per workgroup: 4, 8 or 16
 hipError_t launch_gemv(uint32_t type, const GemvArgs& a, int waves, hipStream_t s);

@@ -51,7 +51,8 @@ EXPORTS = ("re_init", "re_last_error", "re_version", "re_row_bytes", "re_tiled_b
            "re_gguf_get_float", "re_gguf_get_str", "re_gguf_get_array", "re_gguf_tensor_info",
            "re_gguf_find_tensor", "re_gguf_tensor_data", "re_qmat_from_gguf", "re_moe_from_gguf",
            "re_quantize_q8_act", "re_quantize_q8_act_dev", "re_qmat_matmul_i8", "re_qmat_matmul_i8_dev",
-           "re_attention_decode_dev")
+           "re_attention_decode_dev", "re_qmat_gemv_plan")
+GEMV_KERNELS = {0: "split", 1: "rows", 2: "tile", 3: "dense"}
 
 
 class RehipError(RuntimeError):
@@ -150,6 +151,7 @@ def lib() -> C.CDLL:
         L.re_qmat_matmul_i8.argtypes = [_vp, _vp, _vp, _sz, _vp]
         L.re_qmat_matmul_i8_dev.argtypes = [_vp, _vp, _vp, _sz, _vp, _vp]
         L.re_moe_from_gguf.argtypes = [_vp, C.c_char_p, C.c_char_p, C.c_char_p, _sz, _sz, _sz, C.POINTER(_vp)]
+        L.re_qmat_gemv_plan.argtypes = [_vp, _sz] + [C.POINTER(C.c_int)] * 4
         _lib = L
     return _lib
 
@@ -266,6 +268,14 @@ class QMat:
         """y_b = W_b x_b for matrices first .. first + count - 1, one launch (strides in floats)."""
         _check(lib().re_qmat_matvec_stacked_dev(self._h, first, count, _dev_ptr(x_dev), x_stride, _dev_ptr(y_dev),
                                                 y_stride, _stream_ptr(stream)))
+
+    def gemv_plan(self, count: int = 1) -> dict:
+        """Launch shape of the GEMV over `count` matrices of the stack (re_qmat_gemv_plan): kernel
+        ("tile", "rows", "split" or "dense"), rows per workgroup, waves, half-block streaming."""
+        v = [C.c_int() for _ in range(4)]
+        _check(lib().re_qmat_gemv_plan(self._h, count, *[C.byref(x) for x in v]))
+        return {"kernel": GEMV_KERNELS[v[0].value], "rows_per_group": v[1].value, "waves": v[2].value,
+                "half": bool(v[3].value)}
 
     def rows(self) -> int:
         return lib().re_qmat_rows(self._h)

@@ -25,7 +25,7 @@ both backends share this host code, so a greedy comparison between them isolates
 """
 from __future__ import annotations
 
-from dataclasses import dataclass
+from dataclasses import dataclass, field
 
 import numpy as np
 
@@ -169,6 +169,9 @@ def argmax_last(logits: np.ndarray) -> int:
 # ---- weights ------------------------------------------------------------------------------
 @dataclass
 class BlockBytes:
+    """One block's tensors: projection bytes (GGUF blocks, or F32/F16/BF16 elements) and f32 norm
+    and bias vectors. `types` names the ggml type of a projection whose type differs from the
+    model-wide one (a real Q4_K_M file mixes types per tensor)."""
     q: np.ndarray
     k: np.ndarray
     v: np.ndarray
@@ -181,6 +184,7 @@ class BlockBytes:
     q_bias: np.ndarray
     k_bias: np.ndarray
     v_bias: np.ndarray
+    types: dict = field(default_factory=dict)
 
 
 @dataclass
@@ -195,6 +199,8 @@ class ModelBytes:
     ffn_type: int = Q4_K
     down_type: int = Q6_K
     embed_type: int = Q8_0
+    output_type: int | None = None     # None: the embedding's type
+    eos_token_id: int | None = None
 
 
 # standard deviation of one block's (scale-free) value, d = 1: Q4_K sc*q - 7.5*m with sc, m
@@ -249,17 +255,95 @@ def synth_model(seed: int, geom: Geometry = QWEN25_05B, n_layers: int = QWEN25_0
     return ModelBytes(geom, n_vocab, embed, output, output_norm, blocks)
 
 
+def _f32_vector(g, name: str) -> np.ndarray:
+    """An F32 / F16 / BF16 vector tensor widened to f32 (norm weights and biases)."""
+    t = g.tensor(name)
+    raw = np.asarray(g.tensor_bytes(name))
+    if t.ggml_type == 0:
+        return raw.view(np.float32).copy()
+    if t.ggml_type == 1:
+        return raw.view(np.float16).astype(np.float32)
+    if t.ggml_type == 30:
+        return (raw.view(np.uint16).astype(np.uint32) << 16).view(np.float32)
+    raise ValueError(f"tensor '{name}' of ggml type {t.ggml_type} is not a float vector")
+
+
+def model_from_gguf(g) -> ModelBytes:
+    """A dense model from a GGUF file (rehip.Gguf) as DenseRunner::from_model loads it
+    (runner.rs:46-101, model.rs:122-240): hyper-parameters under `<arch>.` or `general.` keys
+    (head_count_kv defaults to head_count, vocab_size to the tokenizer's token count, rope base
+    to 10000, RMS eps to 1e-5); per block attn_norm, attn_q/k/v/output, ffn_norm, ffn_gate/up/down
+    and the optional attn_q/k/v biases (absent = zero); output_norm (or norm), output. Projection
+    bytes are views of the mapping, typed per tensor."""
+    arch = g.get("general.architecture")
+    if not isinstance(arch, str):
+        raise ValueError("missing general.architecture")
+
+    def key(suffix, dflt=None, required=False):
+        for k in (f"{arch}.{suffix}", f"general.{suffix}"):
+            v = g.get(k)
+            if v is not None:
+                return v
+        if required:
+            raise ValueError(f"missing required key '{arch}.{suffix}'")
+        return dflt
+
+    n_heads = int(key("attention.head_count", required=True))
+    d_model = int(key("embedding_length", required=True))
+    n_layers = int(key("block_count", required=True))
+    d_ff = key("feed_forward_length")
+    if d_ff is None:
+        d_ff = key("expert_feed_forward_length", required=True)
+    n_kv = int(key("attention.head_count_kv", n_heads))
+    tokens = g.get("tokenizer.ggml.tokens")
+    n_vocab = int(key("vocab_size", tokens[2] if isinstance(tokens, tuple) else 0))
+    geom = Geometry(d_model=d_model, n_heads=n_heads, n_kv_heads=n_kv, d_ff=int(d_ff),
+                    rope_freq_base=float(key("rope.freq_base", 10000.0)),
+                    rms_eps=float(key("attention.layer_norm_rms_epsilon", 1e-5)))
+    kv = n_kv * geom.head_dim
+
+    def bias(name, n):
+        try:
+            g.tensor(name)
+        except Exception:
+            return np.zeros(n, np.float32)
+        return _f32_vector(g, name)
+
+    names = {"q": "attn_q", "k": "attn_k", "v": "attn_v", "o": "attn_output", "gate": "ffn_gate",
+             "up": "ffn_up", "down": "ffn_down"}
+    blocks = []
+    for i in range(n_layers):
+        p = f"blk.{i}."
+        proj = {f: np.asarray(g.tensor_bytes(p + t + ".weight")) for f, t in names.items()}
+        types = {f: g.tensor(p + t + ".weight").ggml_type for f, t in names.items()}
+        blocks.append(BlockBytes(attn_norm=_f32_vector(g, p + "attn_norm.weight"),
+                                 ffn_norm=_f32_vector(g, p + "ffn_norm.weight"),
+                                 q_bias=bias(p + "attn_q.bias", d_model), k_bias=bias(p + "attn_k.bias", kv),
+                                 v_bias=bias(p + "attn_v.bias", kv), types=types, **proj))
+    try:
+        output_norm = _f32_vector(g, "output_norm.weight")
+    except Exception:
+        output_norm = _f32_vector(g, "norm.weight")
+    eos = g.get("tokenizer.ggml.eos_token_id")
+    return ModelBytes(geom, n_vocab, np.asarray(g.tensor_bytes("token_embd.weight")),
+                      np.asarray(g.tensor_bytes("output.weight")), output_norm, blocks,
+                      embed_type=g.tensor("token_embd.weight").ggml_type,
+                      output_type=g.tensor("output.weight").ggml_type,
+                      eos_token_id=None if eos is None else int(eos))
+
+
 class _Block:
     def __init__(self, b: BlockBytes, mb: ModelBytes, backend):
         g = mb.geom
         d, kv, ff = g.d_model, g.n_kv_heads * g.head_dim, g.d_ff
-        self.q = backend.make(mb.attn_type, b.q, d, d)
-        self.k = backend.make(mb.attn_type, b.k, kv, d)
-        self.v = backend.make(mb.attn_type, b.v, kv, d)
-        self.o = backend.make(mb.attn_type, b.o, d, d)
-        self.gate = backend.make(mb.ffn_type, b.gate, ff, d)
-        self.up = backend.make(mb.ffn_type, b.up, ff, d)
-        self.down = backend.make(mb.down_type, b.down, d, ff)
+        ty = lambda f, dflt: b.types.get(f, dflt)   # noqa: E731
+        self.q = backend.make(ty("q", mb.attn_type), b.q, d, d)
+        self.k = backend.make(ty("k", mb.attn_type), b.k, kv, d)
+        self.v = backend.make(ty("v", mb.attn_type), b.v, kv, d)
+        self.o = backend.make(ty("o", mb.attn_type), b.o, d, d)
+        self.gate = backend.make(ty("gate", mb.ffn_type), b.gate, ff, d)
+        self.up = backend.make(ty("up", mb.ffn_type), b.up, ff, d)
+        self.down = backend.make(ty("down", mb.down_type), b.down, d, ff)
         self.attn_norm, self.ffn_norm = b.attn_norm, b.ffn_norm
         self.q_bias, self.k_bias, self.v_bias = b.q_bias, b.k_bias, b.v_bias
 
@@ -277,7 +361,20 @@ class DenseRunner:
         self.embed = backend.dequant(mb.embed_type, mb.embed).reshape(mb.n_vocab, mb.geom.d_model)
         self.blocks = [_Block(b, mb, backend) for b in mb.blocks]
         self.output_norm = mb.output_norm
-        self.output = backend.make(mb.embed_type, mb.output, mb.n_vocab, mb.geom.d_model)
+        out_t = mb.embed_type if mb.output_type is None else mb.output_type
+        self.output = backend.make(out_t, mb.output, mb.n_vocab, mb.geom.d_model)
+        self.eos_token_id = mb.eos_token_id
+
+    def generate(self, prompt, max_new: int) -> list:
+        """runner.rs:154-164: the prompt followed by up to max_new greedy tokens, each chosen by
+        re-prefilling the whole sequence; stops at the end-of-sequence token."""
+        seq = [int(t) for t in prompt]
+        for _ in range(max_new):
+            t = argmax_last(DenseDecoder(self, len(seq)).prefill(seq))
+            if self.eos_token_id is not None and t == self.eos_token_id:
+                break
+            seq.append(t)
+        return seq
 
     def close(self):
         for b in self.blocks:

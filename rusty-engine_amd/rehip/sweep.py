@@ -244,7 +244,7 @@ def time_load(layers: int, workdir: str, seed: int = 601, variant_env=None):
     import time
 
     from . import MoeExperts, Gguf, Q4_K, Q6_K, repack
-    from . import gguf_writer as W
+    import gguf_writer as W  # noqa: F401 (tests/gguf_writer.py)
     variant_env = variant_env or {}
     E, hidden, inter = 128, 2048, 768
     rng = np.random.default_rng(seed)

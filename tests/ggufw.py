@@ -1,6 +1,6 @@
 """The reference's GGUF header fixture, written with the package's GGUF writer."""
-from rehip.gguf_writer import *  # noqa: F401,F403
-from rehip.gguf_writer import ARRAY, STR, U32, header
+from gguf_writer import *  # noqa: F401,F403
+from gguf_writer import ARRAY, STR, U32, header
 
 
 def synth_gguf() -> bytes:

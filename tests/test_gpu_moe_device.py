@@ -201,3 +201,37 @@ def test_moe_layer_qwen3_shape(T, gate):
         rel = np.linalg.norm(got - want) / np.linalg.norm(want)
         assert rel <= tol, (mode, rel)
     moe.close()
+
+
+def test_moe_qwen3_shape_t512_host_and_device_routed():
+    """C4 at its largest batch: 512 tokens x top-8 = 4096 (token, expert) pairs over 128
+    experts (grouped GEMM tasks, the fused bf16 gate/up pair, the device plan). Device routing
+    picks the oracle router's experts exactly; host-routed and device-routed FFNs both match the
+    oracle (f32 1e-4, bf16 1e-2 relative to norm)."""
+    E, hidden, inter, k, T = 128, 2048, 768, 8, 512
+    gate_b, up, down_, x, _ = moe_case(4512, E, hidden, inter, T, k)
+    rng = np.random.default_rng(4612)
+    rw = (rng.standard_normal((E, hidden)) / np.sqrt(hidden)).astype(np.float32)
+    moe = rehip.MoeExperts(rehip.Q4_K, gate_b, rehip.Q4_K, up, rehip.Q6_K, down_, E, hidden, inter)
+    xd, rwd = B.from_array(x), B.from_array(rw)
+    logits, dids, dw = B(T * E * 4), B(T * k * 4), B(T * k * 4)
+    rehip.moe_router_logits_dev(xd, rwd, T, hidden, E, logits)
+    lg = down(logits, T * E).reshape(T, E)
+    ids = np.zeros((T, k), np.uint32)
+    wts = np.zeros((T, k), np.float32)
+    for t in range(T):
+        ids[t], wts[t] = O.top_k(lg[t], k)
+    rehip.moe_route_dev(logits, T, E, k, rehip.GATE_SOFTMAX, dids, dw)
+    assert np.array_equal(down(dids, T * k, np.int32).reshape(T, k), ids.astype(np.int32))
+    want = O.moe_ffn(rehip.Q4_K, gate_b, rehip.Q4_K, up, rehip.Q6_K, down_, E, hidden, inter, x, T, k,
+                     ids.reshape(-1), wts.reshape(-1))
+    out = B(T * hidden * 4)
+    for mode, tol in [(rehip.MODE_F32, 1e-4), (rehip.MODE_BF16, 1e-2)]:
+        got = moe.forward(x, T, k, ids.reshape(-1), wts.reshape(-1), mode)
+        rel = np.linalg.norm(got - want) / np.linalg.norm(want)
+        assert rel <= tol, ("host-routed", mode, rel)
+        moe.layer_dev(xd, T, rwd, k, rehip.GATE_SOFTMAX, out, mode)
+        got = down(out, T * hidden)
+        rel = np.linalg.norm(got - want) / np.linalg.norm(want)
+        assert rel <= tol, ("device-routed", mode, rel)
+    moe.close()

@@ -278,20 +278,23 @@ def test_gemm_large_tiles_ragged_edges(t):
     assert np.all(np.abs(got32 - exact) <= F32_TOL * absd)
 
 
-@pytest.mark.parametrize("name,t,m,n", [("C1 Q5_0 4864x896", rehip.Q5_0, 4864, 896),
-                                        ("C2 Q6_K 896x4864", rehip.Q6_K, 896, 4864)])
-def test_prefill_961_rows_full_size(name, t, m, n):
-    rng = np.random.default_rng(101 if t == rehip.Q5_0 else 201 + 961)
+@pytest.mark.parametrize("name,t,m,n,rows", [("C1 Q5_0 4864x896 N=961", rehip.Q5_0, 4864, 896, 961),
+                                             ("C2 Q6_K 896x4864 N=961", rehip.Q6_K, 896, 4864, 961),
+                                             ("C2 Q6_K 896x4864 N=64", rehip.Q6_K, 896, 4864, 64),
+                                             ("C1 Q5_0 4864x896 N=64", rehip.Q5_0, 4864, 896, 64)])
+def test_prefill_rows_full_size(name, t, m, n, rows):
+    rng = np.random.default_rng((101 if t == rehip.Q5_0 else 201) + rows)
     w = synth.weight_bytes(rng, t, m, n)
-    x = synth.activations(rng, 961, n)
+    x = synth.activations(rng, rows, n)
     q = qmat(t, w, m, n)
-    exact, absd = f64_product(t, w, m, n, x, 961)
+    exact, absd = f64_product(t, w, m, n, x, rows)
     exact, absd = exact.reshape(-1), absd.reshape(-1)
-    got16 = q.matmul(x, 961, rehip.MODE_BF16)
+    got16 = q.matmul(x, rows, rehip.MODE_BF16)
     assert np.linalg.norm(got16 - exact) / np.linalg.norm(exact) <= BF16_TOL
-    got32 = q.matmul(x, 961, rehip.MODE_F32)
+    got32 = q.matmul(x, rows, rehip.MODE_F32)
     assert np.all(np.abs(got32 - exact) <= F32_TOL * absd)
-    assert np.array_equal(q.matmul(x, 961, rehip.MODE_BF16), got16)      # deterministic
+    assert np.array_equal(q.matmul(x, rows, rehip.MODE_BF16), got16)      # deterministic
+    assert np.array_equal(q.matmul(x, rows, rehip.MODE_F32), got32)
 
 
 # ---- MoE ---------------------------------------------------------------------------------
@@ -354,6 +357,29 @@ def test_moe_qwen3_shape_t32():
     assert np.linalg.norm(got - want) / np.linalg.norm(want) <= BF16_TOL
     got32 = moe.forward(x, T, k, ids, wts, rehip.MODE_F32)
     assert np.linalg.norm(got32 - want) / np.linalg.norm(want) <= 1e-4
+
+
+@pytest.mark.parametrize("ids", [[3, 3], [3, 3, 5, 3], [1, 1, 1, 1], [6, 2, 0, 4]])
+def test_moe_one_token_repeated_expert(ids):
+    """One token whose routing names an expert more than once (rehip.h allows it): the expert
+    gets several gathered rows, so the single-row gate/up tasks do not apply. Host-routed and
+    device-routed calls against the oracle FFN."""
+    E, hidden, inter, k = 8, 512, 256, len(ids)
+    gate, up, down, x, _, _ = moe_case(950 + 10 * k + ids[0], E, hidden, inter, 1, k)
+    idv = np.array(ids, np.uint32)
+    wts = np.linspace(0.1, 0.4, k).astype(np.float32)
+    want = O.moe_ffn(rehip.Q4_K, gate, rehip.Q4_K, up, rehip.Q6_K, down, E, hidden, inter, x, 1, k, idv, wts)
+    moe = rehip.MoeExperts(rehip.Q4_K, gate, rehip.Q4_K, up, rehip.Q6_K, down, E, hidden, inter)
+    dx, did, dw = (hip.DeviceBuffer.from_array(a) for a in (x, idv.astype(np.int32), wts))
+    out = hip.DeviceBuffer(hidden * 4)
+    for mode, tol in [(rehip.MODE_F32, 1e-4), (rehip.MODE_BF16, BF16_TOL)]:
+        got = moe.forward(x, 1, k, idv, wts, mode)
+        assert np.linalg.norm(got - want) / np.linalg.norm(want) <= tol, ("host", mode)
+        moe.forward_routed_dev(dx, 1, k, did, dw, out, mode)
+        hip.synchronize()
+        got = out.download(np.float32, hidden)
+        assert np.linalg.norm(got - want) / np.linalg.norm(want) <= tol, ("device", mode)
+    moe.close()
 
 
 def test_moe_rejects_bad_expert_id():
