@@ -88,6 +88,14 @@ int re_qmat_matmul(re_qmat *q, const float *x, size_t rows, float *y, int mode);
 int re_qmat_matvec_dev(re_qmat *q, const float *d_x, float *d_y, void *stream);
 int re_qmat_matmul_dev(re_qmat *q, const float *d_x, size_t rows, float *d_y, int mode,
                        void *stream);
+/* re_qmat_matmul_dev that allocates nothing, for callers that cannot allocate device memory
+ * (code under HIP graph capture, serving loops, harnesses that forbid hipMalloc). It has no
+ * counterpart in the reference. The GEMM's K-split partial tiles go to a static device scratch of
+ * 32 MiB per GPU instead of a buffer the matrix grows on first use; the same plan, kernels and
+ * results as re_qmat_matmul_dev. A plan whose partials exceed the scratch fails with RE_ERR_SIZE
+ * (the planned splits of every shape fit: the planner caps partial tiles at 32 MiB). The scratch
+ * is shared by every call on a GPU: calls that overlap in time on one GPU race and must not. */
+int re_qmat_matmul_noalloc_dev(re_qmat *q, const float *d_x, size_t rows, float *d_y, int mode, void *stream);
 /* Dequantize the resident weights to d_out[m x n] f32, bit-exact with quant::dequant. */
 int re_qmat_dequant_dev(re_qmat *q, float *d_out, void *stream);
 

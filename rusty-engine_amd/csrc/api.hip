@@ -65,6 +65,8 @@ const char* type_name(uint32_t t) {
   }
 }
 
+int scratch_for_current_device(float** out);
+
 std::once_flag g_init_once;
 int g_init_rc = RE_OK;
 char g_init_msg[512] = "";
@@ -89,6 +91,12 @@ int do_init() {
       g_init_rc = RE_ERR_NODEV;
       snprintf(g_init_msg, sizeof g_init_msg, "device %d is %s, librehip is built for gfx950", dev,
                prop.gcnArchName);
+      return;
+    }
+    float* p = nullptr;                  // the initial device's static scratch address
+    if (scratch_for_current_device(&p) != RE_OK) {
+      g_init_rc = RE_ERR_HIP;
+      snprintf(g_init_msg, sizeof g_init_msg, "static scratch: %s", g_err);
     }
   });
   if (g_init_rc != RE_OK) return fail(g_init_rc, "%s", g_init_msg);
@@ -109,6 +117,13 @@ int check_matrix(uint32_t type, size_t nbytes, size_t m, size_t n, MatGeom* g) {
                 nbytes);
   return RE_OK;
 }
+
+// Scratch of the no-allocation GEMM entry point: the K-split partial tiles live in this array
+// (one copy per GPU, held until the process ends). Host code never passes `scratch` itself to a
+// kernel: that name is a host-side stand-in; g_scratch_dev[dev] holds the device address that
+// hipGetSymbolAddress returns for the device, taken once per device with that device current.
+constexpr size_t kScratchBytes = 32u << 20;
+static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
 
 struct Staging {
   void* p = nullptr;
@@ -374,7 +389,10 @@ int gemv_enqueue(re_qmat* q, const float* d_x, float* d_y, hipStream_t s, const 
   return RE_OK;
 }
 
-int gemm_enqueue(re_qmat* q, const float* d_x, size_t rows, float* d_y, int mode, hipStream_t s) {
+// fixed_partial: nullptr (the matrix's own partial buffer, grown on first use), or a caller-owned
+// buffer of fixed_cap bytes for the split partials (the no-allocation entry point)
+int gemm_enqueue(re_qmat* q, const float* d_x, size_t rows, float* d_y, int mode, hipStream_t s,
+                 float* fixed_partial = nullptr, size_t fixed_cap = 0) {
   const size_t xbytes = rows * q->g.n * sizeof(float);
   if (xbytes >= (1ull << 31) || q->g.bytes >= (1ull << 31))
     return fail(RE_ERR_SIZE, "GEMM operands must stay below 2 GiB (X %zu B, W %zu B)", xbytes, q->g.bytes);
@@ -390,7 +408,10 @@ int gemm_enqueue(re_qmat* q, const float* d_x, size_t rows, float* d_y, int mode
     pl.splits = (steps + pl.steps_per_split - 1) / pl.steps_per_split;
   }
   const size_t part_bytes = (size_t)pl.splits * rows * q->g.m * sizeof(float);
-  if (pl.splits > 1 && part_bytes > q->spart.cap) {
+  if (fixed_partial && pl.splits > 1 && part_bytes > fixed_cap)
+    return fail(RE_ERR_SIZE, "GEMM %zu x %zu x %zu with %d K splits needs %zu bytes of split scratch; the static "
+                "scratch holds %zu", rows, q->g.m, q->g.n, pl.splits, part_bytes, fixed_cap);
+  if (!fixed_partial && pl.splits > 1 && part_bytes > q->spart.cap) {
     // the partial-sum buffer grows on first use; under stream capture nothing may be allocated,
     // so an un-warmed shape runs unsplit (same result up to summation order)
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
@@ -418,9 +439,13 @@ int gemm_enqueue(re_qmat* q, const float* d_x, size_t rows, float* d_y, int mode
   a.tasks = nullptr;
   a.xrow = nullptr;
   if (pl.splits > 1) {
-    int rc = q->spart.ensure(part_bytes);
-    if (rc) return rc;
-    a.partial = (float*)q->spart.p;
+    if (fixed_partial) {
+      a.partial = fixed_partial;
+    } else {
+      int rc = q->spart.ensure(part_bytes);
+      if (rc) return rc;
+      a.partial = (float*)q->spart.p;
+    }
   }
   HIP_TRY(launch_gemm(q->g.type, mode, a, 0, pl.tile, pl.kgroups, s));
   return RE_OK;
@@ -430,7 +455,12 @@ int gemm_enqueue(re_qmat* q, const float* d_x, size_t rows, float* d_y, int mode
 
 extern "C" {
 
-int re_init(void) { return do_init(); }
+int re_init(void) {
+  int rc = do_init();
+  if (rc) return rc;
+  float* p = nullptr;                    // the current device's static scratch address, taken once
+  return scratch_for_current_device(&p);
+}
 
 const char* re_last_error(void) { return g_err; }
 
@@ -675,6 +705,40 @@ int re_qmat_matmul_dev(re_qmat* q, const float* d_x, size_t rows, float* d_y, in
   }
   if (rows == 1) return gemv_enqueue(q, d_x, d_y, (hipStream_t)stream);
   return gemm_enqueue(q, d_x, rows, d_y, mode, (hipStream_t)stream);
+}
+
+namespace {
+constexpr int kScratchDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_dev[kScratchDevices] = {};
+
+// the calling thread's current device's copy of `scratch`
+int scratch_for_current_device(float** out) {
+  int dev = 0;
+  HIP_TRY(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kScratchDevices) return fail(RE_ERR_ARG, "device %d out of range", dev);
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    void* p = nullptr;
+    HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    if (!p) return fail(RE_ERR_HIP, "hipGetSymbolAddress(scratch) returned null");
+    g_scratch_dev[dev] = (float*)p;
+  }
+  *out = g_scratch_dev[dev];
+  return RE_OK;
+}
+}  // namespace
+
+int re_qmat_matmul_noalloc_dev(re_qmat* q, const float* d_x, size_t rows, float* d_y, int mode, void* stream) {
+  if (!q || (rows && (!d_x || !d_y))) return fail(RE_ERR_ARG, "null pointer");
+  if (mode != RE_MODE_BF16 && mode != RE_MODE_F32) return fail(RE_ERR_ARG, "unknown mode %d", mode);
+  if (rows == 0) return RE_OK;
+  if (rows == 1 || q->dense) return re_qmat_matmul_dev(q, d_x, rows, d_y, mode, stream);   // no scratch
+  if (rows > (1u << 24)) return fail(RE_ERR_SIZE, "rows = %zu too large", rows);
+  float* part = nullptr;
+  int rc = scratch_for_current_device(&part);
+  if (rc) return rc;
+  return gemm_enqueue(q, d_x, rows, d_y, mode, (hipStream_t)stream, part, kScratchBytes);
 }
 
 int re_qmat_matvec(re_qmat* q, const float* x, float* y) {

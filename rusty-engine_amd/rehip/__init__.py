@@ -51,7 +51,7 @@ EXPORTS = ("re_init", "re_last_error", "re_version", "re_row_bytes", "re_tiled_b
            "re_gguf_get_float", "re_gguf_get_str", "re_gguf_get_array", "re_gguf_tensor_info",
            "re_gguf_find_tensor", "re_gguf_tensor_data", "re_qmat_from_gguf", "re_moe_from_gguf",
            "re_quantize_q8_act", "re_quantize_q8_act_dev", "re_qmat_matmul_i8", "re_qmat_matmul_i8_dev",
-           "re_attention_decode_dev", "re_qmat_gemv_plan")
+           "re_attention_decode_dev", "re_qmat_gemv_plan", "re_qmat_matmul_noalloc_dev")
 GEMV_KERNELS = {0: "split", 1: "rows", 2: "tile", 3: "dense"}
 
 
@@ -152,6 +152,7 @@ def lib() -> C.CDLL:
         L.re_qmat_matmul_i8_dev.argtypes = [_vp, _vp, _vp, _sz, _vp, _vp]
         L.re_moe_from_gguf.argtypes = [_vp, C.c_char_p, C.c_char_p, C.c_char_p, _sz, _sz, _sz, C.POINTER(_vp)]
         L.re_qmat_gemv_plan.argtypes = [_vp, _sz] + [C.POINTER(C.c_int)] * 4
+        L.re_qmat_matmul_noalloc_dev.argtypes = [_vp, _vp, _sz, _vp, C.c_int, _vp]
         _lib = L
     return _lib
 
@@ -312,6 +313,11 @@ class QMat:
     def matmul_dev(self, x_dev, rows: int, y_dev, mode: int = MODE_BF16, stream=None) -> None:
         _check(lib().re_qmat_matmul_dev(self._h, _dev_ptr(x_dev), rows, _dev_ptr(y_dev), mode,
                                         _stream_ptr(stream)))
+
+    def matmul_noalloc_dev(self, x_dev, rows: int, y_dev, mode: int = MODE_BF16, stream=None) -> None:
+        """matmul_dev that allocates nothing (K-split partials in the library's static scratch)."""
+        _check(lib().re_qmat_matmul_noalloc_dev(self._h, _dev_ptr(x_dev), rows, _dev_ptr(y_dev), mode,
+                                                _stream_ptr(stream)))
 
     def matmul_i8(self, scales, qs, rows: int) -> np.ndarray:
         """matvec/matmul_q8_0_i8 (kernel.rs:145-166) of a Q8_0 matrix against quantized activation
