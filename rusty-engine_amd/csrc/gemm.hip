@@ -497,14 +497,43 @@ __global__ __launch_bounds__(WM* WN * 64 * KG) void gemm_kernel(GemmArgs p) {
   }
 }
 
-// Y[i] = sum over splits, in split order, of partial[split][i]  (i over N * ldy)
-__global__ __launch_bounds__(256) void gemm_reduce_kernel(const float* __restrict__ partial, float* __restrict__ y,
-                                                          size_t n, int splits) {
+// Y[i] = sum over splits, in split order, of partial[split][i]  (i over N * ldy). The loads of
+// eight splits are in flight together (a loop of dependent load-add steps waited one memory
+// round trip per split); the adds keep split order, so the sums are the same bits.
+template <typename V>
+__device__ __forceinline__ V vadd(V a, V b);
+template <> __device__ __forceinline__ float vadd(float a, float b) { return a + b; }
+template <> __device__ __forceinline__ float4 vadd(float4 a, float4 b) {
+  return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+}
+template <typename V>
+__global__ __launch_bounds__(256) void gemm_reduce_kernel(const V* __restrict__ partial, V* __restrict__ y, size_t n,
+                                                          int splits) {
   const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= n) return;
-  float s = partial[i];
-  for (int sp = 1; sp < splits; ++sp) s += partial[(size_t)sp * n + i];
+  V s = partial[i];
+  int sp = 1;
+  for (; sp + 8 <= splits; sp += 8) {
+    V v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = partial[(size_t)(sp + j) * n + i];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s = vadd(s, v[j]);
+  }
+  for (; sp < splits; ++sp) s = vadd(s, partial[(size_t)sp * n + i]);
   y[i] = s;
+}
+
+static hipError_t launch_reduce(const float* partial, float* y, size_t n, int splits, hipStream_t s) {
+  if (n % 4 == 0 && ((uintptr_t)partial & 15) == 0 && ((uintptr_t)y & 15) == 0) {
+    const size_t n4 = n / 4;
+    hipLaunchKernelGGL(gemm_reduce_kernel<float4>, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s,
+                       (const float4*)partial, (float4*)y, n4, splits);
+  } else {
+    hipLaunchKernelGGL(gemm_reduce_kernel<float>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, partial, y, n,
+                       splits);
+  }
+  return hipGetLastError();
 }
 
 // x[i] -> bf16 with round to nearest even (the rounding the bf16-mode GEMM applies to f32 X), 8
@@ -549,10 +578,7 @@ static hipError_t launch_shape(const GemmArgs& a, int ntasks, hipStream_t s) {
     hipLaunchKernelGGL((gemm_kernel<T, F32, false, BM, BN, WM, WN, KG>), dim3((unsigned)grid), dim3(NT), 0, s, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || a.splits == 1) return e;
-    const size_t n = (size_t)a.N * a.ldy;
-    hipLaunchKernelGGL(gemm_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a.partial, a.Y, n,
-                       a.splits);
-    return hipGetLastError();
+    return launch_reduce(a.partial, a.Y, (size_t)a.N * a.ldy, a.splits, s);
   }
 }
 

@@ -433,8 +433,17 @@ __global__ __launch_bounds__(256) void gemv_reduce_kernel(const float* __restric
   const int r = blockIdx.x * 256 + threadIdx.x;
   unsigned long long key = 0;
   if (r < m) {
+    // eight splits' loads in flight at a time, added in split order
     float s = 0.0f;
-    for (int sp = 0; sp < splits; ++sp) s += partial[(size_t)sp * m_pad + r];
+    int sp = 0;
+    for (; sp + 8 <= splits; sp += 8) {
+      float v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = partial[(size_t)(sp + j) * m_pad + r];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) s += v[j];
+    }
+    for (; sp < splits; ++sp) s += partial[(size_t)sp * m_pad + r];
     const float v = add ? s + add[r] : s;
     y[r] = v;
     key = argmax_key(v, r);
