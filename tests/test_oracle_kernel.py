@@ -255,6 +255,24 @@ def test_cpu_baseline_matches_oracle(t):
     assert np.all(np.abs(mv - O.matvec(t, w, m, n, x[:n])) <= 2 * n * 2.0 ** -24 * absd)
 
 
+@pytest.mark.parametrize("t", O.QUANT_TYPES)
+def test_cpu_baseline_gemv_row_split_is_deterministic(t):
+    # qmat.rs:80-127: above 2^18 MACs the rows are split in ceil(m / threads) chunks; each row is
+    # one quant_row_dot, so the result does not depend on the thread count
+    if not O.cpu_has_avx2():
+        pytest.skip("host has no AVX2+FMA")
+    rng = np.random.default_rng(90 + t)
+    m, n = 97, 4096
+    assert m * n >= 1 << 18
+    w = random_rows(rng, t, m, n)
+    x = rng.standard_normal(n).astype(np.float32)
+    one = O.cpu_matvec(t, w, m, n, x, threads=1)
+    for th in (2, 3, 8):
+        assert np.array_equal(O.cpu_matvec(t, w, m, n, x, threads=th), one)
+    absd = O.qmat_absdot(t, w, m, n, x, 1)
+    assert np.all(np.abs(one - O.matvec(t, w, m, n, x)) <= 2 * n * 2.0 ** -24 * absd)
+
+
 @pytest.mark.parametrize("t", [O.Q4_K, O.Q5_K, O.Q6_K])
 def test_cpu_baseline_padded_k_quant_rows(t):
     # K = 896 is not a multiple of 256: rows are stored as 4 whole super-blocks and only the
