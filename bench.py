@@ -565,7 +565,6 @@ def run_sweep(args):
                     r["name"] = name
                     emit(r)
     elif args.sweep == "moe":
-        import oracle  # noqa: F401
         weights = moe_weights(403)
         moe = rehip.MoeExperts(rehip.Q4_K, weights[0], rehip.Q4_K, weights[1], rehip.Q6_K, weights[2],
                                MOE["n_experts"], MOE["hidden"], MOE["inter"])
@@ -619,23 +618,23 @@ def main():
         print(f"bench.py runs on one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
               file=sys.stderr)
         sys.exit(2)
-    if args.sweep:
-        run_sweep(args)
-        return
-
-    import oracle
     import rehip
     from rehip import hip, synth
-
-    t = rehip.Q6_K
     rehip.init()
-    stream = hip.Stream()
     if args.copy_probe:
         src, dst = hip.DeviceBuffer(256 << 20), hip.DeviceBuffer(256 << 20)
         hip.check(hip.hip().hipMemcpy(hip.C.c_void_p(dst.ptr), hip.C.c_void_p(src.ptr), 256 << 20, hip.D2D))
         hip.synchronize()
         src.free()
         dst.free()
+    if args.sweep:
+        run_sweep(args)
+        return
+
+    import oracle
+
+    t = rehip.Q6_K
+    stream = hip.Stream()
 
     # ---- N = 1 GEMV: batched launches over a stack of weight copies ---------------------------
     rng = np.random.default_rng(201 + 1)
