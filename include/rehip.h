@@ -121,6 +121,15 @@ int re_moe_forward(re_moe *e, const float *x, size_t tokens, size_t top_k, const
 int re_moe_forward_dev(re_moe *e, const float *d_x, size_t tokens, size_t top_k,
                        const uint32_t *ids, const float *weights, float *d_out, int mode,
                        void *stream);
+/* Shared expert (moe_layer_forward's `shared`, moe.rs:380-385 and 424-429; combine, moe.rs:339-343):
+ * a dense SwiGLU FFN (gate and up inter x hidden, down hidden x inter, each of any type QMat takes)
+ * run on every token and added after the routed sum, out[t] = sum_j w_j expert_j(x_t) +
+ * down(silu(gate x_t) * up x_t). Once set, every forward call of e adds it (re_moe_forward, _dev,
+ * _routed_dev, re_moe_layer_dev). All three pointers NULL removes it. Call it while no forward
+ * call of e is in flight. */
+int re_moe_set_shared(re_moe *e, uint32_t gate_type, const uint8_t *gate, size_t gate_bytes,
+                      uint32_t up_type, const uint8_t *up, size_t up_bytes,
+                      uint32_t down_type, const uint8_t *down, size_t down_bytes, size_t inter);
 
 /* ---- MoE layer with the routing on the device (moe.rs:75-125, 360-388): no host round trip --
  * re_moe_router_logits_dev: logits[t][e] = router_w[e] . x[t] (router_w f32, n_experts x hidden;

@@ -316,6 +316,19 @@ def moe_ffn(gate_t, gate, up_t, up, down_t, down, n_experts, hidden, inter, x, t
     return out
 
 
+def moe_ffn_shared(gate_t, gate, up_t, up, down_t, down, n_experts, hidden, inter, x, tokens, k, ids,
+                   weights, shared) -> np.ndarray:
+    """moe_layer_forward with a shared expert (moe.rs:360-388): the routed sum of moe_ffn, then the
+    shared expert's FFN (expert_ffn, moe.rs:286-300) added verbatim per element (moe.rs:380-385).
+    shared = (gate_t, gate, up_t, up, down_t, down, inter). The shared FFN is moe_ffn over one
+    expert with weight 1 (the routed combine then yields 0 + 1 * v = v exactly)."""
+    routed = moe_ffn(gate_t, gate, up_t, up, down_t, down, n_experts, hidden, inter, x, tokens, k, ids, weights)
+    sg_t, sg, su_t, su, sd_t, sd, sinter = shared
+    own = moe_ffn(sg_t, sg, su_t, su, sd_t, sd, 1, hidden, sinter, x, tokens, 1, np.zeros(tokens, np.uint32),
+                  np.ones(tokens, np.float32))
+    return (routed + own).astype(np.float32)
+
+
 # ---- CPU baseline -------------------------------------------------------------------------
 def cpu_has_avx2() -> bool:
     return bool(lib().orc_cpu_has_avx2())

@@ -9,6 +9,7 @@
 #include <cstring>
 #include <mutex>
 #include <new>
+#include <string>
 #include <vector>
 
 #include "../../include/rehip.h"
@@ -173,6 +174,10 @@ struct re_moe {
   size_t hmeta_cap = 0;
   hipEvent_t meta_ev = nullptr;
   bool meta_pending = false;
+  // shared expert: a dense SwiGLU FFN of every token, added after the routed sum
+  re_qmat *sh_gate = nullptr, *sh_up = nullptr, *sh_down = nullptr;
+  size_t sh_inter = 0;
+  Staging ssg, ssu, ssh, ssy;
 };
 
 namespace {
@@ -934,6 +939,7 @@ int re_moe_create(uint32_t gate_type, const uint8_t* gate, size_t gate_bytes, ui
 
 void re_moe_destroy(re_moe* e) {
   if (!e) return;
+  (void)re_moe_set_shared(e, 0, nullptr, 0, 0, nullptr, 0, 0, nullptr, 0, 0);
   e->dmeta.release();
   e->droute.release();
   if (e->stream) (void)hipStreamSynchronize(e->stream);
@@ -947,6 +953,52 @@ void re_moe_destroy(re_moe* e) {
   if (e->stream) (void)hipStreamDestroy(e->stream);
   delete e;
 }
+
+// Shared expert (moe.rs:380-385, 424-429): down(silu(gate x) * up x) of every token, added to the
+// routed sum (out[t] = routed[t] + shared[t]). The three matrices are QMats (any type QMat takes).
+int re_moe_set_shared(re_moe* e, uint32_t gate_type, const uint8_t* gate, size_t gate_bytes, uint32_t up_type,
+                      const uint8_t* up, size_t up_bytes, uint32_t down_type, const uint8_t* down, size_t down_bytes,
+                      size_t inter) {
+  if (!e) return fail(RE_ERR_ARG, "null moe");
+  for (re_qmat** q : {&e->sh_gate, &e->sh_up, &e->sh_down}) {
+    re_qmat_destroy(*q);
+    *q = nullptr;
+  }
+  for (Staging* st : {&e->ssg, &e->ssu, &e->ssh, &e->ssy}) st->release();
+  e->sh_inter = 0;
+  if (!gate && !up && !down) return RE_OK;
+  if (!gate || !up || !down) return fail(RE_ERR_ARG, "shared expert: null pointer");
+  int rc;
+  if ((rc = re_qmat_create(gate_type, gate, gate_bytes, inter, e->hidden, &e->sh_gate)) ||
+      (rc = re_qmat_create(up_type, up, up_bytes, inter, e->hidden, &e->sh_up)) ||
+      (rc = re_qmat_create(down_type, down, down_bytes, e->hidden, inter, &e->sh_down))) {
+    const std::string msg = re_last_error();
+    (void)re_moe_set_shared(e, 0, nullptr, 0, 0, nullptr, 0, 0, nullptr, 0, 0);
+    return fail(rc, "shared expert: %s", msg.c_str());
+  }
+  e->sh_inter = inter;
+  return RE_OK;
+}
+
+namespace {
+
+int moe_add_shared(re_moe* e, const float* d_x, size_t tokens, float* d_out, int mode, hipStream_t s) {
+  if (!e->sh_gate) return RE_OK;
+  const size_t act = tokens * e->sh_inter * sizeof(float), out = tokens * e->hidden * sizeof(float);
+  int rc;
+  if ((rc = e->ssg.ensure(act)) || (rc = e->ssu.ensure(act)) || (rc = e->ssh.ensure(act)) || (rc = e->ssy.ensure(out)))
+    return rc;
+  float *g = (float*)e->ssg.p, *u = (float*)e->ssu.p, *h = (float*)e->ssh.p, *y = (float*)e->ssy.p;
+  if ((rc = re_qmat_matmul_dev(e->sh_gate, d_x, tokens, g, mode, s)) ||
+      (rc = re_qmat_matmul_dev(e->sh_up, d_x, tokens, u, mode, s)))
+    return rc;
+  HIP_TRY(launch_swiglu(g, u, h, tokens * e->sh_inter, s));
+  if ((rc = re_qmat_matmul_dev(e->sh_down, h, tokens, y, mode, s))) return rc;
+  HIP_TRY(launch_add(d_out, y, tokens * e->hidden, tokens * e->hidden, d_out, s));
+  return RE_OK;
+}
+
+}  // namespace
 
 // ---- MoE with the routing on the device (row F3: no host round trip) ------------------------
 int re_moe_route_dev(const float* d_logits, size_t tokens, size_t n_experts, size_t top_k, int gate, int* d_ids,
@@ -1139,7 +1191,7 @@ int re_moe_forward_routed_dev(re_moe* e, const float* d_x, size_t tokens, size_t
     HIP_TRY(launch_gemm(e->gd.type, mode, d, sh.max_d, GemmTile::k64x64, kg_d, s));
   }
   HIP_TRY(launch_combine((const float*)e->syp.p, pos, d_weights, d_out, (int)tokens, (int)top_k, (int)e->hidden, s));
-  return RE_OK;
+  return moe_add_shared(e, d_x, tokens, d_out, mode, s);
 }
 
 int re_moe_layer_dev(re_moe* e, const float* d_x, size_t tokens, const float* d_router_w, size_t top_k, int gate,
@@ -1367,7 +1419,7 @@ int re_moe_forward_dev(re_moe* e, const float* d_x, size_t tokens, size_t top_k,
   }
   HIP_TRY(launch_combine((const float*)e->syp.p, (const int*)(dm + off_pos), (const float*)(dm + off_w), d_out,
                          (int)tokens, (int)top_k, (int)e->hidden, s));
-  return RE_OK;
+  return moe_add_shared(e, d_x, tokens, d_out, mode, s);
 }
 
 int re_moe_forward(re_moe* e, const float* x, size_t tokens, size_t top_k, const uint32_t* ids,

@@ -484,12 +484,17 @@ __device__ __forceinline__ float run_dot(const Run& r, const float* __restrict__
       s = __builtin_fmaf(hi[0], q.z, s);
       s = __builtin_fmaf(hi[1], q.w, s);
     } else {
-      // bytes b -> binary16 1024 + b (0x64 as the high byte: exact), two per v_perm_b32, and the
-      // multiply-add takes the half operand directly (v_fma_mix_f32): 1.5 instructions per quant
-      // instead of a convert and an FMA. The 1024 * sum(x) this adds is taken out below with the
-      // run's sum of x.
-      const h16x2_t p01 = __builtin_bit_cast(h16x2_t, __builtin_amdgcn_perm(0x64646464u, r.q[v], 0x04010400u));
-      const h16x2_t p23 = __builtin_bit_cast(h16x2_t, __builtin_amdgcn_perm(0x64646464u, r.q[v], 0x04030402u));
+      // bytes b -> binary16 1024 + b (0x64 as the high byte: exact), two per v_perm_b32; one
+      // v_pk_add_f16 of -(1024 + bias) leaves the signed quant b - bias, exact in binary16, and the
+      // multiply-add takes the half operand directly (v_fma_mix_f32): 2 instructions per quant
+      // instead of a convert, a subtract and an FMA. Subtracting the offset here, before the
+      // products, keeps the sum free of the cancellation a 1024 * sum(x) correction would bring.
+      constexpr _Float16 kSub = (_Float16)(-(1024 + kBias<T>));
+      const h16x2_t sub = {kSub, kSub};
+      const h16x2_t p01 =
+          __builtin_bit_cast(h16x2_t, __builtin_amdgcn_perm(0x64646464u, r.q[v], 0x04010400u)) + sub;
+      const h16x2_t p23 =
+          __builtin_bit_cast(h16x2_t, __builtin_amdgcn_perm(0x64646464u, r.q[v], 0x04030402u)) + sub;
       s = __builtin_fmaf((float)p01[0], q.x, s);
       s = __builtin_fmaf((float)p01[1], q.y, s);
       s = __builtin_fmaf((float)p23[0], q.z, s);
@@ -497,7 +502,8 @@ __device__ __forceinline__ float run_dot(const Run& r, const float* __restrict__
     }
   }
   if constexpr (kNibble<T>) return __builtin_fmaf(r.scale * 512.0f, s, -r.offset * xs[r.e >> 4]);
-  return __builtin_fmaf(r.scale, s, -__builtin_fmaf(1024.0f, r.scale, r.offset) * xs[r.e >> 4]);
+  if constexpr (kBias<T> != 0) return r.scale * s;          // offset = bias * scale, taken out above
+  return __builtin_fmaf(r.scale, s, -r.offset * xs[r.e >> 4]);
 }
 
 // Sum of one value per thread over a workgroup of WAVES waves: xor tree inside each wave, then

@@ -293,6 +293,20 @@ class MoeExperts {
   size_t n_experts() const { return n_experts_; }
   size_t hidden() const { return hidden_; }
   size_t inter() const { return inter_; }
+  bool has_shared() const { return has_shared_; }
+
+  // The shared expert (moe.rs:380-385): a dense SwiGLU FFN (gate/up inter x hidden, down hidden x
+  // inter) whose output every forward call adds after the routed sum, in the same GPU call.
+  void set_shared(uint32_t gate_t, const std::vector<uint8_t>& gate, uint32_t up_t, const std::vector<uint8_t>& up,
+                  uint32_t down_t, const std::vector<uint8_t>& down, size_t inter) {
+    check(re_moe_set_shared(h_.get(), gate_t, gate.data(), gate.size(), up_t, up.data(), up.size(), down_t,
+                            down.data(), down.size(), inter));
+    has_shared_ = true;
+  }
+  void clear_shared() {
+    check(re_moe_set_shared(h_.get(), 0, nullptr, 0, 0, nullptr, 0, 0, nullptr, 0, 0));
+    has_shared_ = false;
+  }
 
   // tokens x hidden activations, tokens x k routing -> tokens x hidden
   std::vector<float> forward(const std::vector<float>& x, size_t tokens, size_t k, const std::vector<uint32_t>& ids,
@@ -308,6 +322,7 @@ class MoeExperts {
  private:
   std::shared_ptr<re_moe> h_;
   size_t n_experts_, hidden_, inter_;
+  bool has_shared_ = false;
 };
 
 // One MoE FFN layer on `tokens` hidden vectors (moe.rs:360-388): router logits on the host
@@ -334,8 +349,9 @@ inline std::vector<float> combine(const std::vector<std::vector<float>>& routed,
   return out;
 }
 
-// `shared`: an optional shared expert (a one-expert MoeExperts) whose FFN output is added
-// verbatim after the routed sum (moe.rs:380-385)
+// The shared expert (moe.rs:380-385) is either set on `experts` (MoeExperts::set_shared: added in
+// the same GPU call) or passed as `shared`, a one-expert MoeExperts whose FFN output is added
+// verbatim after the routed sum.
 inline std::vector<float> moe_layer_forward(const std::vector<float>& hidden, size_t tokens,
                                             const std::vector<float>& router_w, const MoeExperts& experts,
                                             RouterConfig cfg, Precision prec = Precision::Bf16Mfma,

@@ -51,7 +51,7 @@ EXPORTS = ("re_init", "re_last_error", "re_version", "re_row_bytes", "re_tiled_b
            "re_gguf_get_float", "re_gguf_get_str", "re_gguf_get_array", "re_gguf_tensor_info",
            "re_gguf_find_tensor", "re_gguf_tensor_data", "re_qmat_from_gguf", "re_moe_from_gguf",
            "re_quantize_q8_act", "re_quantize_q8_act_dev", "re_qmat_matmul_i8", "re_qmat_matmul_i8_dev",
-           "re_attention_decode_dev", "re_qmat_gemv_plan", "re_qmat_matmul_noalloc_dev")
+           "re_attention_decode_dev", "re_qmat_gemv_plan", "re_qmat_matmul_noalloc_dev", "re_moe_set_shared")
 GEMV_KERNELS = {0: "split", 1: "rows", 2: "tile", 3: "dense"}
 
 
@@ -100,6 +100,7 @@ def lib() -> C.CDLL:
         L.re_moe_destroy.restype = None
         L.re_moe_forward.argtypes = [_vp, _vp, _sz, _sz, _vp, _vp, _vp, C.c_int]
         L.re_moe_forward_dev.argtypes = [_vp, _vp, _sz, _sz, _vp, _vp, _vp, C.c_int, _vp]
+        L.re_moe_set_shared.argtypes = [_vp, C.c_uint32, _vp, _sz, C.c_uint32, _vp, _sz, C.c_uint32, _vp, _sz, _sz]
         L.re_moe_router_logits_dev.argtypes = [_vp, _vp, _sz, _sz, _sz, _vp, _vp]
         L.re_moe_route_dev.argtypes = [_vp, _sz, _sz, _sz, C.c_int, _vp, _vp, _vp]
         L.re_moe_forward_routed_dev.argtypes = [_vp, _vp, _sz, _sz, _vp, _vp, _vp, C.c_int, _vp]
@@ -478,6 +479,18 @@ class MoeExperts:
                                    down_type, d.ctypes.data, d.size, n_experts, hidden, inter, C.byref(h)))
         self._h = h
         self.n_experts, self.hidden, self.inter = n_experts, hidden, inter
+
+    def set_shared(self, gate_type, gate, up_type, up, down_type, down, inter: int) -> None:
+        """Shared expert (moe.rs:380-385): down(silu(gate x) * up x) added to every token's routed sum
+        by every forward call; gate/up inter x hidden, down hidden x inter."""
+        g, u, d = _u8(gate), _u8(up), _u8(down)
+        self._shared = (g, u, d)
+        _check(lib().re_moe_set_shared(self._h, gate_type, g.ctypes.data, g.size, up_type, u.ctypes.data, u.size,
+                                       down_type, d.ctypes.data, d.size, inter))
+
+    def clear_shared(self) -> None:
+        _check(lib().re_moe_set_shared(self._h, 0, None, 0, 0, None, 0, 0, None, 0, 0))
+        self._shared = None
 
     def forward(self, x, tokens: int, top_k: int, ids, weights, mode: int = MODE_BF16) -> np.ndarray:
         xv = _f32(x)

@@ -225,6 +225,18 @@ static void test_moe_layer_adds_shared_expert() {  // moe.rs:788-801
     for (int i = 1; i < 32; ++i) rest += std::fabs(out[i]);
     CHECK(rest < 1e-5f, "off-diagonal %g", rest);
   }
+  // the same shared expert set on the experts: added inside the GPU call, same values
+  ex.set_shared(ORC_Q8_0, ident, ORC_Q8_0, ident, ORC_Q8_0, ident, 32);
+  for (Precision p : {Precision::F32Strict, Precision::Bf16Mfma}) {
+    const auto a = moe_layer_forward(h, 1, router_w, ex, RouterConfig{Gate::Sigmoid, 1}, p);
+    CHECK(std::fabs(a[0] - 2.0f * silu(1.0f)) < 1e-2f, "set_shared out[0] = %g", a[0]);
+    float rest = 0;
+    for (int i = 1; i < 32; ++i) rest += std::fabs(a[i]);
+    CHECK(rest < 1e-5f, "set_shared off-diagonal %g", rest);
+  }
+  ex.clear_shared();
+  const auto none = moe_layer_forward(h, 1, router_w, ex, RouterConfig{Gate::Sigmoid, 1}, Precision::F32Strict);
+  CHECK(std::fabs(none[0] - silu(1.0f)) < 1e-5f, "cleared shared: out[0] = %g", none[0]);
 }
 
 static void test_combine_routed_plus_shared() {  // moe.rs:749-765

@@ -235,3 +235,49 @@ def test_moe_qwen3_shape_t512_host_and_device_routed():
         rel = np.linalg.norm(got - want) / np.linalg.norm(want)
         assert rel <= tol, ("device-routed", mode, rel)
     moe.close()
+
+
+@pytest.mark.parametrize("T", [1, 5, 300])
+def test_shared_expert_every_forward_path(T):
+    """Shared expert (moe.rs:380-385): set on the experts, it is added after the routed sum by the
+    host-routed, device-routed and whole-layer calls alike; against the oracle's routed sum plus
+    shared FFN (f32 1e-4, bf16 1e-2 relative to norm), with its own width (inter 384 beside 256).
+    Cleared, the calls give the routed sum alone again."""
+    E, hidden, inter, sinter, k = 16, 512, 256, 384, 4
+    gate_b, up, down_, x, _ = moe_case(5100 + T, E, hidden, inter, T, k)
+    rng = np.random.default_rng(5200 + T)
+    sg = synth.weight_bytes(rng, rehip.Q4_K, sinter, hidden)
+    su = synth.weight_bytes(rng, rehip.Q4_K, sinter, hidden)
+    sd = synth.weight_bytes(rng, rehip.Q8_0, hidden, sinter)
+    rw = (rng.standard_normal((E, hidden)) / np.sqrt(hidden)).astype(np.float32)
+    moe = rehip.MoeExperts(rehip.Q4_K, gate_b, rehip.Q4_K, up, rehip.Q6_K, down_, E, hidden, inter)
+    xd, rwd = B.from_array(x), B.from_array(rw)
+    logits, dids, dw = B(T * E * 4), B(T * k * 4), B(T * k * 4)
+    rehip.moe_router_logits_dev(xd, rwd, T, hidden, E, logits)
+    lg = down(logits, T * E).reshape(T, E)
+    ids = np.zeros((T, k), np.uint32)
+    wts = np.zeros((T, k), np.float32)
+    for t in range(T):
+        ids[t], wts[t] = O.top_k(lg[t], k)
+    rehip.moe_route_dev(logits, T, E, k, rehip.GATE_SOFTMAX, dids, dw)
+    shared = (rehip.Q4_K, sg, rehip.Q4_K, su, rehip.Q8_0, sd, sinter)
+    want = O.moe_ffn_shared(rehip.Q4_K, gate_b, rehip.Q4_K, up, rehip.Q6_K, down_, E, hidden, inter, x, T, k,
+                            ids.reshape(-1), wts.reshape(-1), shared)
+    routed = O.moe_ffn(rehip.Q4_K, gate_b, rehip.Q4_K, up, rehip.Q6_K, down_, E, hidden, inter, x, T, k,
+                       ids.reshape(-1), wts.reshape(-1))
+    moe.set_shared(*shared)
+    out = B(T * hidden * 4)
+    for mode, tol in [(rehip.MODE_F32, 1e-4), (rehip.MODE_BF16, 1e-2)]:
+        got = {"host": moe.forward(x, T, k, ids.reshape(-1), wts.reshape(-1), mode)}
+        moe.forward_routed_dev(xd, T, k, dids, dw, out, mode)
+        got["routed"] = down(out, T * hidden)
+        moe.layer_dev(xd, T, rwd, k, rehip.GATE_SOFTMAX, out, mode)
+        got["layer"] = down(out, T * hidden)
+        for name, g in got.items():
+            rel = np.linalg.norm(g - want) / np.linalg.norm(want)
+            assert rel <= tol, (name, mode, rel)
+        assert np.array_equal(got["routed"], got["layer"]), mode
+    moe.clear_shared()
+    got = moe.forward(x, T, k, ids.reshape(-1), wts.reshape(-1), rehip.MODE_F32)
+    assert np.linalg.norm(got - routed) / np.linalg.norm(routed) <= 1e-4
+    moe.close()

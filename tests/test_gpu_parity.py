@@ -148,6 +148,75 @@ def test_gemv_launch_shapes(t, rows_per_group, waves, monkeypatch):
     q.close()
 
 
+def sparse_unit_rows(rng, t, m, n):
+    """m rows of n elements of type t whose values are 0 except three +-1 quant steps per row:
+    every other quant sits at the type's zero point (q = bias, or q = 0 with min 0). With such
+    rows sum|w x| is a few |x| while sum(x) over each 16-element run is large, so a dot that
+    carried the zero point through the products would cancel away the answer."""
+    from blockpack import pack_q4_0, pack_q4_k, pack_q5_0, pack_q5_k, pack_q6_k, pack_q8_0
+    qk, _ = rehip.GEOM[t]
+    out = []
+    for r in range(m):
+        zero = {rehip.Q4_0: 8, rehip.Q5_0: 16, rehip.Q8_0: 0, rehip.Q6_K: 32}.get(t, 0)
+        q = np.full(n, zero, np.int64)
+        for j in rng.choice(n, 3, replace=False):
+            q[j] = zero + (1 if t in (rehip.Q4_K, rehip.Q5_K) else int(rng.choice([-1, 1])))
+        for b in range(n // qk):
+            qb = q[b * qk:(b + 1) * qk]
+            d16 = int(rng.integers(0x3400, 0x3C00))           # 0.25 .. 1
+            if t == rehip.Q4_0:
+                out.append(pack_q4_0(d16, qb))
+            elif t == rehip.Q5_0:
+                out.append(pack_q5_0(d16, qb))
+            elif t == rehip.Q8_0:
+                out.append(pack_q8_0(d16, qb))
+            elif t == rehip.Q6_K:
+                out.append(pack_q6_k(d16, rng.integers(1, 127, 16), qb))
+            else:
+                pk = pack_q4_k if t == rehip.Q4_K else pack_q5_k
+                out.append(pk(d16, 0x3C00, rng.integers(1, 63, 8), np.zeros(8, np.int64), qb))
+    return np.frombuffer(b"".join(out), np.uint8)
+
+
+@pytest.mark.parametrize("t", rehip.QUANT_TYPES)
+@pytest.mark.parametrize("rows_per_group", [0, 64, 4])
+def test_gemv_sparse_unit_quants_within_bound(t, rows_per_group, monkeypatch):
+    """The f32 bound |y - y_oracle| <= 2^-10 sum|w x| where sum|w x| is small against sum|x|:
+    rows of zero-point quants with three unit steps, x = 4 + N(0, 1), K = 4096 (the planned
+    kernel, the tile kernel and 4-row groups)."""
+    if rows_per_group:
+        monkeypatch.setenv("REHIP_GEMV_ROWS", str(rows_per_group))
+    rng = np.random.default_rng(7100 + t + rows_per_group)
+    m, n = 96, 4096
+    w = sparse_unit_rows(rng, t, m, n)
+    x = (4.0 + rng.standard_normal(n)).astype(np.float32)
+    q = qmat(t, w, m, n)
+    got = q.matvec(x)
+    want = O.qmat_matvec(t, w, m, n, x)
+    absd = O.qmat_absdot(t, w, m, n, x, 1)
+    assert np.all(np.abs(got.astype(np.float64) - want) <= F32_TOL * absd)
+    q.close()
+
+
+def test_moe_identity_experts_exact_silu():
+    """Q8_0 identity experts (d = 1, quant 1 on the diagonal, moe.rs:768-776 at hidden = inter =
+    32): one token through gate, up, SwiGLU and down gives silu(1) to f32 accuracy."""
+    from blockpack import pack_q8_0
+    rows = []
+    for r in range(32):
+        qv = np.zeros(32, np.int64)
+        qv[r] = 1
+        rows.append(pack_q8_0(0x3C00, qv))
+    ident = np.frombuffer(b"".join(rows), np.uint8)
+    moe = rehip.MoeExperts(rehip.Q8_0, ident, rehip.Q8_0, ident, rehip.Q8_0, ident, 1, 32, 32)
+    x = np.zeros(32, np.float32)
+    x[0] = 1.0
+    for mode in (rehip.MODE_F32, rehip.MODE_BF16):
+        out = moe.forward(x, 1, 1, np.zeros(1, np.uint32), np.ones(1, np.float32), mode)
+        assert abs(float(out[0]) - O.silu(1.0)) <= 2e-7 and np.all(out[1:] == 0), (mode, out[0])
+    moe.close()
+
+
 def test_gemv_reference_fixtures_match_scalar_kernels():
     # kernel.rs fixtures; the oracle's matvec is the reference's scalar GEMV
     for t, w, m, n in [(rehip.Q4_0, q4_blocks(3 * 64 // 32), 3, 64), (rehip.Q5_0, q5_blocks(3 * 64 // 32), 3, 64),

@@ -91,6 +91,51 @@ def test_moe_layer_routes_to_best_expert():
     assert abs(out[0] - 2.0 * O.silu(1.0)) < EPS and np.all(np.abs(out[1:]) < EPS)
 
 
+def test_moe_layer_adds_shared_expert():
+    # expert 0 wins (sigmoid top-1, weight 1) -> [silu(1), 0, ...]; the identity shared expert adds
+    # its own FFN output -> [2*silu(1), 0, ...] (moe.rs:788-800)
+    ident = q8_identity(1)
+    two = ident + ident
+    ids, w = O.top_k_sigmoid(np.array([10.0, 0.0], np.float32), 1)
+    assert list(ids) == [0] and w[0] == 1.0
+    x = np.zeros(32, np.float32)
+    x[0] = 1.0
+    out = O.moe_ffn_shared(O.Q8_0, two, O.Q8_0, two, O.Q8_0, two, 2, 32, 32, x, 1, 1, ids, w,
+                           (O.Q8_0, ident, O.Q8_0, ident, O.Q8_0, ident, 32))
+    assert abs(out[0] - 2.0 * O.silu(1.0)) < EPS and np.all(np.abs(out[1:]) < EPS)
+
+
+def test_shared_expert_is_added_after_the_routed_sum():
+    # combine (moe.rs:306-345): out = sum_j w_j routed_j, then + shared; the shared term is the
+    # expert FFN of every token on its own, with its own width
+    rng = np.random.default_rng(19)
+    E, hidden, inter, sinter, T, k = 4, 64, 32, 96, 3, 2
+
+    def rnd(m, n):
+        raw = rng.integers(0, 256, (m * n // 32, 34), dtype=np.uint8)
+        raw[:, 0:2] = (np.abs(rng.standard_normal(m * n // 32)) * 0.02).astype(np.float16).view(np.uint8).reshape(-1, 2)
+        return raw.reshape(-1)
+
+    gate, up = rnd(E * inter, hidden), rnd(E * inter, hidden)
+    dn = rnd(E * hidden, inter)
+    sg, su, sd = rnd(sinter, hidden), rnd(sinter, hidden), rnd(hidden, sinter)
+    x = rng.standard_normal(T * hidden).astype(np.float32)
+    ids = np.concatenate([rng.permutation(E)[:k] for _ in range(T)]).astype(np.uint32)
+    w = rng.random(T * k).astype(np.float32)
+    routed = O.moe_ffn(O.Q8_0, gate, O.Q8_0, up, O.Q8_0, dn, E, hidden, inter, x, T, k, ids, w)
+    got = O.moe_ffn_shared(O.Q8_0, gate, O.Q8_0, up, O.Q8_0, dn, E, hidden, inter, x, T, k, ids, w,
+                           (O.Q8_0, sg, O.Q8_0, su, O.Q8_0, sd, sinter))
+    SG = O.dequant(O.Q8_0, sg).reshape(sinter, hidden).astype(np.float64)
+    SU = O.dequant(O.Q8_0, su).reshape(sinter, hidden).astype(np.float64)
+    SD = O.dequant(O.Q8_0, sd).reshape(hidden, sinter).astype(np.float64)
+    for t in range(T):
+        xt = x[t * hidden:(t + 1) * hidden].astype(np.float64)
+        g, u = SG @ xt, SU @ xt
+        want = SD @ (g / (1.0 + np.exp(-g)) * u) + routed[t * hidden:(t + 1) * hidden]
+        scale = np.abs(want).max() + 1e-3
+        assert np.all(np.abs(got[t * hidden:(t + 1) * hidden] - want) <= 1e-4 * scale), t
+
+
 def test_moe_ffn_matches_f64_brute_force():
     rng = np.random.default_rng(9)
     E, hidden, inter, T, k = 6, 64, 96, 5, 3
