@@ -214,6 +214,14 @@ bool moe_bf16_acts(const re_moe* e, const float* d_x, int mode) {
          env_size("REHIP_MOE_XB", 1) != 0;
 }
 
+// bf16 mode with one gate/up type: the grouped expert GEMMs with register-decoded weights
+// (moe_qmma.hip) serve every batch of more than one token; a one-token call keeps the expert GEMV
+// (its few tasks want the GEMV's four waves per weight tile). REHIP_MOE_QMMA=0 turns it off.
+bool moe_qmma_path(const re_moe* e, const float* d_x, size_t tokens, int mode) {
+  return moe_bf16_acts(e, d_x, mode) && e->gg.type == e->gu.type && tokens > 1 &&
+         env_size("REHIP_MOE_QMMA", 1) != 0;
+}
+
 // The grouped expert GEMV stages each task's activation rows (kMoeGemvBatch rows of K floats
 // plus their per-16 sums) and the wave partials in LDS; when a projection's rows are too long for
 // that, the grouped GEMM tasks (fixed LDS per tile) serve every batch size.
@@ -1000,6 +1008,52 @@ int moe_add_shared(re_moe* e, const float* d_x, size_t tokens, float* d_out, int
 
 }  // namespace
 
+namespace {
+
+// gate/up pair (h = silu(gate x) * up x as bf16, rows gathered through xrow from the bf16 copy of x
+// in e->sxb) then down (syp, f32) with the register-decoded grouped GEMMs; the task lists and
+// their device counts (nullptr: the launch count is exact) come from the host or device planner
+hipError_t moe_qmma_ffn(re_moe* e, size_t tokens, size_t pairs, int chunk, const int* xrow, const GemmTask* t_gu,
+                        const int* n_gu_dev, int n_gu, const GemmTask* t_d, const int* n_d_dev, int n_d,
+                        hipStream_t s) {
+  GemmArgs a{};
+  a.W = e->d_gate;
+  a.W2 = e->d_up;
+  a.w_bytes = (uint32_t)(e->gg.bytes * e->n_experts);
+  a.w_stride = e->gg.bytes;
+  a.X = e->sxb.p;
+  a.x_bytes = (uint32_t)(tokens * e->hidden * 2);
+  a.xrow = xrow;
+  a.Y = (float*)e->sh.p;
+  a.m = (int)e->inter;
+  a.K = (int)e->hidden;
+  a.KB = (int)e->gg.kb;
+  a.tiles = (int)e->gg.tiles;
+  a.ldy = (int)e->inter;
+  a.tasks = t_gu;
+  a.ntasks = n_gu_dev;
+  hipError_t err = launch_moe_qmma(e->gg.type, true, chunk, a, n_gu, s);
+  if (err != hipSuccess) return err;
+  GemmArgs d{};
+  d.W = e->d_down;
+  d.w_bytes = (uint32_t)(e->gd.bytes * e->n_experts);
+  d.w_stride = e->gd.bytes;
+  d.X = e->sh.p;
+  d.x_bytes = (uint32_t)(pairs * e->inter * 2);
+  d.xrow = nullptr;
+  d.Y = (float*)e->syp.p;
+  d.m = (int)e->hidden;
+  d.K = (int)e->inter;
+  d.KB = (int)e->gd.kb;
+  d.tiles = (int)e->gd.tiles;
+  d.ldy = (int)e->hidden;
+  d.tasks = t_d;
+  d.ntasks = n_d_dev;
+  return launch_moe_qmma(e->gd.type, false, chunk, d, n_d, s);
+}
+
+}  // namespace
+
 // ---- MoE with the routing on the device (row F3: no host round trip) ------------------------
 int re_moe_route_dev(const float* d_logits, size_t tokens, size_t n_experts, size_t top_k, int gate, int* d_ids,
                      float* d_weights, void* stream) {
@@ -1040,14 +1094,17 @@ int re_moe_forward_routed_dev(re_moe* e, const float* d_x, size_t tokens, size_t
     return fail(RE_ERR_SIZE, "MoE operands must stay below 2 GiB");
   hipStream_t s = (hipStream_t)stream;
   // the grouping runs on the device, so the path is chosen from the batch size alone: the
-  // grouped GEMV while an expert would get few rows on average (pairs <= 2 x experts)
-  const bool gemv = pairs <= 2 * e->n_experts && moe_gemv_fits(e);
+  // grouped GEMV while an expert would get few rows on average (pairs <= 2 x experts); the
+  // register-decoded grouped GEMMs take 32-row chunks there (one token tile) and 64 beyond
+  const bool few = pairs <= 2 * e->n_experts;
+  const bool qmma = moe_qmma_path(e, d_x, tokens, mode);
+  const bool gemv = !qmma && few && moe_gemv_fits(e);
   MoePlanShape sh{};
   sh.pairs = (int)pairs;
   sh.k = (int)top_k;
   sh.n_experts = (int)e->n_experts;
   sh.gemv = gemv;
-  sh.chunk = gemv ? (tokens == 1 ? 1 : kMoeGemvBatch) : kMoeTile;
+  sh.chunk = gemv ? (tokens == 1 ? 1 : kMoeGemvBatch) : (qmma && few ? 32 : kMoeTile);
   if (gemv) {
     const int rd = moe_gemv_rows_down();
     const int rgu = tokens == 1 && e->gg.type == e->gu.type ? moe_gemv_rows_gu1() : kMoeGemvRows;
@@ -1121,6 +1178,12 @@ int re_moe_forward_routed_dev(re_moe* e, const float* d_x, size_t tokens, size_t
     d.KB = (int)e->gd.kb;
     d.ldy = (int)e->hidden;
     HIP_TRY(launch_moe_gemv(e->gd.type, false, d, sh.max_d, s));
+  } else if (qmma) {
+    if ((rc = e->sxb.ensure(tokens * e->hidden * 2))) return rc;
+    HIP_TRY(launch_x_to_bf16(d_x, e->sxb.p, tokens * e->hidden, s));
+    const GemmTask* tg = (const GemmTask*)tasks;
+    HIP_TRY(moe_qmma_ffn(e, tokens, pairs, sh.chunk, xrow, tg, ntasks, sh.max_gu, tg + sh.max_gu, ntasks + 1,
+                         sh.max_d, s));
   } else {
     const GemmTask* tg = (const GemmTask*)tasks;
     GemmArgs a{};
@@ -1243,8 +1306,12 @@ int re_moe_forward_dev(re_moe* e, const float* d_x, size_t tokens, size_t top_k,
     return fail(RE_ERR_SIZE, "MoE operands must stay below 2 GiB");
 
   // Few rows per expert (decode-sized batches): grouped GEMV tasks that read each weight once
-  // per kMoeGemvBatch rows. Otherwise MFMA tiles of kMoeTile gathered rows.
-  const bool gemv = pairs <= (size_t)kMoeGemvBatch * touched && moe_gemv_fits(e);
+  // per kMoeGemvBatch rows. Otherwise MFMA tiles of kMoeTile gathered rows. The register-decoded
+  // grouped GEMMs (bf16 mode) take chunks of 32 rows while the rows per expert are few, else 64.
+  const bool few = pairs <= (size_t)kMoeGemvBatch * touched;
+  const bool qmma = moe_qmma_path(e, d_x, tokens, mode);
+  const bool gemv = !qmma && few && moe_gemv_fits(e);
+  const int chunk = qmma && few ? 32 : kMoeTile;
   int max_rows = 0;
   for (size_t x = 0; x < e->n_experts; ++x) max_rows = std::max(max_rows, std::min(count[x], kMoeGemvBatch));
   // 16-row gate/up tasks exist for single-row tasks only (a repeated expert id gives 2+ rows)
@@ -1262,8 +1329,8 @@ int re_moe_forward_dev(re_moe* e, const float* d_x, size_t tokens, size_t top_k,
   } else {
     const int mt_gu = (int)((e->inter + kMoeTile - 1) / kMoeTile), mt_d = (int)((e->hidden + kMoeTile - 1) / kMoeTile);
     for (size_t x = 0; x < e->n_experts; ++x) {
-      for (int r = 0; r < count[x]; r += kMoeTile) {
-        const int rn = std::min(kMoeTile, count[x] - r);
+      for (int r = 0; r < count[x]; r += chunk) {
+        const int rn = std::min(chunk, count[x] - r);
         for (int mt = 0; mt < mt_gu; ++mt) t_gu.push_back({(int)x, mt, start[x] + r, rn});
         for (int mt = 0; mt < mt_d; ++mt) t_d.push_back({(int)x, mt, start[x] + r, rn});
       }
@@ -1349,6 +1416,11 @@ int re_moe_forward_dev(re_moe* e, const float* d_x, size_t tokens, size_t top_k,
     d.KB = (int)e->gd.kb;
     d.ldy = (int)e->hidden;
     HIP_TRY(launch_moe_gemv(e->gd.type, false, d, (int)n_d, s));
+  } else if (qmma) {
+    if ((rc = e->sxb.ensure(tokens * e->hidden * 2))) return rc;
+    HIP_TRY(launch_x_to_bf16(d_x, e->sxb.p, tokens * e->hidden, s));
+    HIP_TRY(moe_qmma_ffn(e, tokens, pairs, chunk, (const int*)dm, (const GemmTask*)(dm + off_tgu), nullptr, (int)n_gu,
+                         (const GemmTask*)(dm + off_td), nullptr, (int)n_d, s));
   } else {
     GemmArgs a{};
     a.X = d_x;

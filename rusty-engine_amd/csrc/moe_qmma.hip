@@ -1,0 +1,338 @@
+// Grouped expert GEMM with register-decoded weights, bf16 mode (moe.rs:288-300, 360-388): the
+// gate/up pair (SwiGLU written as bf16 h) and the down projection of the experts the router hit.
+//
+// One wave per task (GemmTask: expert, 64-row weight tile, up to 64 gathered activation rows),
+// over the whole K. Lane r loads row r's raw 32-element chunk from the tiled slab (one
+// contiguous 1 KiB plane read per wave, lane = row), decodes both 16-element runs to bf16
+// (scale * q - offset in f32, as the reference's dequantizer, then rounded), and
+// v_permlane32_swap exchanges lane halves so that lanes 0-31 / 32-63 hold k 0-7 / 8-15 of rows
+// 0-31 (B operand of row group 0) and of rows 32-63 (row group 1). Each run is then one
+// v_mfma_f32_32x32x16_bf16 per (row group, 32-row token tile), the A operand (tokens x 16 k) read
+// straight from the bf16 activation rows in L2. Weights never touch LDS: a weight is decoded once
+// and feeds every token of the task, so the decode costs ~2-3 VALU operations per weight
+// whatever the batch, against ~5-8 for the LDS-staged grouped GEMM and the expert GEMV.
+//
+// The K order inside a chunk follows the block format (the A operand of run a reads the
+// activations at the run's own k offset), so X needs no reordering.
+#include <hip/hip_runtime.h>
+
+#include <cstdlib>
+
+#include "deq.hpp"
+#include "kernels.hpp"
+
+namespace rehip {
+
+namespace {
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
+typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2_t;
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16_t;
+typedef __attribute__((__vector_size__(2 * sizeof(float)))) float f32x2_t;
+
+constexpr uint32_t kQOob = 0x80000000u;   // a byte offset past every buffer: the load returns 0
+
+__device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
+  bf16x2_t v;
+  v[0] = (__bf16)a;
+  v[1] = (__bf16)b;
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// The 16 values of a run (scale * q - offset, each exact in f32 as in the reference's
+// dequantizer) rounded to bf16 pairs: lo = elements 0-7, hi = elements 8-15.
+template <int T>
+__device__ __forceinline__ void run_bf16(const Run& r, uint32_t lo[4], uint32_t hi[4]) {
+  float v[16];
+  if constexpr (kNibble<T>) {
+    // 4-bit quants as fp8 e4m3 bytes are exactly q * 2^-9 (two per instruction)
+    const float sc = r.scale * 512.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const f32x2_t a = __builtin_amdgcn_cvt_pk_f32_fp8(r.q[i], false);
+      const f32x2_t b = __builtin_amdgcn_cvt_pk_f32_fp8(r.q[i], true);
+      v[4 * i + 0] = __builtin_fmaf(sc, a[0], -r.offset);
+      v[4 * i + 1] = __builtin_fmaf(sc, a[1], -r.offset);
+      v[4 * i + 2] = __builtin_fmaf(sc, b[0], -r.offset);
+      v[4 * i + 3] = __builtin_fmaf(sc, b[1], -r.offset);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = run_value(r, i);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    lo[i] = pack_bf16(v[2 * i], v[2 * i + 1]);
+    hi[i] = pack_bf16(v[8 + 2 * i], v[8 + 2 * i + 1]);
+  }
+}
+
+// lo/hi of this lane's row -> B operands of row group 0 (rows 0-31) and 1 (rows 32-63): lanes
+// 0-31 take k 0-7 (lo), lanes 32-63 k 8-15 (hi) of row lane % 32 of the group.
+__device__ __forceinline__ void halves_to_frags(const uint32_t lo[4], const uint32_t hi[4], bf16x8_t& g0,
+                                                bf16x8_t& g1) {
+  uint32_t a[4], b[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    // swaps lanes 32-63 of lo with lanes 0-31 of hi: lo becomes group 0's operand, hi group 1's
+    const auto s = __builtin_amdgcn_permlane32_swap(lo[i], hi[i], false, false);
+    a[i] = s[0];
+    b[i] = s[1];
+  }
+  g0 = __builtin_bit_cast(bf16x8_t, make_uint4(a[0], a[1], a[2], a[3]));
+  g1 = __builtin_bit_cast(bf16x8_t, make_uint4(b[0], b[1], b[2], b[3]));
+}
+
+// B operands of both runs of a decoded chunk, both row groups
+struct Frags {
+  bf16x8_t a0, a1, b0, b1;   // run a (groups 0, 1), run b (groups 0, 1)
+  int ea, eb;                // element offsets of runs a and b inside the block
+};
+
+template <int T>
+__device__ __forceinline__ void decode_frags(const typename Blk<T>::CR& raw, int cc, Frags& f) {
+  Run a, b;
+  Blk<T>::decode_chunk(raw, cc, a, b);
+  uint32_t lo[4], hi[4];
+  run_bf16<T>(a, lo, hi);
+  halves_to_frags(lo, hi, f.a0, f.a1);
+  run_bf16<T>(b, lo, hi);
+  halves_to_frags(lo, hi, f.b0, f.b1);
+  f.ea = a.e;
+  f.eb = b.e;
+}
+
+__device__ __forceinline__ bf16x8_t ld_x(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const i32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+  return __builtin_bit_cast(bf16x8_t, v);
+}
+
+}  // namespace
+
+// NT token tiles of 32 (tasks of up to 32 * NT rows); DUAL: W (gate) and W2 (up) side by side,
+// Y receives h = silu(gate) * up as bf16; else Y receives f32. KS waves per task split the
+// blocks of K between them (wave w takes blocks w, w + KS, ...); their sums are added in wave
+// order through LDS at the end (deterministic).
+template <int T, bool DUAL, int NT, int KS>
+__global__ __launch_bounds__(64 * KS) void moe_qmma_kernel(GemmArgs p) {
+  using B = Blk<T>;
+  constexpr int NCH = B::NCH;                       // 32-element chunks per block
+  if (p.ntasks && (int)blockIdx.x >= *p.ntasks) return;   // grid sized for the most tasks
+  const GemmTask t = p.tasks[blockIdx.x];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int rn = t.rn;
+  const int nt = (rn + 31) >> 5;                    // token tiles holding rows (uniform)
+
+  const __amdgpu_buffer_rsrc_t wr = make_rsrc(p.W, p.w_bytes);
+  const __amdgpu_buffer_rsrc_t wr2 = make_rsrc(DUAL ? p.W2 : p.W, p.w_bytes);
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(p.X, p.x_bytes);
+  const uint32_t wbase = (uint32_t)((size_t)t.expert * p.w_stride) +
+                         (uint32_t)t.mtile * (uint32_t)p.KB * (uint32_t)B::SLAB;
+
+  // this lane's activation row in each token tile (A operand row lane % 32), k half lane / 32
+  uint32_t xoff[NT];
+#pragma unroll
+  for (int j = 0; j < NT; ++j) {
+    const int rl = 32 * j + (lane & 31);
+    uint32_t o = kQOob;
+    if (rl < rn) {
+      const int row = p.xrow ? p.xrow[t.r0 + rl] : t.r0 + rl;
+      o = ((uint32_t)row * (uint32_t)p.K + 8u * (uint32_t)(lane >> 5)) * 2u;
+    }
+    xoff[j] = o;
+  }
+
+  f32x16_t acc[2][NT], acc2[DUAL ? 2 : 1][DUAL ? NT : 1];
+#pragma unroll
+  for (int g = 0; g < 2; ++g)
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[g][j][r] = 0.0f;
+  if constexpr (DUAL) {
+#pragma unroll
+    for (int g = 0; g < 2; ++g)
+#pragma unroll
+      for (int j = 0; j < NT; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc2[g][j][r] = 0.0f;
+  }
+
+  const int nch = p.KB * NCH;
+  auto load = [&](int c, typename B::CR& raw, const __amdgpu_buffer_rsrc_t& rs) {
+    const int kb = c / NCH, cc = c - kb * NCH;
+    const uint32_t slab = c < nch ? wbase + (uint32_t)kb * (uint32_t)B::SLAB : kQOob;
+    B::bload_chunk(rs, slab, lane, cc, raw);
+  };
+  // A operands of chunk c: runs a and b of every token tile
+  struct XOps { bf16x8_t a[NT], b[NT]; };
+  // (runs at or past K, the padding of rows stored as whole blocks, read zeros: K % 16 == 0, so a
+  // run is wholly inside or outside)
+  auto load_x = [&](int c, int ea, int eb, XOps& x) {
+    const int kb = c / NCH;
+    const int ka = kb * B::QK + ea, kbe = kb * B::QK + eb;
+    const bool in_a = c < nch && ka < p.K, in_b = c < nch && kbe < p.K;
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      x.a[j] = ld_x(xr, j < nt && in_a ? xoff[j] + (uint32_t)ka * 2u : kQOob);
+      x.b[j] = ld_x(xr, j < nt && in_b ? xoff[j] + (uint32_t)kbe * 2u : kQOob);
+    }
+  };
+  // run element offsets of chunk cc (the Blk<T>::dec layouts; the same for every row)
+  auto run_e = [&](int c, int& ea, int& eb) {
+    const int cc = c % NCH;
+    if constexpr (B::QK == 32) {
+      ea = 0; eb = 16;
+    } else if constexpr (T == T_Q6_K) {
+      ea = 128 * (cc >> 2) + 32 * ((cc >> 1) & 1) + 16 * (cc & 1); eb = ea + 64;
+    } else {
+      ea = 64 * (cc >> 1) + 16 * (cc & 1); eb = ea + 32;
+    }
+  };
+
+  // Two register sets, A and B, take alternate chunks: while chunk c is decoded from set A, the
+  // loads of chunk c + 1 (set B) are in flight, and set A is refilled with chunk c + 2 right after
+  // its decode. Named sets (not a rotated copy) let the waits count only the older loads. Chunks
+  // past the end load zeros and add nothing, so an odd chunk count needs no tail.
+  auto mma = [&](const XOps& x, const Frags& f, f32x16_t (&a)[2][NT]) {
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      a[0][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x.a[j], f.a0, a[0][j], 0, 0, 0);
+      a[1][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x.a[j], f.a1, a[1][j], 0, 0, 0);
+      a[0][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x.b[j], f.b0, a[0][j], 0, 0, 0);
+      a[1][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x.b[j], f.b1, a[1][j], 0, 0, 0);
+    }
+  };
+  auto load_all = [&](int c, typename B::CR& r, typename B::CR& q, XOps& x) {
+    load(c, r, wr);
+    if constexpr (DUAL) load(c, q, wr2);
+    int ea, eb;
+    run_e(c, ea, eb);
+    load_x(c, ea, eb, x);
+  };
+  auto step = [&](int c, const typename B::CR& r, const typename B::CR& q, const XOps& x) {
+    Frags f;
+    decode_frags<T>(r, c % NCH, f);
+    mma(x, f, acc);
+    if constexpr (DUAL) {
+      Frags f2;
+      decode_frags<T>(q, c % NCH, f2);
+      mma(x, f2, acc2);
+    }
+  };
+  // U chunks per iteration, a whole number of blocks, unrolled so that every chunk's position in
+  // its block (and so its decode) is a compile-time constant
+  constexpr int U = NCH >= 2 ? NCH : 2;
+  // this wave's groups of U chunks: c0 = (i * KS + wave) * U for i = 0, 1, ...
+  typename B::CR r[2], q[2];
+  XOps x[2];
+  const int first = wave * U;
+  load_all(first, r[0], q[0], x[0]);
+  load_all(first + 1, r[1], q[1], x[1]);
+  for (int c0 = first; c0 < nch; c0 += U * KS) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      step(c0 + u, r[u & 1], q[u & 1], x[u & 1]);
+      // keep the loads in program order behind the step that frees their registers, so the wait
+      // before the next step counts only these (younger) loads
+      __builtin_amdgcn_sched_barrier(0);
+      load_all(u + 2 < U ? c0 + u + 2 : c0 + U * KS + u + 2 - U, r[u & 1], q[u & 1], x[u & 1]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  if constexpr (KS > 1) {
+    // waves 1 .. KS-1 hand their sums to wave 0, which adds them in wave order
+    constexpr int NACC = 2 * NT * 16 * (DUAL ? 2 : 1);
+    __shared__ float red[(KS - 1) * NACC * 64];
+    if (wave > 0) {
+      float* dst = red + (wave - 1) * NACC * 64 + lane;
+#pragma unroll
+      for (int g = 0; g < 2; ++g)
+#pragma unroll
+        for (int j = 0; j < NT; ++j)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            dst[((g * NT + j) * 16 + e) * 64] = acc[g][j][e];
+            if constexpr (DUAL) dst[(((2 + g) * NT + j) * 16 + e) * 64] = acc2[g][j][e];
+          }
+    }
+    __syncthreads();
+    if (wave > 0) return;
+#pragma unroll
+    for (int w = 1; w < KS; ++w) {
+      const float* src = red + (w - 1) * NACC * 64 + lane;
+#pragma unroll
+      for (int g = 0; g < 2; ++g)
+#pragma unroll
+        for (int j = 0; j < NT; ++j)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            acc[g][j][e] += src[((g * NT + j) * 16 + e) * 64];
+            if constexpr (DUAL) acc2[g][j][e] += src[(((2 + g) * NT + j) * 16 + e) * 64];
+          }
+    }
+  }
+
+  // D[token i][row n]: lane holds row n = 32 g + lane % 32 and tokens 8 (r / 4) + 4 (lane / 32) + r % 4
+  const int col = t.mtile * 64 + (lane & 31);
+#pragma unroll
+  for (int g = 0; g < 2; ++g) {
+    const int row = col + 32 * g;
+    if (row >= p.m) continue;
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      if (j >= nt) continue;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int i = 32 * j + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        if (i >= rn) continue;
+        const size_t o = (size_t)(t.r0 + i) * (size_t)p.ldy + (size_t)row;
+        if constexpr (DUAL) {
+          reinterpret_cast<__bf16*>(p.Y)[o] = (__bf16)silu_mul(acc[g][j][r], acc2[g][j][r]);
+        } else {
+          p.Y[o] = acc[g][j][r];
+        }
+      }
+    }
+  }
+}
+
+hipError_t launch_moe_qmma(uint32_t type, bool dual, int max_rows, const GemmArgs& a, int ntasks, hipStream_t s) {
+  if (ntasks <= 0) return hipSuccess;
+  if (max_rows < 1 || max_rows > 64) return hipErrorInvalidValue;
+  const bool one = max_rows <= 32;
+  // waves per task: two split K where the tasks are few rows each (more waves in flight), one
+  // for 64-row tasks; REHIP_QMMA_KS = 1 / 2 overrides
+  int ks = one ? 2 : 1;
+  if (const char* v = std::getenv("REHIP_QMMA_KS"); v && (v[0] == '1' || v[0] == '2' || v[0] == '4') && !v[1])
+    ks = v[0] - '0';
+  if (ks == 4 && !one) ks = 2;
+  const dim3 grid((unsigned)ntasks), block(64 * ks);
+#define REHIP_QMMA_L(TT, DU, NT, KS) hipLaunchKernelGGL((moe_qmma_kernel<TT, DU, NT, KS>), grid, block, 0, s, a)
+#define REHIP_QMMA(TT)                                                    \
+  case TT:                                                                \
+    if (dual) {                                                           \
+      if (one) { if (ks == 4) REHIP_QMMA_L(TT, true, 1, 4); else if (ks == 2) REHIP_QMMA_L(TT, true, 1, 2); else REHIP_QMMA_L(TT, true, 1, 1); } \
+      else { if (ks == 2) REHIP_QMMA_L(TT, true, 2, 2); else REHIP_QMMA_L(TT, true, 2, 1); }     \
+    } else {                                                              \
+      if (one) { if (ks == 4) REHIP_QMMA_L(TT, false, 1, 4); else if (ks == 2) REHIP_QMMA_L(TT, false, 1, 2); else REHIP_QMMA_L(TT, false, 1, 1); } \
+      else { if (ks == 2) REHIP_QMMA_L(TT, false, 2, 2); else REHIP_QMMA_L(TT, false, 2, 1); }     \
+    }                                                                     \
+    break;
+  switch (type) {
+    REHIP_QMMA(T_Q4_0)
+    REHIP_QMMA(T_Q5_0)
+    REHIP_QMMA(T_Q8_0)
+    REHIP_QMMA(T_Q4_K)
+    REHIP_QMMA(T_Q5_K)
+    REHIP_QMMA(T_Q6_K)
+    default:
+      return hipErrorInvalidValue;
+  }
+#undef REHIP_QMMA
+#undef REHIP_QMMA_L
+  return hipGetLastError();
+}
+
+}  // namespace rehip

@@ -85,6 +85,7 @@ def test_grouped_gemm_bf16_activations_bit_identical(T, E, k, gt, dt, monkeypatc
     idd, wd = B.from_array(ids.reshape(-1)), B.from_array(wts.reshape(-1))
     res = {}
     # f32 rows staged per tile; bf16 rows with gate and up apart; bf16 rows with the fused pair
+    monkeypatch.setenv("REHIP_MOE_QMMA", "0")       # the LDS-staged grouped GEMMs
     for xb, pair in (("0", "0"), ("1", "0"), ("1", "1")):
         monkeypatch.setenv("REHIP_MOE_XB", xb)
         monkeypatch.setenv("REHIP_MOE_PAIR", pair)
@@ -280,4 +281,47 @@ def test_shared_expert_every_forward_path(T):
     moe.clear_shared()
     got = moe.forward(x, T, k, ids.reshape(-1), wts.reshape(-1), rehip.MODE_F32)
     assert np.linalg.norm(got - routed) / np.linalg.norm(routed) <= 1e-4
+    moe.close()
+
+
+QMMA_CASES = [(5, 16, 4, rehip.Q4_K, rehip.Q6_K), (40, 16, 4, rehip.Q4_K, rehip.Q6_K),
+              (300, 32, 4, rehip.Q4_K, rehip.Q6_K), (64, 16, 2, rehip.Q5_K, rehip.Q5_K),
+              (64, 16, 2, rehip.Q8_0, rehip.Q4_0), (70, 8, 2, rehip.Q5_0, rehip.Q8_0),
+              (33, 4, 4, rehip.Q6_K, rehip.Q4_K)]
+
+
+@pytest.mark.parametrize("T,E,k,gt,dt", QMMA_CASES)
+def test_register_decoded_grouped_gemm(T, E, k, gt, dt, monkeypatch):
+    """bf16 mode, more than one token: the grouped expert GEMMs with register-decoded weights
+    (moe_qmma.hip), host- and device-routed, with 32-row chunks (few rows per expert) and 64-row
+    chunks (ragged: 33, 40, 70 rows per expert and more), against the oracle at the bf16 bar. Where
+    the path they replace is the LDS-staged grouped GEMM (many rows per expert), its operands are
+    the same bf16 values, so the two agree to f32 summation order (1e-4 relative to norm: an
+    ulp-level difference of a gate/up sum can flip the bf16 rounding of h); with few rows per
+    expert the replaced path is the f32 expert GEMV."""
+    hidden, inter = 512, 320
+    gate, up, down_, x, logits = moe_case(990 + T + E + gt, E, hidden, inter, T, k, gt, dt)
+    ids = np.zeros((T, k), np.int32)
+    wts = np.zeros((T, k), np.float32)
+    for t in range(T):
+        ids[t], wts[t] = O.top_k(logits[t], k)
+    moe = rehip.MoeExperts(gt, gate, gt, up, dt, down_, E, hidden, inter)
+    xd = B.from_array(x)
+    idd, wd = B.from_array(ids.reshape(-1)), B.from_array(wts.reshape(-1))
+    res = {}
+    for q in ("0", "1"):
+        monkeypatch.setenv("REHIP_MOE_QMMA", q)
+        out = B(T * hidden * 4)
+        moe.forward_routed_dev(xd, T, k, idd, wd, out, rehip.MODE_BF16)
+        res[q] = (moe.forward(x, T, k, ids.reshape(-1).astype(np.uint32), wts.reshape(-1), rehip.MODE_BF16),
+                  down(out, T * hidden))
+    want = O.moe_ffn(gt, gate, gt, up, dt, down_, E, hidden, inter, x, T, k,
+                     ids.reshape(-1).astype(np.uint32), wts.reshape(-1))
+    touched = len(np.unique(ids))
+    many = {"host-routed": T * k > 4 * touched, "device-routed": T * k > 2 * E}
+    for i, name in enumerate(("host-routed", "device-routed")):
+        a, b = res["0"][i], res["1"][i]
+        if many[name]:
+            assert np.linalg.norm(b - a) / np.linalg.norm(a) <= 1e-4, name
+        assert np.linalg.norm(b - want) / np.linalg.norm(want) <= 1e-2, name
     moe.close()
