@@ -1010,6 +1010,16 @@ int moe_add_shared(re_moe* e, const float* d_x, size_t tokens, float* d_out, int
 
 namespace {
 
+// With 64-row chunks the down projection's tasks cover 128 weight rows (two tiles per wave, each
+// activation load feeding twice the weights); with 32-row chunks one tile (more, shorter tasks
+// suit the few rows). REHIP_QMMA_DOWN2 = 0 / 1 overrides.
+int moe_qmma_down_pair(int chunk) {
+  const size_t v = env_size("REHIP_QMMA_DOWN2", 2);
+  if (v == 0 || v == 1) return v ? kQmmaTwoTiles : kQmmaOneTile;
+  return chunk > 32 ? kQmmaTwoTiles : kQmmaOneTile;
+}
+int moe_qmma_down_rows(int chunk) { return moe_qmma_down_pair(chunk) == kQmmaTwoTiles ? 128 : 64; }
+
 // gate/up pair (h = silu(gate x) * up x as bf16, rows gathered through xrow from the bf16 copy of x
 // in e->sxb) then down (syp, f32) with the register-decoded grouped GEMMs; the task lists and
 // their device counts (nullptr: the launch count is exact) come from the host or device planner
@@ -1032,7 +1042,7 @@ hipError_t moe_qmma_ffn(re_moe* e, size_t tokens, size_t pairs, int chunk, const
   a.ldy = (int)e->inter;
   a.tasks = t_gu;
   a.ntasks = n_gu_dev;
-  hipError_t err = launch_moe_qmma(e->gg.type, true, chunk, a, n_gu, s);
+  hipError_t err = launch_moe_qmma(e->gg.type, kQmmaGateUp, chunk, a, n_gu, s);
   if (err != hipSuccess) return err;
   GemmArgs d{};
   d.W = e->d_down;
@@ -1049,7 +1059,7 @@ hipError_t moe_qmma_ffn(re_moe* e, size_t tokens, size_t pairs, int chunk, const
   d.ldy = (int)e->hidden;
   d.tasks = t_d;
   d.ntasks = n_d_dev;
-  return launch_moe_qmma(e->gd.type, false, chunk, d, n_d, s);
+  return launch_moe_qmma(e->gd.type, moe_qmma_down_pair(chunk), chunk, d, n_d, s);
 }
 
 }  // namespace
@@ -1115,7 +1125,8 @@ int re_moe_forward_routed_dev(re_moe* e, const float* d_x, size_t tokens, size_t
   } else {
     sh.rows_gu = sh.rows_d = kMoeTile;
     sh.tiles_gu = (int)((e->inter + kMoeTile - 1) / kMoeTile);
-    sh.tiles_d = (int)((e->hidden + kMoeTile - 1) / kMoeTile);
+    const int rows_d = qmma ? moe_qmma_down_rows(sh.chunk) : kMoeTile;
+    sh.tiles_d = (int)((e->hidden + rows_d - 1) / rows_d);
   }
   const int max_chunks = (int)((pairs + sh.chunk - 1) / sh.chunk + std::min(pairs, e->n_experts));
   sh.max_gu = max_chunks * sh.tiles_gu;
@@ -1327,7 +1338,8 @@ int re_moe_forward_dev(re_moe* e, const float* d_x, size_t tokens, size_t top_k,
           v_d.push_back({(int)x, (int)row, start[x] + r, np});
       }
   } else {
-    const int mt_gu = (int)((e->inter + kMoeTile - 1) / kMoeTile), mt_d = (int)((e->hidden + kMoeTile - 1) / kMoeTile);
+    const int rows_d = qmma ? moe_qmma_down_rows(chunk) : kMoeTile;
+    const int mt_gu = (int)((e->inter + kMoeTile - 1) / kMoeTile), mt_d = (int)((e->hidden + rows_d - 1) / rows_d);
     for (size_t x = 0; x < e->n_experts; ++x) {
       for (int r = 0; r < count[x]; r += chunk) {
         const int rn = std::min(chunk, count[x] - r);

@@ -177,12 +177,15 @@ constexpr int kMoeGemvWaves = 4;
 constexpr int kMoeGemvBatch = 4;   // gathered rows per task
 // dual: gate and up (W0, W1) with SwiGLU output; else one matrix
 hipError_t launch_moe_gemv(uint32_t type, bool dual, const MoeGemvArgs& a, int ntasks, hipStream_t s);
-// Grouped expert GEMM with register-decoded weights, bf16 mode (moe_qmma.hip): one wave per GemmTask
-// (64-row weight tile, up to max_rows <= 64 gathered rows), X bf16 rows (gathered through xrow when
-// given). dual: W (gate) and W2 (up) of one geometry, Y receives h = silu(gate) * up as bf16;
-// else Y receives f32. Uses W, W2, w_bytes, w_stride, X, x_bytes, xrow, Y, m, K, KB, ldy, tasks,
-// ntasks of GemmArgs.
-hipError_t launch_moe_qmma(uint32_t type, bool dual, int max_rows, const GemmArgs& a, int ntasks, hipStream_t s);
+// Grouped expert GEMM with register-decoded weights, bf16 mode (moe_qmma.hip): GemmTasks of up to
+// max_rows <= 64 gathered rows, X bf16 rows (gathered through xrow when given). pair:
+//   kQmmaOneTile   64-row weight tile mtile of W, Y receives f32;
+//   kQmmaGateUp    the tile of W (gate) and W2 (up) of one geometry, Y receives h = silu(gate) * up
+//                  as bf16;
+//   kQmmaTwoTiles  128 rows (tiles 2 mtile, 2 mtile + 1) of W, Y receives f32.
+// Uses W, W2, w_bytes, w_stride, X, x_bytes, xrow, Y, m, K, KB, ldy, tasks, ntasks of GemmArgs.
+constexpr int kQmmaOneTile = 0, kQmmaGateUp = 1, kQmmaTwoTiles = 2;
+hipError_t launch_moe_qmma(uint32_t type, int pair, int max_rows, const GemmArgs& a, int ntasks, hipStream_t s);
 
 // Dense transformer steps on device buffers (layer.hip)
 hipError_t launch_rmsnorm(const float* x, const float* w, int rows, int d, float eps, float* out, hipStream_t s);

@@ -109,11 +109,16 @@ __device__ __forceinline__ bf16x8_t ld_x(__amdgpu_buffer_rsrc_t r, uint32_t off)
 
 }  // namespace
 
-// NT token tiles of 32 (tasks of up to 32 * NT rows); DUAL: W (gate) and W2 (up) side by side,
-// Y receives h = silu(gate) * up as bf16; else Y receives f32. KS waves per task split the
-// blocks of K between them (wave w takes blocks w, w + KS, ...); their sums are added in wave
-// order through LDS at the end (deterministic).
-template <int T, bool DUAL, int NT, int KS>
+// NT token tiles of 32 (tasks of up to 32 * NT rows). PAIR selects the weights of a task:
+//   kOneTile   one 64-row tile (mtile) of W, Y receives f32;
+//   kGateUp    the tile of W (gate) and of W2 (up) side by side, Y receives h = silu(gate) * up
+//              as bf16;
+//   kTwoTiles  tiles 2 mtile and 2 mtile + 1 of W (128 rows per task: every activation operand
+//              load feeds twice the weights), Y receives f32.
+// KS waves per task split the blocks of K between them (wave w takes blocks w, w + KS, ...);
+// their sums are added in wave order through LDS at the end (deterministic).
+constexpr int kOneTile = 0, kGateUp = 1, kTwoTiles = 2;
+template <int T, int PAIR, int NT, int KS>
 __global__ __launch_bounds__(64 * KS) void moe_qmma_kernel(GemmArgs p) {
   using B = Blk<T>;
   constexpr int NCH = B::NCH;                       // 32-element chunks per block
@@ -125,10 +130,15 @@ __global__ __launch_bounds__(64 * KS) void moe_qmma_kernel(GemmArgs p) {
   const int nt = (rn + 31) >> 5;                    // token tiles holding rows (uniform)
 
   const __amdgpu_buffer_rsrc_t wr = make_rsrc(p.W, p.w_bytes);
-  const __amdgpu_buffer_rsrc_t wr2 = make_rsrc(DUAL ? p.W2 : p.W, p.w_bytes);
+  constexpr bool DUAL = PAIR != kOneTile;           // a second set of weight registers
+  const __amdgpu_buffer_rsrc_t wr2 = make_rsrc(PAIR == kGateUp ? p.W2 : p.W, p.w_bytes);
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(p.X, p.x_bytes);
+  const int tile0 = PAIR == kTwoTiles ? 2 * t.mtile : t.mtile;
   const uint32_t wbase = (uint32_t)((size_t)t.expert * p.w_stride) +
-                         (uint32_t)t.mtile * (uint32_t)p.KB * (uint32_t)B::SLAB;
+                         (uint32_t)tile0 * (uint32_t)p.KB * (uint32_t)B::SLAB;
+  // second set: the up tile (same offset, other matrix) or the next tile of W (a tile past the
+  // expert's last one reads the following bytes of the stack; its rows are not stored)
+  const uint32_t wbase2 = PAIR == kTwoTiles ? wbase + (uint32_t)p.KB * (uint32_t)B::SLAB : wbase;
 
   // this lane's activation row in each token tile (A operand row lane % 32), k half lane / 32
   uint32_t xoff[NT];
@@ -160,9 +170,9 @@ __global__ __launch_bounds__(64 * KS) void moe_qmma_kernel(GemmArgs p) {
   }
 
   const int nch = p.KB * NCH;
-  auto load = [&](int c, typename B::CR& raw, const __amdgpu_buffer_rsrc_t& rs) {
+  auto load = [&](int c, typename B::CR& raw, const __amdgpu_buffer_rsrc_t& rs, uint32_t base) {
     const int kb = c / NCH, cc = c - kb * NCH;
-    const uint32_t slab = c < nch ? wbase + (uint32_t)kb * (uint32_t)B::SLAB : kQOob;
+    const uint32_t slab = c < nch ? base + (uint32_t)kb * (uint32_t)B::SLAB : kQOob;
     B::bload_chunk(rs, slab, lane, cc, raw);
   };
   // A operands of chunk c: runs a and b of every token tile
@@ -205,8 +215,8 @@ __global__ __launch_bounds__(64 * KS) void moe_qmma_kernel(GemmArgs p) {
     }
   };
   auto load_all = [&](int c, typename B::CR& r, typename B::CR& q, XOps& x) {
-    load(c, r, wr);
-    if constexpr (DUAL) load(c, q, wr2);
+    load(c, r, wr, wbase);
+    if constexpr (DUAL) load(c, q, wr2, wbase2);
     int ea, eb;
     run_e(c, ea, eb);
     load_x(c, ea, eb, x);
@@ -275,9 +285,9 @@ __global__ __launch_bounds__(64 * KS) void moe_qmma_kernel(GemmArgs p) {
   }
 
   // D[token i][row n]: lane holds row n = 32 g + lane % 32 and tokens 8 (r / 4) + 4 (lane / 32) + r % 4
-  const int col = t.mtile * 64 + (lane & 31);
+  const int col = tile0 * 64 + (lane & 31);
 #pragma unroll
-  for (int g = 0; g < 2; ++g) {
+  for (int g = 0; g < (PAIR == kTwoTiles ? 4 : 2); ++g) {
     const int row = col + 32 * g;
     if (row >= p.m) continue;
 #pragma unroll
@@ -288,8 +298,10 @@ __global__ __launch_bounds__(64 * KS) void moe_qmma_kernel(GemmArgs p) {
         const int i = 32 * j + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
         if (i >= rn) continue;
         const size_t o = (size_t)(t.r0 + i) * (size_t)p.ldy + (size_t)row;
-        if constexpr (DUAL) {
+        if constexpr (PAIR == kGateUp) {
           reinterpret_cast<__bf16*>(p.Y)[o] = (__bf16)silu_mul(acc[g][j][r], acc2[g][j][r]);
+        } else if constexpr (PAIR == kTwoTiles) {
+          p.Y[o] = g < 2 ? acc[g & 1][j][r] : acc2[g & 1][j][r];
         } else {
           p.Y[o] = acc[g][j][r];
         }
@@ -298,27 +310,24 @@ __global__ __launch_bounds__(64 * KS) void moe_qmma_kernel(GemmArgs p) {
   }
 }
 
-hipError_t launch_moe_qmma(uint32_t type, bool dual, int max_rows, const GemmArgs& a, int ntasks, hipStream_t s) {
+hipError_t launch_moe_qmma(uint32_t type, int pair, int max_rows, const GemmArgs& a, int ntasks, hipStream_t s) {
   if (ntasks <= 0) return hipSuccess;
-  if (max_rows < 1 || max_rows > 64) return hipErrorInvalidValue;
+  if (max_rows < 1 || max_rows > 64 || pair < kOneTile || pair > kTwoTiles) return hipErrorInvalidValue;
   const bool one = max_rows <= 32;
   // waves per task: two split K where the tasks are few rows each (more waves in flight), one
   // for 64-row tasks; REHIP_QMMA_KS = 1 / 2 overrides
   int ks = one ? 2 : 1;
-  if (const char* v = std::getenv("REHIP_QMMA_KS"); v && (v[0] == '1' || v[0] == '2' || v[0] == '4') && !v[1])
-    ks = v[0] - '0';
-  if (ks == 4 && !one) ks = 2;
+  if (const char* v = std::getenv("REHIP_QMMA_KS"); v && (v[0] == '1' || v[0] == '2') && !v[1]) ks = v[0] - '0';
   const dim3 grid((unsigned)ntasks), block(64 * ks);
-#define REHIP_QMMA_L(TT, DU, NT, KS) hipLaunchKernelGGL((moe_qmma_kernel<TT, DU, NT, KS>), grid, block, 0, s, a)
-#define REHIP_QMMA(TT)                                                    \
-  case TT:                                                                \
-    if (dual) {                                                           \
-      if (one) { if (ks == 4) REHIP_QMMA_L(TT, true, 1, 4); else if (ks == 2) REHIP_QMMA_L(TT, true, 1, 2); else REHIP_QMMA_L(TT, true, 1, 1); } \
-      else { if (ks == 2) REHIP_QMMA_L(TT, true, 2, 2); else REHIP_QMMA_L(TT, true, 2, 1); }     \
-    } else {                                                              \
-      if (one) { if (ks == 4) REHIP_QMMA_L(TT, false, 1, 4); else if (ks == 2) REHIP_QMMA_L(TT, false, 1, 2); else REHIP_QMMA_L(TT, false, 1, 1); } \
-      else { if (ks == 2) REHIP_QMMA_L(TT, false, 2, 2); else REHIP_QMMA_L(TT, false, 2, 1); }     \
-    }                                                                     \
+#define REHIP_QMMA_L(TT, PA, NT, KS) hipLaunchKernelGGL((moe_qmma_kernel<TT, PA, NT, KS>), grid, block, 0, s, a)
+#define REHIP_QMMA_P(TT, PA)                                                                        \
+  if (one) { if (ks == 2) REHIP_QMMA_L(TT, PA, 1, 2); else REHIP_QMMA_L(TT, PA, 1, 1); }            \
+  else { if (ks == 2) REHIP_QMMA_L(TT, PA, 2, 2); else REHIP_QMMA_L(TT, PA, 2, 1); }
+#define REHIP_QMMA(TT)                                                     \
+  case TT:                                                                 \
+    if (pair == kGateUp) { REHIP_QMMA_P(TT, kGateUp) }                     \
+    else if (pair == kTwoTiles) { REHIP_QMMA_P(TT, kTwoTiles) }            \
+    else { REHIP_QMMA_P(TT, kOneTile) }                                    \
     break;
   switch (type) {
     REHIP_QMMA(T_Q4_0)
@@ -331,6 +340,7 @@ hipError_t launch_moe_qmma(uint32_t type, bool dual, int max_rows, const GemmArg
       return hipErrorInvalidValue;
   }
 #undef REHIP_QMMA
+#undef REHIP_QMMA_P
 #undef REHIP_QMMA_L
   return hipGetLastError();
 }
