@@ -1528,7 +1528,6 @@ int re_moe_forward(re_moe* e, const float* x, size_t tokens, size_t top_k, const
 // ---- device-resident transformer steps ----------------------------------------------------------
 struct re_ffn {
   re_qmat *gate = nullptr, *up = nullptr;
-  MoeGemvTask* d_tasks = nullptr;
   int ntasks = 0;
 };
 
@@ -1677,28 +1676,19 @@ int re_ffn_create(re_qmat* gate, re_qmat* up, re_ffn** out) {
   if (gate->g.type != up->g.type || gate->g.m != up->g.m || gate->g.n != up->g.n)
     return fail(RE_ERR_SIZE, "ffn: gate and up must share type and shape");
   if (gate->g.n > (size_t)kGemvRowsMaxK) return fail(RE_ERR_SIZE, "ffn: rows longer than %d", kGemvRowsMaxK);
-  std::vector<MoeGemvTask> t;
-  for (size_t row = 0; row < gate->g.m; row += kFfnGemvRows) t.push_back({0, (int)row, 0, 1});
   re_ffn* f = new (std::nothrow) re_ffn();
   if (!f) return fail(RE_ERR_ARG, "out of memory");
   f->gate = gate;
   f->up = up;
-  f->ntasks = (int)t.size();
-  if (hipMalloc(&f->d_tasks, t.size() * sizeof(MoeGemvTask)) != hipSuccess) {
-    delete f;
-    return fail(RE_ERR_HIP, "hipMalloc of ffn tasks failed");
-  }
-  if (hipMemcpy(f->d_tasks, t.data(), t.size() * sizeof(MoeGemvTask), hipMemcpyHostToDevice) != hipSuccess) {
-    re_ffn_destroy(f);
-    return fail(RE_ERR_HIP, "upload of ffn tasks failed");
-  }
+  // one workgroup per kFfnGemvRows weight rows; the kernel derives its rows from the workgroup
+  // index (no task list to load)
+  f->ntasks = (int)((gate->g.m + kFfnGemvRows - 1) / kFfnGemvRows);
   *out = f;
   return RE_OK;
 }
 
 void re_ffn_destroy(re_ffn* f) {
   if (!f) return;
-  if (f->d_tasks) (void)hipFree(f->d_tasks);
   delete f;
 }
 
@@ -1715,7 +1705,7 @@ int re_ffn_forward_dev(re_ffn* f, const float* d_x, const float* d_norm_w, float
   g.X = d_x;
   g.xrow = nullptr;
   g.Y = d_h;
-  g.tasks = f->d_tasks;
+  g.tasks = nullptr;                    // rows from the workgroup index
   g.m = (int)f->gate->g.m;
   g.K = (int)f->gate->g.n;
   g.KB = (int)f->gate->g.kb;

@@ -52,6 +52,9 @@ template <> inline constexpr int kBias<T_Q4_0> = 8;
 template <> inline constexpr int kBias<T_Q5_0> = 16;
 template <> inline constexpr int kBias<T_Q8_0> = 128;
 template <> inline constexpr int kBias<T_Q6_K> = 32;
+// run_dot reads the per-16 sums of x only where it takes an offset out after the products: the
+// 4-bit types (their bias or min) and Q5_K (its min)
+template <int T> inline constexpr bool kNeedXs16 = kNibble<T> || kBias<T> == 0;
 
 // Plane slab offsets: plane p of a 64-row slab starts at 64 * (sum of widths before p).
 //

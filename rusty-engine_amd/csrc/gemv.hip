@@ -79,14 +79,16 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs p) {
     reinterpret_cast<float4*>(xl)[i] = v;
   }
   __syncthreads();
-  for (int i = threadIdx.x; i < nv / 4; i += WAVES * 64) {
-    const float4* q = reinterpret_cast<const float4*>(xl + 16 * i);
-    float s = 0.0f;
+  if constexpr (kNeedXs16<T>) {   // per-16 sums of x: only the dots that take out an offset use them
+    for (int i = threadIdx.x; i < nv / 4; i += WAVES * 64) {
+      const float4* q = reinterpret_cast<const float4*>(xl + 16 * i);
+      float s = 0.0f;
 #pragma unroll
-    for (int v = 0; v < 4; ++v) { const float4 t = q[v]; s += t.x; s += t.y; s += t.z; s += t.w; }
-    xs16[i] = s;
+      for (int v = 0; v < 4; ++v) { const float4 t = q[v]; s += t.x; s += t.y; s += t.z; s += t.w; }
+      xs16[i] = s;
+    }
+    __syncthreads();
   }
-  __syncthreads();
 
   float acc = 0.0f;
   for (int base = u0; base < u_end; base += D * WAVES) {
@@ -197,14 +199,16 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_rows_kernel(GemvArgs p) {
     reinterpret_cast<float4*>(xl)[i] = v;
   }
   __syncthreads();
-  for (int i = threadIdx.x; i < nv / 4; i += WAVES * 64) {
-    const float4* q = reinterpret_cast<const float4*>(xl + 16 * i);
-    float s = 0.0f;
+  if constexpr (kNeedXs16<T>) {   // per-16 sums of x: only the dots that take out an offset use them
+    for (int i = threadIdx.x; i < nv / 4; i += WAVES * 64) {
+      const float4* q = reinterpret_cast<const float4*>(xl + 16 * i);
+      float s = 0.0f;
 #pragma unroll
-    for (int v = 0; v < 4; ++v) { const float4 t = q[v]; s += t.x; s += t.y; s += t.z; s += t.w; }
-    xs16[i] = s;
+      for (int v = 0; v < 4; ++v) { const float4 t = q[v]; s += t.x; s += t.y; s += t.z; s += t.w; }
+      xs16[i] = s;
+    }
+    __syncthreads();
   }
-  __syncthreads();
 
   float acc = 0.0f;
   for (int base = slot; base < u_end; base += D * S) {
@@ -335,14 +339,16 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_tile_kernel(GemvArgs p) {
     reinterpret_cast<float4*>(xl)[i] = v;
   }
   __syncthreads();
-  for (int i = threadIdx.x; i < nx / 16; i += WAVES * 64) {
-    const float4* q = reinterpret_cast<const float4*>(xl + 16 * i);
-    float t = 0.0f;
+  if constexpr (kNeedXs16<T>) {   // per-16 sums of x: only the dots that take out an offset use them
+    for (int i = threadIdx.x; i < nx / 16; i += WAVES * 64) {
+      const float4* q = reinterpret_cast<const float4*>(xl + 16 * i);
+      float t = 0.0f;
 #pragma unroll
-    for (int v = 0; v < 4; ++v) { const float4 u = q[v]; t += u.x; t += u.y; t += u.z; t += u.w; }
-    xs16[i] = t;
+      for (int v = 0; v < 4; ++v) { const float4 u = q[v]; t += u.x; t += u.y; t += u.z; t += u.w; }
+      xs16[i] = t;
+    }
+    __syncthreads();
   }
-  __syncthreads();
 
   float acc = 0.0f;
   auto step = [&](int st, const typename B::R (&r)[G]) {

@@ -157,7 +157,7 @@ struct MoeGemvArgs {
   const float* X;             // activation rows, K floats each
   const int* xrow;            // X row of gathered row p (nullptr = p itself)
   float* Y;                   // output row of gathered row p: Y + p * ldy
-  const MoeGemvTask* tasks;
+  const MoeGemvTask* tasks;   // nullptr: workgroup b takes rows b * rows_per_task.. of expert 0, activation row 0
   int m, K, KB, ldy;          // weight rows and row length (per expert)
   int max_rows;               // largest np over the tasks
   const float* norm_w;        // nullptr, or each X row is RMS-normalised first (as GemvArgs)

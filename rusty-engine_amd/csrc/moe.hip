@@ -379,8 +379,13 @@ __global__ __launch_bounds__(WAVES * 64) void moe_gemv_kernel(MoeGemvArgs a) {
   constexpr int S = WAVES * G;
   constexpr int NM = DUAL ? 2 : 1;
   extern __shared__ __attribute__((aligned(16))) float smem[];
-  if (a.ntasks && (int)blockIdx.x >= *a.ntasks) return;   // grid sized for the most tasks
-  const MoeGemvTask task = a.tasks[blockIdx.x];
+  // tasks from the list, or (tasks == nullptr: one activation row, expert 0, the decoder's gate/up
+  // pair) row block blockIdx.x, with no dependent load before the first weight loads
+  MoeGemvTask task{0, (int)blockIdx.x * R, 0, 1};
+  if (a.tasks) {
+    if (a.ntasks && (int)blockIdx.x >= *a.ntasks) return;   // grid sized for the most tasks
+    task = a.tasks[blockIdx.x];
+  }
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int KP = a.KB * B::QK;
@@ -432,14 +437,16 @@ __global__ __launch_bounds__(WAVES * 64) void moe_gemv_kernel(MoeGemvArgs a) {
     reinterpret_cast<float4*>(xl)[i] = v;
   }
   __syncthreads();
-  for (int i = threadIdx.x; i < NB * (KP / 16); i += WAVES * 64) {
-    const float4* q = reinterpret_cast<const float4*>(xl + 16 * i);
-    float sum = 0.0f;
+  if constexpr (kNeedXs16<T>) {   // per-16 sums of x: only the dots that take out an offset use them
+    for (int i = threadIdx.x; i < NB * (KP / 16); i += WAVES * 64) {
+      const float4* q = reinterpret_cast<const float4*>(xl + 16 * i);
+      float sum = 0.0f;
 #pragma unroll
-    for (int v = 0; v < 4; ++v) { const float4 t = q[v]; sum += t.x; sum += t.y; sum += t.z; sum += t.w; }
-    xs16[i] = sum;
+      for (int v = 0; v < 4; ++v) { const float4 t = q[v]; sum += t.x; sum += t.y; sum += t.z; sum += t.w; }
+      xs16[i] = sum;
+    }
+    __syncthreads();
   }
-  __syncthreads();
 
   float acc[NM][NB];
 #pragma unroll
