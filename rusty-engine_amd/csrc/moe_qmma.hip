@@ -119,11 +119,9 @@ __device__ __forceinline__ bf16x8_t ld_x(__amdgpu_buffer_rsrc_t r, uint32_t off)
 // their sums are added in wave order through LDS at the end (deterministic).
 constexpr int kOneTile = 0, kGateUp = 1, kTwoTiles = 2;
 template <int T, int PAIR, int NT, int KS>
-__global__ __launch_bounds__(64 * KS) void moe_qmma_kernel(GemmArgs p) {
+__device__ __forceinline__ void qmma_task(const GemmArgs& p, const GemmTask& t) {
   using B = Blk<T>;
   constexpr int NCH = B::NCH;                       // 32-element chunks per block
-  if (p.ntasks && (int)blockIdx.x >= *p.ntasks) return;   // grid sized for the most tasks
-  const GemmTask t = p.tasks[blockIdx.x];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int rn = t.rn;
@@ -308,6 +306,20 @@ __global__ __launch_bounds__(64 * KS) void moe_qmma_kernel(GemmArgs p) {
       }
     }
   }
+}
+
+// A task of at most 32 rows runs the one-tile body (no MFMAs on an empty second token tile).
+template <int T, int PAIR, int NT, int KS>
+__global__ __launch_bounds__(64 * KS) void moe_qmma_kernel(GemmArgs p) {
+  if (p.ntasks && (int)blockIdx.x >= *p.ntasks) return;   // grid sized for the most tasks
+  const GemmTask t = p.tasks[blockIdx.x];
+  if constexpr (NT == 2) {
+    if (t.rn <= 32) {
+      qmma_task<T, PAIR, 1, KS>(p, t);
+      return;
+    }
+  }
+  qmma_task<T, PAIR, NT, KS>(p, t);
 }
 
 hipError_t launch_moe_qmma(uint32_t type, int pair, int max_rows, const GemmArgs& a, int ntasks, hipStream_t s) {
