@@ -42,10 +42,11 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
 // treated as -inf (the reference's partial_cmp leaves their order unspecified).
 constexpr int kRouteMaxExperts = 1024;
 
+// EPL = experts per lane (n_experts <= 64 EPL).
+template <int EPL>
 __global__ __launch_bounds__(64) void moe_route_kernel(const float* __restrict__ logits, int n_experts, int k,
                                                        int gate, int* __restrict__ ids,
                                                        float* __restrict__ weights) {
-  constexpr int EPL = kRouteMaxExperts / 64;
   __shared__ float topv[kRouteMaxExperts];
   __shared__ int topi[kRouteMaxExperts];
   const int t = blockIdx.x, lane = threadIdx.x;
@@ -130,59 +131,76 @@ __global__ __launch_bounds__(256) void moe_router_logits_kernel(const float* __r
   if (lane == 0) logits[(size_t)t * n_experts + e] = a;
 }
 
-// Grouping on the device, one 1024-thread workgroup: keys (expert << 13 | pair) are sorted by a
-// bitonic network in LDS (pair order inside an expert: the host grouping's order), then
-// xrow[slot] = pair / k and pos[pair] = slot; per-expert counts and starts give the chunks
-// (runs of `chunk` gathered rows) and the task lists, laid out exactly as the host planner lays
-// them out (expert, then chunk, then weight-row task). Pairs with an expert id out of range get
-// pos = -1 and no task (the combine skips them).
+// Grouping on the device, one 1024-thread workgroup, as a stable counting sort by expert (pair
+// order inside an expert: the host grouping's order). Wave w ranks the pairs of its own segment
+// (16 contiguous segments, a multiple of 64 pairs each) 64 at a time: the lanes holding the same
+// expert are found by one ballot per bit of the expert id (each lane keeps the ballots that agree
+// with its bits), a lane's rank is the count of those lanes below it plus the wave's running
+// count of that expert, kept in LDS. Per-expert prefix sums over the waves and over the experts
+// then give slot = start[e] + earlier waves' count + rank, xrow[slot] = pair / k and
+// pos[pair] = slot; per-expert counts and starts give the chunks (runs of `chunk` gathered rows)
+// and the task lists, laid out exactly as the host planner lays them out (expert, then chunk,
+// then weight-row task). Pairs with an expert id out of range get pos = -1 and no task (the
+// combine skips them).
 __device__ __forceinline__ int* meta_xrow(void* m) { return (int*)m; }
 
-__global__ __launch_bounds__(1024) void moe_plan_kernel(const int* __restrict__ ids, MoePlanShape sh,
-                                                        int* __restrict__ meta) {
-  __shared__ uint32_t key[kMoeMaxDevicePairs];
+constexpr int kPlanWaves = 16;
+
+__global__ __launch_bounds__(64 * kPlanWaves) void moe_plan_kernel(const int* __restrict__ ids, MoePlanShape sh,
+                                                                   int* __restrict__ meta) {
+  __shared__ uint32_t key[kMoeMaxDevicePairs];              // (expert << 16) | rank in the segment
+  __shared__ int hist[kPlanWaves * kRouteMaxExperts];       // per wave and expert
   __shared__ int cnt[kRouteMaxExperts], start[kRouteMaxExperts], cstart[kRouteMaxExperts + 1];
-  const int P = sh.pairs, E = sh.n_experts, tid = threadIdx.x;
+  const int P = sh.pairs, E = sh.n_experts, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   int* xrow = meta;
   int* pos = meta + P;
   int* ntasks = meta + 2 * P;
   uint8_t* tasks = (uint8_t*)(meta + 2 * P + 4);
-  int n2 = 1;
-  while (n2 < P) n2 <<= 1;
-  for (int e = tid; e < E; e += 1024) cnt[e] = 0;
-  __syncthreads();
-  for (int p = tid; p < n2; p += 1024) {
-    uint32_t kk = 0xffffffffu;
+  const int seg = (P + 64 * kPlanWaves - 1) / (64 * kPlanWaves) * 64;   // pairs per wave (<= 512)
+  const int nb = 32 - __builtin_clz((unsigned)max(E - 1, 1));            // bits of an expert id
+  int* wh = hist + w * kRouteMaxExperts;   // this wave's counts: only this wave touches them before the barrier
+  for (int e = lane; e < E; e += 64) wh[e] = 0;
+  const uint64_t below = (1ull << lane) - 1, above = ~((2ull << lane) - 1);
+  for (int base = w * seg; base < min(P, (w + 1) * seg); base += 64) {
+    const int p = base + lane;
+    int e = -1;
     if (p < P) {
-      const int e = ids[p];
-      if (e >= 0 && e < E) {
-        kk = ((uint32_t)e << 13) | (uint32_t)p;
-        atomicAdd(&cnt[e], 1);
-      } else {
+      e = ids[p];
+      if (e < 0 || e >= E) {
         pos[p] = -1;
+        key[p] = 0xffffffffu;
+        e = -1;
       }
     }
-    key[p] = kk;
+    const bool valid = e >= 0;
+    uint64_t same = __ballot(valid);
+    for (int b = 0; b < nb; ++b) {
+      const bool bit = valid && ((e >> b) & 1);
+      const uint64_t bal = __ballot(bit);
+      same &= bit ? bal : ~bal;
+    }
+    if (valid) {
+      const int prev = wh[e];
+      key[p] = ((uint32_t)e << 16) | (uint32_t)(prev + __popcll(same & below));
+      if ((same & above) == 0) wh[e] = prev + __popcll(same);   // the highest lane of the expert
+    }
   }
   __syncthreads();
-  // bitonic sort, ascending
-  for (int size = 2; size <= n2; size <<= 1) {
-    for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      for (int i = tid; i < n2 / 2; i += 1024) {
-        const int lo = 2 * i - (i & (stride - 1));
-        const int hi = lo + stride;
-        const bool up = (lo & size) == 0;
-        const uint32_t a = key[lo], b = key[hi];
-        if ((a > b) == up) { key[lo] = b; key[hi] = a; }
-      }
-      __syncthreads();
+  // per expert: the waves' counts become exclusive offsets, their sum the expert's count
+  for (int e = tid; e < E; e += 64 * kPlanWaves) {
+    int run = 0;
+    for (int v = 0; v < kPlanWaves; ++v) {
+      const int c = hist[v * kRouteMaxExperts + e];
+      hist[v * kRouteMaxExperts + e] = run;
+      run += c;
     }
+    cnt[e] = run;
   }
+  __syncthreads();
   // row starts and chunk starts per expert: an exclusive scan over the block, one expert per
   // thread (E <= 1024): wave scans, then the wave totals in order
-  __shared__ int wsum[2][16];
+  __shared__ int wsum[2][kPlanWaves];
   {
-    const int lane = tid & 63, w = tid >> 6;
     const int c = tid < E ? cnt[tid] : 0;
     const int ch = tid < E ? (c + sh.chunk - 1) / sh.chunk : 0;
     int sc = c, sch = ch;
@@ -194,7 +212,7 @@ __global__ __launch_bounds__(1024) void moe_plan_kernel(const int* __restrict__ 
     if (lane == 63) { wsum[0][w] = sc; wsum[1][w] = sch; }
     __syncthreads();
     int base = 0, cbase = 0, ctot = 0;
-    for (int j = 0; j < 16; ++j) {
+    for (int j = 0; j < kPlanWaves; ++j) {
       if (j < w) { base += wsum[0][j]; cbase += wsum[1][j]; }
       ctot += wsum[1][j];
     }
@@ -209,12 +227,13 @@ __global__ __launch_bounds__(1024) void moe_plan_kernel(const int* __restrict__ 
     }
   }
   __syncthreads();
-  for (int i = tid; i < P; i += 1024) {
-    const uint32_t kk = key[i];
+  for (int p = tid; p < P; p += 64 * kPlanWaves) {
+    const uint32_t kk = key[p];
     if (kk == 0xffffffffu) continue;
-    const int p = (int)(kk & 0x1fffu);
-    xrow[i] = p / sh.k;
-    pos[p] = i;
+    const int e = (int)(kk >> 16);
+    const int slot = start[e] + hist[(p / seg) * kRouteMaxExperts + e] + (int)(kk & 0xffffu);
+    xrow[slot] = p / sh.k;
+    pos[p] = slot;
   }
   const int nch = cstart[E];
   const int n_gu = min(nch * sh.tiles_gu, sh.max_gu), n_d = min(nch * sh.tiles_d, sh.max_d);
@@ -254,8 +273,18 @@ size_t moe_meta_bytes(const MoePlanShape& sh) {
 
 hipError_t launch_moe_route(const float* logits, int tokens, int n_experts, int k, int gate, int* ids,
                             float* weights, hipStream_t s) {
-  hipLaunchKernelGGL(moe_route_kernel, dim3((unsigned)tokens), dim3(64), 0, s, logits, n_experts, k, gate, ids,
-                     weights);
+  const int epl = (n_experts + 63) / 64;
+  if (epl <= 1)
+    hipLaunchKernelGGL(moe_route_kernel<1>, dim3((unsigned)tokens), dim3(64), 0, s, logits, n_experts, k, gate, ids, weights);
+  else if (epl <= 2)
+    hipLaunchKernelGGL(moe_route_kernel<2>, dim3((unsigned)tokens), dim3(64), 0, s, logits, n_experts, k, gate, ids, weights);
+  else if (epl <= 4)
+    hipLaunchKernelGGL(moe_route_kernel<4>, dim3((unsigned)tokens), dim3(64), 0, s, logits, n_experts, k, gate, ids, weights);
+  else if (epl <= 8)
+    hipLaunchKernelGGL(moe_route_kernel<8>, dim3((unsigned)tokens), dim3(64), 0, s, logits, n_experts, k, gate, ids, weights);
+  else
+    hipLaunchKernelGGL(moe_route_kernel<kRouteMaxExperts / 64>, dim3((unsigned)tokens), dim3(64), 0, s, logits, n_experts, k,
+                       gate, ids, weights);
   return hipGetLastError();
 }
 
