@@ -222,6 +222,15 @@ bool moe_qmma_path(const re_moe* e, const float* d_x, size_t tokens, int mode) {
          env_size("REHIP_MOE_QMMA", 1) != 0;
 }
 
+// Gathered rows per grouped-GEMM task: 32 (one token tile) while the experts get few rows each,
+// else 64; REHIP_MOE_CHUNK = 32 / 64 overrides for the register-decoded GEMMs.
+int moe_qmma_chunk(bool qmma, bool few) {
+  if (!qmma) return kMoeTile;
+  const size_t v = env_size("REHIP_MOE_CHUNK", 0);
+  if (v == 32 || v == 64) return (int)v;
+  return few ? 32 : kMoeTile;
+}
+
 // The grouped expert GEMV stages each task's activation rows (kMoeGemvBatch rows of K floats
 // plus their per-16 sums) and the wave partials in LDS; when a projection's rows are too long for
 // that, the grouped GEMM tasks (fixed LDS per tile) serve every batch size.
@@ -1114,7 +1123,7 @@ int re_moe_forward_routed_dev(re_moe* e, const float* d_x, size_t tokens, size_t
   sh.k = (int)top_k;
   sh.n_experts = (int)e->n_experts;
   sh.gemv = gemv;
-  sh.chunk = gemv ? (tokens == 1 ? 1 : kMoeGemvBatch) : (qmma && few ? 32 : kMoeTile);
+  sh.chunk = gemv ? (tokens == 1 ? 1 : kMoeGemvBatch) : moe_qmma_chunk(qmma, few);
   if (gemv) {
     const int rd = moe_gemv_rows_down();
     const int rgu = tokens == 1 && e->gg.type == e->gu.type ? moe_gemv_rows_gu1() : kMoeGemvRows;
@@ -1138,8 +1147,11 @@ int re_moe_forward_routed_dev(re_moe* e, const float* d_x, size_t tokens, size_t
     return rc;
   const bool dual = gemv && e->gg.type == e->gu.type;
   if (!dual && ((rc = e->sg.ensure(act)) || (rc = e->su.ensure(act)))) return rc;
+  // the bf16 copy of X (grouped GEMMs in bf16 mode) is made by the planning launch
+  const bool xb = !gemv && moe_bf16_acts(e, d_x, mode);
+  if (xb && (rc = e->sxb.ensure(tokens * e->hidden * 2))) return rc;
   int* dm = (int*)e->dmeta.p;
-  HIP_TRY(launch_moe_plan(d_ids, sh, dm, s));
+  HIP_TRY(launch_moe_plan(d_ids, sh, dm, d_x, xb ? e->sxb.p : nullptr, tokens * e->hidden, s));
   const int* xrow = dm;
   const int* pos = dm + pairs;
   const int* ntasks = dm + 2 * pairs;
@@ -1190,8 +1202,6 @@ int re_moe_forward_routed_dev(re_moe* e, const float* d_x, size_t tokens, size_t
     d.ldy = (int)e->hidden;
     HIP_TRY(launch_moe_gemv(e->gd.type, false, d, sh.max_d, s));
   } else if (qmma) {
-    if ((rc = e->sxb.ensure(tokens * e->hidden * 2))) return rc;
-    HIP_TRY(launch_x_to_bf16(d_x, e->sxb.p, tokens * e->hidden, s));
     const GemmTask* tg = (const GemmTask*)tasks;
     HIP_TRY(moe_qmma_ffn(e, tokens, pairs, sh.chunk, xrow, tg, ntasks, sh.max_gu, tg + sh.max_gu, ntasks + 1,
                          sh.max_d, s));
@@ -1214,10 +1224,7 @@ int re_moe_forward_routed_dev(re_moe* e, const float* d_x, size_t tokens, size_t
     a.w_bytes = (uint32_t)(e->gg.bytes * e->n_experts);
     a.W = e->d_gate;
     a.Y = (float*)e->sg.p;
-    const bool xb = moe_bf16_acts(e, d_x, mode);
     if (xb) {
-      if ((rc = e->sxb.ensure(tokens * e->hidden * 2))) return rc;
-      HIP_TRY(launch_x_to_bf16(d_x, e->sxb.p, tokens * e->hidden, s));
       a.X = e->sxb.p;
       a.x_bytes = (uint32_t)(tokens * e->hidden * 2);
       a.x_bf16 = 1;
@@ -1322,7 +1329,7 @@ int re_moe_forward_dev(re_moe* e, const float* d_x, size_t tokens, size_t top_k,
   const bool few = pairs <= (size_t)kMoeGemvBatch * touched;
   const bool qmma = moe_qmma_path(e, d_x, tokens, mode);
   const bool gemv = !qmma && few && moe_gemv_fits(e);
-  const int chunk = qmma && few ? 32 : kMoeTile;
+  const int chunk = moe_qmma_chunk(qmma, few);
   int max_rows = 0;
   for (size_t x = 0; x < e->n_experts; ++x) max_rows = std::max(max_rows, std::min(count[x], kMoeGemvBatch));
   // 16-row gate/up tasks exist for single-row tasks only (a repeated expert id gives 2+ rows)

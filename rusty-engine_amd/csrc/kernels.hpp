@@ -235,7 +235,9 @@ struct MoePlanShape {
   int max_gu, max_d;            // capacity of the task lists
 };
 size_t moe_meta_bytes(const MoePlanShape& sh);
-hipError_t launch_moe_plan(const int* ids, const MoePlanShape& sh, void* meta, hipStream_t s);
+// x / xb / n: also round the n floats of x to bf16 into xb (n % 8 == 0), or xb = nullptr
+hipError_t launch_moe_plan(const int* ids, const MoePlanShape& sh, void* meta, const float* x, void* xb, size_t n,
+                           hipStream_t s);
 hipError_t launch_swiglu(const float* g, const float* u, float* h, size_t n, hipStream_t s);
 hipError_t launch_swiglu_bf16(const float* g, const float* u, void* h, size_t n, hipStream_t s);
 hipError_t launch_combine(const float* yp, const int* pos, const float* w, float* out, int tokens,

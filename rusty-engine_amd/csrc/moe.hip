@@ -6,7 +6,11 @@
 #include "deq.hpp"
 #include "kernels.hpp"
 
+#include <algorithm>
+
 namespace rehip {
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
 
 
 // h = silu(g) * u, silu(x) = x * (1 / (1 + exp(-x)))  (moe.rs:44-51, 280-283)
@@ -18,20 +22,40 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const float* __restrict__ g
 }
 
 // out[t][c] = sum over j = 0..k-1, in order, of w[t*k+j] * yp[pos[t*k+j]][c]; the sum starts
-// from 0 and every step is a rounded multiply then a rounded add (moe.rs:376-383).
+// from 0 and every step is a rounded multiply then a rounded add (moe.rs:376-383). A thread
+// takes V consecutive columns; the rows of eight pairs are loaded before any is added, so a
+// token's k row reads overlap instead of following one another.
+template <int V>
 __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ yp, const int* __restrict__ pos,
                                                       const float* __restrict__ w, float* __restrict__ out,
                                                       int k, int hidden) {
+  typedef __attribute__((__vector_size__(V * sizeof(float)))) float fv;
   const int t = blockIdx.y;
-  const int c = blockIdx.x * 256 + threadIdx.x;
+  const int c = (blockIdx.x * 256 + threadIdx.x) * V;
   if (c >= hidden) return;
-  float o = 0.0f;
-  for (int j = 0; j < k; ++j) {
-    const int p = pos[t * k + j];
-    if (p < 0) continue;                  // expert id out of range (device routing input)
-    o = __fadd_rn(o, __fmul_rn(w[t * k + j], yp[(size_t)p * hidden + c]));
+  fv o;
+#pragma unroll
+  for (int v = 0; v < V; ++v) o[v] = 0.0f;
+  for (int j0 = 0; j0 < k; j0 += 8) {
+    int pj[8];
+    float wj[8];
+    fv y[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      pj[j] = j0 + j < k ? pos[t * k + j0 + j] : -1;   // -1: past k, or an expert id out of range
+      wj[j] = j0 + j < k ? w[t * k + j0 + j] : 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (pj[j] >= 0) y[j] = *reinterpret_cast<const fv*>(yp + (size_t)pj[j] * hidden + c);
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (pj[j] >= 0) {
+#pragma unroll
+        for (int v = 0; v < V; ++v) o[v] = __fadd_rn(o[v], __fmul_rn(wj[j], y[j][v]));
+      }
   }
-  out[(size_t)t * hidden + c] = o;
+  *reinterpret_cast<fv*>(out + (size_t)t * hidden + c) = o;
 }
 
 // ---- device-side routing and grouping (no host round trip) --------------------------------
@@ -146,8 +170,8 @@ __device__ __forceinline__ int* meta_xrow(void* m) { return (int*)m; }
 
 constexpr int kPlanWaves = 16;
 
-__global__ __launch_bounds__(64 * kPlanWaves) void moe_plan_kernel(const int* __restrict__ ids, MoePlanShape sh,
-                                                                   int* __restrict__ meta) {
+__device__ __forceinline__ void moe_plan_body(const int* __restrict__ ids, const MoePlanShape& sh,
+                                              int* __restrict__ meta) {
   __shared__ uint32_t key[kMoeMaxDevicePairs];              // (expert << 16) | rank in the segment
   __shared__ int hist[kPlanWaves * kRouteMaxExperts];       // per wave and expert
   __shared__ int cnt[kRouteMaxExperts], start[kRouteMaxExperts], cstart[kRouteMaxExperts + 1];
@@ -161,17 +185,24 @@ __global__ __launch_bounds__(64 * kPlanWaves) void moe_plan_kernel(const int* __
   int* wh = hist + w * kRouteMaxExperts;   // this wave's counts: only this wave touches them before the barrier
   for (int e = lane; e < E; e += 64) wh[e] = 0;
   const uint64_t below = (1ull << lane) - 1, above = ~((2ull << lane) - 1);
-  for (int base = w * seg; base < min(P, (w + 1) * seg); base += 64) {
-    const int p = base + lane;
-    int e = -1;
-    if (p < P) {
-      e = ids[p];
-      if (e < 0 || e >= E) {
-        pos[p] = -1;
-        key[p] = 0xffffffffu;
-        e = -1;
-      }
+  // the wave's ids, all loads in flight at once (seg <= 512: at most 8 per lane)
+  constexpr int kSub = kMoeMaxDevicePairs / (64 * kPlanWaves);
+  int ev[kSub];
+#pragma unroll
+  for (int i = 0; i < kSub; ++i) {
+    const int p = w * seg + 64 * i + lane;
+    ev[i] = 64 * i < seg && p < P ? ids[p] : -1;
+  }
+#pragma unroll
+  for (int i = 0; i < kSub; ++i) {
+    const int p = w * seg + 64 * i + lane;
+    if (64 * i >= seg || w * seg + 64 * i >= P) break;   // uniform
+    int e = ev[i];
+    if (p < P && (e < 0 || e >= E)) {
+      pos[p] = -1;
+      key[p] = 0xffffffffu;
     }
+    if (e >= E) e = -1;
     const bool valid = e >= 0;
     uint64_t same = __ballot(valid);
     for (int b = 0; b < nb; ++b) {
@@ -187,14 +218,17 @@ __global__ __launch_bounds__(64 * kPlanWaves) void moe_plan_kernel(const int* __
   }
   __syncthreads();
   // per expert: the waves' counts become exclusive offsets, their sum the expert's count
-  for (int e = tid; e < E; e += 64 * kPlanWaves) {
+  if (tid < E) {
+    int c[kPlanWaves];
+#pragma unroll
+    for (int v = 0; v < kPlanWaves; ++v) c[v] = hist[v * kRouteMaxExperts + tid];
     int run = 0;
+#pragma unroll
     for (int v = 0; v < kPlanWaves; ++v) {
-      const int c = hist[v * kRouteMaxExperts + e];
-      hist[v * kRouteMaxExperts + e] = run;
-      run += c;
+      hist[v * kRouteMaxExperts + tid] = run;
+      run += c[v];
     }
-    cnt[e] = run;
+    cnt[tid] = run;
   }
   __syncthreads();
   // row starts and chunk starts per expert: an exclusive scan over the block, one expert per
@@ -227,7 +261,10 @@ __global__ __launch_bounds__(64 * kPlanWaves) void moe_plan_kernel(const int* __
     }
   }
   __syncthreads();
-  for (int p = tid; p < P; p += 64 * kPlanWaves) {
+#pragma unroll
+  for (int i = 0; i < kSub; ++i) {
+    const int p = tid + 64 * kPlanWaves * i;
+    if (p >= P) break;
     const uint32_t kk = key[p];
     if (kk == 0xffffffffu) continue;
     const int e = (int)(kk >> 16);
@@ -248,21 +285,51 @@ __global__ __launch_bounds__(64 * kPlanWaves) void moe_plan_kernel(const int* __
     r0 = start[e] + r;
     rn = min(sh.chunk, cnt[e] - r);
   };
-  // one thread per chunk: its expert once, then its weight-row tasks (task t = chunk * tiles + tile)
+  // one thread per chunk finds its expert, then the tasks are written with consecutive threads on
+  // consecutive records (task t = chunk * tiles + tile). The chunk table reuses the sort keys:
+  // expert << 20 | first row << 7 | rows (rows <= 64, first row < 8192, expert < 1024).
+  __syncthreads();                                   // every key has been read above
   for (int c = tid; c < nch; c += 1024) {
     int e, r0, rn;
     chunk_of(c, e, r0, rn);
-    if (sh.gemv) {
-      MoeGemvTask* tg = (MoeGemvTask*)tasks;
-      MoeGemvTask* td = tg + sh.max_gu;
-      for (int j = 0, t = c * sh.tiles_gu; j < sh.tiles_gu && t < n_gu; ++j, ++t) tg[t] = {e, j * sh.rows_gu, r0, rn};
-      for (int j = 0, t = c * sh.tiles_d; j < sh.tiles_d && t < n_d; ++j, ++t) td[t] = {e, j * sh.rows_d, r0, rn};
-    } else {
-      GemmTask* tg = (GemmTask*)tasks;
-      GemmTask* td = tg + sh.max_gu;
-      for (int j = 0, t = c * sh.tiles_gu; j < sh.tiles_gu && t < n_gu; ++j, ++t) tg[t] = {e, j, r0, rn};
-      for (int j = 0, t = c * sh.tiles_d; j < sh.tiles_d && t < n_d; ++j, ++t) td[t] = {e, j, r0, rn};
+    key[c] = ((uint32_t)e << 20) | ((uint32_t)r0 << 7) | (uint32_t)rn;
+  }
+  __syncthreads();
+  auto write_tasks = [&](uint8_t* list, int n, int tiles, int rows) {
+    for (int t0 = 0; t0 < n; t0 += 4096) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int t = t0 + 1024 * u + tid;
+        if (t >= n) break;
+        const int c = t / tiles, j = t - c * tiles;
+        const uint32_t kc = key[c];
+        const int e = (int)(kc >> 20), r0 = (int)((kc >> 7) & 0x1fffu), rn = (int)(kc & 0x7fu);
+        if (sh.gemv) reinterpret_cast<MoeGemvTask*>(list)[t] = {e, j * rows, r0, rn};
+        else reinterpret_cast<GemmTask*>(list)[t] = {e, j, r0, rn};
+      }
     }
+  };
+  const size_t rec = sh.gemv ? sizeof(MoeGemvTask) : sizeof(GemmTask);
+  write_tasks(tasks, n_gu, sh.tiles_gu, sh.rows_gu);
+  write_tasks(tasks + (size_t)sh.max_gu * rec, n_d, sh.tiles_d, sh.rows_d);
+}
+
+// The bf16 copy of X for the grouped GEMMs rides along with the plan: workgroups 1.. convert
+// (round to nearest even, as x_to_bf16_kernel), workgroup 0 plans.
+__global__ __launch_bounds__(64 * kPlanWaves) void moe_plan_convert_kernel(const int* __restrict__ ids,
+                                                                           MoePlanShape sh, int* __restrict__ meta,
+                                                                           const float4* __restrict__ x,
+                                                                           bf16x8_t* __restrict__ xb, size_t n8) {
+  if (blockIdx.x == 0) {
+    moe_plan_body(ids, sh, meta);
+    return;
+  }
+  for (size_t i = (size_t)(blockIdx.x - 1) * 1024 + threadIdx.x; i < n8; i += (size_t)(gridDim.x - 1) * 1024) {
+    const float4 a = x[2 * i], b = x[2 * i + 1];
+    bf16x8_t o;
+    o[0] = (__bf16)a.x; o[1] = (__bf16)a.y; o[2] = (__bf16)a.z; o[3] = (__bf16)a.w;
+    o[4] = (__bf16)b.x; o[5] = (__bf16)b.y; o[6] = (__bf16)b.z; o[7] = (__bf16)b.w;
+    xb[i] = o;
   }
 }
 
@@ -357,8 +424,13 @@ hipError_t launch_moe_router_logits(const float* x, const float* router_w, int t
   return hipGetLastError();
 }
 
-hipError_t launch_moe_plan(const int* ids, const MoePlanShape& sh, void* meta, hipStream_t s) {
-  hipLaunchKernelGGL(moe_plan_kernel, dim3(1), dim3(1024), 0, s, ids, sh, (int*)meta);
+hipError_t launch_moe_plan(const int* ids, const MoePlanShape& sh, void* meta, const float* x, void* xb, size_t n,
+                           hipStream_t s) {
+  if (xb && n % 8) return hipErrorInvalidValue;
+  const size_t n8 = xb ? n / 8 : 0;
+  const unsigned conv = (unsigned)std::min<size_t>((n8 + 1023) / 1024, 255);
+  hipLaunchKernelGGL(moe_plan_convert_kernel, dim3(1 + conv), dim3(64 * kPlanWaves), 0, s, ids, sh, (int*)meta,
+                     (const float4*)x, (bf16x8_t*)xb, n8);
   return hipGetLastError();
 }
 
@@ -385,8 +457,14 @@ hipError_t launch_swiglu(const float* g, const float* u, float* h, size_t n, hip
 hipError_t launch_combine(const float* yp, const int* pos, const float* w, float* out, int tokens, int k,
                           int hidden, hipStream_t s) {
   if (tokens == 0) return hipSuccess;
-  hipLaunchKernelGGL(combine_kernel, dim3((unsigned)((hidden + 255) / 256), (unsigned)tokens), dim3(256), 0, s,
-                     yp, pos, w, out, k, hidden);
+  // four columns a thread where every row start is 16-byte aligned
+  const bool v4 = hidden % 4 == 0 && ((uintptr_t)yp | (uintptr_t)out) % 16 == 0;
+  if (v4)
+    hipLaunchKernelGGL(combine_kernel<4>, dim3((unsigned)((hidden / 4 + 255) / 256), (unsigned)tokens), dim3(256), 0,
+                       s, yp, pos, w, out, k, hidden);
+  else
+    hipLaunchKernelGGL(combine_kernel<1>, dim3((unsigned)((hidden + 255) / 256), (unsigned)tokens), dim3(256), 0, s,
+                       yp, pos, w, out, k, hidden);
   return hipGetLastError();
 }
 
