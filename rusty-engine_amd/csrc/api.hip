@@ -145,6 +145,26 @@ struct Staging {
   }
 };
 
+// pinned host buffer (grown on demand) and the device's address of it
+struct Pinned {
+  void* h = nullptr;
+  void* d = nullptr;
+  size_t cap = 0;
+  int ensure(size_t bytes) {
+    if (bytes <= cap) return RE_OK;
+    release();
+    HIP_TRY(hipHostMalloc(&h, bytes, hipHostMallocDefault));
+    HIP_TRY(hipHostGetDevicePointer(&d, h, 0));
+    cap = bytes;
+    return RE_OK;
+  }
+  void release() {
+    if (h) (void)hipHostFree(h);
+    h = d = nullptr;
+    cap = 0;
+  }
+};
+
 }  // namespace
 
 struct re_qmat {
@@ -158,6 +178,7 @@ struct re_qmat {
   std::mutex mu;
   hipStream_t stream = nullptr;
   Staging sx, sy, spart;
+  Pinned hx, hy;                          // host-pointer calls: x staged for the copy, y written in place
 };
 
 struct re_moe {
@@ -167,6 +188,7 @@ struct re_moe {
   std::mutex mu;
   hipStream_t stream = nullptr;
   Staging sx, sout, sg, su, sh, syp, smeta;
+  Pinned hx, hout;                        // host-buffer calls: pinned staging of x and out
   Staging sxb;                            // bf16 copy of the activation rows (grouped GEMM path)
   Staging dmeta, droute;                  // device-routed path: plan + task lists; logits, ids, weights
   // pinned host staging of the per-call routing metadata, reused once its last upload is done
@@ -595,6 +617,8 @@ void re_qmat_destroy(re_qmat* q) {
   q->sx.release();
   q->sy.release();
   q->spart.release();
+  q->hx.release();
+  q->hy.release();
   if (q->stream) (void)hipStreamDestroy(q->stream);
   delete q;
 }
@@ -775,11 +799,28 @@ int re_qmat_matmul(re_qmat* q, const float* x, size_t rows, float* y, int mode) 
   std::lock_guard<std::mutex> lk(q->mu);
   const size_t xb = rows * q->g.n * sizeof(float), yb = rows * q->g.m * sizeof(float);
   int rc;
-  if ((rc = q->sx.ensure(xb)) || (rc = q->sy.ensure(yb))) return rc;
-  HIP_TRY(hipMemcpyAsync(q->sx.p, x, xb, hipMemcpyHostToDevice, q->stream));
-  if ((rc = re_qmat_matmul_dev(q, (const float*)q->sx.p, rows, (float*)q->sy.p, mode, q->stream))) return rc;
-  HIP_TRY(hipMemcpyAsync(y, q->sy.p, yb, hipMemcpyDeviceToHost, q->stream));
+  // x goes through pinned staging (a DMA copy, no pageable bounce); the kernels write y straight
+  // into pinned host memory, read back after the stream synchronizes. REHIP_HOST_IO = 0: pageable
+  // copies both ways, 1: pinned copies both ways.
+  const size_t io = env_size("REHIP_HOST_IO", 2);
+  if ((rc = q->sx.ensure(xb))) return rc;
+  if (io == 0) {
+    if ((rc = q->sy.ensure(yb))) return rc;
+    HIP_TRY(hipMemcpyAsync(q->sx.p, x, xb, hipMemcpyHostToDevice, q->stream));
+    if ((rc = re_qmat_matmul_dev(q, (const float*)q->sx.p, rows, (float*)q->sy.p, mode, q->stream))) return rc;
+    HIP_TRY(hipMemcpyAsync(y, q->sy.p, yb, hipMemcpyDeviceToHost, q->stream));
+    HIP_TRY(hipStreamSynchronize(q->stream));
+    return RE_OK;
+  }
+  if ((rc = q->hx.ensure(xb)) || (rc = q->hy.ensure(yb))) return rc;
+  if (io == 1 && (rc = q->sy.ensure(yb))) return rc;
+  std::memcpy(q->hx.h, x, xb);
+  HIP_TRY(hipMemcpyAsync(q->sx.p, q->hx.h, xb, hipMemcpyHostToDevice, q->stream));
+  float* dy = io == 1 ? (float*)q->sy.p : (float*)q->hy.d;
+  if ((rc = re_qmat_matmul_dev(q, (const float*)q->sx.p, rows, dy, mode, q->stream))) return rc;
+  if (io == 1) HIP_TRY(hipMemcpyAsync(q->hy.h, q->sy.p, yb, hipMemcpyDeviceToHost, q->stream));
   HIP_TRY(hipStreamSynchronize(q->stream));
+  std::memcpy(y, q->hy.h, yb);
   return RE_OK;
 }
 
@@ -964,6 +1005,8 @@ void re_moe_destroy(re_moe* e) {
   if (e->d_up) (void)hipFree(e->d_up);
   if (e->d_down) (void)hipFree(e->d_down);
   for (Staging* s : {&e->sx, &e->sout, &e->sg, &e->su, &e->sh, &e->syp, &e->smeta, &e->sxb}) s->release();
+  e->hx.release();
+  e->hout.release();
   if (e->meta_ev) (void)hipEventSynchronize(e->meta_ev);
   if (e->meta_ev) (void)hipEventDestroy(e->meta_ev);
   if (e->hmeta) (void)hipHostFree(e->hmeta);
@@ -1521,13 +1564,17 @@ int re_moe_forward(re_moe* e, const float* x, size_t tokens, size_t top_k, const
   std::lock_guard<std::mutex> lk(e->mu);
   int rc;
   const size_t xb = tokens * e->hidden * sizeof(float);
-  if ((rc = e->sx.ensure(xb)) || (rc = e->sout.ensure(xb))) return rc;
-  HIP_TRY(hipMemcpyAsync(e->sx.p, x, xb, hipMemcpyHostToDevice, e->stream));
+  if ((rc = e->sx.ensure(xb)) || (rc = e->sout.ensure(xb)) || (rc = e->hx.ensure(xb)) || (rc = e->hout.ensure(xb)))
+    return rc;
+  // through pinned staging: the copies are DMA transfers without a pageable bounce
+  std::memcpy(e->hx.h, x, xb);
+  HIP_TRY(hipMemcpyAsync(e->sx.p, e->hx.h, xb, hipMemcpyHostToDevice, e->stream));
   if ((rc = re_moe_forward_dev(e, (const float*)e->sx.p, tokens, top_k, ids, weights, (float*)e->sout.p, mode,
                                e->stream)))
     return rc;
-  HIP_TRY(hipMemcpyAsync(out, e->sout.p, xb, hipMemcpyDeviceToHost, e->stream));
+  HIP_TRY(hipMemcpyAsync(e->hout.h, e->sout.p, xb, hipMemcpyDeviceToHost, e->stream));
   HIP_TRY(hipStreamSynchronize(e->stream));
+  std::memcpy(out, e->hout.h, xb);
   return RE_OK;
 }
 

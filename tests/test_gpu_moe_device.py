@@ -134,6 +134,29 @@ def test_forward_routed_equals_host_routed(T, E, k):
     moe.close()
 
 
+def test_host_routed_large_batch_then_small():
+    """More (token, expert) pairs than the device planner takes (8192), which only the host-routed
+    call serves, then a small call on the same experts (staging buffers already grown); against
+    the oracle (f32 1e-4, bf16 1e-2 relative to norm)."""
+    E, hidden, inter, k = 16, 256, 256, 8
+    for T in (1040, 7):
+        gate, up, down_, x, logits = moe_case(5000 + T, E, hidden, inter, T, k)
+        ids = np.zeros((T, k), np.uint32)
+        wts = np.zeros((T, k), np.float32)
+        for t in range(T):
+            ids[t], wts[t] = O.top_k(logits[t], k)
+        if T == 1040:
+            moe = rehip.MoeExperts(rehip.Q4_K, gate, rehip.Q4_K, up, rehip.Q6_K, down_, E, hidden, inter)
+            g0, u0, d0 = gate, up, down_
+        want = O.moe_ffn(rehip.Q4_K, g0, rehip.Q4_K, u0, rehip.Q6_K, d0, E, hidden, inter, x, T, k,
+                         ids.reshape(-1), wts.reshape(-1))
+        for mode, tol in [(rehip.MODE_F32, 1e-4), (rehip.MODE_BF16, 1e-2)]:
+            got = moe.forward(x, T, k, ids.reshape(-1), wts.reshape(-1), mode)
+            rel = np.linalg.norm(got - want) / np.linalg.norm(want)
+            assert rel <= tol, (T, mode, rel)
+    moe.close()
+
+
 def test_forward_routed_skips_out_of_range_ids():
     E, hidden, inter, T, k = 8, 256, 128, 3, 2
     gate, up, down_, x, logits = moe_case(77, E, hidden, inter, T, k)

@@ -92,7 +92,13 @@ def test_resident_dequant_matches_flat_dequant(t):
     assert np.array_equal(out.download().view(np.uint32), want.view(np.uint32))
 
 
-def test_device_entry_points_match_host_entry_points():
+@pytest.mark.parametrize("io", ["0", "1", "2"])
+def test_device_entry_points_match_host_entry_points(io, monkeypatch):
+    """Host-pointer calls (re_qmat_matvec / re_qmat_matmul) give the device calls' bits whatever
+    the transfer: pageable copies (REHIP_HOST_IO=0), pinned copies (1), or pinned x with y written
+    by the kernels straight into pinned host memory (2, the default), including a split GEMV and
+    a split-K GEMM whose reduce writes y."""
+    monkeypatch.setenv("REHIP_HOST_IO", io)
     rng = np.random.default_rng(17)
     t, m, n, rows = rehip.Q4_K, 256, 1024, 33
     w = synth.weight_bytes(rng, t, m, n)
@@ -107,6 +113,19 @@ def test_device_entry_points_match_host_entry_points():
     q.matvec_dev(dx, dy, stream=s)
     s.synchronize()
     assert np.array_equal(dy.download(count=m), q.matvec(x[:n]))
+    q.close()
+    for t, m, n, rows in [(rehip.Q6_K, 96, 14336, 1), (rehip.Q6_K, 896, 4864, 64), (rehip.Q5_0, 4864, 896, 1)]:
+        w = synth.weight_bytes(rng, t, m, n)
+        x = synth.activations(rng, rows, n)
+        q = qmat(t, w, m, n)
+        dx = hip.DeviceBuffer.from_array(x)
+        dy = hip.DeviceBuffer(rows * m * 4)
+        q.matmul_dev(dx, rows, dy, rehip.MODE_F32, stream=s)
+        s.synchronize()
+        assert np.array_equal(dy.download(), q.matmul(x, rows, rehip.MODE_F32)), (t, m, n, rows)
+        if rows == 1:
+            assert np.array_equal(dy.download(), q.matvec(x)), (t, m, n)
+        q.close()
     s.destroy()
 
 
