@@ -10,6 +10,8 @@ X[N x 4864]:
   `warmup` untimed ones; value = algorithmic bytes per launch (per copy: stored GGUF weight
   bytes + f32 x + f32 y) / average launch time from HIP events on the launch stream.
   single_launch: one 3.6 MB GEMV per launch (the latency a decode step sees).
+* host_matvec: re_qmat_matvec with host pointers per decode projection (x in, GEMV, y out,
+  synchronise): what QMat::matvec costs a host caller per call.
 * gemm: the prefill GEMMs of the two matmul configurations, C1 Q5_0 W[4864 x 896] and
   C2 Q6_K W[896 x 4864], at N = 961 and N = 64, in bf16-MFMA mode and in the f32-strict mode
   (the reference's precision), each against its roofline: FLOP = 2 N m K over the bf16 (2.5
@@ -246,6 +248,29 @@ def time_gemv_batched(t, m, k, launches, seed):
     nbytes = algorithmic_bytes(t, m, k, 1) * copies
     return {"type": rehip.TYPE_NAMES[t], "m": m, "k": k, "copies": copies, "us_per_launch": us, "bytes": nbytes,
             "gbs": nbytes / (us * 1e-6) / 1e9, "frac_hbm": nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, "plan": plan}
+
+
+def time_host_matvec(calls=200):
+    """re_qmat_matvec with host pointers (what QMat::matvec costs a host caller): copy x in, the
+    GEMV, y back, stream synchronisation, per call, for the Qwen2.5-0.5B decode projections."""
+    import rehip
+    from rehip import synth
+    res = {}
+    for name, t, m, k in (("q_o", rehip.Q4_K, 896, 896), ("k_v", rehip.Q4_K, 128, 896),
+                          ("gate_up", rehip.Q4_K, 4864, 896), ("down", rehip.Q6_K, 896, 4864),
+                          ("lm_head", rehip.Q8_0, 151936, 896)):
+        rng = np.random.default_rng(311)
+        q = rehip.QMat.from_bytes(t, synth.weight_bytes(rng, t, m, k), m, k)
+        x = synth.activations(rng, 1, k).reshape(-1)
+        for _ in range(20):
+            q.matvec(x)
+        n = calls if m < 100000 else calls // 4
+        t0 = time.perf_counter()
+        for _ in range(n):
+            q.matvec(x)
+        res[name] = {"type": rehip.TYPE_NAMES[t], "m": m, "k": k, "us_per_call": (time.perf_counter() - t0) / n * 1e6}
+        q.close()
+    return res
 
 
 def decode_floor_bytes(mb):
@@ -684,6 +709,7 @@ def main():
 
     single_ms = timed(lambda: singles(min(ns, 200)), lambda: singles(ns), ns)
     stack.close()
+    host_mv = time_host_matvec()
 
     # ---- prefill GEMMs: C1 and C2 at N = 961 and C2 at N = 64, both modes -------------------------
     gemm = {}
@@ -737,6 +763,7 @@ def main():
                           "frac_hbm": per_copy / (single_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
                           "note": "one 3.6 MB GEMV per launch, back to back in a graph: bounded by the "
                                   "per-launch floor, not HBM"},
+        "host_matvec": host_mv,
         "gemm": gemm,
         "moe": moe_res,
         "parity_ok": parity_ok and all(v.get("parity_ok", True) for v in gemm.values()),
