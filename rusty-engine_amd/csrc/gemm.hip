@@ -656,12 +656,17 @@ GemmPlan plan_gemm(int m, int n, int K, int mode) {
     pl.kgroups = 1;
   } else {
     pl.tile = GemmTile::k64x64;
-    pl.kgroups = gemm_kgroups(pl.tile, mode, t64, steps);
+    // f32 over many tiles: spread K over workgroups rather than over K-groups inside them (C2 at
+    // N = 961: 224 tiles, two K splits of one group each, 116 instead of 129 us for one K-group
+    // pair per split)
+    const bool wide = mode == 1 && t64 >= 128;
+    pl.kgroups = wide ? 1 : gemm_kgroups(pl.tile, mode, t64, steps);
     // few tiles over a deep K: also split the K steps over workgroups when the partial tiles stay
     // small (each split keeps >= 2 steps per K-group)
     const long groups = t64 * pl.kgroups;
-    if (groups < 512 && steps >= 4 * pl.kgroups) {
-      long splits = (512 + groups - 1) / groups;
+    const long target = wide ? 448 : 512;
+    if (groups < target && steps >= 4 * pl.kgroups) {
+      long splits = (target + groups - 1) / groups;
       splits = std::min<long>(splits, steps / (2 * pl.kgroups));
       const long partial_bytes = splits * (long)n * m * 4;
       if (partial_bytes <= (16l << 20) && splits > 1) pl.splits = (int)splits;
