@@ -166,8 +166,6 @@ __global__ __launch_bounds__(256) void moe_router_logits_kernel(const float* __r
 // and the task lists, laid out exactly as the host planner lays them out (expert, then chunk,
 // then weight-row task). Pairs with an expert id out of range get pos = -1 and no task (the
 // combine skips them).
-__device__ __forceinline__ int* meta_xrow(void* m) { return (int*)m; }
-
 constexpr int kPlanWaves = 16;
 
 __device__ __forceinline__ void moe_plan_body(const int* __restrict__ ids, const MoePlanShape& sh,

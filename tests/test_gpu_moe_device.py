@@ -134,6 +134,26 @@ def test_forward_routed_equals_host_routed(T, E, k):
     moe.close()
 
 
+@pytest.mark.parametrize("T,E,k", [(1023, 520, 8), (1024, 520, 8), (257, 1, 1), (96, 3, 2)])
+def test_device_planner_extremes(T, E, k):
+    """The device planner at its limits: 8184 and 8192 (token, expert) pairs (every wave's
+    segment full, ten-bit expert ids), one expert, and a pair count that is not a multiple of 64.
+    Device-routed equals host-routed bit for bit (both take the grouped GEMM path here)."""
+    hidden, inter = 256, 256
+    gate, up, down_, x, logits = moe_case(7000 + T + E, E, hidden, inter, T, k)
+    ids = np.argsort(-logits, axis=1, kind="stable")[:, :k].astype(np.int32)
+    wts = np.random.default_rng(T).uniform(0.1, 1.0, (T, k)).astype(np.float32)
+    moe = rehip.MoeExperts(rehip.Q4_K, gate, rehip.Q4_K, up, rehip.Q6_K, down_, E, hidden, inter)
+    xd, idd, wd = B.from_array(x), B.from_array(ids.reshape(-1)), B.from_array(wts.reshape(-1))
+    for mode in (rehip.MODE_F32, rehip.MODE_BF16):
+        out = B(T * hidden * 4)
+        moe.forward_routed_dev(xd, T, k, idd, wd, out, mode)
+        got = down(out, T * hidden)
+        host = moe.forward(x, T, k, ids.reshape(-1).astype(np.uint32), wts.reshape(-1), mode)
+        assert np.array_equal(got, host), mode
+    moe.close()
+
+
 def test_host_routed_large_batch_then_small():
     """More (token, expert) pairs than the device planner takes (8192), which only the host-routed
     call serves, then a small call on the same experts (staging buffers already grown); against
