@@ -1058,6 +1058,61 @@ int moe_add_shared(re_moe* e, const float* d_x, size_t tokens, float* d_out, int
   return RE_OK;
 }
 
+// One token routed to k <= 8 experts with one gate/up type: the gate/up GEMV tasks come straight
+// from the ids (no planning launch) and the down projection and the combine are one launch.
+// REHIP_MOE_ONE=0 keeps the general path.
+static bool moe_one_token_ok(const re_moe* e, size_t tokens, size_t top_k) {
+  return tokens == 1 && top_k <= (size_t)kMoeOneTokenMaxK && e->gg.type == e->gu.type && moe_gemv_fits(e) &&
+         moe_down_combine_lds(e->gd.type, (int)e->gd.kb, (int)top_k) <= kMaxLdsBytes &&
+         env_size("REHIP_MOE_ONE", 1) != 0;
+}
+
+// d_ids / d_w: device ids and weights, or nullptr with h_ids / h_w on the host (passed by value)
+static int moe_one_token(re_moe* e, const float* d_x, size_t top_k, const int* d_ids, const float* d_w,
+                         const uint32_t* h_ids, const float* h_w, float* d_out, int mode, hipStream_t s) {
+  int rc;
+  if ((rc = e->sh.ensure(top_k * e->inter * sizeof(float)))) return rc;
+  const int rgu = moe_gemv_rows_gu1();
+  MoeGemvArgs g{};
+  g.rows_per_task = rgu;
+  g.max_rows = 1;
+  g.X = d_x;
+  g.ids = d_ids;
+  g.id_inline = d_ids ? 0 : 1;
+  if (!d_ids)
+    for (size_t j = 0; j < top_k; ++j) g.id_v[j] = (int)h_ids[j];
+  g.id_tiles = (int)((e->inter + rgu - 1) / rgu);
+  g.n_experts = (int)e->n_experts;
+  g.m = (int)e->inter;
+  g.K = (int)e->hidden;
+  g.KB = (int)e->gg.kb;
+  g.ldy = (int)e->inter;
+  g.w_stride = e->gg.bytes;
+  g.W0 = e->d_gate;
+  g.W1 = e->d_up;
+  g.Y = (float*)e->sh.p;
+  HIP_TRY(launch_moe_gemv(e->gg.type, true, g, (int)top_k * g.id_tiles, s));
+  MoeDownCombineArgs d{};
+  d.W = e->d_down;
+  d.w_stride = e->gd.bytes;
+  d.H = (const float*)e->sh.p;
+  d.ids = d_ids;
+  d.wts = d_w;
+  if (!d_ids)
+    for (size_t j = 0; j < top_k; ++j) {
+      d.id_v[j] = (int)h_ids[j];
+      d.w_v[j] = h_w[j];
+    }
+  d.out = d_out;
+  d.m = (int)e->hidden;
+  d.K = (int)e->inter;
+  d.KB = (int)e->gd.kb;
+  d.k = (int)top_k;
+  d.n_experts = (int)e->n_experts;
+  HIP_TRY(launch_moe_down_combine(e->gd.type, d, s));
+  return moe_add_shared(e, d_x, 1, d_out, mode, s);
+}
+
 }  // namespace
 
 namespace {
@@ -1155,6 +1210,8 @@ int re_moe_forward_routed_dev(re_moe* e, const float* d_x, size_t tokens, size_t
       pairs * e->inter * sizeof(float) >= (1ull << 31))
     return fail(RE_ERR_SIZE, "MoE operands must stay below 2 GiB");
   hipStream_t s = (hipStream_t)stream;
+  if (moe_one_token_ok(e, tokens, top_k))
+    return moe_one_token(e, d_x, top_k, d_ids, d_weights, nullptr, nullptr, d_out, mode, s);
   // the grouping runs on the device, so the path is chosen from the batch size alone: the
   // grouped GEMV while an expert would get few rows on average (pairs <= 2 x experts); the
   // register-decoded grouped GEMMs take 32-row chunks there (one token tile) and 64 beyond
@@ -1347,6 +1404,10 @@ int re_moe_forward_dev(re_moe* e, const float* d_x, size_t tokens, size_t top_k,
   for (size_t p = 0; p < pairs; ++p)
     if (ids[p] >= e->n_experts) return fail(RE_ERR_ARG, "expert id %u out of range (%zu experts)", ids[p], e->n_experts);
   hipStream_t s = (hipStream_t)stream;
+
+  // one token: its ids and weights ride in the kernel arguments (no upload)
+  if (moe_one_token_ok(e, tokens, top_k))
+    return moe_one_token(e, d_x, top_k, nullptr, nullptr, ids, weights, d_out, mode, s);
 
   // group the pairs by expert, keeping (token, slot) order inside an expert
   std::vector<int> count(e->n_experts + 1, 0), start(e->n_experts + 1, 0);

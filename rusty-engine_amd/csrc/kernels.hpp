@@ -164,7 +164,31 @@ struct MoeGemvArgs {
   float norm_eps;
   const int* ntasks;          // nullptr, or the task count on the device (larger grids exit early)
   int rows_per_task;          // kMoeGemvRows, or kFfnGemvRows (single-row dual launches only)
+  // one activation row routed to k experts (tasks == nullptr, ids or id_inline): workgroup b takes
+  // rows (b % id_tiles) * rows_per_task.. of expert ids[b / id_tiles] (id_v when id_inline) and
+  // writes output row b / id_tiles; an id outside [0, n_experts) leaves its row unwritten (the
+  // down + combine launch skips it)
+  const int* ids;
+  int id_tiles, n_experts, id_inline;
+  int id_v[8];
 };
+// Down projection and combine of one token routed to k <= kMoeOneTokenMaxK experts, one launch:
+// out[r] = sum over j (in order, skipping ids outside [0, n_experts)) of w[j] * (Wd[ids[j]] row r . h[j])
+constexpr int kMoeOneTokenMaxK = 8;
+static_assert(sizeof(MoeGemvArgs::id_v) / sizeof(int) == kMoeOneTokenMaxK, "inline ids of a one-token call");
+struct MoeDownCombineArgs {
+  const uint8_t* W;           // tiled slabs of the down stack (expert 0)
+  size_t w_stride;            // bytes between experts
+  const float* H;             // k rows of K floats (SwiGLU outputs)
+  const int* ids;             // device ids and weights, or nullptr: id_v / w_v (host calls)
+  const float* wts;
+  float* out;                 // m floats
+  int m, K, KB, k, n_experts;
+  int id_v[kMoeOneTokenMaxK];
+  float w_v[kMoeOneTokenMaxK];
+};
+hipError_t launch_moe_down_combine(uint32_t type, const MoeDownCombineArgs& a, hipStream_t s);
+size_t moe_down_combine_lds(uint32_t type, int KB, int k);
 // weight rows per expert task: with 16, staging the task's activation rows costs as many bytes
 // as its weights; 64 leaves too few tasks
 constexpr int kMoeGemvRows = 32;

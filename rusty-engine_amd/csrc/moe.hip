@@ -490,6 +490,11 @@ __global__ __launch_bounds__(WAVES * 64) void moe_gemv_kernel(MoeGemvArgs a) {
   if (a.tasks) {
     if (a.ntasks && (int)blockIdx.x >= *a.ntasks) return;   // grid sized for the most tasks
     task = a.tasks[blockIdx.x];
+  } else if (a.ids || a.id_inline) {
+    const int j = (int)blockIdx.x / a.id_tiles;
+    const int e = a.ids ? a.ids[j] : a.id_v[j];
+    if (e < 0 || e >= a.n_experts) return;
+    task = {e, ((int)blockIdx.x - j * a.id_tiles) * R, j, 1};
   }
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -528,7 +533,7 @@ __global__ __launch_bounds__(WAVES * 64) void moe_gemv_kernel(MoeGemvArgs a) {
     float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
     if (nb < task.np && k < a.K) {
       const int p = task.p0 + nb;
-      const int xr = a.xrow ? a.xrow[p] : p;
+      const int xr = a.ids || a.id_inline ? 0 : (a.xrow ? a.xrow[p] : p);   // routed by ids: the one row
       v = *reinterpret_cast<const float4*>(a.X + (size_t)xr * a.K + k);
       if (a.norm_w) {
         float t = __builtin_fmaf(v.x, v.x, __builtin_fmaf(v.y, v.y, __builtin_fmaf(v.z, v.z, v.w * v.w)));
@@ -630,6 +635,182 @@ __global__ __launch_bounds__(WAVES * 64) void moe_gemv_kernel(MoeGemvArgs a) {
       float* y = a.Y + (size_t)(task.p0 + nb) * a.ldy + wrow;
       *y = DUAL ? silu_mul(v[0], v[NM - 1]) : v[0];
     }
+  }
+}
+
+// One token's down projection and weighted combine in one launch (moe.rs:376-383 after
+// moe.rs:288-300): a workgroup owns R output rows and runs over the k routed experts' weight
+// rows for them (lane l serves row l % R; the 64 / R lane groups of every wave take the chunks
+// of expert after expert in turn, so one load reads R * 16 contiguous bytes), each dotted with
+// that expert's SwiGLU row staged in LDS. The k sums of a row fold over lane groups by a fixed
+// xor tree and over waves in wave order; then out[r] = sum over j in order of w[j] * y[j][r]
+// (each a rounded multiply then a rounded add, from 0), skipping ids out of range, as the
+// combine. Row blocks are given to XCDs in contiguous runs (workgroup b runs on XCD b % 8).
+template <int T, int R, int WAVES, int D>
+__global__ __launch_bounds__(WAVES * 64) void moe_down_combine_kernel(MoeDownCombineArgs a) {
+  using B = Blk<T>;
+  constexpr int NCH = B::NCH;
+  constexpr int KM = kMoeOneTokenMaxK;
+  constexpr int G = 64 / R;
+  constexpr int S = WAVES * G;
+  extern __shared__ __attribute__((aligned(16))) float smem[];
+  const int nblk = (a.m + R - 1) / R;
+  const int per = (nblk + 7) / 8;
+  const int blk = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
+  if (blk >= nblk) return;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int KP = a.KB * B::QK;
+  float* hl = smem;                      // [k][KP]
+  float* hs16 = smem + KM * KP;          // [k][KP/16]
+  float* red = hs16 + KM * (KP / 16);    // [WAVES][KM][R]
+  const int row = blk * R + (lane % R);
+  const int tile = row >> 6, rr = row & 63;
+  const int slot = wave * G + lane / R;
+  const int u_pair = a.KB * NCH;         // units (chunks) per expert row
+  const int k = a.k;
+  int ex[KM];
+  bool ok[KM];
+#pragma unroll
+  for (int j = 0; j < KM; ++j) {
+    ex[j] = j < k ? (a.ids ? a.ids[j] : a.id_v[j]) : -1;
+    ok[j] = ex[j] >= 0 && ex[j] < a.n_experts;
+  }
+  // unit u: chunk u % u_pair of expert j = u / u_pair (an id out of range reads expert 0, unused)
+  auto base_of = [&](int j) {
+    int e = 0;
+#pragma unroll
+    for (int q = 0; q < KM; ++q)
+      if (q == j && ok[q]) e = ex[q];
+    return a.W + (size_t)e * a.w_stride + (size_t)tile * a.KB * B::SLAB;
+  };
+  const int u_end = k * u_pair;
+  typename B::CR ring[D];
+#pragma unroll
+  for (int i = 0; i < D; ++i) {
+    const int u = slot + i * S;
+    if (u < u_end) {
+      const int j = u / u_pair, c = u - j * u_pair;
+      B::load_chunk(base_of(j) + (size_t)(c / NCH) * B::SLAB, rr, c % NCH, ring[i]);
+    }
+  }
+  for (int i = threadIdx.x; i < k * KP / 4; i += WAVES * 64) {
+    const int j = i / (KP / 4), q = 4 * (i - j * (KP / 4));
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (q < a.K) v = *reinterpret_cast<const float4*>(a.H + (size_t)j * a.K + q);
+    reinterpret_cast<float4*>(hl)[j * (KP / 4) + q / 4] = v;
+  }
+  __syncthreads();
+  if constexpr (kNeedXs16<T>) {
+    for (int i = threadIdx.x; i < k * (KP / 16); i += WAVES * 64) {
+      const int j = i / (KP / 16), q = i - j * (KP / 16);
+      const float4* hv = reinterpret_cast<const float4*>(hl + j * KP + 16 * q);
+      float sum = 0.0f;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) { const float4 t = hv[v]; sum += t.x; sum += t.y; sum += t.z; sum += t.w; }
+      hs16[j * (KP / 16) + q] = sum;
+    }
+    __syncthreads();
+  }
+  float acc[KM];
+#pragma unroll
+  for (int j = 0; j < KM; ++j) acc[j] = 0.0f;
+  for (int b0 = slot; b0 < u_end; b0 += D * S) {
+#pragma unroll
+    for (int i = 0; i < D; ++i) {
+      const int u = b0 + i * S;
+      if (u < u_end) {
+        const int j = u / u_pair, c = u - j * u_pair;
+        const int kb = c / NCH, cc = c - kb * NCH;
+        Run ra, rb;
+        B::decode_chunk(ring[i], cc, ra, rb);
+        const int un = u + D * S;
+        if (un < u_end) {
+          const int jn = un / u_pair, cn = un - jn * u_pair;
+          B::load_chunk(base_of(jn) + (size_t)(cn / NCH) * B::SLAB, rr, cn % NCH, ring[i]);
+        }
+        const float* hb = hl + j * KP + kb * B::QK;
+        const float* hs = hs16 + j * (KP / 16) + kb * (B::QK / 16);
+        const int valid = a.K - kb * B::QK;
+        float d = 0.0f;
+        if (ra.e < valid) d += run_dot<T>(ra, hb, hs);
+        if (rb.e < valid) d += run_dot<T>(rb, hb, hs);
+#pragma unroll
+        for (int q = 0; q < KM; ++q)
+          if (q == j) acc[q] += d;
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < KM; ++j) {
+    if (j >= k) break;
+    float v = acc[j];
+#pragma unroll
+    for (int off = R; off < 64; off *= 2) v += __shfl_xor(v, off, 64);
+    if (lane < R) red[(wave * KM + j) * R + lane] = v;
+  }
+  __syncthreads();
+  if ((int)threadIdx.x < R) {
+    const int r = threadIdx.x;
+    float o = 0.0f;
+#pragma unroll
+    for (int j = 0; j < KM; ++j) {
+      if (j >= k) break;
+      if (!ok[j]) continue;
+      float y = red[(0 * KM + j) * R + r];
+#pragma unroll
+      for (int w = 1; w < WAVES; ++w) y += red[(w * KM + j) * R + r];
+      o = __fadd_rn(o, __fmul_rn(a.ids ? a.wts[j] : a.w_v[j], y));
+    }
+    const int orow = blk * R + r;
+    if (orow < a.m) a.out[orow] = o;
+  }
+}
+
+// 8 rows a workgroup (256 workgroups at hidden 2048), 8 waves (measured 15.7 against 17.6 us for 4
+// waves at the Qwen3-30B-A3B shape, and slower with 16 waves or 4 loads in flight per slot)
+constexpr int kDownCombineRows = 8, kDownCombineWaves = 8;
+
+template <int T>
+static size_t down_combine_lds(int KB) {
+  const size_t KP = (size_t)KB * Blk<T>::QK;
+  return (kMoeOneTokenMaxK * KP * 17 / 16 + (size_t)kDownCombineWaves * kMoeOneTokenMaxK * kDownCombineRows) *
+         sizeof(float);
+}
+
+template <int T>
+static hipError_t launch_down_combine_t(const MoeDownCombineArgs& a, hipStream_t s) {
+  const size_t lds = down_combine_lds<T>(a.KB);
+  if (lds > kMaxLdsBytes || a.k < 1 || a.k > kMoeOneTokenMaxK) return hipErrorInvalidValue;
+  const int nblk = (a.m + kDownCombineRows - 1) / kDownCombineRows;
+  const unsigned grid = (unsigned)((nblk + 7) / 8 * 8);
+  hipLaunchKernelGGL((moe_down_combine_kernel<T, kDownCombineRows, kDownCombineWaves, 2>), dim3(grid),
+                     dim3(kDownCombineWaves * 64), lds, s, a);
+  return hipGetLastError();
+}
+
+size_t moe_down_combine_lds(uint32_t type, int KB, int k) {
+  (void)k;
+  switch (type) {
+    case T_Q4_0: return down_combine_lds<T_Q4_0>(KB);
+    case T_Q5_0: return down_combine_lds<T_Q5_0>(KB);
+    case T_Q8_0: return down_combine_lds<T_Q8_0>(KB);
+    case T_Q4_K: return down_combine_lds<T_Q4_K>(KB);
+    case T_Q5_K: return down_combine_lds<T_Q5_K>(KB);
+    case T_Q6_K: return down_combine_lds<T_Q6_K>(KB);
+    default: return ~(size_t)0;
+  }
+}
+
+hipError_t launch_moe_down_combine(uint32_t type, const MoeDownCombineArgs& a, hipStream_t s) {
+  switch (type) {
+    case T_Q4_0: return launch_down_combine_t<T_Q4_0>(a, s);
+    case T_Q5_0: return launch_down_combine_t<T_Q5_0>(a, s);
+    case T_Q8_0: return launch_down_combine_t<T_Q8_0>(a, s);
+    case T_Q4_K: return launch_down_combine_t<T_Q4_K>(a, s);
+    case T_Q5_K: return launch_down_combine_t<T_Q5_K>(a, s);
+    case T_Q6_K: return launch_down_combine_t<T_Q6_K>(a, s);
+    default: return hipErrorInvalidValue;
   }
 }
 

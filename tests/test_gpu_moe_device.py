@@ -177,10 +177,14 @@ def test_host_routed_large_batch_then_small():
     moe.close()
 
 
-def test_forward_routed_skips_out_of_range_ids():
-    E, hidden, inter, T, k = 8, 256, 128, 3, 2
+@pytest.mark.parametrize("T,k,rows", [(3, 2, [[1, 9], [2, 3], [-1, 4]]), (1, 4, [[5, -1, 9, 2]]),
+                                      (1, 8, [[7, 0, 8, 3, 3, -5, 1, 6]])])
+def test_forward_routed_skips_out_of_range_ids(T, k, rows):
+    """Pairs whose expert id is outside [0, n_experts) add nothing (the grouped path and the
+    one-token path alike)."""
+    E, hidden, inter = 8, 256, 128
     gate, up, down_, x, logits = moe_case(77, E, hidden, inter, T, k)
-    ids = np.array([[1, 9], [2, 3], [-1, 4]], np.int32)
+    ids = np.array(rows, np.int32)
     wts = np.full((T, k), 0.5, np.float32)
     moe = rehip.MoeExperts(rehip.Q4_K, gate, rehip.Q4_K, up, rehip.Q6_K, down_, E, hidden, inter)
     out = B(T * hidden * 4)
