@@ -1079,7 +1079,7 @@ static int moe_one_token(re_moe* e, const float* d_x, size_t top_k, const int* d
   g.X = d_x;
   g.ids = d_ids;
   g.id_inline = d_ids ? 0 : 1;
-  if (!d_ids)
+  if (g.id_inline)
     for (size_t j = 0; j < top_k; ++j) g.id_v[j] = (int)h_ids[j];
   g.id_tiles = (int)((e->inter + rgu - 1) / rgu);
   g.n_experts = (int)e->n_experts;

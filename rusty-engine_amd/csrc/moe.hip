@@ -66,22 +66,20 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
 // treated as -inf (the reference's partial_cmp leaves their order unspecified).
 constexpr int kRouteMaxExperts = 1024;
 
-// EPL = experts per lane (n_experts <= 64 EPL).
+// One wave routes one token (`row` holds its n_experts scores): up to EPL experts per lane, of
+// which the first ceil(n_experts / 64) are used. Lane 0 writes the k ids and weights to ids[] /
+// weights[] (global memory or LDS); topv / topi: k entries of scratch that lane 0 alone touches.
 template <int EPL>
-__global__ __launch_bounds__(64) void moe_route_kernel(const float* __restrict__ logits, int n_experts, int k,
-                                                       int gate, int* __restrict__ ids,
-                                                       float* __restrict__ weights) {
-  __shared__ float topv[kRouteMaxExperts];
-  __shared__ int topi[kRouteMaxExperts];
-  const int t = blockIdx.x, lane = threadIdx.x;
-  const float* row = logits + (size_t)t * n_experts;
+__device__ __forceinline__ void route_token(const float* row, int n_experts, int k, int gate, int lane,
+                                            float* topv, int* topi, int* ids, float* weights) {
+  const int epl = (n_experts + 63) / 64;
   float v[EPL];
   bool taken[EPL];
 #pragma unroll
   for (int j = 0; j < EPL; ++j) {
     const int e = lane + 64 * j;
     float x = -INFINITY;
-    if (e < n_experts) {
+    if (j < epl && e < n_experts) {
       x = row[e];
       if (gate == 1) x = 1.0f / (1.0f + expf(-x));     // sigmoid (moe.rs:43-46)
       if (x != x) x = -INFINITY;
@@ -94,6 +92,7 @@ __global__ __launch_bounds__(64) void moe_route_kernel(const float* __restrict__
     int be = 0x7fffffff;
 #pragma unroll
     for (int j = 0; j < EPL; ++j) {
+      if (j >= epl) break;                             // uniform
       const int e = lane + 64 * j;
       if (!taken[j] && (v[j] > bv || (v[j] == bv && e < be))) { bv = v[j]; be = e; }
     }
@@ -108,15 +107,14 @@ __global__ __launch_bounds__(64) void moe_route_kernel(const float* __restrict__
       if (lane + 64 * j == be) taken[j] = true;
     if (lane == 0) { topv[r] = bv; topi[r] = be; }
   }
-  __syncthreads();
   if (lane != 0) return;
   if (gate == 1) {
     // weights = sig / sum of the chosen sigs, summed in order (moe.rs:108-117)
     float ws = 0.0f;
     for (int r = 0; r < k; ++r) ws += topv[r];
     for (int r = 0; r < k; ++r) {
-      ids[t * k + r] = topi[r];
-      weights[t * k + r] = ws == 0.0f ? 0.0f : topv[r] / ws;
+      ids[r] = topi[r];
+      weights[r] = ws == 0.0f ? 0.0f : topv[r] / ws;
     }
   } else {
     // softmax over the chosen logits (moe.rs:53-72): max, exp(v - max), sequential sum, divide
@@ -128,10 +126,22 @@ __global__ __launch_bounds__(64) void moe_route_kernel(const float* __restrict__
       sum += topv[r];
     }
     for (int r = 0; r < k; ++r) {
-      ids[t * k + r] = topi[r];
-      weights[t * k + r] = sum != 0.0f ? topv[r] / sum : topv[r];
+      ids[r] = topi[r];
+      weights[r] = sum != 0.0f ? topv[r] / sum : topv[r];
     }
   }
+}
+
+// EPL = experts per lane (n_experts <= 64 EPL).
+template <int EPL>
+__global__ __launch_bounds__(64) void moe_route_kernel(const float* __restrict__ logits, int n_experts, int k,
+                                                       int gate, int* __restrict__ ids,
+                                                       float* __restrict__ weights) {
+  __shared__ float topv[kRouteMaxExperts];
+  __shared__ int topi[kRouteMaxExperts];
+  const int t = blockIdx.x;
+  route_token<EPL>(logits + (size_t)t * n_experts, n_experts, k, gate, threadIdx.x, topv, topi, ids + (size_t)t * k,
+                   weights + (size_t)t * k);
 }
 
 // logits[t][e] = router_w[e] . x[t] (the f32 matvec of moe.rs:367): x[t] staged in LDS, one wave
@@ -670,10 +680,12 @@ __global__ __launch_bounds__(WAVES * 64) void moe_down_combine_kernel(MoeDownCom
   const int u_pair = a.KB * NCH;         // units (chunks) per expert row
   const int k = a.k;
   int ex[KM];
+  float wv[KM];
   bool ok[KM];
 #pragma unroll
   for (int j = 0; j < KM; ++j) {
     ex[j] = j < k ? (a.ids ? a.ids[j] : a.id_v[j]) : -1;
+    wv[j] = j < k ? (a.ids ? a.wts[j] : a.w_v[j]) : 0.0f;
     ok[j] = ex[j] >= 0 && ex[j] < a.n_experts;
   }
   // unit u: chunk u % u_pair of expert j = u / u_pair (an id out of range reads expert 0, unused)
@@ -760,7 +772,7 @@ __global__ __launch_bounds__(WAVES * 64) void moe_down_combine_kernel(MoeDownCom
       float y = red[(0 * KM + j) * R + r];
 #pragma unroll
       for (int w = 1; w < WAVES; ++w) y += red[(w * KM + j) * R + r];
-      o = __fadd_rn(o, __fmul_rn(a.ids ? a.wts[j] : a.w_v[j], y));
+      o = __fadd_rn(o, __fmul_rn(wv[j], y));
     }
     const int orow = blk * R + r;
     if (orow < a.m) a.out[orow] = o;
