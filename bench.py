@@ -393,9 +393,9 @@ def time_load(layers, workdir, seed=601):
 
 
 def calibrate(log=print):
-    """What this GPU reaches: a 1 GiB streaming read (default and nontemporal cache policy), a
-    dependency-free bf16 MFMA stream over every CU, and the per-launch floor of a graph of empty
-    kernels."""
+    """What this GPU reaches: a 1 GiB streaming read (interleaved over the grid, or one contiguous
+    run per workgroup; default and nontemporal cache policy), a dependency-free bf16 MFMA stream
+    over every CU, and the per-launch floor of a graph of empty kernels."""
     from rehip import hip
     L = C.CDLL(os.path.join(ROOT, "rusty-engine_amd", "librecalib.so"))
     L.cal_stream_read.argtypes = [C.c_void_p, C.c_uint64, C.c_int, C.c_void_p, C.c_int, C.c_void_p]
@@ -406,13 +406,18 @@ def calibrate(log=print):
     buf = hip.DeviceBuffer(nbytes)
     hip.check(hip.hip().hipMemset(C.c_void_p(buf.ptr), 1, C.c_size_t(nbytes)))
     out = {}
-    for grid in (2048, 4096):
+    L.cal_stream_read_chunk.argtypes = L.cal_stream_read.argtypes
+    for grid in (1024, 2048, 4096):
         sink = hip.DeviceBuffer(grid * 256 * 4)
         for nt in (0, 1):
-            us = graph_time_us(s, lambda: L.cal_stream_read(buf.ptr, nbytes, nt, sink.ptr, grid, s.cuda_stream), 10)
-            key = f"stream_read_{'nontemporal' if nt else 'default'}_grid{grid}_gbs"
-            out[key] = nbytes / (us * 1e-6) / 1e9
-            log(f"calib: {key} {out[key]:.0f}")
+            for pattern, fn in (("interleaved", L.cal_stream_read), ("contiguous", L.cal_stream_read_chunk)):
+                if pattern == "interleaved" and grid == 1024:
+                    continue
+                us = graph_time_us(s, lambda: fn(buf.ptr, nbytes, nt, sink.ptr, grid, s.cuda_stream), 10)
+                read = nbytes if pattern == "interleaved" else (nbytes // 16 // grid // 4096) * 4096 * 16 * grid
+                key = f"stream_read_{pattern}_{'nontemporal' if nt else 'default'}_grid{grid}_gbs"
+                out[key] = read / (us * 1e-6) / 1e9
+                log(f"calib: {key} {out[key]:.0f}")
         sink.free()
     buf.free()
     grid, iters = 256 * 8, 512

@@ -1,5 +1,6 @@
-// Machine calibration kernels for bench.py (not part of the product ABI): a streaming read of a
-// device buffer, a dependency-free MFMA stream and an empty kernel. bench.py times them with HIP
+// Machine calibration kernels for bench.py (not part of the product ABI): streaming reads of a
+// device buffer (interleaved over the grid, or one contiguous run per workgroup), a
+// dependency-free MFMA stream and an empty kernel. bench.py times them with HIP
 // events to measure what this GPU reaches (HBM read bandwidth with the default and the
 // nontemporal cache policy, bf16 MFMA throughput, the per-launch floor of a graph of kernels).
 #include <hip/hip_runtime.h>
@@ -45,6 +46,29 @@ __global__ __launch_bounds__(256) void stream_read_kernel(const uint8_t* p, uint
   sink[tid] = acc;
 }
 
+// Every workgroup reads its own contiguous run of 16-byte words (bytes / 16 / gridDim words,
+// the tail below one run unread), sixteen loads in flight per lane; one word per thread is
+// written to sink.
+template <int AUX>
+__global__ __launch_bounds__(256) void stream_read_chunk_kernel(const uint8_t* p, uint64_t bytes, uint32_t* sink) {
+  const uint64_t run = bytes / 16 / gridDim.x;
+  const uint64_t b = (uint64_t)blockIdx.x * run;
+  uint32_t acc = 0;
+  for (uint64_t i = threadIdx.x; i + 15 * 256 < run; i += 16 * 256) {
+    i32x4_t v[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const uint64_t o = (b + i + (uint64_t)j * 256) * 16;
+      const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<uint8_t*>(p) + (o & ~((uint64_t)(1u << 30) - 1)), (short)0, (int)0x7fffffff, 0x00020000);
+      v[j] = __builtin_amdgcn_raw_buffer_load_b128(rw, (int)(o & ((1u << 30) - 1)), 0, AUX);
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j) acc ^= (uint32_t)(v[j][0] ^ v[j][1] ^ v[j][2] ^ v[j][3]);
+  }
+  sink[(uint64_t)blockIdx.x * 256 + threadIdx.x] = acc;
+}
+
 // Each wave runs `iters` rounds of 8 independent v_mfma_f32_32x32x16_bf16 on register operands
 // (8 accumulators, no dependency inside a round) and writes one value per wave.
 __global__ __launch_bounds__(256) void mfma_stream_kernel(float* out, int iters) {
@@ -85,6 +109,18 @@ int cal_stream_read(const void* p, uint64_t bytes, int nontemporal, uint32_t* si
                        (const uint8_t*)p, bytes, sink);
   else
     hipLaunchKernelGGL(stream_read_kernel<0>, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream,
+                       (const uint8_t*)p, bytes, sink);
+  return (int)hipGetLastError();
+}
+
+// the same bytes read as one contiguous run per workgroup (bytes / 16 / grid words each; the
+// bytes read are grid * that * 16)
+int cal_stream_read_chunk(const void* p, uint64_t bytes, int nontemporal, uint32_t* sink, int grid, void* stream) {
+  if (nontemporal)
+    hipLaunchKernelGGL(stream_read_chunk_kernel<2>, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream,
+                       (const uint8_t*)p, bytes, sink);
+  else
+    hipLaunchKernelGGL(stream_read_chunk_kernel<0>, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream,
                        (const uint8_t*)p, bytes, sink);
   return (int)hipGetLastError();
 }
