@@ -173,7 +173,10 @@ def time_moe(moe, weights, tokens, mode, reps, seed=401, check=False):
     dw = hip.DeviceBuffer.from_array(np.asarray(wts, np.float32))
     rw = hip.DeviceBuffer.from_array((np.random.default_rng(seed + 3).standard_normal((E, H)) / np.sqrt(H))
                                      .astype(np.float32))
-    us_routed = graph_time_us(s, lambda: moe.forward_routed_dev(dx, tokens, k, did, dw, dy, mode, stream=s), reps)
+    # device-routed and whole-layer graphs: the best of three timed replays (the first replays of a
+    # process run up to ~10 % slower while the clocks settle)
+    us_routed = min(graph_time_us(s, lambda: moe.forward_routed_dev(dx, tokens, k, did, dw, dy, mode, stream=s), reps)
+                    for _ in range(3))
     r_ok = None
     if check:
         got = dy.download(np.float32, tokens * H)
@@ -182,8 +185,8 @@ def time_moe(moe, weights, tokens, mode, reps, seed=401, check=False):
                               ids.reshape(-1), wts.reshape(-1))
         rel = float(np.linalg.norm(got - want) / np.linalg.norm(want))
         r_ok = rel
-    us_layer = graph_time_us(s, lambda: moe.layer_dev(dx, tokens, rw, k, rehip.GATE_SOFTMAX, dy, mode, stream=s),
-                             reps)
+    us_layer = min(graph_time_us(s, lambda: moe.layer_dev(dx, tokens, rw, k, rehip.GATE_SOFTMAX, dy, mode, stream=s),
+                                 reps) for _ in range(3))
     s.destroy()
     hit = len(np.unique(ids))
     per_expert = sum(a.size for a in weights) // E

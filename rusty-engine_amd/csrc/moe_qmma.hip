@@ -102,6 +102,46 @@ __device__ __forceinline__ void decode_frags(const typename Blk<T>::CR& raw, int
   f.eb = b.e;
 }
 
+// vector memory instructions of one Blk<T>::bload_chunk
+template <int T> inline constexpr int kChunkLoads = 0;
+template <> inline constexpr int kChunkLoads<T_Q4_0> = 2;
+template <> inline constexpr int kChunkLoads<T_Q5_0> = 3;
+template <> inline constexpr int kChunkLoads<T_Q8_0> = 3;
+template <> inline constexpr int kChunkLoads<T_Q4_K> = 2;
+template <> inline constexpr int kChunkLoads<T_Q5_K> = 3;
+template <> inline constexpr int kChunkLoads<T_Q6_K> = 4;
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// s_waitcnt with only the vector-memory counter bounded (expcnt and lgkmcnt at their maximum)
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// Activations staged in LDS (XL): a stage is two consecutive chunks of K, 64 bf16 of each row
+// (128 bytes: one cache line, or for Q6_K two half lines) in eight 16-byte units. Unit u of stage
+// st starts at K index xl_unit_k<T>(st, u); the A operand of run a / b of chunk 2 st + cl starts at
+// unit xl_run_unit<T>(cl, b) (plus lane / 32).
+template <int T>
+__device__ __forceinline__ int xl_unit_k(int st, int u) {
+  if constexpr (Blk<T>::QK == 32) {
+    return 64 * st + 8 * u;                                   // blocks 2 st, 2 st + 1
+  } else if constexpr (T == T_Q6_K) {
+    const int kb = st >> 2, m = (st & 3) >> 1, half = st & 1;  // chunks 4m + 2 half + {0, 1}
+    const int k0 = 256 * kb + 128 * m + 32 * half;
+    return u < 4 ? k0 + 8 * u : k0 + 64 + 8 * (u - 4);
+  } else {
+    return 256 * (st >> 2) + 64 * (st & 3) + 8 * u;          // chunks 2g, 2g + 1 of a block
+  }
+}
+template <int T>
+__device__ __forceinline__ constexpr int xl_run_unit(int cl, bool b) {
+  if constexpr (Blk<T>::QK == 32) return 4 * cl + (b ? 2 : 0);
+  else return 2 * cl + (b ? 4 : 0);
+}
+
 __device__ __forceinline__ bf16x8_t ld_x(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   const i32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
   return __builtin_bit_cast(bf16x8_t, v);
@@ -118,8 +158,8 @@ __device__ __forceinline__ bf16x8_t ld_x(__amdgpu_buffer_rsrc_t r, uint32_t off)
 // KS waves per task split the blocks of K between them (wave w takes blocks w, w + KS, ...);
 // their sums are added in wave order through LDS at the end (deterministic).
 constexpr int kOneTile = 0, kGateUp = 1, kTwoTiles = 2;
-template <int T, int PAIR, int NT, int KS>
-__device__ __forceinline__ void qmma_task(const GemmArgs& p, const GemmTask& t) {
+template <int T, int PAIR, int NT, int KS, bool XL>
+__device__ __forceinline__ void qmma_task(const GemmArgs& p, const GemmTask& t, uint8_t* xs) {
   using B = Blk<T>;
   constexpr int NCH = B::NCH;                       // 32-element chunks per block
   const int lane = threadIdx.x & 63;
@@ -234,19 +274,96 @@ __device__ __forceinline__ void qmma_task(const GemmArgs& p, const GemmTask& t) 
   constexpr int U = NCH >= 2 ? NCH : 2;
   // this wave's groups of U chunks: c0 = (i * KS + wave) * U for i = 0, 1, ...
   typename B::CR r[2], q[2];
-  XOps x[2];
   const int first = wave * U;
-  load_all(first, r[0], q[0], x[0]);
-  load_all(first + 1, r[1], q[1], x[1]);
-  for (int c0 = first; c0 < nch; c0 += U * KS) {
+  if constexpr (XL) {
+    // Activations through LDS: each stage (two chunks) of this wave's token rows is copied by
+    // LDS DMA, one stage ahead, as whole 128-byte runs of a row (a line per row instead of a
+    // 16-byte operand load per lane and run). Instruction i puts rows 8 i .. 8 i + 7 in the stage
+    // buffer, row-major at 128 bytes a row, 16-byte unit u of a row at position u ^ (row & 7)
+    // (so the 32 rows an operand read touches spread over the banks); lane l copies row
+    // 8 i + l / 8, position l % 8. Rows past the task and K past the end read zeros.
+    constexpr int LW = kChunkLoads<T> * (DUAL ? 2 : 1);   // weight loads per chunk
+    constexpr int ND = NT * 4;                            // LDS DMA instructions per stage
+    constexpr int SB = NT * 32 * 128;                     // stage buffer bytes
+    uint32_t xo[ND];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      step(c0 + u, r[u & 1], q[u & 1], x[u & 1]);
-      // keep the loads in program order behind the step that frees their registers, so the wait
-      // before the next step counts only these (younger) loads
-      __builtin_amdgcn_sched_barrier(0);
-      load_all(u + 2 < U ? c0 + u + 2 : c0 + U * KS + u + 2 - U, r[u & 1], q[u & 1], x[u & 1]);
-      __builtin_amdgcn_sched_barrier(0);
+    for (int i = 0; i < ND; ++i) {
+      const int rl = 8 * i + (lane >> 3);
+      uint32_t o = kQOob;
+      if (rl < rn) {
+        const int row = p.xrow ? p.xrow[t.r0 + rl] : t.r0 + rl;
+        o = (uint32_t)row * (uint32_t)p.K * 2u;
+      }
+      xo[i] = o;
+    }
+    const int pos = lane & 7;
+    auto dma = [&](int c, int buf) {                      // the stage of chunks c, c + 1
+      uint8_t* dst = xs + buf * SB;
+      const int st = c >> 1;
+#pragma unroll
+      for (int i = 0; i < ND; ++i) {
+        const int rl = 8 * i + (lane >> 3);
+        const int k = xl_unit_k<T>(st, pos ^ (rl & 7));
+        const uint32_t o = c < nch && xo[i] != kQOob && k < p.K ? xo[i] + (uint32_t)k * 2u : kQOob;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void_t*)(dst + 1024 * i), 16, (int)o, 0, 0, 0);
+      }
+    };
+    auto read_x = [&](int buf, int cl, XOps& x) {
+      const uint8_t* src = xs + buf * SB;
+#pragma unroll
+      for (int j = 0; j < NT; ++j) {
+        const int row = 32 * j + (lane & 31);
+        const int ua = xl_run_unit<T>(cl, false) + (lane >> 5), ub = xl_run_unit<T>(cl, true) + (lane >> 5);
+        x.a[j] = *reinterpret_cast<const bf16x8_t*>(src + row * 128 + ((ua ^ (row & 7)) << 4));
+        x.b[j] = *reinterpret_cast<const bf16x8_t*>(src + row * 128 + ((ub ^ (row & 7)) << 4));
+      }
+    };
+    auto load_w = [&](int c, typename B::CR& rr, typename B::CR& qq) {
+      load(c, rr, wr, wbase);
+      if constexpr (DUAL) load(c, qq, wr2, wbase2);
+    };
+    auto next_c = [&](int c0, int u) { return u < U ? c0 + u : c0 + U * KS + u - U; };
+    // issue order DMA(s), W(2s), W(2s + 1), DMA(s + 1), ...: when stage s is read, the loads
+    // younger than its DMA are at most two chunks of weights and one stage of DMA
+    dma(first, 0);
+    load_w(first, r[0], q[0]);
+    load_w(first + 1, r[1], q[1]);
+    dma(next_c(first, 2), 1);
+    int buf = 0;
+    for (int c0 = first; c0 < nch; c0 += U * KS) {
+#pragma unroll
+      for (int u = 0; u < U; u += 2) {
+        wait_vmcnt<2 * LW + ND>();
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          XOps x;
+          read_x(buf, h, x);
+          step(c0 + u + h, r[h], q[h], x);
+          __builtin_amdgcn_sched_barrier(0);
+          load_w(next_c(c0, u + h + 2), r[h], q[h]);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        dma(next_c(c0, u + 4), buf);
+        __builtin_amdgcn_sched_barrier(0);
+        buf ^= 1;
+      }
+    }
+    wait_vmcnt<0>();                                      // no LDS DMA outlives the task
+  } else {
+    XOps x[2];
+    load_all(first, r[0], q[0], x[0]);
+    load_all(first + 1, r[1], q[1], x[1]);
+    for (int c0 = first; c0 < nch; c0 += U * KS) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        step(c0 + u, r[u & 1], q[u & 1], x[u & 1]);
+        // keep the loads in program order behind the step that frees their registers, so the wait
+        // before the next step counts only these (younger) loads
+        __builtin_amdgcn_sched_barrier(0);
+        load_all(u + 2 < U ? c0 + u + 2 : c0 + U * KS + u + 2 - U, r[u & 1], q[u & 1], x[u & 1]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
   }
   if constexpr (KS > 1) {
@@ -309,17 +426,20 @@ __device__ __forceinline__ void qmma_task(const GemmArgs& p, const GemmTask& t) 
 }
 
 // A task of at most 32 rows runs the one-tile body (no MFMAs on an empty second token tile).
-template <int T, int PAIR, int NT, int KS>
+// XL: activations staged in LDS (two stage buffers per wave).
+template <int T, int PAIR, int NT, int KS, bool XL>
 __global__ __launch_bounds__(64 * KS) void moe_qmma_kernel(GemmArgs p) {
   if (p.ntasks && (int)blockIdx.x >= *p.ntasks) return;   // grid sized for the most tasks
   const GemmTask t = p.tasks[blockIdx.x];
+  __shared__ __attribute__((aligned(16))) uint8_t xs[XL ? KS * 2 * NT * 32 * 128 : 16];
+  uint8_t* mine = xs + (XL ? (threadIdx.x >> 6) * 2 * NT * 32 * 128 : 0);
   if constexpr (NT == 2) {
     if (t.rn <= 32) {
-      qmma_task<T, PAIR, 1, KS>(p, t);
+      qmma_task<T, PAIR, 1, KS, XL>(p, t, mine);
       return;
     }
   }
-  qmma_task<T, PAIR, NT, KS>(p, t);
+  qmma_task<T, PAIR, NT, KS, XL>(p, t, mine);
 }
 
 hipError_t launch_moe_qmma(uint32_t type, int pair, int max_rows, const GemmArgs& a, int ntasks, hipStream_t s) {
@@ -331,7 +451,18 @@ hipError_t launch_moe_qmma(uint32_t type, int pair, int max_rows, const GemmArgs
   int ks = one ? 2 : 1;
   if (const char* v = std::getenv("REHIP_QMMA_KS"); v && (v[0] == '1' || v[0] == '2') && !v[1]) ks = v[0] - '0';
   const dim3 grid((unsigned)ntasks), block(64 * ks);
-#define REHIP_QMMA_L(TT, PA, NT, KS) hipLaunchKernelGGL((moe_qmma_kernel<TT, PA, NT, KS>), grid, block, 0, s, a)
+  // activations staged in LDS for the two-tile tasks of 64 rows (each staged run feeds 128
+  // weight rows; measured at 512 tokens on the Qwen3-30B-A3B shape: down 61.1 against 65.8 us,
+  // while the gate/up pair and the 32-row tasks ran slower staged), else read from L2 per run;
+  // REHIP_QMMA_XL = 1 / 0 forces either
+  const char* xv = std::getenv("REHIP_QMMA_XL");
+  bool xl = pair == kTwoTiles && !one;
+  if (xv && (xv[0] == '0' || xv[0] == '1') && !xv[1]) xl = xv[0] == '1';
+#define REHIP_QMMA_L(TT, PA, NT, KS)                                                              \
+  do {                                                                                            \
+    if (xl) hipLaunchKernelGGL((moe_qmma_kernel<TT, PA, NT, KS, true>), grid, block, 0, s, a);    \
+    else hipLaunchKernelGGL((moe_qmma_kernel<TT, PA, NT, KS, false>), grid, block, 0, s, a);      \
+  } while (0)
 #define REHIP_QMMA_P(TT, PA)                                                                        \
   if (one) { if (ks == 2) REHIP_QMMA_L(TT, PA, 1, 2); else REHIP_QMMA_L(TT, PA, 1, 1); }            \
   else { if (ks == 2) REHIP_QMMA_L(TT, PA, 2, 2); else REHIP_QMMA_L(TT, PA, 2, 1); }
