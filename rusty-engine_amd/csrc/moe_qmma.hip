@@ -279,7 +279,7 @@ __device__ __forceinline__ void qmma_task(const GemmArgs& p, const GemmTask& t, 
     // Activations through LDS: each stage (two chunks) of this wave's token rows is copied by
     // LDS DMA, one stage ahead, as whole 128-byte runs of a row (a line per row instead of a
     // 16-byte operand load per lane and run). Instruction i puts rows 8 i .. 8 i + 7 in the stage
-    // buffer, row-major at 128 bytes a row, 16-byte unit u of a row at position u ^ (row & 7)
+    // buffer, row-major at 128 bytes a row, 16-byte unit u of a row at position u ^ ((row >> 1) & 7)
     // (so the 32 rows an operand read touches spread over the banks); lane l copies row
     // 8 i + l / 8, position l % 8. Rows past the task and K past the end read zeros.
     constexpr int LW = kChunkLoads<T> * (DUAL ? 2 : 1);   // weight loads per chunk
@@ -303,7 +303,7 @@ __device__ __forceinline__ void qmma_task(const GemmArgs& p, const GemmTask& t, 
 #pragma unroll
       for (int i = 0; i < ND; ++i) {
         const int rl = 8 * i + (lane >> 3);
-        const int k = xl_unit_k<T>(st, pos ^ (rl & 7));
+        const int k = xl_unit_k<T>(st, pos ^ ((rl >> 1) & 7));
         const uint32_t o = c < nch && xo[i] != kQOob && k < p.K ? xo[i] + (uint32_t)k * 2u : kQOob;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void_t*)(dst + 1024 * i), 16, (int)o, 0, 0, 0);
       }
@@ -314,8 +314,8 @@ __device__ __forceinline__ void qmma_task(const GemmArgs& p, const GemmTask& t, 
       for (int j = 0; j < NT; ++j) {
         const int row = 32 * j + (lane & 31);
         const int ua = xl_run_unit<T>(cl, false) + (lane >> 5), ub = xl_run_unit<T>(cl, true) + (lane >> 5);
-        x.a[j] = *reinterpret_cast<const bf16x8_t*>(src + row * 128 + ((ua ^ (row & 7)) << 4));
-        x.b[j] = *reinterpret_cast<const bf16x8_t*>(src + row * 128 + ((ub ^ (row & 7)) << 4));
+        x.a[j] = *reinterpret_cast<const bf16x8_t*>(src + row * 128 + ((ua ^ ((row >> 1) & 7)) << 4));
+        x.b[j] = *reinterpret_cast<const bf16x8_t*>(src + row * 128 + ((ub ^ ((row >> 1) & 7)) << 4));
       }
     };
     auto load_w = [&](int c, typename B::CR& rr, typename B::CR& qq) {
