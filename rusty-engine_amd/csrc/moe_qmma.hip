@@ -111,6 +111,52 @@ template <> inline constexpr int kChunkLoads<T_Q4_K> = 2;
 template <> inline constexpr int kChunkLoads<T_Q5_K> = 3;
 template <> inline constexpr int kChunkLoads<T_Q6_K> = 4;
 
+// K-quant blocks: the block-wide planes (Q4_K / Q5_K: d, dmin and the scales; Q6_K: the scales and
+// d) are loaded once per block and shared by its eight chunks, so a chunk loads only its quant
+// planes and the scales of a pair of chunks are computed once (the decode sees the same values)
+template <int T> inline constexpr bool kBlockHead = Blk<T>::QK == 256;
+template <int T> inline constexpr int kChunkOwnLoads = kBlockHead<T> ? (T == T_Q4_K ? 1 : 2) : kChunkLoads<T>;
+struct BlockHead {
+  uint4 h;       // Q4_K / Q5_K: the head plane; Q6_K: the scales plane
+  uint32_t d;    // Q6_K: d
+};
+template <int T>
+__device__ __forceinline__ void load_head(__amdgpu_buffer_rsrc_t rs, uint32_t slab, int lane, BlockHead& h) {
+  if constexpr (T == T_Q6_K) {
+    h.h = bld16(rs, slab + 1024 * 12 + lane * 16);
+    h.d = bld2(rs, slab + 1024 * 13 + lane * 2);
+  } else {
+    h.h = bld16(rs, slab + lane * 16);
+    h.d = 0;
+  }
+}
+// the chunk's own planes only
+template <int T>
+__device__ __forceinline__ void load_own(__amdgpu_buffer_rsrc_t rs, uint32_t slab, int lane, int cc,
+                                         typename Blk<T>::CR& r) {
+  if constexpr (T == T_Q4_K) {
+    r.qs = bld16(rs, slab + 1024 * (1 + cc) + lane * 16);
+  } else if constexpr (T == T_Q5_K) {
+    r.qh = bld16(rs, slab + 1024 * (1 + (cc & 1)) + lane * 16);
+    r.qs = bld16(rs, slab + 1024 * (3 + cc) + lane * 16);
+  } else if constexpr (T == T_Q6_K) {
+    r.ql = bld16(rs, slab + 1024 * cc + lane * 16);
+    r.qh = bld16(rs, slab + 1024 * (8 + 2 * (cc >> 2) + (cc & 1)) + lane * 16);
+  } else {
+    Blk<T>::bload_chunk(rs, slab, lane, cc, r);
+  }
+}
+template <int T>
+__device__ __forceinline__ typename Blk<T>::CR with_head(typename Blk<T>::CR r, const BlockHead& h) {
+  if constexpr (T == T_Q6_K) {
+    r.sc = h.h;
+    r.d = h.d;
+  } else if constexpr (kBlockHead<T>) {
+    r.head = h.h;
+  }
+  return r;
+}
+
 typedef __attribute__((address_space(3))) void lds_void_t;
 
 // s_waitcnt with only the vector-memory counter bounded (expcnt and lgkmcnt at their maximum)
@@ -211,7 +257,16 @@ __device__ __forceinline__ void qmma_task(const GemmArgs& p, const GemmTask& t, 
   auto load = [&](int c, typename B::CR& raw, const __amdgpu_buffer_rsrc_t& rs, uint32_t base) {
     const int kb = c / NCH, cc = c - kb * NCH;
     const uint32_t slab = c < nch ? base + (uint32_t)kb * (uint32_t)B::SLAB : kQOob;
-    B::bload_chunk(rs, slab, lane, cc, raw);
+    load_own<T>(rs, slab, lane, cc, raw);
+  };
+  // the block heads of the block holding chunk c (first chunk of a block), both weight sets
+  BlockHead hc{}, hc2{}, hn{}, hn2{};
+  auto load_heads = [&](int c, BlockHead& h, BlockHead& h2) {
+    if constexpr (kBlockHead<T>) {
+      const int kb = c / NCH;
+      load_head<T>(wr, c < nch ? wbase + (uint32_t)kb * (uint32_t)B::SLAB : kQOob, lane, h);
+      if constexpr (DUAL) load_head<T>(wr2, c < nch ? wbase2 + (uint32_t)kb * (uint32_t)B::SLAB : kQOob, lane, h2);
+    }
   };
   // A operands of chunk c: runs a and b of every token tile
   struct XOps { bf16x8_t a[NT], b[NT]; };
@@ -261,11 +316,11 @@ __device__ __forceinline__ void qmma_task(const GemmArgs& p, const GemmTask& t, 
   };
   auto step = [&](int c, const typename B::CR& r, const typename B::CR& q, const XOps& x) {
     Frags f;
-    decode_frags<T>(r, c % NCH, f);
+    decode_frags<T>(with_head<T>(r, hc), c % NCH, f);
     mma(x, f, acc);
     if constexpr (DUAL) {
       Frags f2;
-      decode_frags<T>(q, c % NCH, f2);
+      decode_frags<T>(with_head<T>(q, hc2), c % NCH, f2);
       mma(x, f2, acc2);
     }
   };
@@ -282,7 +337,8 @@ __device__ __forceinline__ void qmma_task(const GemmArgs& p, const GemmTask& t, 
     // buffer, row-major at 128 bytes a row, 16-byte unit u of a row at position u ^ ((row >> 1) & 7)
     // (so the 32 rows an operand read touches spread over the banks); lane l copies row
     // 8 i + l / 8, position l % 8. Rows past the task and K past the end read zeros.
-    constexpr int LW = kChunkLoads<T> * (DUAL ? 2 : 1);   // weight loads per chunk
+    constexpr int LW = kChunkOwnLoads<T> * (DUAL ? 2 : 1);   // weight loads per chunk (heads not counted:
+                                                              // a head load among them only waits longer)
     constexpr int ND = NT * 4;                            // LDS DMA instructions per stage
     constexpr int SB = NT * 32 * 128;                     // stage buffer bytes
     uint32_t xo[ND];
@@ -326,6 +382,7 @@ __device__ __forceinline__ void qmma_task(const GemmArgs& p, const GemmTask& t, 
     // issue order DMA(s), W(2s), W(2s + 1), DMA(s + 1), ...: when stage s is read, the loads
     // younger than its DMA are at most two chunks of weights and one stage of DMA
     dma(first, 0);
+    load_heads(first, hc, hc2);
     load_w(first, r[0], q[0]);
     load_w(first + 1, r[1], q[1]);
     dma(next_c(first, 2), 1);
@@ -341,6 +398,7 @@ __device__ __forceinline__ void qmma_task(const GemmArgs& p, const GemmTask& t, 
           read_x(buf, h, x);
           step(c0 + u + h, r[h], q[h], x);
           __builtin_amdgcn_sched_barrier(0);
+          if (u + h + 2 == U) load_heads(next_c(c0, U), hn, hn2);
           load_w(next_c(c0, u + h + 2), r[h], q[h]);
           __builtin_amdgcn_sched_barrier(0);
         }
@@ -348,10 +406,13 @@ __device__ __forceinline__ void qmma_task(const GemmArgs& p, const GemmTask& t, 
         __builtin_amdgcn_sched_barrier(0);
         buf ^= 1;
       }
+      hc = hn;
+      hc2 = hn2;
     }
     wait_vmcnt<0>();                                      // no LDS DMA outlives the task
   } else {
     XOps x[2];
+    load_heads(first, hc, hc2);
     load_all(first, r[0], q[0], x[0]);
     load_all(first + 1, r[1], q[1], x[1]);
     for (int c0 = first; c0 < nch; c0 += U * KS) {
@@ -361,9 +422,12 @@ __device__ __forceinline__ void qmma_task(const GemmArgs& p, const GemmTask& t, 
         // keep the loads in program order behind the step that frees their registers, so the wait
         // before the next step counts only these (younger) loads
         __builtin_amdgcn_sched_barrier(0);
+        if (u + 2 == U) load_heads(c0 + U * KS, hn, hn2);
         load_all(u + 2 < U ? c0 + u + 2 : c0 + U * KS + u + 2 - U, r[u & 1], q[u & 1], x[u & 1]);
         __builtin_amdgcn_sched_barrier(0);
       }
+      hc = hn;
+      hc2 = hn2;
     }
   }
   if constexpr (KS > 1) {
