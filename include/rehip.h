@@ -207,16 +207,24 @@ size_t re_attention_work_bytes(size_t rows, size_t n_heads, size_t head_dim, siz
 int re_attention_dev(const float *d_q, const float *d_kcache, const float *d_vcache, size_t rows,
                      size_t n_heads, size_t n_kv_heads, size_t head_dim, size_t max_seq,
                      const int *d_pos, float *d_work, size_t work_bytes, float *d_ctx, void *stream);
+/* NeoX RoPE table (infer.rs:90-139): d_table[(p * head_dim/2 + i) * 2 + {0, 1}] = cos, sin of pair
+ * i's angle at position p, for p < rows (rows * head_dim floats), computed exactly as the rotation
+ * kernels compute them, so a rotation read from the table has the same bits. head_dim even. */
+int re_rope_table_dev(float theta, size_t head_dim, size_t rows, float *d_table, void *stream);
 /* One decode row's attention with the q/k/v epilogue folded in (forward.rs:347-363, 437-470):
  * d_q / d_k / d_v are the raw projection outputs of the row (no bias, not rotated); q and k get
  * their biases and NeoX RoPE at *d_pos, v its bias, k and v are appended at cache row *d_pos
  * (not stored at or past max_seq), and attention over rows 0..*d_pos is written to d_ctx
  * (n_heads x head_dim). Same results as re_qkv_rope_append_dev followed by re_attention_dev with
- * rows = 1, in two kernels instead of three. d_work: re_attention_work_bytes(1, ...) bytes. */
+ * rows = 1, in two kernels instead of three. d_rope: NULL, or re_rope_table_dev's table for theta
+ * and head_dim with max_seq rows; with it (head_dim % 8 == 0 and q, k, v, biases and table 16-byte
+ * aligned) the rotation reads its cosines and sines instead of computing them (same results,
+ * shorter critical path). d_work: re_attention_work_bytes(1, ...) bytes. */
 int re_attention_decode_dev(const float *d_q, const float *d_k, const float *d_v, const float *d_bq,
                             const float *d_bk, const float *d_bv, size_t n_heads, size_t n_kv_heads,
-                            size_t head_dim, float theta, const int *d_pos, float *d_kcache, float *d_vcache,
-                            size_t max_seq, float *d_work, size_t work_bytes, float *d_ctx, void *stream);
+                            size_t head_dim, float theta, const float *d_rope, const int *d_pos, float *d_kcache,
+                            float *d_vcache, size_t max_seq, float *d_work, size_t work_bytes, float *d_ctx,
+                            void *stream);
 /* The q/k/v projections' epilogue (forward.rs:347-363, 437-449): q = q + bq and k = k + bk
  * rotated (NeoX, as re_rope_dev) at position *d_pos + r, v = v + bv; rotated q written to
  * d_qout (rows x n_heads x head_dim), k and v appended at cache rows *d_pos + r (rows past

@@ -268,8 +268,10 @@ bool moe_gemv_fits(const re_moe* e) {
 // GEMV launch shape. Work units are 32-quant chunks (KB * chunks-per-block per row).
 // Rows up to kGemvRowsMaxK long use the row-group kernel: the rows per workgroup are the largest
 // of 64/16/8/4 that still give >= 512 workgroups (two per CU), and the waves per workgroup are
-// the fewest of 4/8/16 that leave each lane-group slot at most 2 units (4 for 64-row groups), so
-// a slot's loads are all in flight at once. Longer rows split the row over workgroups (partials
+// the fewest of 4/8/16 that leave each lane-group slot one unit (up to 16 waves; 4 units for
+// 64-row groups), so a slot's loads are all in flight at once and a latency-bound launch spends
+// little time in any one wave (Q6_K down projection of the Qwen2.5-0.5B decode step: 16 waves
+// instead of 8, 787 -> 780 us per token). Longer rows split the row over workgroups (partials
 // + a reduce kernel). Measured on MI355X over the Qwen2.5-0.5B projections in all six types.
 // Row-group shape for `tiles` 64-row tiles (of one matrix, or of a whole stack in one launch)
 // whose rows have `units` 32-quant chunks.
@@ -280,7 +282,7 @@ void rows_shape(size_t tiles, size_t units, size_t nch, int* rows_per_group, int
     if (tiles * 64 / (size_t)c >= 512) break;
   }
   if (const size_t e = env_size("REHIP_GEMV_ROWS", 0); e == 64 || e == 16 || e == 8 || e == 4) r = (int)e;
-  const size_t per_slot = r == 64 ? 4 : 2;
+  const size_t per_slot = r == 64 ? 4 : 1;
   const size_t slots = (units + per_slot - 1) / per_slot;
   const size_t per_wave = 64 / (size_t)r;
   const size_t w = (slots + per_wave - 1) / per_wave;
@@ -1701,10 +1703,18 @@ int re_attention_dev(const float* d_q, const float* d_kcache, const float* d_vca
   return RE_OK;
 }
 
+int re_rope_table_dev(float theta, size_t head_dim, size_t rows, float* d_table, void* stream) {
+  if (!d_table) return fail(RE_ERR_ARG, "null pointer");
+  if (head_dim == 0 || head_dim % 2 || head_dim > 256 || rows == 0 || rows > 32768)
+    return fail(RE_ERR_SIZE, "rope table head_dim %zu rows %zu", head_dim, rows);
+  HIP_TRY(launch_rope_table(theta, (int)head_dim, (int)rows, d_table, (hipStream_t)stream));
+  return RE_OK;
+}
+
 int re_attention_decode_dev(const float* d_q, const float* d_k, const float* d_v, const float* d_bq, const float* d_bk,
                             const float* d_bv, size_t n_heads, size_t n_kv_heads, size_t head_dim, float theta,
-                            const int* d_pos, float* d_kcache, float* d_vcache, size_t max_seq, float* d_work,
-                            size_t work_bytes, float* d_ctx, void* stream) {
+                            const float* d_rope, const int* d_pos, float* d_kcache, float* d_vcache, size_t max_seq,
+                            float* d_work, size_t work_bytes, float* d_ctx, void* stream) {
   if (!d_q || !d_k || !d_v || !d_pos || !d_kcache || !d_vcache || !d_work || !d_ctx)
     return fail(RE_ERR_ARG, "null pointer");
   if (n_heads == 0 || n_kv_heads == 0 || n_heads % n_kv_heads || head_dim == 0 || head_dim % 4 || head_dim > 256 ||
@@ -1717,7 +1727,7 @@ int re_attention_decode_dev(const float* d_q, const float* d_k, const float* d_v
     return fail(RE_ERR_SIZE, "attention workspace of %zu bytes, need %zu", work_bytes,
                 re_attention_work_bytes(1, n_heads, head_dim, max_seq));
   HIP_TRY(launch_attention_decode(d_q, d_k, d_v, d_bq, d_bk, d_bv, (int)n_heads, (int)n_kv_heads, (int)head_dim, theta,
-                                  d_pos, d_kcache, d_vcache, (int)max_seq, d_work, d_ctx, (hipStream_t)stream));
+                                  d_rope, d_pos, d_kcache, d_vcache, (int)max_seq, d_work, d_ctx, (hipStream_t)stream));
   return RE_OK;
 }
 

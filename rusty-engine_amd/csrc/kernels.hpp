@@ -220,9 +220,11 @@ hipError_t launch_kv_append(const float* k, const float* v, int rows, int kv_dim
 size_t attention_work_floats(int rows, int heads, int hd, int max_seq);
 // One decode row: the q|k|v epilogue (bias, RoPE at *pos, k/v appended at row *pos) folded into
 // the key-split attention; q/k/v are the raw projection outputs of the row
+hipError_t launch_rope_table(float base, int hd, int rows, float* tab, hipStream_t s);
 hipError_t launch_attention_decode(const float* q, const float* k, const float* v, const float* bq, const float* bk,
-                                   const float* bv, int heads, int kv_heads, int hd, float base, const int* pos,
-                                   float* kc, float* vc, int max_seq, float* work, float* ctx, hipStream_t s);
+                                   const float* bv, int heads, int kv_heads, int hd, float base, const float* rope,
+                                   const int* pos, float* kc, float* vc, int max_seq, float* work, float* ctx,
+                                   hipStream_t s);
 hipError_t launch_attention(const float* q, const float* kc, const float* vc, int rows, int heads, int kv_heads,
                             int hd, int max_seq, const int* pos, float* work, float* ctx, hipStream_t s);
 // q/k/v projections (+ bias) -> rotated q (rows x heads*hd), rotated k and v appended at cache rows *pos + r

@@ -252,19 +252,67 @@ struct DecodeQkv {
   float base;           // RoPE theta
   float* kc_out;        // caches, written at row *pos
   float* vc_out;
+  const float2* rope;   // null, or (cos, sin) of every pair at positions 0 .. rope_rows - 1
+  int rope_rows;
 };
 
-// NeoX rotation of the pair (x0, x1) = (x[i], x[i + hd/2]) at position p (infer.rs:90-139); shared
-// by qkv_rope_append_kernel and the folded decode epilogue, so both give the same bits
-__device__ __forceinline__ void rope_pair(float x0, float x1, int i, int hd, int p, float base, float& o0, float& o1) {
+// NeoX rotation of the pair (x0, x1) = (x[i], x[i + hd/2]) at position p (infer.rs:90-139): the
+// angle's cosine and sine, and the rotation. Shared by qkv_rope_append_kernel, the folded decode
+// epilogue and rope_table_kernel, so every path gives the same bits.
+__device__ __forceinline__ void rope_cs(int i, int hd, int p, float base, float& c, float& sn) {
   const float f = 1.0f / powf(base, (float)(2 * i) / (float)hd);
   const float a = (float)p * f;
-  const float c = cosf(a), sn = sinf(a);
+  c = cosf(a);
+  sn = sinf(a);
+}
+__device__ __forceinline__ void rope_rot(float x0, float x1, float c, float sn, float& o0, float& o1) {
   o0 = x0 * c - x1 * sn;
   o1 = x1 * c + x0 * sn;
 }
+__device__ __forceinline__ void rope_pair(float x0, float x1, int i, int hd, int p, float base, float& o0, float& o1) {
+  float c, sn;
+  rope_cs(i, hd, p, base, c, sn);
+  rope_rot(x0, x1, c, sn, o0, o1);
+}
 
-template <int NC, bool QKV>   // kc / vc are not __restrict__: with QKV the new row is stored through dq
+// tab[p * hd/2 + i] = (cos, sin) of pair i's angle at position p, for p < rows
+__global__ __launch_bounds__(256) void rope_table_kernel(float base, int hd, int rows, float2* __restrict__ tab) {
+  const int half = hd >> 1;
+  const size_t n = (size_t)rows * (size_t)half;
+  for (size_t e = (size_t)blockIdx.x * 256 + threadIdx.x; e < n; e += (size_t)gridDim.x * 256) {
+    const int p = (int)(e / (size_t)half), i = (int)(e - (size_t)p * (size_t)half);
+    float c, sn;
+    rope_cs(i, hd, p, base, c, sn);
+    tab[e] = make_float2(c, sn);
+  }
+}
+
+// Dims d .. d + 3 of a rotated head vector from the raw ones (own), their rotation partners
+// (par, at d + hd/2 when lo, else d - hd/2) and the (cos, sin) of pairs i .. i + 3
+// (cs0 = pairs i, i + 1; cs1 = i + 2, i + 3): the x0 side of each pair when lo, else the x1 side.
+__device__ __forceinline__ float4 rope4(float4 own, float4 par, float4 cs0, float4 cs1, bool lo) {
+  const float o[4] = {own.x, own.y, own.z, own.w}, q[4] = {par.x, par.y, par.z, par.w};
+  const float c[4] = {cs0.x, cs0.z, cs1.x, cs1.z}, sn[4] = {cs0.y, cs0.w, cs1.y, cs1.w};
+  float r[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    float o0, o1;
+    if (lo) {
+      rope_rot(o[j], q[j], c[j], sn[j], o0, o1);
+      r[j] = o0;
+    } else {
+      rope_rot(q[j], o[j], c[j], sn[j], o0, o1);
+      r[j] = o1;
+    }
+  }
+  return make_float4(r[0], r[1], r[2], r[3]);
+}
+__device__ __forceinline__ float4 add4(float4 a, float4 b) { return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w); }
+
+// TAB (with QKV, hd % 8 == 0, dq.rope given): each lane rotates its own dims of q, and the team
+// holding the new key those of k, in registers with the table's (cos, sin); no LDS pass or barrier
+// comes before the scores.
+template <int NC, bool QKV, bool TAB = false>   // kc / vc are not __restrict__: with QKV the new row is stored through dq
 __global__ __launch_bounds__(256) void attention_split_kernel(const float* __restrict__ q, const float* kc,
                                                               const float* vc, int heads, int kv_heads,
                                                               int hd, int max_seq, const int* __restrict__ pos,
@@ -296,7 +344,51 @@ __global__ __launch_bounds__(256) void attention_split_kernel(const float* __res
   const bool has_new = QKV && p0 >= 0 && p0 < max_seq && p0 >= j0 && p0 < j0 + jn;
   const int half = hd >> 1, t = threadIdx.x;
   float qx0 = 0.0f, qx1 = 0.0f, kx0 = 0.0f, kx1 = 0.0f, vx = 0.0f;
-  if constexpr (QKV) {
+  // TAB: raw q of this lane's dims and their partners (biased), the new key's and value's (every
+  // team of the split holding key p0: teams past the split's last key, jn - 1, read that row too),
+  // and the (cos, sin) of their pairs
+  float4 tq[NC], tqp[NC], tk[NC], tkp[NC], tv[NC], tc0[NC], tc1[NC];
+  const bool newteam = TAB && has_new;
+  if constexpr (TAB) {
+    const bool from_tab = p0 >= 0 && p0 < dq.rope_rows;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int d = 4 * tl + 64 * c;
+      const int dd = d < hd ? d : 0;
+      const bool lo = dd < half;
+      const int dp = lo ? dd + half : dd - half, i0 = lo ? dd : dd - half;
+      const float* qr = q + (size_t)h * hd;
+      tq[c] = *reinterpret_cast<const float4*>(qr + dd);
+      tqp[c] = *reinterpret_cast<const float4*>(qr + dp);
+      if (dq.bq) {
+        tq[c] = add4(tq[c], *reinterpret_cast<const float4*>(dq.bq + (size_t)h * hd + dd));
+        tqp[c] = add4(tqp[c], *reinterpret_cast<const float4*>(dq.bq + (size_t)h * hd + dp));
+      }
+      if (from_tab) {
+        const float2* cs = dq.rope + (size_t)p0 * half + i0;
+        tc0[c] = *reinterpret_cast<const float4*>(cs);
+        tc1[c] = *reinterpret_cast<const float4*>(cs + 2);
+      } else {                           // a position past the table: computed here
+        float cv[4], sv[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) rope_cs(i0 + j, hd, p0, dq.base, cv[j], sv[j]);
+        tc0[c] = make_float4(cv[0], sv[0], cv[1], sv[1]);
+        tc1[c] = make_float4(cv[2], sv[2], cv[3], sv[3]);
+      }
+      if (newteam) {
+        const float* kr = dq.ks + (size_t)kvh * hd;
+        const float* vr = dq.vs + (size_t)kvh * hd;
+        tk[c] = *reinterpret_cast<const float4*>(kr + dd);
+        tkp[c] = *reinterpret_cast<const float4*>(kr + dp);
+        tv[c] = *reinterpret_cast<const float4*>(vr + dd);
+        if (dq.bk) {
+          tk[c] = add4(tk[c], *reinterpret_cast<const float4*>(dq.bk + (size_t)kvh * hd + dd));
+          tkp[c] = add4(tkp[c], *reinterpret_cast<const float4*>(dq.bk + (size_t)kvh * hd + dp));
+        }
+        if (dq.bv) tv[c] = add4(tv[c], *reinterpret_cast<const float4*>(dq.bv + (size_t)kvh * hd + dd));
+      }
+    }
+  } else if constexpr (QKV) {
     if (t < half) {
       const float* qr = q + (size_t)h * hd;
       qx0 = qr[t];
@@ -338,8 +430,33 @@ __global__ __launch_bounds__(256) void attention_split_kernel(const float* __res
       vv[u][c] = d < hd ? *reinterpret_cast<const float4*>(vbase + row + d) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
   }
+  float4 qv[NC];
+  if constexpr (TAB) {
+    // the kv group's first q head appends, from the team whose own key is p0
+    const bool app = newteam && team == ((jn - 1) & 15) && h % (heads / kv_heads) == 0;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int d = 4 * tl + 64 * c;
+      const bool lo = d < half;
+      qv[c] = d < hd ? rope4(tq[c], tqp[c], tc0[c], tc1[c], lo) : make_float4(0.f, 0.f, 0.f, 0.f);
+      if (newteam && d < hd) {
+        const float4 kn = rope4(tk[c], tkp[c], tc0[c], tc1[c], lo);
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          if (j0 + min(16 * u + team, jn - 1) == p0) {   // the row read for key p0 (or past it)
+            kv[u][c] = kn;
+            vv[u][c] = tv[c];
+          }
+        }
+        if (app) {
+          *reinterpret_cast<float4*>(dq.kc_out + (size_t)p0 * kv_dim + (size_t)kvh * hd + d) = kn;
+          *reinterpret_cast<float4*>(dq.vc_out + (size_t)p0 * kv_dim + (size_t)kvh * hd + d) = tv[c];
+        }
+      }
+    }
+  }
   // QKV: rotated q in part[0..hd), the new key and value in part[256..256+hd), part[512..512+hd)
-  if constexpr (QKV) {
+  if constexpr (QKV && !TAB) {
     if (t < half) {
       rope_pair(qx0, qx1, t, hd, p0, dq.base, part[t], part[t + half]);
       if (has_new) rope_pair(kx0, kx1, t, hd, p0, dq.base, part[256 + t], part[256 + t + half]);
@@ -353,14 +470,15 @@ __global__ __launch_bounds__(256) void attention_split_kernel(const float* __res
       }
     }
   }
-  const float* qh = QKV ? part : q + ((size_t)r * heads + h) * hd;
-  float4 qv[NC];
+  if constexpr (!TAB) {
+    const float* qh = QKV ? part : q + ((size_t)r * heads + h) * hd;
 #pragma unroll
-  for (int c = 0; c < NC; ++c) {
-    const int d = 4 * tl + 64 * c;
-    qv[c] = d < hd ? *reinterpret_cast<const float4*>(qh + d) : make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int c = 0; c < NC; ++c) {
+      const int d = 4 * tl + 64 * c;
+      qv[c] = d < hd ? *reinterpret_cast<const float4*>(qh + d) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
   }
-  if (has_new) {                         // the new key is the split's last: from LDS, not the cache
+  if (!TAB && has_new) {                 // the new key is the split's last: from LDS, not the cache
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       if (j0 + min(16 * u + team, jn - 1) == p0) {
@@ -375,22 +493,30 @@ __global__ __launch_bounds__(256) void attention_split_kernel(const float* __res
       }
     }
   }
+  // the U keys' dots, then their team reductions interleaved (no key's shuffle rounds wait on
+  // another's); each key's terms add in the same order either way
+  float a[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    a[u] = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      a[u] = __builtin_fmaf(qv[c].x, kv[u][c].x, a[u]);
+      a[u] = __builtin_fmaf(qv[c].y, kv[u][c].y, a[u]);
+      a[u] = __builtin_fmaf(qv[c].z, kv[u][c].z, a[u]);
+      a[u] = __builtin_fmaf(qv[c].w, kv[u][c].w, a[u]);
+    }
+  }
+#pragma unroll
+  for (int off = 8; off > 0; off >>= 1)
+#pragma unroll
+    for (int u = 0; u < U; ++u) a[u] += __shfl_xor(a[u], off, 64);
   float mx = -INFINITY;
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    float a = 0.0f;
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      a = __builtin_fmaf(qv[c].x, kv[u][c].x, a);
-      a = __builtin_fmaf(qv[c].y, kv[u][c].y, a);
-      a = __builtin_fmaf(qv[c].z, kv[u][c].z, a);
-      a = __builtin_fmaf(qv[c].w, kv[u][c].w, a);
-    }
-#pragma unroll
-    for (int off = 8; off > 0; off >>= 1) a += __shfl_xor(a, off, 64);
     const int jj = 16 * u + team;
     if (tl == 0 && jj < jn) {
-      const float v = a * scale;
+      const float v = a[u] * scale;
       sc[jj] = v;
       mx = fmaxf(mx, v);
     }
@@ -813,12 +939,35 @@ hipError_t launch_attention(const float* q, const float* kc, const float* vc, in
                        max_seq, pos, ctx);
   return hipGetLastError();
 }
+hipError_t launch_rope_table(float base, int hd, int rows, float* tab, hipStream_t s) {
+  const size_t n = (size_t)rows * (size_t)(hd / 2);
+  const unsigned grid = (unsigned)std::min<size_t>((n + 255) / 256, 4096);
+  hipLaunchKernelGGL(rope_table_kernel, dim3(grid), dim3(256), 0, s, base, hd, rows, reinterpret_cast<float2*>(tab));
+  return hipGetLastError();
+}
 hipError_t launch_attention_decode(const float* q, const float* k, const float* v, const float* bq, const float* bk,
-                                   const float* bv, int heads, int kv_heads, int hd, float base, const int* pos,
-                                   float* kc, float* vc, int max_seq, float* work, float* ctx, hipStream_t s) {
+                                   const float* bv, int heads, int kv_heads, int hd, float base, const float* rope,
+                                   const int* pos, float* kc, float* vc, int max_seq, float* work, float* ctx,
+                                   hipStream_t s) {
   const int nsp = (max_seq + kAttnSplitKeys - 1) / kAttnSplitKeys;
   const dim3 grid((unsigned)heads, 1u, (unsigned)nsp);
-  const DecodeQkv dq{k, v, bq, bk, bv, base, kc, vc};
+  const DecodeQkv dq{k, v, bq, bk, bv, base, kc, vc, reinterpret_cast<const float2*>(rope), max_seq};
+  auto a16 = [](const void* x) { return ((uintptr_t)x & 15) == 0; };   // null passes
+  if (rope && hd % 8 == 0 && a16(rope) && a16(q) && a16(k) && a16(v) && a16(bq) && a16(bk) && a16(bv)) {
+    if (hd <= 64)
+      hipLaunchKernelGGL((attention_split_kernel<1, true, true>), grid, dim3(256), 0, s, q, kc, vc, heads, kv_heads,
+                         hd, max_seq, pos, work, dq);
+    else if (hd <= 128)
+      hipLaunchKernelGGL((attention_split_kernel<2, true, true>), grid, dim3(256), 0, s, q, kc, vc, heads, kv_heads,
+                         hd, max_seq, pos, work, dq);
+    else
+      hipLaunchKernelGGL((attention_split_kernel<4, true, true>), grid, dim3(256), 0, s, q, kc, vc, heads, kv_heads,
+                         hd, max_seq, pos, work, dq);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(attention_combine_kernel, dim3((unsigned)heads, 1u), dim3(64), 0, s, work, heads, hd, nsp, ctx);
+    return hipGetLastError();
+  }
   if (hd <= 64)
     hipLaunchKernelGGL((attention_split_kernel<1, true>), grid, dim3(256), 0, s, q, kc, vc, heads, kv_heads, hd,
                        max_seq, pos, work, dq);

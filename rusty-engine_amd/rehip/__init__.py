@@ -51,7 +51,8 @@ EXPORTS = ("re_init", "re_last_error", "re_version", "re_row_bytes", "re_tiled_b
            "re_gguf_get_float", "re_gguf_get_str", "re_gguf_get_array", "re_gguf_tensor_info",
            "re_gguf_find_tensor", "re_gguf_tensor_data", "re_qmat_from_gguf", "re_moe_from_gguf",
            "re_quantize_q8_act", "re_quantize_q8_act_dev", "re_qmat_matmul_i8", "re_qmat_matmul_i8_dev",
-           "re_attention_decode_dev", "re_qmat_gemv_plan", "re_qmat_matmul_noalloc_dev", "re_moe_set_shared")
+           "re_attention_decode_dev", "re_qmat_gemv_plan", "re_qmat_matmul_noalloc_dev", "re_moe_set_shared",
+           "re_rope_table_dev")
 GEMV_KERNELS = {0: "split", 1: "rows", 2: "tile", 3: "dense"}
 
 
@@ -146,7 +147,8 @@ def lib() -> C.CDLL:
         L.re_gguf_tensor_data.argtypes = [_vp, _sz, C.POINTER(_vp), C.POINTER(_sz)]
         L.re_qmat_from_gguf.argtypes = [_vp, C.c_char_p, _sz, _sz, C.POINTER(_vp)]
         L.re_attention_decode_dev.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, C.c_float, _vp, _vp, _vp,
-                                              _sz, _vp, _sz, _vp, _vp]
+                                              _vp, _sz, _vp, _sz, _vp, _vp]
+        L.re_rope_table_dev.argtypes = [C.c_float, _sz, _sz, _vp, _vp]
         L.re_quantize_q8_act.argtypes = [_vp, _sz, _sz, _vp, _vp]
         L.re_quantize_q8_act_dev.argtypes = [_vp, _sz, _sz, _vp, _vp, _vp]
         L.re_qmat_matmul_i8.argtypes = [_vp, _vp, _vp, _sz, _vp]
@@ -399,12 +401,18 @@ def qkv_rope_append_dev(q, ldq, k, ldk, v, ldv, bq, bk, bv, rows, n_heads, n_kv_
 
 
 def attention_decode_dev(q, k, v, bq, bk, bv, n_heads, n_kv_heads, head_dim, theta, pos, kcache, vcache, max_seq,
-                         work, work_bytes, ctx, stream=None):
+                         work, work_bytes, ctx, stream=None, rope=None):
     """One decode row: q/k/v bias + RoPE + cache append folded into the key-split attention
-    (re_attention_decode_dev)."""
+    (re_attention_decode_dev); `rope`: None, or a rope_table_dev table with max_seq rows."""
     _check(lib().re_attention_decode_dev(_p(q), _p(k), _p(v), _p(bq), _p(bk), _p(bv), n_heads, n_kv_heads, head_dim,
-                                         theta, _p(pos), _p(kcache), _p(vcache), max_seq, _p(work), work_bytes,
-                                         _p(ctx), _stream_ptr(stream)))
+                                         theta, _p(rope), _p(pos), _p(kcache), _p(vcache), max_seq, _p(work),
+                                         work_bytes, _p(ctx), _stream_ptr(stream)))
+
+
+def rope_table_dev(theta, head_dim, rows, table, stream=None):
+    """(cos, sin) of every NeoX rotation pair at positions 0 .. rows - 1 into `table`
+    (rows * head_dim floats; re_rope_table_dev)."""
+    _check(lib().re_rope_table_dev(theta, head_dim, rows, _p(table), _stream_ptr(stream)))
 
 
 def decode_advance_dev(best, tok, pos, delta, hist=None, hist_len=0, stream=None):

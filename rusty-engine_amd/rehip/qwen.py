@@ -480,7 +480,7 @@ class DeviceDecoder:
 
     def __init__(self, mb: ModelBytes, max_seq: int, mode: int = MODE_F32, prefill_rows: int = 1024,
                  use_graph: bool = True):
-        from . import Ffn, attention_work_bytes, hip
+        from . import Ffn, attention_work_bytes, hip, rope_table_dev
         self.mb, self.mode, self.max_seq = mb, mode, max_seq
         self.use_graph = use_graph
         g = self.g = mb.geom
@@ -525,6 +525,9 @@ class DeviceDecoder:
         self.hist = B.from_array(np.zeros(max_seq, np.int32))
         self.toks = B(cap * 4)
         self.stream = hip.Stream()
+        # RoPE (cos, sin) of every position: the decode attention reads them instead of computing
+        self.rope = B(max_seq * hd * 4)
+        rope_table_dev(g.rope_freq_base, hd, max_seq, self.rope, self.stream)
         self.graph = None
         self.seq_len = 0
 
@@ -544,7 +547,7 @@ class DeviceDecoder:
         attention_decode_dev(self.qkv, _Offset(self.qkv, 4 * d), _Offset(self.qkv, 4 * (d + kv)), blk["q_bias"],
                              blk["k_bias"], blk["v_bias"], g.n_heads, g.n_kv_heads, g.head_dim, g.rope_freq_base,
                              self.pos, blk["kc"], blk["vc"], self.max_seq, self.work, self.work_bytes, self.ctx,
-                             self.stream)
+                             self.stream, rope=self.rope)
 
     def _attention(self, blk, rows):
         from . import attention_dev

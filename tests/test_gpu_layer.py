@@ -53,6 +53,20 @@ def test_rope(rows, heads, hd, pos0, off):
     np.testing.assert_allclose(got, want, rtol=0, atol=5e-4)
 
 
+@pytest.mark.parametrize("hd,rows,base", [(64, 2048, 1e6), (128, 300, 1e4), (2, 5, 1e4)])
+def test_rope_table(hd, rows, base):
+    """re_rope_table_dev against the host (cos, sin) of the NeoX angles (forward.rs rope tables),
+    interleaved per pair; its bits against the computed rotation are pinned by the decode
+    attention test."""
+    tab = B(rows * hd * 4)
+    rehip.rope_table_dev(base, hd, rows, tab)
+    got = down(tab, rows * hd).reshape(rows, hd // 2, 2)
+    cos, sin = qwen.rope_table(rows, 0, hd, base)
+    np.testing.assert_allclose(got[:, :, 0], cos, rtol=0, atol=5e-4)
+    np.testing.assert_allclose(got[:, :, 1], sin, rtol=0, atol=5e-4)
+    assert got[0, :, 0].tolist() == [1.0] * (hd // 2) and got[0, :, 1].tolist() == [0.0] * (hd // 2)
+
+
 def test_kv_append_and_bounds():
     kv, max_seq = 128, 16
     rng = np.random.default_rng(3)
@@ -343,19 +357,25 @@ def test_device_decoder_qwen_shape_64_steps_match_cpu_path():
     assert got == want, next(i for i, (a, b) in enumerate(zip(got, want)) if a != b)
 
 
+@pytest.mark.parametrize("rope", [False, True])
 @pytest.mark.parametrize("nh,nkv,hd,pos0,bias", [(14, 2, 64, 0, True), (14, 2, 64, 37, True), (14, 2, 64, 127, False),
                                                  (14, 2, 64, 128, True), (4, 4, 128, 300, True),
-                                                 (2, 1, 256, 511, True), (14, 2, 64, 512, True)])
-def test_attention_decode_equals_epilogue_then_attention(nh, nkv, hd, pos0, bias):
+                                                 (2, 1, 256, 511, True), (14, 2, 64, 512, True),
+                                                 (3, 1, 68, 77, True)])
+def test_attention_decode_equals_epilogue_then_attention(nh, nkv, hd, pos0, bias, rope):
     """re_attention_decode_dev (q|k|v epilogue folded into the split attention) against
     re_qkv_rope_append_dev + re_attention_dev on the same raw projection row: identical context
     and caches, including the split boundary (position 128), the last cache row and a position
-    past the cache (nothing stored, the old keys attended)."""
+    past the cache (nothing stored, the old keys attended). With `rope` the decode reads its
+    cosines and sines from re_rope_table_dev's table (rotation in registers), so the bit equality
+    also pins the table against the computed rotation; a position past the table computes them,
+    and head_dim 68 (not a multiple of 8) keeps the computing kernel."""
     max_seq = 512
     rng = np.random.default_rng(pos0 + nh)
     kvd = nkv * hd
-    kc0 = np.zeros((max_seq, kvd), np.float32)
-    vc0 = np.zeros((max_seq, kvd), np.float32)
+    # rows not yet written hold NaN (a fresh cache is not cleared): no lane may fold them in
+    kc0 = np.full((max_seq, kvd), np.nan, np.float32)
+    vc0 = np.full((max_seq, kvd), np.nan, np.float32)
     n_old = min(pos0, max_seq)
     kc0[:n_old] = rng.standard_normal((n_old, kvd))
     vc0[:n_old] = rng.standard_normal((n_old, kvd))
@@ -380,10 +400,14 @@ def test_attention_decode_equals_epilogue_then_attention(nh, nkv, hd, pos0, bias
     # folded path
     kc_b, vc_b = B.from_array(kc0), B.from_array(vc0)
     ctx_b = B(nh * hd * 4)
+    tab = None
+    if rope:
+        tab = B(max_seq * hd * 4)
+        rehip.rope_table_dev(theta, hd, max_seq, tab)
     rehip.attention_decode_dev(dq, qwen._Offset(dq, kd), qwen._Offset(dq, vd), bqd, bkd, bvd, nh, nkv, hd, theta, pd, kc_b, vc_b,
-                               max_seq, B.from_array(np.full(wb // 4, np.nan, np.float32)), wb, ctx_b)
+                               max_seq, B.from_array(np.full(wb // 4, np.nan, np.float32)), wb, ctx_b, rope=tab)
     a, b = down(ctx_a, nh * hd), down(ctx_b, nh * hd)
     assert np.isfinite(b).all()
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
-    assert np.array_equal(down(kc_a, max_seq * kvd), down(kc_b, max_seq * kvd))
-    assert np.array_equal(down(vc_a, max_seq * kvd), down(vc_b, max_seq * kvd))
+    assert np.array_equal(down(kc_a, max_seq * kvd).view(np.uint32), down(kc_b, max_seq * kvd).view(np.uint32))
+    assert np.array_equal(down(vc_a, max_seq * kvd).view(np.uint32), down(vc_b, max_seq * kvd).view(np.uint32))
