@@ -104,10 +104,12 @@ def test_grouped_gemm_bf16_activations_bit_identical(T, E, k, gt, dt, monkeypatc
 
 
 @pytest.mark.parametrize("T,E,k", [(1, 16, 4), (5, 16, 4), (40, 16, 4), (3, 128, 8), (300, 32, 4)])
-def test_forward_routed_equals_host_routed(T, E, k):
-    """Device grouping/tasks vs the host planner: the same kernels over the same rows, so the
-    outputs are identical whenever both pick the same path (GEMV for few rows per expert,
-    grouped GEMM otherwise)."""
+def test_forward_routed_equals_host_routed(T, E, k, monkeypatch):
+    """Device grouping/tasks vs the host planner (REHIP_MOE_HOST_GROUP=1: the host-routed call
+    groups on the host instead of handing its ids to the device planner): the same kernels over
+    the same rows, so the outputs are identical whenever both pick the same path (GEMV for few
+    rows per expert, grouped GEMM otherwise)."""
+    monkeypatch.setenv("REHIP_MOE_HOST_GROUP", "1")
     hidden, inter = 512, 256
     gate, up, down_, x, logits = moe_case(900 + T + E, E, hidden, inter, T, k)
     ids = np.zeros((T, k), np.int32)
@@ -135,10 +137,12 @@ def test_forward_routed_equals_host_routed(T, E, k):
 
 
 @pytest.mark.parametrize("T,E,k", [(1023, 520, 8), (1024, 520, 8), (257, 1, 1), (96, 3, 2)])
-def test_device_planner_extremes(T, E, k):
+def test_device_planner_extremes(T, E, k, monkeypatch):
     """The device planner at its limits: 8184 and 8192 (token, expert) pairs (every wave's
     segment full, ten-bit expert ids), one expert, and a pair count that is not a multiple of 64.
-    Device-routed equals host-routed bit for bit (both take the grouped GEMM path here)."""
+    Device-routed equals host-routed with the host planner (REHIP_MOE_HOST_GROUP=1) bit for bit
+    (both take the grouped GEMM path here)."""
+    monkeypatch.setenv("REHIP_MOE_HOST_GROUP", "1")
     hidden, inter = 256, 256
     gate, up, down_, x, logits = moe_case(7000 + T + E, E, hidden, inter, T, k)
     ids = np.argsort(-logits, axis=1, kind="stable")[:, :k].astype(np.int32)
@@ -151,6 +155,31 @@ def test_device_planner_extremes(T, E, k):
         got = down(out, T * hidden)
         host = moe.forward(x, T, k, ids.reshape(-1).astype(np.uint32), wts.reshape(-1), mode)
         assert np.array_equal(got, host), mode
+    moe.close()
+
+
+@pytest.mark.parametrize("T,E,k,hidden,inter", [(32, 128, 8, 2048, 768), (5, 16, 4, 512, 256), (300, 32, 4, 512, 256),
+                                                (2, 8, 8, 256, 256)])
+def test_host_routed_hands_ids_to_device_planner(T, E, k, hidden, inter):
+    """A host-routed call of up to 2048 (token, expert) pairs uploads its ids and weights and runs
+    the device-routed launches: bit for bit the device-routed result, over repeated calls (the
+    pinned staging reused), in both modes; and within tolerance of the oracle."""
+    gate, up, down_, x, logits = moe_case(3300 + T + E, E, hidden, inter, T, k)
+    ids = np.argsort(-logits, axis=1, kind="stable")[:, :k].astype(np.int32)
+    wts = np.random.default_rng(T + 5).uniform(0.1, 1.0, (T, k)).astype(np.float32)
+    moe = rehip.MoeExperts(rehip.Q4_K, gate, rehip.Q4_K, up, rehip.Q6_K, down_, E, hidden, inter)
+    xd, idd, wd = B.from_array(x), B.from_array(ids.reshape(-1)), B.from_array(wts.reshape(-1))
+    want = O.moe_ffn(rehip.Q4_K, gate, rehip.Q4_K, up, rehip.Q6_K, down_, E, hidden, inter, x, T, k,
+                     ids.reshape(-1).astype(np.uint32), wts.reshape(-1))
+    for mode, tol in [(rehip.MODE_F32, 1e-4), (rehip.MODE_BF16, 1e-2)]:
+        out = B(T * hidden * 4)
+        moe.forward_routed_dev(xd, T, k, idd, wd, out, mode)
+        routed = down(out, T * hidden)
+        for _ in range(3):
+            host = moe.forward(x, T, k, ids.reshape(-1).astype(np.uint32), wts.reshape(-1), mode)
+            assert np.array_equal(host.view(np.uint32), routed.view(np.uint32)), mode
+        rel = np.linalg.norm(host - want) / np.linalg.norm(want)
+        assert rel <= tol, (mode, rel)
     moe.close()
 
 
