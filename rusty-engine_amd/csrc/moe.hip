@@ -753,29 +753,36 @@ __global__ __launch_bounds__(WAVES * 64) void moe_down_combine_kernel(MoeDownCom
       }
     }
   }
+  // every expert slot's lane-group fold at once (slots past k hold zeros), so the shuffle rounds
+  // of different slots overlap instead of running one slot after another
 #pragma unroll
-  for (int j = 0; j < KM; ++j) {
-    if (j >= k) break;
-    float v = acc[j];
+  for (int off = R; off < 64; off *= 2)
 #pragma unroll
-    for (int off = R; off < 64; off *= 2) v += __shfl_xor(v, off, 64);
-    if (lane < R) red[(wave * KM + j) * R + lane] = v;
+    for (int j = 0; j < KM; ++j) acc[j] += __shfl_xor(acc[j], off, 64);
+  if (lane < R) {
+#pragma unroll
+    for (int j = 0; j < KM; ++j) red[(wave * KM + j) * R + lane] = acc[j];
   }
   __syncthreads();
-  if ((int)threadIdx.x < R) {
-    const int r = threadIdx.x;
-    float o = 0.0f;
+  // wave 0: lane (j, r) = (lane / R, lane % R) adds slot j's wave sums for row r in wave order;
+  // lane r then gathers the KM slot sums and combines them in slot order
+  static_assert(R * KM == 64, "one lane per (slot, row)");
+  if (wave == 0) {
+    const int j = lane / R, r = lane % R;
+    float y = red[(0 * KM + j) * R + r];
 #pragma unroll
-    for (int j = 0; j < KM; ++j) {
-      if (j >= k) break;
-      if (!ok[j]) continue;
-      float y = red[(0 * KM + j) * R + r];
+    for (int w = 1; w < WAVES; ++w) y += red[(w * KM + j) * R + r];
+    float ys[KM];
 #pragma unroll
-      for (int w = 1; w < WAVES; ++w) y += red[(w * KM + j) * R + r];
-      o = __fadd_rn(o, __fmul_rn(wv[j], y));
+    for (int q = 0; q < KM; ++q) ys[q] = __shfl(y, q * R + r, 64);
+    if (lane < R) {
+      float o = 0.0f;
+#pragma unroll
+      for (int q = 0; q < KM; ++q)
+        if (q < k && ok[q]) o = __fadd_rn(o, __fmul_rn(wv[q], ys[q]));
+      const int orow = blk * R + r;
+      if (orow < a.m) a.out[orow] = o;
     }
-    const int orow = blk * R + r;
-    if (orow < a.m) a.out[orow] = o;
   }
 }
 
