@@ -378,7 +378,9 @@ __device__ __forceinline__ void qmma_task(const GemmArgs& p, const GemmTask& t, 
       load(c, rr, wr, wbase);
       if constexpr (DUAL) load(c, qq, wr2, wbase2);
     };
-    auto next_c = [&](int c0, int u) { return u < U ? c0 + u : c0 + U * KS + u - U; };
+    // chunk u of this wave's chunks from c0 on (u may reach two groups ahead: U is 2 for the
+    // 32-element blocks, and the stage DMA looks four chunks ahead)
+    auto next_c = [&](int c0, int u) { return c0 + (u / U) * U * KS + u % U; };
     // issue order DMA(s), W(2s), W(2s + 1), DMA(s + 1), ...: when stage s is read, the loads
     // younger than its DMA are at most two chunks of weights and one stage of DMA
     dma(first, 0);

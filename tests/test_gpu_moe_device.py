@@ -401,3 +401,40 @@ def test_register_decoded_grouped_gemm(T, E, k, gt, dt, monkeypatch):
             assert np.linalg.norm(b - a) / np.linalg.norm(a) <= 1e-4, name
         assert np.linalg.norm(b - want) / np.linalg.norm(want) <= 1e-2, name
     moe.close()
+
+
+
+QMMA_FORCED_TYPES = [(rehip.Q4_K, rehip.Q6_K), (rehip.Q5_K, rehip.Q4_K), (rehip.Q6_K, rehip.Q5_K),
+                     (rehip.Q4_0, rehip.Q8_0), (rehip.Q5_0, rehip.Q4_0), (rehip.Q8_0, rehip.Q5_0)]
+
+
+@pytest.mark.parametrize("gt,dt", QMMA_FORCED_TYPES)
+@pytest.mark.parametrize("ks,xl", [("2", None), ("2", "0"), ("1", "1")])
+def test_qmma_forced_wave_split_and_staging(gt, dt, ks, xl, monkeypatch):
+    """The register-decoded expert GEMMs with 64-row tasks (300 tokens over 16 experts; an
+    expert's ragged last chunk runs the one-tile body) under the launch overrides: K split over
+    two waves of a task (REHIP_QMMA_KS=2) with the down projection's activations staged in LDS
+    (the stage copy runs four chunks ahead, two of a wave's groups for the 32-element block
+    types), the same with staging off, and staging forced onto the gate/up pair. Host- and
+    device-routed against the oracle at the bf16 bar."""
+    T, E, k, hidden, inter = 300, 16, 4, 512, 320
+    gate, up, down_, x, logits = moe_case(1234 + gt + 7 * dt, E, hidden, inter, T, k, gt, dt)
+    ids = np.zeros((T, k), np.int32)
+    wts = np.zeros((T, k), np.float32)
+    for t in range(T):
+        ids[t], wts[t] = O.top_k(logits[t], k)
+    moe = rehip.MoeExperts(gt, gate, gt, up, dt, down_, E, hidden, inter)
+    monkeypatch.setenv("REHIP_MOE_QMMA", "1")
+    monkeypatch.setenv("REHIP_QMMA_KS", ks)
+    if xl:
+        monkeypatch.setenv("REHIP_QMMA_XL", xl)
+    out = B(T * hidden * 4)
+    moe.forward_routed_dev(B.from_array(x), T, k, B.from_array(ids.reshape(-1)), B.from_array(wts.reshape(-1)),
+                           out, rehip.MODE_BF16)
+    got = {"device-routed": down(out, T * hidden),
+           "host-routed": moe.forward(x, T, k, ids.reshape(-1).astype(np.uint32), wts.reshape(-1), rehip.MODE_BF16)}
+    want = O.moe_ffn(gt, gate, gt, up, dt, down_, E, hidden, inter, x, T, k,
+                     ids.reshape(-1).astype(np.uint32), wts.reshape(-1))
+    for name, g in got.items():
+        assert np.linalg.norm(g - want) / np.linalg.norm(want) <= 1e-2, name
+    moe.close()
