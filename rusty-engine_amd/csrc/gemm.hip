@@ -377,18 +377,28 @@ __global__ __launch_bounds__(WM* WN * 64 * KG) void gemm_kernel(GemmArgs p) {
         }
       }
     } else {
-#pragma unroll 8
-      for (int kk = 0; kk < BK / 2; ++kk) {
-        float av[TM], bv[TN];
+      // each lane reads four consecutive k of its row (one 16-byte LDS read: the 32 rows of a
+      // read, 132 floats apart, cover all banks) and feeds four v_mfma_f32_32x32x2f32: MFMA q of
+      // the eight-k slice kk takes k = 8 kk + q (lanes 0-31) and 8 kk + 4 + q (lanes 32-63), for
+      // the weights and the activations alike
+      const float* wsrc = Ws + (BM / WM * wm + (lane & 31)) * LD + 4 * (lane >> 5);
+      const float* xsrc = Xs + (BN / WN * wn + (lane & 31)) * LD + 4 * (lane >> 5);
+#pragma unroll 4
+      for (int kk = 0; kk < BK / 8; ++kk) {
+        float4 av[TM], bv[TN];
 #pragma unroll
-        for (int i = 0; i < TM; ++i) av[i] = Ws[(BM / WM * wm + 32 * i + (lane & 31)) * LD + 2 * kk + (lane >> 5)];
+        for (int i = 0; i < TM; ++i) av[i] = *reinterpret_cast<const float4*>(wsrc + 32 * i * LD + 8 * kk);
 #pragma unroll
-        for (int j = 0; j < TN; ++j) bv[j] = Xs[(BN / WN * wn + 32 * j + (lane & 31)) * LD + 2 * kk + (lane >> 5)];
+        for (int j = 0; j < TN; ++j) bv[j] = *reinterpret_cast<const float4*>(xsrc + 32 * j * LD + 8 * kk);
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
-          for (int j = 0; j < TN; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i], bv[j], acc[i][j], 0, 0, 0);
+          for (int j = 0; j < TN; ++j) {
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i].x, bv[j].x, acc[i][j], 0, 0, 0);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i].y, bv[j].y, acc[i][j], 0, 0, 0);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i].z, bv[j].z, acc[i][j], 0, 0, 0);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i].w, bv[j].w, acc[i][j], 0, 0, 0);
+          }
       }
     }
 #pragma unroll
