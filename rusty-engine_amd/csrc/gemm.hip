@@ -383,21 +383,29 @@ __global__ __launch_bounds__(WM* WN * 64 * KG) void gemm_kernel(GemmArgs p) {
       // the weights and the activations alike
       const float* wsrc = Ws + (BM / WM * wm + (lane & 31)) * LD + 4 * (lane >> 5);
       const float* xsrc = Xs + (BN / WN * wn + (lane & 31)) * LD + 4 * (lane >> 5);
-#pragma unroll 4
+      // slice kk + 1 is read from LDS while the MFMAs of slice kk run
+      float4 av[2][TM], bv[2][TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) av[0][i] = *reinterpret_cast<const float4*>(wsrc + 32 * i * LD);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) bv[0][j] = *reinterpret_cast<const float4*>(xsrc + 32 * j * LD);
+#pragma unroll
       for (int kk = 0; kk < BK / 8; ++kk) {
-        float4 av[TM], bv[TN];
+        const int cur = kk & 1, nxt = cur ^ 1;
+        if (kk + 1 < BK / 8) {
 #pragma unroll
-        for (int i = 0; i < TM; ++i) av[i] = *reinterpret_cast<const float4*>(wsrc + 32 * i * LD + 8 * kk);
+          for (int i = 0; i < TM; ++i) av[nxt][i] = *reinterpret_cast<const float4*>(wsrc + 32 * i * LD + 8 * (kk + 1));
 #pragma unroll
-        for (int j = 0; j < TN; ++j) bv[j] = *reinterpret_cast<const float4*>(xsrc + 32 * j * LD + 8 * kk);
+          for (int j = 0; j < TN; ++j) bv[nxt][j] = *reinterpret_cast<const float4*>(xsrc + 32 * j * LD + 8 * (kk + 1));
+        }
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
           for (int j = 0; j < TN; ++j) {
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i].x, bv[j].x, acc[i][j], 0, 0, 0);
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i].y, bv[j].y, acc[i][j], 0, 0, 0);
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i].z, bv[j].z, acc[i][j], 0, 0, 0);
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i].w, bv[j].w, acc[i][j], 0, 0, 0);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[cur][i].x, bv[cur][j].x, acc[i][j], 0, 0, 0);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[cur][i].y, bv[cur][j].y, acc[i][j], 0, 0, 0);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[cur][i].z, bv[cur][j].z, acc[i][j], 0, 0, 0);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[cur][i].w, bv[cur][j].w, acc[i][j], 0, 0, 0);
           }
       }
     }
