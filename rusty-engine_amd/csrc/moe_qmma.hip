@@ -102,6 +102,26 @@ __device__ __forceinline__ void decode_frags(const typename Blk<T>::CR& raw, int
   f.eb = b.e;
 }
 
+// Half tile (32 weight rows per wave): lanes 0-31 decode run a of rows 0-31, lanes 32-63 run b of
+// the same rows; one v_permlane32_swap per dword then leaves run a's B operand in a0 (lanes 0-31
+// k 0-7, lanes 32-63 k 8-15) and run b's in b0. Every weight is still decoded once.
+template <int T>
+__device__ __forceinline__ void decode_frags_half(const typename Blk<T>::CR& raw, int cc, Frags& f) {
+  Run a, b;
+  Blk<T>::decode_chunk(raw, cc, a, b);
+  const bool up = (threadIdx.x & 32) != 0;
+  Run r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) r.q[i] = up ? b.q[i] : a.q[i];
+  r.scale = up ? b.scale : a.scale;
+  r.offset = up ? b.offset : a.offset;
+  uint32_t lo[4], hi[4];
+  run_bf16<T>(r, lo, hi);
+  halves_to_frags(lo, hi, f.a0, f.b0);
+  f.ea = a.e;
+  f.eb = b.e;
+}
+
 // vector memory instructions of one Blk<T>::bload_chunk
 template <int T> inline constexpr int kChunkLoads = 0;
 template <> inline constexpr int kChunkLoads<T_Q4_0> = 2;
@@ -203,13 +223,20 @@ __device__ __forceinline__ bf16x8_t ld_x(__amdgpu_buffer_rsrc_t r, uint32_t off)
 //              load feeds twice the weights), Y receives f32.
 // KS waves per task split the blocks of K between them (wave w takes blocks w, w + KS, ...);
 // their sums are added in wave order through LDS at the end (deterministic).
+// H (staged activations only, one K wave): two waves share the task, each taking 32 of the
+// tile's rows (half = wave), and one staging of the activation rows in LDS, each wave copying
+// half of every stage.
 constexpr int kOneTile = 0, kGateUp = 1, kTwoTiles = 2;
-template <int T, int PAIR, int NT, int KS, bool XL>
+template <int T, int PAIR, int NT, int KS, bool XL, bool H>
 __device__ __forceinline__ void qmma_task(const GemmArgs& p, const GemmTask& t, uint8_t* xs) {
   using B = Blk<T>;
+  static_assert(!H || (XL && KS == 1 && PAIR != kTwoTiles), "half tiles: staged activations, one K wave, one tile");
   constexpr int NCH = B::NCH;                       // 32-element chunks per block
+  constexpr int RG = H ? 1 : 2;                     // 32-row groups per weight set
   const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int half = H ? __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) : 0;
+  const int wave = H ? 0 : __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lrow = H ? 32 * half + (lane & 31) : lane;   // the slab row this lane loads
   const int rn = t.rn;
   const int nt = (rn + 31) >> 5;                    // token tiles holding rows (uniform)
 
@@ -237,16 +264,16 @@ __device__ __forceinline__ void qmma_task(const GemmArgs& p, const GemmTask& t, 
     xoff[j] = o;
   }
 
-  f32x16_t acc[2][NT], acc2[DUAL ? 2 : 1][DUAL ? NT : 1];
+  f32x16_t acc[RG][NT], acc2[DUAL ? RG : 1][DUAL ? NT : 1];
 #pragma unroll
-  for (int g = 0; g < 2; ++g)
+  for (int g = 0; g < RG; ++g)
 #pragma unroll
     for (int j = 0; j < NT; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[g][j][r] = 0.0f;
   if constexpr (DUAL) {
 #pragma unroll
-    for (int g = 0; g < 2; ++g)
+    for (int g = 0; g < RG; ++g)
 #pragma unroll
       for (int j = 0; j < NT; ++j)
 #pragma unroll
@@ -257,15 +284,15 @@ __device__ __forceinline__ void qmma_task(const GemmArgs& p, const GemmTask& t, 
   auto load = [&](int c, typename B::CR& raw, const __amdgpu_buffer_rsrc_t& rs, uint32_t base) {
     const int kb = c / NCH, cc = c - kb * NCH;
     const uint32_t slab = c < nch ? base + (uint32_t)kb * (uint32_t)B::SLAB : kQOob;
-    load_own<T>(rs, slab, lane, cc, raw);
+    load_own<T>(rs, slab, lrow, cc, raw);
   };
   // the block heads of the block holding chunk c (first chunk of a block), both weight sets
   BlockHead hc{}, hc2{}, hn{}, hn2{};
   auto load_heads = [&](int c, BlockHead& h, BlockHead& h2) {
     if constexpr (kBlockHead<T>) {
       const int kb = c / NCH;
-      load_head<T>(wr, c < nch ? wbase + (uint32_t)kb * (uint32_t)B::SLAB : kQOob, lane, h);
-      if constexpr (DUAL) load_head<T>(wr2, c < nch ? wbase2 + (uint32_t)kb * (uint32_t)B::SLAB : kQOob, lane, h2);
+      load_head<T>(wr, c < nch ? wbase + (uint32_t)kb * (uint32_t)B::SLAB : kQOob, lrow, h);
+      if constexpr (DUAL) load_head<T>(wr2, c < nch ? wbase2 + (uint32_t)kb * (uint32_t)B::SLAB : kQOob, lrow, h2);
     }
   };
   // A operands of chunk c: runs a and b of every token tile
@@ -298,14 +325,18 @@ __device__ __forceinline__ void qmma_task(const GemmArgs& p, const GemmTask& t, 
   // loads of chunk c + 1 (set B) are in flight, and set A is refilled with chunk c + 2 right after
   // its decode. Named sets (not a rotated copy) let the waits count only the older loads. Chunks
   // past the end load zeros and add nothing, so an odd chunk count needs no tail.
-  auto mma = [&](const XOps& x, const Frags& f, f32x16_t (&a)[2][NT]) {
+  auto mma = [&](const XOps& x, const Frags& f, f32x16_t (&a)[RG][NT]) {
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
       a[0][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x.a[j], f.a0, a[0][j], 0, 0, 0);
-      a[1][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x.a[j], f.a1, a[1][j], 0, 0, 0);
+      if constexpr (!H) a[RG - 1][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x.a[j], f.a1, a[RG - 1][j], 0, 0, 0);
       a[0][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x.b[j], f.b0, a[0][j], 0, 0, 0);
-      a[1][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x.b[j], f.b1, a[1][j], 0, 0, 0);
+      if constexpr (!H) a[RG - 1][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x.b[j], f.b1, a[RG - 1][j], 0, 0, 0);
     }
+  };
+  auto decode = [&](const typename B::CR& raw, int cc, Frags& f) {
+    if constexpr (H) decode_frags_half<T>(raw, cc, f);
+    else decode_frags<T>(raw, cc, f);
   };
   auto load_all = [&](int c, typename B::CR& r, typename B::CR& q, XOps& x) {
     load(c, r, wr, wbase);
@@ -316,11 +347,11 @@ __device__ __forceinline__ void qmma_task(const GemmArgs& p, const GemmTask& t, 
   };
   auto step = [&](int c, const typename B::CR& r, const typename B::CR& q, const XOps& x) {
     Frags f;
-    decode_frags<T>(with_head<T>(r, hc), c % NCH, f);
+    decode(with_head<T>(r, hc), c % NCH, f);
     mma(x, f, acc);
     if constexpr (DUAL) {
       Frags f2;
-      decode_frags<T>(with_head<T>(q, hc2), c % NCH, f2);
+      decode(with_head<T>(q, hc2), c % NCH, f2);
       mma(x, f2, acc2);
     }
   };
@@ -340,28 +371,30 @@ __device__ __forceinline__ void qmma_task(const GemmArgs& p, const GemmTask& t, 
     constexpr int LW = kChunkOwnLoads<T> * (DUAL ? 2 : 1);   // weight loads per chunk (heads not counted:
                                                               // a head load among them only waits longer)
     constexpr int ND = NT * 4;                            // LDS DMA instructions per stage
+    constexpr int NDW = H ? ND / 2 : ND;                  // of them, issued by this wave
     constexpr int SB = NT * 32 * 128;                     // stage buffer bytes
-    uint32_t xo[ND];
+    const int i0 = H ? half * NDW : 0;                    // this wave's first instruction
+    uint32_t xo[NDW];
 #pragma unroll
-    for (int i = 0; i < ND; ++i) {
-      const int rl = 8 * i + (lane >> 3);
+    for (int ii = 0; ii < NDW; ++ii) {
+      const int rl = 8 * (i0 + ii) + (lane >> 3);
       uint32_t o = kQOob;
       if (rl < rn) {
         const int row = p.xrow ? p.xrow[t.r0 + rl] : t.r0 + rl;
         o = (uint32_t)row * (uint32_t)p.K * 2u;
       }
-      xo[i] = o;
+      xo[ii] = o;
     }
     const int pos = lane & 7;
     auto dma = [&](int c, int buf) {                      // the stage of chunks c, c + 1
       uint8_t* dst = xs + buf * SB;
       const int st = c >> 1;
 #pragma unroll
-      for (int i = 0; i < ND; ++i) {
-        const int rl = 8 * i + (lane >> 3);
+      for (int ii = 0; ii < NDW; ++ii) {
+        const int rl = 8 * (i0 + ii) + (lane >> 3);
         const int k = xl_unit_k<T>(st, pos ^ ((rl >> 1) & 7));
-        const uint32_t o = c < nch && xo[i] != kQOob && k < p.K ? xo[i] + (uint32_t)k * 2u : kQOob;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void_t*)(dst + 1024 * i), 16, (int)o, 0, 0, 0);
+        const uint32_t o = c < nch && xo[ii] != kQOob && k < p.K ? xo[ii] + (uint32_t)k * 2u : kQOob;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void_t*)(dst + 1024 * (i0 + ii)), 16, (int)o, 0, 0, 0);
       }
     };
     auto read_x = [&](int buf, int cl, XOps& x) {
@@ -382,7 +415,10 @@ __device__ __forceinline__ void qmma_task(const GemmArgs& p, const GemmTask& t, 
     // 32-element blocks, and the stage DMA looks four chunks ahead)
     auto next_c = [&](int c0, int u) { return c0 + (u / U) * U * KS + u % U; };
     // issue order DMA(s), W(2s), W(2s + 1), DMA(s + 1), ...: when stage s is read, the loads
-    // younger than its DMA are at most two chunks of weights and one stage of DMA
+    // younger than its DMA are at most two chunks of weights and one stage of DMA. H: three stage
+    // buffers; both waves pass a barrier before reading a stage (the other wave's half of the
+    // copy has landed), and a buffer is refilled only two stages after it was read, so that
+    // barrier also orders the refill after the other wave's reads.
     dma(first, 0);
     load_heads(first, hc, hc2);
     load_w(first, r[0], q[0]);
@@ -392,7 +428,12 @@ __device__ __forceinline__ void qmma_task(const GemmArgs& p, const GemmTask& t, 
     for (int c0 = first; c0 < nch; c0 += U * KS) {
 #pragma unroll
       for (int u = 0; u < U; u += 2) {
-        wait_vmcnt<2 * LW + ND>();
+        wait_vmcnt<2 * LW + NDW>();
+        if constexpr (H) {
+          asm volatile("" ::: "memory");
+          __builtin_amdgcn_s_barrier();
+          asm volatile("" ::: "memory");
+        }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
@@ -404,9 +445,15 @@ __device__ __forceinline__ void qmma_task(const GemmArgs& p, const GemmTask& t, 
           load_w(next_c(c0, u + h + 2), r[h], q[h]);
           __builtin_amdgcn_sched_barrier(0);
         }
-        dma(next_c(c0, u + 4), buf);
-        __builtin_amdgcn_sched_barrier(0);
-        buf ^= 1;
+        if constexpr (H) {
+          dma(next_c(c0, u + 4), buf == 0 ? 2 : buf - 1);
+          __builtin_amdgcn_sched_barrier(0);
+          buf = buf == 2 ? 0 : buf + 1;
+        } else {
+          dma(next_c(c0, u + 4), buf);
+          __builtin_amdgcn_sched_barrier(0);
+          buf ^= 1;
+        }
       }
       hc = hn;
       hc2 = hn2;
@@ -434,18 +481,18 @@ __device__ __forceinline__ void qmma_task(const GemmArgs& p, const GemmTask& t, 
   }
   if constexpr (KS > 1) {
     // waves 1 .. KS-1 hand their sums to wave 0, which adds them in wave order
-    constexpr int NACC = 2 * NT * 16 * (DUAL ? 2 : 1);
+    constexpr int NACC = RG * NT * 16 * (DUAL ? 2 : 1);
     __shared__ float red[(KS - 1) * NACC * 64];
     if (wave > 0) {
       float* dst = red + (wave - 1) * NACC * 64 + lane;
 #pragma unroll
-      for (int g = 0; g < 2; ++g)
+      for (int g = 0; g < RG; ++g)
 #pragma unroll
         for (int j = 0; j < NT; ++j)
 #pragma unroll
           for (int e = 0; e < 16; ++e) {
             dst[((g * NT + j) * 16 + e) * 64] = acc[g][j][e];
-            if constexpr (DUAL) dst[(((2 + g) * NT + j) * 16 + e) * 64] = acc2[g][j][e];
+            if constexpr (DUAL) dst[(((RG + g) * NT + j) * 16 + e) * 64] = acc2[g][j][e];
           }
     }
     __syncthreads();
@@ -454,21 +501,21 @@ __device__ __forceinline__ void qmma_task(const GemmArgs& p, const GemmTask& t, 
     for (int w = 1; w < KS; ++w) {
       const float* src = red + (w - 1) * NACC * 64 + lane;
 #pragma unroll
-      for (int g = 0; g < 2; ++g)
+      for (int g = 0; g < RG; ++g)
 #pragma unroll
         for (int j = 0; j < NT; ++j)
 #pragma unroll
           for (int e = 0; e < 16; ++e) {
             acc[g][j][e] += src[((g * NT + j) * 16 + e) * 64];
-            if constexpr (DUAL) acc2[g][j][e] += src[(((2 + g) * NT + j) * 16 + e) * 64];
+            if constexpr (DUAL) acc2[g][j][e] += src[(((RG + g) * NT + j) * 16 + e) * 64];
           }
     }
   }
 
   // D[token i][row n]: lane holds row n = 32 g + lane % 32 and tokens 8 (r / 4) + 4 (lane / 32) + r % 4
-  const int col = tile0 * 64 + (lane & 31);
+  const int col = tile0 * 64 + (H ? 32 * half : 0) + (lane & 31);
 #pragma unroll
-  for (int g = 0; g < (PAIR == kTwoTiles ? 4 : 2); ++g) {
+  for (int g = 0; g < (PAIR == kTwoTiles ? 4 : RG); ++g) {
     const int row = col + 32 * g;
     if (row >= p.m) continue;
 #pragma unroll
@@ -493,19 +540,33 @@ __device__ __forceinline__ void qmma_task(const GemmArgs& p, const GemmTask& t, 
 
 // A task of at most 32 rows runs the one-tile body (no MFMAs on an empty second token tile).
 // XL: activations staged in LDS (two stage buffers per wave).
-template <int T, int PAIR, int NT, int KS, bool XL>
-__global__ __launch_bounds__(64 * KS) void moe_qmma_kernel(GemmArgs p) {
+// H: two waves per task (32 weight rows each) sharing three stage buffers.
+template <int T, int PAIR, int NT, int KS, bool XL, bool H>
+__global__ __launch_bounds__(64 * KS * (H ? 2 : 1)) void moe_qmma_kernel(GemmArgs p) {
   if (p.ntasks && (int)blockIdx.x >= *p.ntasks) return;   // grid sized for the most tasks
   const GemmTask t = p.tasks[blockIdx.x];
-  __shared__ __attribute__((aligned(16))) uint8_t xs[XL ? KS * 2 * NT * 32 * 128 : 16];
-  uint8_t* mine = xs + (XL ? (threadIdx.x >> 6) * 2 * NT * 32 * 128 : 0);
+  __shared__ __attribute__((aligned(16))) uint8_t xs[!XL ? 16 : H ? 3 * NT * 32 * 128 : KS * 2 * NT * 32 * 128];
+  uint8_t* mine = xs + (XL && !H ? (threadIdx.x >> 6) * 2 * NT * 32 * 128 : 0);
   if constexpr (NT == 2) {
     if (t.rn <= 32) {
-      qmma_task<T, PAIR, 1, KS, XL>(p, t, mine);
+      qmma_task<T, PAIR, 1, KS, XL, H>(p, t, mine);
       return;
     }
   }
-  qmma_task<T, PAIR, NT, KS, XL>(p, t, mine);
+  qmma_task<T, PAIR, NT, KS, XL, H>(p, t, mine);
+}
+
+template <int T, int PA, int NT, int KS>
+static void launch_qmma_v(bool xl, bool h, int ntasks, hipStream_t s, const GemmArgs& a) {
+  const dim3 grid((unsigned)ntasks);
+  if constexpr (PA != kTwoTiles && KS == 1) {
+    if (h) {
+      hipLaunchKernelGGL((moe_qmma_kernel<T, PA, NT, 1, true, true>), grid, dim3(128), 0, s, a);
+      return;
+    }
+  }
+  if (xl) hipLaunchKernelGGL((moe_qmma_kernel<T, PA, NT, KS, true, false>), grid, dim3(64 * KS), 0, s, a);
+  else hipLaunchKernelGGL((moe_qmma_kernel<T, PA, NT, KS, false, false>), grid, dim3(64 * KS), 0, s, a);
 }
 
 hipError_t launch_moe_qmma(uint32_t type, int pair, int max_rows, const GemmArgs& a, int ntasks, hipStream_t s) {
@@ -516,7 +577,6 @@ hipError_t launch_moe_qmma(uint32_t type, int pair, int max_rows, const GemmArgs
   // for 64-row tasks; REHIP_QMMA_KS = 1 / 2 overrides
   int ks = one ? 2 : 1;
   if (const char* v = std::getenv("REHIP_QMMA_KS"); v && (v[0] == '1' || v[0] == '2') && !v[1]) ks = v[0] - '0';
-  const dim3 grid((unsigned)ntasks), block(64 * ks);
   // activations staged in LDS for the two-tile tasks of 64 rows (each staged run feeds 128
   // weight rows; measured at 512 tokens on the Qwen3-30B-A3B shape: down 61.1 against 65.8 us,
   // while the gate/up pair and the 32-row tasks ran slower staged), else read from L2 per run;
@@ -524,14 +584,20 @@ hipError_t launch_moe_qmma(uint32_t type, int pair, int max_rows, const GemmArgs
   const char* xv = std::getenv("REHIP_QMMA_XL");
   bool xl = pair == kTwoTiles && !one;
   if (xv && (xv[0] == '0' || xv[0] == '1') && !xv[1]) xl = xv[0] == '1';
-#define REHIP_QMMA_L(TT, PA, NT, KS)                                                              \
-  do {                                                                                            \
-    if (xl) hipLaunchKernelGGL((moe_qmma_kernel<TT, PA, NT, KS, true>), grid, block, 0, s, a);    \
-    else hipLaunchKernelGGL((moe_qmma_kernel<TT, PA, NT, KS, false>), grid, block, 0, s, a);      \
-  } while (0)
-#define REHIP_QMMA_P(TT, PA)                                                                        \
-  if (one) { if (ks == 2) REHIP_QMMA_L(TT, PA, 1, 2); else REHIP_QMMA_L(TT, PA, 1, 1); }            \
-  else { if (ks == 2) REHIP_QMMA_L(TT, PA, 2, 2); else REHIP_QMMA_L(TT, PA, 2, 1); }
+  // the gate/up pair of 64-row tasks: two 32-row waves per task sharing one staging of the rows.
+  // One-wave whole-tile tasks hold 233 VGPRs (two per SIMD), so at 512 tokens on the
+  // Qwen3-30B-A3B shape 1536 tasks sit 1.5 per SIMD and half the SIMDs idle at the end; the
+  // halves hold 150 (all 3072 waves resident): 154.2 -> 151.7 us per call, the same bits.
+  // REHIP_QMMA_H = 1 / 0 forces either (never with a K split or two tiles)
+  const char* hv = std::getenv("REHIP_QMMA_H");
+  bool h = pair == kGateUp && !one;
+  if (hv && (hv[0] == '0' || hv[0] == '1') && !hv[1]) h = hv[0] == '1';
+  h = h && ks == 1 && pair != kTwoTiles;
+#define REHIP_QMMA_P(TT, PA)                                                         \
+  if (one) { if (ks == 2) launch_qmma_v<TT, PA, 1, 2>(xl, h, ntasks, s, a);          \
+             else launch_qmma_v<TT, PA, 1, 1>(xl, h, ntasks, s, a); }                \
+  else { if (ks == 2) launch_qmma_v<TT, PA, 2, 2>(xl, h, ntasks, s, a);              \
+         else launch_qmma_v<TT, PA, 2, 1>(xl, h, ntasks, s, a); }
 #define REHIP_QMMA(TT)                                                     \
   case TT:                                                                 \
     if (pair == kGateUp) { REHIP_QMMA_P(TT, kGateUp) }                     \
@@ -550,7 +616,6 @@ hipError_t launch_moe_qmma(uint32_t type, int pair, int max_rows, const GemmArgs
   }
 #undef REHIP_QMMA
 #undef REHIP_QMMA_P
-#undef REHIP_QMMA_L
   return hipGetLastError();
 }
 

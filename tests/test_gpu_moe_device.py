@@ -438,3 +438,40 @@ def test_qmma_forced_wave_split_and_staging(gt, dt, ks, xl, monkeypatch):
     for name, g in got.items():
         assert np.linalg.norm(g - want) / np.linalg.norm(want) <= 1e-2, name
     moe.close()
+
+
+@pytest.mark.parametrize("gt,dt", QMMA_FORCED_TYPES)
+@pytest.mark.parametrize("T", [300, 40])
+def test_qmma_half_tile_waves_bit_identical(gt, dt, T, monkeypatch):
+    """Two 32-row waves per expert task sharing one LDS staging of the activation rows
+    (REHIP_QMMA_H=1: lanes 0-31 of a wave decode one run of a chunk, lanes 32-63 the other; each
+    wave copies half of every stage) give the same bits as whole-tile tasks with the same
+    staging: every output sums the same MFMA products in the same order. 300 tokens over 16
+    experts make 64-row tasks with ragged last chunks, 40 tokens 32-row ones; host- and
+    device-routed, and against the oracle."""
+    E, k, hidden, inter = 16, 4, 512, 320
+    gate, up, down_, x, logits = moe_case(4321 + T + gt + 7 * dt, E, hidden, inter, T, k, gt, dt)
+    ids = np.zeros((T, k), np.int32)
+    wts = np.zeros((T, k), np.float32)
+    for t in range(T):
+        ids[t], wts[t] = O.top_k(logits[t], k)
+    moe = rehip.MoeExperts(gt, gate, gt, up, dt, down_, E, hidden, inter)
+    xd = B.from_array(x)
+    idd, wd = B.from_array(ids.reshape(-1)), B.from_array(wts.reshape(-1))
+    monkeypatch.setenv("REHIP_MOE_QMMA", "1")
+    monkeypatch.setenv("REHIP_QMMA_KS", "1")
+    monkeypatch.setenv("REHIP_QMMA_XL", "1")
+    res = {}
+    for h in ("0", "1"):
+        monkeypatch.setenv("REHIP_QMMA_H", h)
+        out = B(T * hidden * 4)
+        moe.forward_routed_dev(xd, T, k, idd, wd, out, rehip.MODE_BF16)
+        res[h] = (moe.forward(x, T, k, ids.reshape(-1).astype(np.uint32), wts.reshape(-1), rehip.MODE_BF16),
+                  down(out, T * hidden))
+    want = O.moe_ffn(gt, gate, gt, up, dt, down_, E, hidden, inter, x, T, k,
+                     ids.reshape(-1).astype(np.uint32), wts.reshape(-1))
+    for i, name in enumerate(("host-routed", "device-routed")):
+        a, b = res["0"][i], res["1"][i]
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), name
+        assert np.linalg.norm(b - want) / np.linalg.norm(want) <= 1e-2, name
+    moe.close()
