@@ -170,29 +170,40 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_rows_kernel(GemvArgs p) {
 
   const uint8_t* tbase = p.W + (size_t)mb * p.w_stride + (size_t)tile * p.KB * B::SLAB;
   const int u_end = p.KB * NCH;
+  // this thread's first activation (and norm weight) goes out before the weight loads: loads
+  // retire in order, so the staging below then waits for it alone and overlaps the weights'
+  // round trip
+  const int nv = nx / 4;
+  float4 x0 = make_float4(0.f, 0.f, 0.f, 0.f), w0 = x0;
+  if ((int)threadIdx.x < nv && 4 * (int)threadIdx.x < p.K) {
+    x0 = *reinterpret_cast<const float4*>(xin + 4 * threadIdx.x);
+    if (p.norm_w) w0 = *reinterpret_cast<const float4*>(p.norm_w + 4 * threadIdx.x);
+  }
+  __builtin_amdgcn_sched_barrier(0);
   typename B::CR ring[D];
 #pragma unroll
   for (int i = 0; i < D; ++i) {
     const int u = slot + i * S;
     if (u < u_end) B::load_chunk(tbase + (size_t)(u / NCH) * B::SLAB, rr, u % NCH, ring[i]);
   }
+  __builtin_amdgcn_sched_barrier(0);
 
   // RMS-norm prologue: x * w is staged and the sum of squares kept per thread; the row's
   // 1/rms multiplies the finished dot (W (x inv w) = inv W (x w)), so the norm adds no pass or
   // barrier before the weights are consumed.
-  const int nv = nx / 4;
   float ss = 0.0f;
   for (int i = threadIdx.x; i < nv; i += WAVES * 64) {
     const int k = 4 * i;
     float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
     if (k < p.K) {
-      v = *reinterpret_cast<const float4*>(xin + k);
+      const bool first = i == (int)threadIdx.x;
+      v = first ? x0 : *reinterpret_cast<const float4*>(xin + k);
       if (p.norm_w) {
         ss = __builtin_fmaf(v.x, v.x, ss);
         ss = __builtin_fmaf(v.y, v.y, ss);
         ss = __builtin_fmaf(v.z, v.z, ss);
         ss = __builtin_fmaf(v.w, v.w, ss);
-        const float4 w = *reinterpret_cast<const float4*>(p.norm_w + k);
+        const float4 w = first ? w0 : *reinterpret_cast<const float4*>(p.norm_w + k);
         v = make_float4(v.x * w.x, v.y * w.y, v.z * w.z, v.w * w.w);
       }
     }

@@ -522,6 +522,21 @@ __global__ __launch_bounds__(WAVES * 64) void moe_gemv_kernel(MoeGemvArgs a) {
   const int slot = wave * G + lane / R;
   const int u_end = a.KB * NCH;
 
+  // this thread's first activation (and norm weight) goes out before the weight loads: loads
+  // retire in order, so the staging below then waits for it alone and overlaps the weights'
+  // round trip
+  const int nv = KP / 4;
+  float4 x0 = make_float4(0.f, 0.f, 0.f, 0.f), w0 = x0;
+  {
+    const int i = threadIdx.x, nb = i / nv, k = 4 * (i - nb * nv);
+    if (i < NB * nv && nb < task.np && k < a.K) {
+      const int p = task.p0 + nb;
+      const int xr = a.ids || a.id_inline ? 0 : (a.xrow ? a.xrow[p] : p);
+      x0 = *reinterpret_cast<const float4*>(a.X + (size_t)xr * a.K + k);
+      if (a.norm_w) w0 = *reinterpret_cast<const float4*>(a.norm_w + k);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
   typename B::CR ring0[D], ring1[D];
 #pragma unroll
   for (int i = 0; i < D; ++i) {
@@ -531,10 +546,10 @@ __global__ __launch_bounds__(WAVES * 64) void moe_gemv_kernel(MoeGemvArgs a) {
       if constexpr (DUAL) B::load_chunk(t1 + (size_t)(u / NCH) * B::SLAB, rr, u % NCH, ring1[i]);
     }
   }
+  __builtin_amdgcn_sched_barrier(0);
 
   // stage the task's activation rows (zero past K and past np); with an RMS-norm, x * w is
   // staged, each thread keeps its rows' sums of squares, and 1/rms scales the finished dots
-  const int nv = KP / 4;
   float ss[NB];
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) ss[nb] = 0.0f;
@@ -542,15 +557,16 @@ __global__ __launch_bounds__(WAVES * 64) void moe_gemv_kernel(MoeGemvArgs a) {
     const int nb = i / nv, k = 4 * (i - nb * nv);
     float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
     if (nb < task.np && k < a.K) {
+      const bool first = i == (int)threadIdx.x;
       const int p = task.p0 + nb;
       const int xr = a.ids || a.id_inline ? 0 : (a.xrow ? a.xrow[p] : p);   // routed by ids: the one row
-      v = *reinterpret_cast<const float4*>(a.X + (size_t)xr * a.K + k);
+      v = first ? x0 : *reinterpret_cast<const float4*>(a.X + (size_t)xr * a.K + k);
       if (a.norm_w) {
         float t = __builtin_fmaf(v.x, v.x, __builtin_fmaf(v.y, v.y, __builtin_fmaf(v.z, v.z, v.w * v.w)));
 #pragma unroll
         for (int q = 0; q < NB; ++q)
           if (q == nb) ss[q] += t;
-        const float4 w = *reinterpret_cast<const float4*>(a.norm_w + k);
+        const float4 w = first ? w0 : *reinterpret_cast<const float4*>(a.norm_w + k);
         v = make_float4(v.x * w.x, v.y * w.y, v.z * w.z, v.w * w.w);
       }
     }
