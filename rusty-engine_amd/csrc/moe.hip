@@ -713,6 +713,19 @@ __global__ __launch_bounds__(WAVES * 64) void moe_down_combine_kernel(MoeDownCom
     return a.W + (size_t)e * a.w_stride + (size_t)tile * a.KB * B::SLAB;
   };
   const int u_end = k * u_pair;
+  // this thread's first rows of h go out before the weight loads (loads retire in order, so
+  // the staging then waits for them alone and overlaps the weights' round trip)
+  constexpr int PRE = 4;
+  const int nh = k * KP / 4;
+  float4 hp[PRE];
+#pragma unroll
+  for (int r = 0; r < PRE; ++r) {
+    const int i = (int)threadIdx.x + r * WAVES * 64;
+    const int j = i / (KP / 4), q = 4 * (i - j * (KP / 4));
+    hp[r] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (i < nh && q < a.K) hp[r] = *reinterpret_cast<const float4*>(a.H + (size_t)j * a.K + q);
+  }
+  __builtin_amdgcn_sched_barrier(0);
   typename B::CR ring[D];
 #pragma unroll
   for (int i = 0; i < D; ++i) {
@@ -722,7 +735,13 @@ __global__ __launch_bounds__(WAVES * 64) void moe_down_combine_kernel(MoeDownCom
       B::load_chunk(base_of(j) + (size_t)(c / NCH) * B::SLAB, rr, c % NCH, ring[i]);
     }
   }
-  for (int i = threadIdx.x; i < k * KP / 4; i += WAVES * 64) {
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int r = 0; r < PRE; ++r) {
+    const int i = (int)threadIdx.x + r * WAVES * 64;
+    if (i < nh) reinterpret_cast<float4*>(hl)[i] = hp[r];
+  }
+  for (int i = (int)threadIdx.x + PRE * WAVES * 64; i < nh; i += WAVES * 64) {
     const int j = i / (KP / 4), q = 4 * (i - j * (KP / 4));
     float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
     if (q < a.K) v = *reinterpret_cast<const float4*>(a.H + (size_t)j * a.K + q);
