@@ -148,14 +148,12 @@ template <> struct Blk<T_Q4_0> {
   }
 };
 
-// spread bits 0..3 of v to bit 4 of bytes 0..3: copies of the nibble at bits 0, 7, 14 and 21
-// put bit b of copy b at 7b + b = 8b, shifted to 8b + 4 (full-rate shifts and ors; a multiply by
-// 0x00204081 compiles to the quarter-rate v_mul_lo_u32)
+// spread bits 0..3 of v to bit 4 of bytes 0..3: the nibble moved to bits 4..7, times
+// 1 + 2^7 + 2^14 + 2^21, puts copies at shifts 0, 7, 14, 21 (no overlap, so no carries) and bit b
+// of copy b at 4 + b + 7b = 8b + 4. Both factors fit 24 bits, so this is the full-rate
+// v_mul_u32_u24 (a shift-or chain was folded by the compiler into the quarter-rate v_mul_lo_u32).
 __device__ __forceinline__ uint32_t bits4_to_byte_bit4(uint32_t v) {
-  uint32_t t = v & 0xFu;
-  t |= t << 7;
-  t |= t << 14;
-  return (t << 4) & 0x10101010u;
+  return __umul24((v & 0xFu) << 4, 0x00204081u) & 0x10101010u;
 }
 
 template <> struct Blk<T_Q5_0> {

@@ -502,7 +502,13 @@ __global__ __launch_bounds__(WM* WN * 64 * KG) void gemm_kernel(GemmArgs p) {
         if (xl0 + xr < rn) {
           float* yrow = Y + (size_t)(r0 + xl0 + xr) * p.ldy;
           if (wr + 3 < p.m) {
-            *reinterpret_cast<float4*>(yrow + wr) = v;
+            if (!GROUPED && p.splits == 1) {
+              // the finished output of a dense launch is not read again by this launch: streaming
+              // (nontemporal) stores keep it from occupying L2 (C1 N = 961: 25.0 -> 21.2 us)
+              __builtin_nontemporal_store(f32x4_t{v.x, v.y, v.z, v.w}, reinterpret_cast<f32x4_t*>(yrow + wr));
+            } else {
+              *reinterpret_cast<float4*>(yrow + wr) = v;
+            }
           } else {
             if (wr < p.m) yrow[wr] = v.x;
             if (wr + 1 < p.m) yrow[wr + 1] = v.y;
@@ -524,6 +530,11 @@ template <> __device__ __forceinline__ float vadd(float a, float b) { return a +
 template <> __device__ __forceinline__ float4 vadd(float4 a, float4 b) {
   return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
 }
+// the reduced output is final: streaming (nontemporal) stores
+__device__ __forceinline__ void store_final(float* p, float v) { __builtin_nontemporal_store(v, p); }
+__device__ __forceinline__ void store_final(float4* p, float4 v) {
+  __builtin_nontemporal_store(f32x4_t{v.x, v.y, v.z, v.w}, reinterpret_cast<f32x4_t*>(p));
+}
 template <typename V>
 __global__ __launch_bounds__(256) void gemm_reduce_kernel(const V* __restrict__ partial, V* __restrict__ y, size_t n,
                                                           int splits) {
@@ -539,7 +550,7 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(const V* __restrict__ 
     for (int j = 0; j < 8; ++j) s = vadd(s, v[j]);
   }
   for (; sp < splits; ++sp) s = vadd(s, partial[(size_t)sp * n + i]);
-  y[i] = s;
+  store_final(y + i, s);
 }
 
 static hipError_t launch_reduce(const float* partial, float* y, size_t n, int splits, hipStream_t s) {
