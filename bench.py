@@ -6,9 +6,11 @@ X[N x 4864]:
 
 * value: N = 1 GEMV, one batched launch over a stack of weight copies (> 512 MiB in all, so
   every byte comes from HBM, not from the 256 MiB MALL): y_b = W_b x for every copy b
-  (re_qmat_matvec_stacked_dev). The timed region replays a HIP graph of `steps` launches after
-  `warmup` untimed ones; value = algorithmic bytes per launch (per copy: stored GGUF weight
-  bytes + f32 x + f32 y) / average launch time from HIP events on the launch stream.
+  (re_qmat_matvec_stacked_dev). After `warmup` untimed launches, a HIP graph of exactly `steps`
+  launches is replayed until at least 400 launches are timed, each replay between its own pair
+  of HIP events on the launch stream; ms_per_step is the median replay's time per launch, and
+  value = algorithmic bytes per launch (per copy: stored GGUF weight bytes + f32 x + f32 y) /
+  ms_per_step.
   single_launch: one 3.6 MB GEMV per launch (the latency a decode step sees).
 * host_matvec: re_qmat_matvec with host pointers per decode projection (x in, GEMV, y out,
   synchronise): what QMat::matvec costs a host caller per call.
@@ -152,51 +154,80 @@ def time_moe(moe, weights, tokens, mode, reps, seed=401, check=False):
     """Expert FFN of `tokens` tokens (re_moe_forward_dev: host grouping, metadata upload, grouped
     kernels, combine), per call over `reps` calls; the same FFN with device routing
     (re_moe_forward_routed_dev) and the whole layer with the f32 router (re_moe_layer_dev), each
-    as a replayed graph. Bytes: weights of the experts hit + X + out."""
+    as a replayed graph. Bytes: weights of the experts hit + X + out.
+
+    Consecutive calls cycle through R = 32 different routings (and token rows) for T <= 32: at
+    T = 1 they touch ~112 of the 128 experts (~340 MB, more than the 256 MiB MALL), so a call's
+    experts were last read ~31 calls earlier and come mostly from HBM rather than the MALL. At
+    T = 512 every call touches all 128 experts (392 MB), so one routing suffices."""
     import oracle
     import rehip
     from rehip import hip, synth
     E, H, I, k = MOE["n_experts"], MOE["hidden"], MOE["inter"], MOE["top_k"]
-    ids, wts, _ = synth.router(np.random.default_rng(seed + 1 + tokens), tokens, E, k)
-    x = synth.activations(np.random.default_rng(seed + 2 + tokens), tokens, H)
-    dx = hip.DeviceBuffer.from_array(x)
+    R = 32 if tokens <= 32 else 1
+    routes = [synth.router(np.random.default_rng(seed + 1 + tokens + 1000 * r), tokens, E, k)[:2] for r in range(R)]
+    xs = [synth.activations(np.random.default_rng(seed + 2 + tokens + 1000 * r), tokens, H) for r in range(R)]
+    dxs = [hip.DeviceBuffer.from_array(x) for x in xs]
     dy = hip.DeviceBuffer(tokens * H * 4)
     s = hip.Stream()
-    moe.forward_dev(dx, tokens, k, ids, wts, dy, mode, stream=s)
+    cyc = [0]
+
+    def nxt():
+        i = cyc[0] % R
+        cyc[0] += 1
+        return i
+
+    for r in range(R):
+        moe.forward_dev(dxs[r], tokens, k, routes[r][0], routes[r][1], dy, mode, stream=s)
     s.synchronize()
     t0 = time.perf_counter()
     for _ in range(reps):
-        moe.forward_dev(dx, tokens, k, ids, wts, dy, mode, stream=s)
+        i = nxt()
+        moe.forward_dev(dxs[i], tokens, k, routes[i][0], routes[i][1], dy, mode, stream=s)
     s.synchronize()
     us = (time.perf_counter() - t0) / reps * 1e6
-    did = hip.DeviceBuffer.from_array(np.asarray(ids, np.int32))
-    dw = hip.DeviceBuffer.from_array(np.asarray(wts, np.float32))
+    dids = [hip.DeviceBuffer.from_array(np.asarray(ids, np.int32)) for ids, _ in routes]
+    dws = [hip.DeviceBuffer.from_array(np.asarray(w, np.float32)) for _, w in routes]
     rw = hip.DeviceBuffer.from_array((np.random.default_rng(seed + 3).standard_normal((E, H)) / np.sqrt(H))
                                      .astype(np.float32))
+
+    def routed():
+        i = nxt()
+        moe.forward_routed_dev(dxs[i], tokens, k, dids[i], dws[i], dy, mode, stream=s)
+
+    def layer():
+        i = nxt()
+        moe.layer_dev(dxs[i], tokens, rw, k, rehip.GATE_SOFTMAX, dy, mode, stream=s)
+
     # device-routed and whole-layer graphs: the best of three timed replays (the first replays of a
     # process run up to ~10 % slower while the clocks settle)
-    us_routed = min(graph_time_us(s, lambda: moe.forward_routed_dev(dx, tokens, k, did, dw, dy, mode, stream=s), reps)
-                    for _ in range(3))
+    us_routed = min(graph_time_us(s, routed, reps) for _ in range(3))
     r_ok = None
     if check:
+        cyc[0] = 0
+        routed()                            # routing 0 into dy
+        s.synchronize()
         got = dy.download(np.float32, tokens * H)
         gate, up, down = weights
-        want = oracle.moe_ffn(rehip.Q4_K, gate, rehip.Q4_K, up, rehip.Q6_K, down, E, H, I, x, tokens, k,
+        ids, wts = routes[0]
+        want = oracle.moe_ffn(rehip.Q4_K, gate, rehip.Q4_K, up, rehip.Q6_K, down, E, H, I, xs[0], tokens, k,
                               ids.reshape(-1), wts.reshape(-1))
-        rel = float(np.linalg.norm(got - want) / np.linalg.norm(want))
-        r_ok = rel
-    us_layer = min(graph_time_us(s, lambda: moe.layer_dev(dx, tokens, rw, k, rehip.GATE_SOFTMAX, dy, mode, stream=s),
-                                 reps) for _ in range(3))
+        r_ok = float(np.linalg.norm(got - want) / np.linalg.norm(want))
+    us_layer = min(graph_time_us(s, layer, reps) for _ in range(3))
     s.destroy()
-    hit = len(np.unique(ids))
+    hits = [len(np.unique(ids)) for ids, _ in routes]
+    union = len(np.unique(np.concatenate([ids.reshape(-1) for ids, _ in routes])))
     per_expert = sum(a.size for a in weights) // E
-    nbytes = hit * per_expert + 2 * tokens * H * 4
+    nbytes = float(np.mean(hits)) * per_expert + 2 * tokens * H * 4
     flop = 2.0 * tokens * k * 3 * H * I
-    r = {"tokens": tokens, "pairs": tokens * k, "experts_hit": int(hit), "mode": "f32" if mode == 1 else "bf16",
+    r = {"tokens": tokens, "pairs": tokens * k, "experts_hit": float(np.mean(hits)), "mode": "f32" if mode == 1 else "bf16",
          "us": us, "bytes": int(nbytes), "gbs": nbytes / (us * 1e-6) / 1e9,
          "frac_hbm": nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, "tflops": flop / (us * 1e-6) / 1e12,
          "us_device_routed": us_routed, "frac_hbm_device_routed": nbytes / (us_routed * 1e-6) / 1e9 / HBM_PEAK_GBS,
-         "us_layer_device": us_layer}
+         "us_layer_device": us_layer, "routings_cycled": R,
+         "weights_cycled_mb": round(union * per_expert / 1e6, 1),
+         "cache": "cold: the cycled experts exceed the 256 MiB MALL" if union * per_expert > MALL_BYTES
+                  else "MALL-warm: the cycled experts fit the 256 MiB MALL"}
     if r_ok is not None:
         r["rel_err_vs_oracle"] = r_ok
     return r
@@ -416,7 +447,7 @@ def calibrate(log=print):
             for pattern, fn in (("interleaved", L.cal_stream_read), ("contiguous", L.cal_stream_read_chunk)):
                 if pattern == "interleaved" and grid == 1024:
                     continue
-                us = graph_time_us(s, lambda: fn(buf.ptr, nbytes, nt, sink.ptr, grid, s.cuda_stream), 10)
+                us = graph_time_us(s, lambda: fn(buf.ptr, nbytes, nt, sink.ptr, grid, s.handle), 10)
                 read = nbytes if pattern == "interleaved" else (nbytes // 16 // grid // 4096) * 4096 * 16 * grid
                 key = f"stream_read_{pattern}_{'nontemporal' if nt else 'default'}_grid{grid}_gbs"
                 out[key] = read / (us * 1e-6) / 1e9
@@ -425,11 +456,11 @@ def calibrate(log=print):
     buf.free()
     grid, iters = 256 * 8, 512
     mo = hip.DeviceBuffer(grid * 4 * 4)
-    us = graph_time_us(s, lambda: L.cal_mfma(mo.ptr, grid, iters, s.cuda_stream), 10)
+    us = graph_time_us(s, lambda: L.cal_mfma(mo.ptr, grid, iters, s.handle), 10)
     out["mfma_bf16_32x32x16_tflops"] = grid * 4 * iters * 8 * 32768 / (us * 1e-6) / 1e12
     log(f"calib: mfma {out['mfma_bf16_32x32x16_tflops']:.0f} TFLOP/s")
     mo.free()
-    out["empty_kernel_graph_us"] = graph_time_us(s, lambda: L.cal_empty(s.cuda_stream), 1000)
+    out["empty_kernel_graph_us"] = graph_time_us(s, lambda: L.cal_empty(s.handle), 1000)
     s.destroy()
     return out
 
@@ -685,20 +716,29 @@ def main():
 
     e0, e1 = hip.Event(), hip.Event()
 
-    def timed(fn_warm, fn_timed, n):
+    def timed(fn_warm, fn_timed, n, replays=1):
+        """ms per launch: `fn_warm` once untimed, then the graph of `fn_timed` (n launches) replayed
+        `replays` times, each replay its own event pair around exactly n launches; the median
+        replay (and every replay's figure)."""
         gw = hip.Graph(stream, fn_warm)
         gt = hip.Graph(stream, fn_timed)
         gw.launch()
         stream.synchronize()
-        e0.record(stream)
-        gt.launch()
-        e1.record(stream)
-        e1.synchronize()
+        per = []
+        for _ in range(replays):
+            e0.record(stream)
+            gt.launch()
+            e1.record(stream)
+            e1.synchronize()
+            per.append(e0.elapsed_ms(e1) / n)
         gw.destroy()
         gt.destroy()
-        return e0.elapsed_ms(e1) / n
+        return float(np.median(per)), per
 
-    gemv_ms = timed(lambda: batched(warmup), lambda: batched(steps), steps)
+    # at least 400 timed launches whatever --steps is: the K-step graph is replayed (the first few
+    # replays after a short warmup can run ~20 % slow while clocks settle; the median is robust)
+    replays = max(1, -(-400 // max(steps, 1)))
+    gemv_ms, gemv_per = timed(lambda: batched(warmup), lambda: batched(steps), steps, replays)
     # parity of the timed kernel against the oracle: every copy's output
     ys = dy.download(np.float32, copies * M).reshape(copies, M)
     y_ref = oracle.qmat_matvec(t, w, M, K, x1)
@@ -715,7 +755,7 @@ def main():
         for i in range(n):
             stack.matvec_stacked_dev(i % copies, 1, dx, 0, dy, M, stream=stream)
 
-    single_ms = timed(lambda: singles(min(ns, 200)), lambda: singles(ns), ns)
+    single_ms, _ = timed(lambda: singles(min(ns, 200)), lambda: singles(ns), ns)
     stack.close()
     host_mv = time_host_matvec()
 
@@ -763,7 +803,9 @@ def main():
         "data": "synthetic (seeded PCG64 GGUF Q6_K blocks, finite f16 scales; X ~ N(0,1))",
         "config": {"workload": "Q6_K down projection W[896x4864], X[N x 4864] f32: N=1 GEMV batched over "
                                f"{copies} weight copies per launch (+ C1/C2 GEMMs, MoE, decode)",
-                   "weight_copies_per_launch": copies, "graph_replay": True, "gemv_plan": plan},
+                   "weight_copies_per_launch": copies, "graph_replay": True, "gemv_plan": plan,
+                   "timed_launches": replays * steps, "graph_replays": replays,
+                   "ms_per_step_replays": [round(v, 6) for v in gemv_per]},
         "roofline": {"bound": "hbm", "achieved": round(gemv_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gemv_gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                      "algorithmic_bytes_per_launch": gemv_bytes, "avg_launch_us": gemv_ms * 1e3},

@@ -94,7 +94,10 @@ int re_qmat_matmul_dev(re_qmat *q, const float *d_x, size_t rows, float *d_y, in
  * 32 MiB per GPU instead of a buffer the matrix grows on first use; the same plan, kernels and
  * results as re_qmat_matmul_dev. A plan whose partials exceed the scratch fails with RE_ERR_SIZE
  * (the planned splits of every shape fit: the planner caps partial tiles at 32 MiB). The scratch
- * is shared by every call on a GPU: calls that overlap in time on one GPU race and must not. */
+ * is shared by every call on a GPU. Outside stream capture, a call on a different stream than the
+ * previous call on that GPU first waits for the previous call's launches (an event set up once per
+ * device), so calls from several streams or threads stay ordered. Inside stream capture no
+ * ordering is added: replays of captured graphs that use the scratch must not overlap in time. */
 int re_qmat_matmul_noalloc_dev(re_qmat *q, const float *d_x, size_t rows, float *d_y, int mode, void *stream);
 /* Dequantize the resident weights to d_out[m x n] f32, bit-exact with quant::dequant. */
 int re_qmat_dequant_dev(re_qmat *q, float *d_out, void *stream);
@@ -125,8 +128,10 @@ int re_moe_forward_dev(re_moe *e, const float *d_x, size_t tokens, size_t top_k,
  * a dense SwiGLU FFN (gate and up inter x hidden, down hidden x inter, each of any type QMat takes)
  * run on every token and added after the routed sum, out[t] = sum_j w_j expert_j(x_t) +
  * down(silu(gate x_t) * up x_t). Once set, every forward call of e adds it (re_moe_forward, _dev,
- * _routed_dev, re_moe_layer_dev). All three pointers NULL removes it. Call it while no forward
- * call of e is in flight. */
+ * _routed_dev, re_moe_layer_dev). All three pointers NULL removes it. It takes e's lock (held
+ * by re_moe_forward) and waits for the device to drain before freeing the previous shared
+ * matrices, so forwards queued before the call finish with them; device-pointer forwards that
+ * another thread enqueues while it runs are not ordered with it. */
 int re_moe_set_shared(re_moe *e, uint32_t gate_type, const uint8_t *gate, size_t gate_bytes,
                       uint32_t up_type, const uint8_t *up, size_t up_bytes,
                       uint32_t down_type, const uint8_t *down, size_t down_bytes, size_t inter);

@@ -66,7 +66,7 @@ const char* type_name(uint32_t t) {
   }
 }
 
-int scratch_for_current_device(float** out);
+int scratch_for_current_device(float** out, int* dev_out = nullptr);
 
 std::once_flag g_init_once;
 int g_init_rc = RE_OK;
@@ -759,9 +759,15 @@ namespace {
 constexpr int kScratchDevices = 64;
 std::mutex g_scratch_mu;
 float* g_scratch_dev[kScratchDevices] = {};
+// per device: an event recorded after the last no-allocation call's launches, and that call's
+// stream (a call on another stream waits on the event first)
+hipEvent_t g_scratch_ev[kScratchDevices] = {};
+hipStream_t g_scratch_last[kScratchDevices] = {};
+bool g_scratch_used[kScratchDevices] = {};
 
-// the calling thread's current device's copy of `scratch`
-int scratch_for_current_device(float** out) {
+// the calling thread's current device's copy of `scratch` and its ordering event, both set up
+// once per device (re_init, or the first call on the device)
+int scratch_for_current_device(float** out, int* dev_out) {
   int dev = 0;
   HIP_TRY(hipGetDevice(&dev));
   if (dev < 0 || dev >= kScratchDevices) return fail(RE_ERR_ARG, "device %d out of range", dev);
@@ -770,9 +776,11 @@ int scratch_for_current_device(float** out) {
     void* p = nullptr;
     HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
     if (!p) return fail(RE_ERR_HIP, "hipGetSymbolAddress(scratch) returned null");
+    HIP_TRY(hipEventCreateWithFlags(&g_scratch_ev[dev], hipEventDisableTiming));
     g_scratch_dev[dev] = (float*)p;
   }
   *out = g_scratch_dev[dev];
+  if (dev_out) *dev_out = dev;
   return RE_OK;
 }
 }  // namespace
@@ -784,9 +792,23 @@ int re_qmat_matmul_noalloc_dev(re_qmat* q, const float* d_x, size_t rows, float*
   if (rows == 1 || q->dense) return re_qmat_matmul_dev(q, d_x, rows, d_y, mode, stream);   // no scratch
   if (rows > (1u << 24)) return fail(RE_ERR_SIZE, "rows = %zu too large", rows);
   float* part = nullptr;
-  int rc = scratch_for_current_device(&part);
+  int dev = 0;
+  int rc = scratch_for_current_device(&part, &dev);
   if (rc) return rc;
-  return gemm_enqueue(q, d_x, rows, d_y, mode, (hipStream_t)stream, part, kScratchBytes);
+  const hipStream_t s = (hipStream_t)stream;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  HIP_TRY(hipStreamIsCapturing(s, &cs));
+  // under capture the caller orders the replays of graphs that share the scratch
+  if (cs != hipStreamCaptureStatusNone) return gemm_enqueue(q, d_x, rows, d_y, mode, s, part, kScratchBytes);
+  // outside capture, calls on different streams of one GPU are ordered through the device's event
+  // (the lock also orders calls from different threads); calls on one stream are ordered by it
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (g_scratch_used[dev] && g_scratch_last[dev] != s) HIP_TRY(hipStreamWaitEvent(s, g_scratch_ev[dev], 0));
+  if ((rc = gemm_enqueue(q, d_x, rows, d_y, mode, s, part, kScratchBytes))) return rc;
+  HIP_TRY(hipEventRecord(g_scratch_ev[dev], s));
+  g_scratch_last[dev] = s;
+  g_scratch_used[dev] = true;
+  return RE_OK;
 }
 
 int re_qmat_matvec(re_qmat* q, const float* x, float* y) {
@@ -997,12 +1019,25 @@ int re_moe_create(uint32_t gate_type, const uint8_t* gate, size_t gate_bytes, ui
   return RE_OK;
 }
 
+namespace {
+// drops the shared expert's matrices and scratch (the caller holds e->mu or owns e exclusively,
+// and no queued launch uses them any more)
+void moe_clear_shared(re_moe* e) {
+  for (re_qmat** q : {&e->sh_gate, &e->sh_up, &e->sh_down}) {
+    re_qmat_destroy(*q);
+    *q = nullptr;
+  }
+  for (Staging* st : {&e->ssg, &e->ssu, &e->ssh, &e->ssy}) st->release();
+  e->sh_inter = 0;
+}
+}  // namespace
+
 void re_moe_destroy(re_moe* e) {
   if (!e) return;
-  (void)re_moe_set_shared(e, 0, nullptr, 0, 0, nullptr, 0, 0, nullptr, 0, 0);
+  if (e->stream) (void)hipStreamSynchronize(e->stream);
+  moe_clear_shared(e);
   e->dmeta.release();
   e->droute.release();
-  if (e->stream) (void)hipStreamSynchronize(e->stream);
   if (e->d_gate) (void)hipFree(e->d_gate);
   if (e->d_up) (void)hipFree(e->d_up);
   if (e->d_down) (void)hipFree(e->d_down);
@@ -1022,20 +1057,20 @@ int re_moe_set_shared(re_moe* e, uint32_t gate_type, const uint8_t* gate, size_t
                       const uint8_t* up, size_t up_bytes, uint32_t down_type, const uint8_t* down, size_t down_bytes,
                       size_t inter) {
   if (!e) return fail(RE_ERR_ARG, "null moe");
-  for (re_qmat** q : {&e->sh_gate, &e->sh_up, &e->sh_down}) {
-    re_qmat_destroy(*q);
-    *q = nullptr;
-  }
-  for (Staging* st : {&e->ssg, &e->ssu, &e->ssh, &e->ssy}) st->release();
-  e->sh_inter = 0;
-  if (!gate && !up && !down) return RE_OK;
-  if (!gate || !up || !down) return fail(RE_ERR_ARG, "shared expert: null pointer");
+  if ((gate || up || down) && (!gate || !up || !down)) return fail(RE_ERR_ARG, "shared expert: null pointer");
+  // a host forward holds e->mu while it runs the shared expert; launches already queued by any
+  // forward (host or device-pointer, on any stream) may still read the old matrices, so the device
+  // drains before they are freed (a set-up call, not a hot path)
+  std::lock_guard<std::mutex> lk(e->mu);
+  HIP_TRY(hipDeviceSynchronize());
+  moe_clear_shared(e);
+  if (!gate) return RE_OK;
   int rc;
   if ((rc = re_qmat_create(gate_type, gate, gate_bytes, inter, e->hidden, &e->sh_gate)) ||
       (rc = re_qmat_create(up_type, up, up_bytes, inter, e->hidden, &e->sh_up)) ||
       (rc = re_qmat_create(down_type, down, down_bytes, e->hidden, inter, &e->sh_down))) {
     const std::string msg = re_last_error();
-    (void)re_moe_set_shared(e, 0, nullptr, 0, 0, nullptr, 0, 0, nullptr, 0, 0);
+    moe_clear_shared(e);
     return fail(rc, "shared expert: %s", msg.c_str());
   }
   e->sh_inter = inter;

@@ -214,14 +214,16 @@ def dequant(ggml_type: int, data) -> np.ndarray:
 
 
 def _dev_ptr(t) -> int:
-    """Device address of a device buffer (rehip.hip.DeviceBuffer or anything with data_ptr())."""
-    return int(t.data_ptr())
+    """Device address of a device buffer: a rehip.hip.DeviceBuffer (or a view with a `ptr`), or
+    an integer address."""
+    return int(t) if isinstance(t, int) else int(t.ptr)
 
 
 def _stream_ptr(stream) -> int | None:
+    """HIP stream handle of a rehip.hip.Stream, an integer handle, or None (the default stream)."""
     if stream is None:
         return None
-    return int(getattr(stream, "cuda_stream", stream))
+    return int(stream) if isinstance(stream, int) else int(stream.handle)
 
 
 class QMat:

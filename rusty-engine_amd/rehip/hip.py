@@ -78,9 +78,6 @@ class DeviceBuffer:
         b.upload(a)
         return b
 
-    def data_ptr(self) -> int:
-        return self.ptr
-
     def upload(self, a: np.ndarray) -> None:
         a = np.ascontiguousarray(a)
         assert a.nbytes <= self.nbytes
@@ -112,15 +109,15 @@ class Stream:
     def __init__(self):
         s = C.c_void_p()
         check(hip().hipStreamCreate(C.byref(s)))
-        self.cuda_stream = s.value
+        self.handle = s.value
 
     def synchronize(self) -> None:
-        check(hip().hipStreamSynchronize(C.c_void_p(self.cuda_stream)))
+        check(hip().hipStreamSynchronize(C.c_void_p(self.handle)))
 
     def destroy(self) -> None:
-        if self.cuda_stream:
-            hip().hipStreamDestroy(C.c_void_p(self.cuda_stream))
-            self.cuda_stream = None
+        if self.handle:
+            hip().hipStreamDestroy(C.c_void_p(self.handle))
+            self.handle = None
 
 
 class Event:
@@ -130,7 +127,7 @@ class Event:
         self.ev = e.value
 
     def record(self, stream: Stream | None = None) -> None:
-        check(hip().hipEventRecord(C.c_void_p(self.ev), C.c_void_p(stream.cuda_stream if stream else None)))
+        check(hip().hipEventRecord(C.c_void_p(self.ev), C.c_void_p(stream.handle if stream else None)))
 
     def synchronize(self) -> None:
         check(hip().hipEventSynchronize(C.c_void_p(self.ev)))
@@ -147,12 +144,12 @@ class Graph:
 
     def __init__(self, stream: Stream, fn):
         H = hip()
-        check(H.hipStreamBeginCapture(C.c_void_p(stream.cuda_stream), 0))   # hipStreamCaptureModeGlobal
+        check(H.hipStreamBeginCapture(C.c_void_p(stream.handle), 0))   # hipStreamCaptureModeGlobal
         try:
             fn()
         finally:
             g = C.c_void_p()
-            rc = H.hipStreamEndCapture(C.c_void_p(stream.cuda_stream), C.byref(g))
+            rc = H.hipStreamEndCapture(C.c_void_p(stream.handle), C.byref(g))
         check(rc)
         self.graph = g.value
         ex = C.c_void_p()
@@ -161,7 +158,7 @@ class Graph:
         self.stream = stream
 
     def launch(self) -> None:
-        check(hip().hipGraphLaunch(C.c_void_p(self.exec), C.c_void_p(self.stream.cuda_stream)))
+        check(hip().hipGraphLaunch(C.c_void_p(self.exec), C.c_void_p(self.stream.handle)))
 
     def destroy(self) -> None:
         if self.exec:

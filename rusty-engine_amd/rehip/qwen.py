@@ -677,7 +677,4 @@ class _Offset:
     """A device address inside a buffer (for passing a row of a larger buffer)."""
 
     def __init__(self, buf, byte_offset: int):
-        self._p = buf.data_ptr() + byte_offset
-
-    def data_ptr(self) -> int:
-        return self._p
+        self.ptr = buf.ptr + byte_offset

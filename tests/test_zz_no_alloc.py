@@ -96,3 +96,31 @@ def test_noalloc_rejects_plans_beyond_the_scratch(monkeypatch):
         q.matmul_noalloc_dev(dx, rows, dy, rehip.MODE_BF16)
     assert e.value.code == rehip.RE_ERR_SIZE and "static scratch" in e.value.message
     q.close()
+
+
+def test_noalloc_two_streams_without_host_sync():
+    # two matrices whose split plans both use the scratch, called alternately on two streams with
+    # no host synchronisation in between: each call waits for the other stream's previous call, so
+    # every output equals the allocating entry point's
+    t, m, n = rehip.Q6_K, 896, 4864
+    rng = np.random.default_rng(8000)
+    qa = rehip.QMat.from_bytes(t, synth.weight_bytes(rng, t, m, n), m, n)
+    qb = rehip.QMat.from_bytes(t, synth.weight_bytes(rng, t, m, n), m, n)
+    rows = (961, 512, 700, 961)
+    xs = [hip.DeviceBuffer.from_array(synth.activations(rng, r, n)) for r in rows]
+    ys = [hip.DeviceBuffer(r * m * 4) for r in rows]
+    sa, sb = hip.Stream(), hip.Stream()
+    for i, r in enumerate(rows):
+        (qa if i % 2 == 0 else qb).matmul_noalloc_dev(xs[i], r, ys[i], rehip.MODE_BF16,
+                                                      stream=sa if i % 2 == 0 else sb)
+    sa.synchronize()
+    sb.synchronize()
+    for i, r in enumerate(rows):
+        want = hip.DeviceBuffer(r * m * 4)
+        (qa if i % 2 == 0 else qb).matmul_dev(xs[i], r, want, rehip.MODE_BF16)
+        hip.synchronize()
+        assert np.array_equal(ys[i].download(np.float32, r * m), want.download(np.float32, r * m)), i
+    sa.destroy()
+    sb.destroy()
+    qa.close()
+    qb.close()
