@@ -540,13 +540,14 @@ def run_e2e(args, cpu_ok):
         t0 = time.perf_counter()
         logits = dec.prefill(prompt)
         t1 = time.perf_counter()
+        first = logits.copy()
         toks = [qwen.argmax_last(logits)]
         for _ in range(steps - 1):
             toks.append(qwen.argmax_last(dec.step(toks[-1])))
         t2 = time.perf_counter()
         if hasattr(r, "close"):
             r.close()
-        return toks, t1 - t0, (steps - 1) / (t2 - t1) if steps > 1 else None
+        return toks, t1 - t0, (steps - 1) / (t2 - t1) if steps > 1 else None, first
 
     def device_decode(steps, mode):
         """DeviceDecoder: everything on the GPU, one graph replay per token. Two rates: with a
@@ -561,6 +562,7 @@ def run_e2e(args, cpu_ok):
         t0 = time.perf_counter()
         toks = [dd.prefill(prompt)]
         t1 = time.perf_counter()
+        prefill_logits = dd.logits()
         toks.append(dd.step())
         t2 = time.perf_counter()
         for _ in range(steps - 2):
@@ -575,11 +577,11 @@ def run_e2e(args, cpu_ok):
         t5 = time.perf_counter()
         replay_toks = dd.history(len(prompt), steps)
         dd.close()
-        return toks, t1 - t0, (steps - 2) / (t3 - t2), (steps - 2) / (t5 - t4), replay_toks == toks
+        return toks, t1 - t0, (steps - 2) / (t3 - t2), (steps - 2) / (t5 - t4), replay_toks == toks, prefill_logits
 
-    dtoks, dpre_s, dtps, dtps_replay, replay_same = device_decode(args.e2e_steps, rehip.MODE_F32)
-    _, dpre_bf16, _, _, _ = device_decode(3, rehip.MODE_BF16)
-    toks, pre_s, tps = decode(qwen.HipBackend(rehip.MODE_F32), args.e2e_steps)
+    dtoks, dpre_s, dtps, dtps_replay, replay_same, _ = device_decode(args.e2e_steps, rehip.MODE_F32)
+    _, dpre_bf16, _, _, _, bf16_logits = device_decode(3, rehip.MODE_BF16)
+    toks, pre_s, tps, f32_logits = decode(qwen.HipBackend(rehip.MODE_F32), args.e2e_steps)
     res = {"model": "Qwen2.5-0.5B-shaped (24 layers, 896/14/2 heads, d_ff 4864, vocab 151936), Q4_K_M mix, "
                     "random init seed 501",
            "prompt_tokens": len(prompt), "decode_steps": args.e2e_steps, "matmul_mode": "f32",
@@ -594,12 +596,18 @@ def run_e2e(args, cpu_ok):
                                "note": "attention, norms, RoPE, argmax and residuals on the GPU; one HIP graph "
                                        "replay per decode step; decode_tok_s reads the token back after every "
                                        "step, decode_tok_s_replay replays the steps back to back"}}
+    gate_ref, gate_vs = f32_logits, "GPU f32 host-step prefill logits"
     if cpu_ok:
         from oracle.backend import CpuBackend
         n = min(args.e2e_cpu_steps, args.e2e_steps)
-        ctoks, cpre_s, ctps = decode(CpuBackend(), n)
+        ctoks, cpre_s, ctps, cpu_logits = decode(CpuBackend(), n)
         res.update({"prefill_s_cpu": cpre_s, "decode_tok_s_cpu": ctps, "cpu_decode_steps": n,
                     "greedy_identical": ctoks == toks[:n] and ctoks == dtoks[:n], "greedy_compared_steps": n})
+        gate_ref, gate_vs = cpu_logits, "CPU f32 prefill logits (reference-restated kernels)"
+    # the bf16 prefill's logits under the reference's profile gate (tests/qwen35_parity.rs:45-52)
+    gate = qwen.logit_profile_check(gate_ref, bf16_logits)
+    gate.update({"against": gate_vs, "logit_tol": qwen.LOGIT_TOL, "tie_floor": qwen.TIE_FLOOR})
+    res["device_resident"]["prefill_bf16_profile_gate"] = gate
     return res
 
 
@@ -821,6 +829,8 @@ def main():
         "e2e": e2e,
     }
     if e2e and e2e.get("greedy_identical") is False:
+        out["parity_ok"] = False
+    if e2e and not e2e["device_resident"]["prefill_bf16_profile_gate"]["ok"]:
         out["parity_ok"] = False
     if moe_res and any(v.get("rel_err_vs_oracle", 0) > 1e-2 for v in moe_res.values()):
         out["parity_ok"] = False

@@ -166,6 +166,31 @@ def argmax_last(logits: np.ndarray) -> int:
     return int(np.flatnonzero(logits == mx)[-1])
 
 
+# the reference's logit-profile gate (tests/qwen35_parity.rs:45-52)
+LOGIT_TOL = 0.75    # nats: |(got - max got) - (ref - max ref)| over the reference's top-5
+TIE_FLOOR = 0.5     # nats: the reference's top1 - top2 margin from which the argmax must agree
+
+
+def logit_profile_check(ref: np.ndarray, got: np.ndarray, top: int = 5, tol: float = LOGIT_TOL,
+                        tie_floor: float = TIE_FLOOR) -> dict:
+    """The profile gate of tests/qwen35_parity.rs:12-20, 45-52 for one position: for each of the
+    reference's `top` tokens, the gap of `got`'s logit to `got`'s maximum must match the gap of
+    the reference's logit to the reference's maximum within `tol` (a logit gap equals the
+    log-softmax gap); the argmax must agree where the reference's top-1 leads its top-2 by at
+    least `tie_floor`. Returns the worst gap deviation, whether the argmax was required and
+    matched, and `ok`."""
+    ref = np.asarray(ref, np.float64)
+    got = np.asarray(got, np.float64)
+    order = np.argsort(-ref, kind="stable")[:top]
+    dev = np.abs((got[order] - got.max()) - (ref[order] - ref.max()))
+    margin = float(ref[order[0]] - ref[order[1]])
+    decisive = margin >= tie_floor
+    same = argmax_last(got) == argmax_last(ref)
+    worst = float(dev.max())
+    return {"worst_gap_dev": worst, "margin": margin, "decisive": bool(decisive), "argmax_same": bool(same),
+            "ok": bool(worst <= tol and (same or not decisive))}
+
+
 # ---- weights ------------------------------------------------------------------------------
 @dataclass
 class BlockBytes:
@@ -481,6 +506,7 @@ class DeviceDecoder:
     def __init__(self, mb: ModelBytes, max_seq: int, mode: int = MODE_F32, prefill_rows: int = 1024,
                  use_graph: bool = True):
         from . import Ffn, attention_work_bytes, hip, rope_table_dev
+        self._check_supported(mb)
         self.mb, self.mode, self.max_seq = mb, mode, max_seq
         self.use_graph = use_graph
         g = self.g = mb.geom
@@ -503,7 +529,8 @@ class DeviceDecoder:
             blk["qkv"] = QMat.from_bytes(mb.attn_type, np.concatenate([b.q, b.k, b.v]), d + 2 * kv, d)
             blk["ffn"] = Ffn(blk["gate"], blk["up"])
             self.blocks.append(blk)
-        self.output = QMat.from_bytes(mb.embed_type, mb.output, mb.n_vocab, d)
+        out_t = mb.output_type if mb.output_type is not None else mb.embed_type
+        self.output = QMat.from_bytes(out_t, mb.output, mb.n_vocab, d)
         self.output_norm = B.from_array(mb.output_norm)
         self.embed = B.from_array(dequant(mb.embed_type, mb.embed))
         cap = self.cap
@@ -530,6 +557,33 @@ class DeviceDecoder:
         rope_table_dev(g.rope_freq_base, hd, max_seq, self.rope, self.stream)
         self.graph = None
         self.seq_len = 0
+
+    @staticmethod
+    def _check_supported(mb: ModelBytes) -> None:
+        """The shapes and types the device-resident step covers, checked before anything is
+        allocated: quantized projections (the fused norm / residual / SwiGLU / argmax epilogues
+        exist for the quant GEMVs only; dense F32/F16/BF16 models run on DenseDecoder with
+        HipBackend), one type for q, k and v (one fused matrix) and one for gate and up (one
+        paired launch), rows a multiple of 32 elements, and head_dim a multiple of 4 up to 256 (the
+        attention kernels). Raises ValueError naming what is outside."""
+        from . import GEOM
+        g = mb.geom
+        out_t = mb.output_type if mb.output_type is not None else mb.embed_type
+        for name, t in (("attention", mb.attn_type), ("ffn", mb.ffn_type), ("down", mb.down_type),
+                        ("embedding", mb.embed_type), ("output", out_t)):
+            if t not in GEOM:
+                raise ValueError(f"DeviceDecoder: the {name} weights are ggml type {t}, which has no fused "
+                                 "GEMV kernel (quantized Q4_0/Q5_0/Q8_0/Q4_K/Q5_K/Q6_K only); run dense models "
+                                 "on DenseDecoder with HipBackend")
+        for i, b in enumerate(mb.blocks):
+            if b.types:
+                raise ValueError(f"DeviceDecoder: block {i} overrides tensor types {sorted(b.types)}; the device "
+                                 "step takes one attention type (fused q|k|v) and one ffn type (paired gate/up)")
+        if g.d_model % g.n_heads or g.head_dim % 4 or g.head_dim > 256 or g.n_heads % g.n_kv_heads:
+            raise ValueError(f"DeviceDecoder: head_dim {g.d_model}/{g.n_heads} with {g.n_kv_heads} KV heads; the "
+                             "attention kernels take head_dim a multiple of 4 up to 256 and whole query groups")
+        if g.d_model % 32 or g.d_ff % 32:
+            raise ValueError(f"DeviceDecoder: d_model {g.d_model} and d_ff {g.d_ff} must be multiples of 32")
 
     # -- pieces ----------------------------------------------------------------------------
     def _qkv_post(self, blk, rows):

@@ -47,3 +47,58 @@ def test_tiny_model_decode_matches_cpu_path():
     got, _ = run(mb, qwen.HipBackend(rehip.MODE_F32), prompt, 20)
     want, _ = run(mb, CpuBackend(), prompt, 20)
     assert got == want
+
+
+GATE_STEPS = 24
+
+
+@pytest.fixture(scope="module")
+def cpu_reference(model):
+    """The f32 CPU path (reference-restated kernels): prefill logits and GATE_STEPS greedy steps,
+    with every position's logits."""
+    prompt = np.random.default_rng(502).integers(0, model.n_vocab, 961)
+    r = qwen.DenseRunner(model, CpuBackend())
+    dec = qwen.DenseDecoder(r, len(prompt) + GATE_STEPS + 1)
+    logits = [dec.prefill(prompt).copy()]
+    toks = [qwen.argmax_last(logits[0])]
+    for _ in range(GATE_STEPS):
+        logits.append(dec.step(toks[-1]).copy())
+        toks.append(qwen.argmax_last(logits[-1]))
+    return prompt, toks, logits
+
+
+def _gate_all(ref_logits, got_logits):
+    res = [qwen.logit_profile_check(r, g) for r, g in zip(ref_logits, got_logits)]
+    bad = [(i, c) for i, c in enumerate(res) if not c["ok"]]
+    assert not bad, bad[:3]
+    return res
+
+
+def test_bf16_profile_gate_host_step_path(model, cpu_reference):
+    # bf16 MFMA projections (HipBackend), host attention/norms, teacher-forced on the CPU path's
+    # greedy tokens: every position passes the reference's profile gate against the f32 CPU logits
+    prompt, toks, ref = cpu_reference
+    r = qwen.DenseRunner(model, qwen.HipBackend(rehip.MODE_BF16))
+    dec = qwen.DenseDecoder(r, len(prompt) + GATE_STEPS + 1)
+    got = [dec.prefill(prompt).copy()]
+    for t in toks[:GATE_STEPS]:
+        got.append(dec.step(t).copy())
+    r.close()
+    res = _gate_all(ref, got)
+    assert sum(c["decisive"] for c in res) >= 1   # the gate exercised the argmax condition
+
+
+def test_bf16_profile_gate_device_decoder(model, cpu_reference):
+    # the device-resident decoder in bf16 mode (bf16 MFMA prefill GEMMs, decode GEMVs): prefill and
+    # GATE_STEPS teacher-forced decode steps, each position gated against the f32 CPU logits
+    prompt, toks, ref = cpu_reference
+    dd = qwen.DeviceDecoder(model, max_seq=len(prompt) + GATE_STEPS + 1, mode=rehip.MODE_BF16,
+                            prefill_rows=len(prompt))
+    dd.prefill(prompt)
+    got = [dd.logits()]
+    for t in toks[:GATE_STEPS]:
+        dd.tok.upload(np.array([t], np.int32))      # force the CPU path's token
+        dd.step()
+        got.append(dd.logits())
+    dd.close()
+    _gate_all(ref, got)
