@@ -146,9 +146,21 @@ int re_moe_set_shared(re_moe *e, uint32_t gate_type, const uint8_t *gate, size_t
  * re_moe_forward_routed_dev: re_moe_forward_dev with device ids/weights (tokens x top_k); the
  *   grouping by expert and the task lists are built by a kernel; tokens * top_k <= 8192. An id
  *   outside [0, n_experts) contributes nothing.
- * re_moe_layer_dev: the three in one stream (scratch for logits/ids/weights is kept by e). */
+ * re_moe_layer_dev: the three in one stream (scratch for logits/ids/weights is kept by e).
+ * re_moe_route_group_dev: the bias-corrected group routers (moe.rs:126-268): scores
+ *   sigmoid(logit + bias[e]) (bias entries past bias_len count as 0; d_bias may be NULL with
+ *   bias_len 0), experts in n_groups contiguous groups (expert e in group e * ng / n_experts,
+ *   ng = n_groups clamped to 1 ..= n_experts), only the top_k_group best groups eligible
+ *   (0 = every group), the top_k best eligible experts renormalised over their scores.
+ *   RE_GATE_GROUP scores a group by its summed scores (route_group, moe.rs:132-194),
+ *   RE_GATE_NOAUX_TC by its two best (route_noaux_tc, moe.rs:196-268, DeepSeek-V3 / Qwen3).
+ *   Ties go to the lower group / expert index. When the eligible groups hold fewer than top_k
+ *   experts, the remaining slots get id -1 and weight 0 (they contribute nothing downstream).
+ * re_moe_layer_group_dev: router logits, group routing and the FFN in one stream. */
 #define RE_GATE_SOFTMAX 0
 #define RE_GATE_SIGMOID 1
+#define RE_GATE_GROUP 2
+#define RE_GATE_NOAUX_TC 3
 int re_moe_router_logits_dev(const float *d_x, const float *d_router_w, size_t tokens, size_t hidden,
                              size_t n_experts, float *d_logits, void *stream);
 int re_moe_route_dev(const float *d_logits, size_t tokens, size_t n_experts, size_t top_k, int gate,
@@ -157,6 +169,12 @@ int re_moe_forward_routed_dev(re_moe *e, const float *d_x, size_t tokens, size_t
                               const float *d_weights, float *d_out, int mode, void *stream);
 int re_moe_layer_dev(re_moe *e, const float *d_x, size_t tokens, const float *d_router_w, size_t top_k,
                      int gate, float *d_out, int mode, void *stream);
+int re_moe_route_group_dev(const float *d_logits, size_t tokens, size_t n_experts, size_t top_k, int gate,
+                           const float *d_bias, size_t bias_len, size_t n_groups, size_t top_k_group,
+                           int *d_ids, float *d_weights, void *stream);
+int re_moe_layer_group_dev(re_moe *e, const float *d_x, size_t tokens, const float *d_router_w, size_t top_k,
+                           int gate, const float *d_bias, size_t bias_len, size_t n_groups,
+                           size_t top_k_group, float *d_out, int mode, void *stream);
 
 /* ---- device-resident transformer steps (src/forward.rs, src/infer.rs, src/runner.rs) ------
  * Device pointers, enqueued on `stream`. Positions come from a device int (*d_pos) so that a

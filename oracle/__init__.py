@@ -93,6 +93,9 @@ def lib():
         L.orc_top_k.restype = _sz
         L.orc_top_k_sigmoid.argtypes = [_f32p, _sz, _sz, _u32p, _f32p]
         L.orc_top_k_sigmoid.restype = _sz
+        for fn in (L.orc_route_group, L.orc_route_noaux_tc):
+            fn.argtypes = [_f32p, _sz, C.c_void_p, _sz, _sz, _sz, _sz, _u32p, _f32p]
+            fn.restype = _sz
         L.orc_moe_ffn.argtypes = [C.c_uint32, _u8p, _sz, C.c_uint32, _u8p, _sz, C.c_uint32, _u8p, _sz,
                                   _sz, _sz, _sz, _f32p, _sz, _sz, _u32p, _f32p, _f32p]
         L.orc_cpu_matmul.argtypes = [C.c_uint32, _u8p, _sz, _sz, _f32p, _sz, _f32p, C.c_int]
@@ -302,6 +305,27 @@ def top_k_sigmoid(scores, k: int):
     w = np.zeros(max(kk, 1), np.float32)
     n = lib().orc_top_k_sigmoid(s, s.size, k, ids, w)
     return ids[:n].copy(), w[:n].copy()
+
+
+def _route_groups(fn, logits, bias, n_groups: int, top_k: int, top_k_group):
+    s = _f32(logits)
+    b = None if bias is None else _f32(bias)
+    kk = min(top_k, s.size)
+    ids = np.zeros(max(kk, 1), np.uint32)
+    w = np.zeros(max(kk, 1), np.float32)
+    n = fn(s, s.size, None if b is None else b.ctypes.data, 0 if b is None else b.size, n_groups, top_k,
+           0 if top_k_group is None else top_k_group, ids, w)
+    return ids[:n].copy(), w[:n].copy()
+
+
+def route_group(logits, bias, n_groups: int, top_k: int, top_k_group=None):
+    """moe.rs:132-194: group score = the group's summed sigmoid(logit + bias); None = every group."""
+    return _route_groups(lib().orc_route_group, logits, bias, n_groups, top_k, top_k_group)
+
+
+def route_noaux_tc(logits, bias, n_groups: int, top_k: int, top_k_group=None):
+    """moe.rs:196-268: group score = the sum of the group's two best sigmoid(logit + bias)."""
+    return _route_groups(lib().orc_route_noaux_tc, logits, bias, n_groups, top_k, top_k_group)
 
 
 def moe_ffn(gate_t, gate, up_t, up, down_t, down, n_experts, hidden, inter, x, tokens, k, ids,

@@ -8,6 +8,7 @@
 #include "oracle.h"
 #include "blocks.h"
 
+#include <float.h>
 #include <math.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -587,6 +588,74 @@ size_t orc_top_k_sigmoid(const float *scores, size_t n, size_t k, uint32_t *ids,
     free(sig);
     free(idx);
     return k;
+}
+
+/* moe.rs:132-268, both group routers: `top2` selects the group score (0: the group's sum,
+ * route_group; 1: its top two, route_noaux_tc). Every step in the reference's order: scores in
+ * index order, group sums accumulated in index order from 0.0, groups and candidates ranked by
+ * the stable descending sort, the weight sum accumulated in rank order. */
+static size_t route_groups(const float *logits, size_t n, const float *bias, size_t bias_len, size_t n_groups,
+                           size_t top_k, size_t top_k_group, int top2, uint32_t *ids, float *weights) {
+    if (n == 0) return 0;
+    float *ex = (float *)malloc(n * sizeof(float));
+    uint32_t *cand = (uint32_t *)malloc(n * sizeof(uint32_t));
+    size_t ng = n_groups < 1 ? 1 : n_groups;
+    if (ng > n) ng = n;
+    float *gscore = (float *)malloc(ng * sizeof(float));
+    float *t1 = (float *)malloc(ng * sizeof(float));
+    float *t2 = (float *)malloc(ng * sizeof(float));
+    uint32_t *gorder = (uint32_t *)malloc(ng * sizeof(uint32_t));
+    unsigned char *allowed = (unsigned char *)malloc(ng);
+    size_t k = 0;
+    if (!ex || !cand || !gscore || !t1 || !t2 || !gorder || !allowed) goto out;
+    for (size_t i = 0; i < n; ++i) ex[i] = orc_sigmoid(logits[i] + (bias && i < bias_len ? bias[i] : 0.0f));
+    for (size_t g = 0; g < ng; ++g) { gscore[g] = 0.0f; t1[g] = -FLT_MAX; t2[g] = -FLT_MAX; }
+    for (size_t i = 0; i < n; ++i) {
+        const size_t g = i * ng / n;
+        if (!top2) {
+            gscore[g] += ex[i];                       /* moe.rs:157-160 */
+        } else if (ex[i] >= t1[g]) {                  /* moe.rs:222-231 */
+            t2[g] = t1[g];
+            t1[g] = ex[i];
+        } else if (ex[i] > t2[g]) {
+            t2[g] = ex[i];
+        }
+    }
+    if (top2)
+        for (size_t g = 0; g < ng; ++g) gscore[g] = t1[g] + (t2[g] == -FLT_MAX ? 0.0f : t2[g]);   /* moe.rs:232-234 */
+    if (top_k_group == 0) {                           /* None: every group */
+        memset(allowed, 1, ng);
+    } else {                                          /* moe.rs:165-179, 238-252 */
+        for (size_t g = 0; g < ng; ++g) gorder[g] = (uint32_t)g;
+        stable_sort_desc(gscore, gorder, ng);
+        memset(allowed, 0, ng);
+        const size_t take = top_k_group < ng ? top_k_group : ng;
+        for (size_t j = 0; j < take; ++j) allowed[gorder[j]] = 1;
+    }
+    size_t nc = 0;                                    /* moe.rs:182-193, 255-267 */
+    for (size_t i = 0; i < n; ++i)
+        if (allowed[i * ng / n]) cand[nc++] = (uint32_t)i;
+    stable_sort_desc(ex, cand, nc);
+    k = top_k < nc ? top_k : nc;
+    float wsum = 0.0f;
+    for (size_t j = 0; j < k; ++j) wsum += ex[cand[j]];
+    for (size_t j = 0; j < k; ++j) {
+        ids[j] = cand[j];
+        weights[j] = wsum == 0.0f ? 0.0f : ex[cand[j]] / wsum;
+    }
+out:
+    free(ex); free(cand); free(gscore); free(t1); free(t2); free(gorder); free(allowed);
+    return k;
+}
+
+size_t orc_route_group(const float *logits, size_t n, const float *bias, size_t bias_len, size_t n_groups,
+                       size_t top_k, size_t top_k_group, uint32_t *ids, float *weights) {
+    return route_groups(logits, n, bias, bias_len, n_groups, top_k, top_k_group, 0, ids, weights);
+}
+
+size_t orc_route_noaux_tc(const float *logits, size_t n, const float *bias, size_t bias_len, size_t n_groups,
+                          size_t top_k, size_t top_k_group, uint32_t *ids, float *weights) {
+    return route_groups(logits, n, bias, bias_len, n_groups, top_k, top_k_group, 1, ids, weights);
 }
 
 /* moe.rs:271-277 on a dequantized (padded-row) matrix */

@@ -103,6 +103,19 @@ size_t orc_top_k(const float *scores, size_t n, size_t k, uint32_t *ids, float *
 size_t orc_top_k_sigmoid(const float *scores, size_t n, size_t k, uint32_t *ids,
                          float *weights);
 
+/* Bias-corrected group routing (moe.rs:126-268): scores sigmoid(logit + bias[i]) (bias entries
+ * past bias_len count as 0), experts split into n_groups contiguous groups (group_of(i) =
+ * i * ng / n, ng = clamp(n_groups, 1, n)); the top_k_group best groups are eligible
+ * (top_k_group 0: every group, the reference's None); the top_k best eligible experts are
+ * renormalised over their scores. orc_route_group scores a group by the sum of its scores
+ * (route_group, moe.rs:132-194), orc_route_noaux_tc by the sum of its top two (route_noaux_tc,
+ * moe.rs:196-268). ids/weights hold min(top_k, n) entries; returns the count written (fewer
+ * when the eligible groups hold fewer experts). */
+size_t orc_route_group(const float *logits, size_t n, const float *bias, size_t bias_len, size_t n_groups,
+                       size_t top_k, size_t top_k_group, uint32_t *ids, float *weights);
+size_t orc_route_noaux_tc(const float *logits, size_t n, const float *bias, size_t bias_len, size_t n_groups,
+                          size_t top_k, size_t top_k_group, uint32_t *ids, float *weights);
+
 /* Quantized expert FFN layer for a batch of tokens (moe.rs:288-300 + 360-388 applied to
  * dequantized experts): for token t, out[t] = sum over its k routed experts, in routing
  * order, of weight * down(silu(gate x) * up x). gate/up are inter x hidden, down is

@@ -1221,6 +1221,23 @@ int re_moe_route_dev(const float* d_logits, size_t tokens, size_t n_experts, siz
   return RE_OK;
 }
 
+int re_moe_route_group_dev(const float* d_logits, size_t tokens, size_t n_experts, size_t top_k, int gate,
+                           const float* d_bias, size_t bias_len, size_t n_groups, size_t top_k_group, int* d_ids,
+                           float* d_weights, void* stream) {
+  if (!d_logits || !d_ids || !d_weights) return fail(RE_ERR_ARG, "null pointer");
+  if (bias_len && !d_bias) return fail(RE_ERR_ARG, "null bias with bias_len %zu", bias_len);
+  if (gate != RE_GATE_GROUP && gate != RE_GATE_NOAUX_TC) return fail(RE_ERR_ARG, "unknown group gate %d", gate);
+  if (tokens == 0) return RE_OK;
+  if (n_experts == 0 || n_experts > 1024 || top_k == 0 || top_k > n_experts || tokens > (1u << 24))
+    return fail(RE_ERR_SIZE, "route: %zu experts (<= 1024), top_k %zu, %zu tokens", n_experts, top_k, tokens);
+  // the reference clamps the group count to 1 ..= n (n_groups.max(1).min(n), moe.rs:150, 217)
+  const size_t ng = std::min(std::max<size_t>(n_groups, 1), n_experts);
+  HIP_TRY(launch_moe_route_group(d_logits, (int)tokens, (int)n_experts, (int)top_k, gate == RE_GATE_NOAUX_TC ? 1 : 0,
+                                 d_bias, (int)std::min(bias_len, n_experts), (int)ng,
+                                 (int)std::min(top_k_group, ng), d_ids, d_weights, (hipStream_t)stream));
+  return RE_OK;
+}
+
 int re_moe_router_logits_dev(const float* d_x, const float* d_router_w, size_t tokens, size_t hidden,
                              size_t n_experts, float* d_logits, void* stream) {
   if (!d_x || !d_router_w || !d_logits) return fail(RE_ERR_ARG, "null pointer");
@@ -1412,8 +1429,14 @@ int re_moe_forward_routed_dev(re_moe* e, const float* d_x, size_t tokens, size_t
   return moe_add_shared(e, d_x, tokens, d_out, mode, s);
 }
 
-int re_moe_layer_dev(re_moe* e, const float* d_x, size_t tokens, const float* d_router_w, size_t top_k, int gate,
-                     float* d_out, int mode, void* stream) {
+}  // extern "C"
+
+namespace {
+// router logits -> route (`route(logits, ids, weights)`) -> the FFN, in one stream; the scratch
+// for the logits, ids and weights is kept by e
+template <typename Route>
+int moe_layer(re_moe* e, const float* d_x, size_t tokens, const float* d_router_w, size_t top_k, float* d_out,
+              int mode, void* stream, Route route) {
   if (!e || !d_x || !d_router_w || !d_out) return fail(RE_ERR_ARG, "null pointer");
   if (tokens == 0) return RE_OK;
   if (tokens > 65535) return fail(RE_ERR_SIZE, "%zu tokens", tokens);
@@ -1426,8 +1449,27 @@ int re_moe_layer_dev(re_moe* e, const float* d_x, size_t tokens, const float* d_
   int* ids = (int*)((uint8_t*)e->droute.p + logit_bytes);
   float* w = (float*)((uint8_t*)e->droute.p + logit_bytes + id_bytes);
   if ((rc = re_moe_router_logits_dev(d_x, d_router_w, tokens, e->hidden, E, logits, stream))) return rc;
-  if ((rc = re_moe_route_dev(logits, tokens, E, top_k, gate, ids, w, stream))) return rc;
+  if ((rc = route(logits, ids, w))) return rc;
   return re_moe_forward_routed_dev(e, d_x, tokens, top_k, ids, w, d_out, mode, stream);
+}
+}  // namespace
+
+extern "C" {
+
+int re_moe_layer_dev(re_moe* e, const float* d_x, size_t tokens, const float* d_router_w, size_t top_k, int gate,
+                     float* d_out, int mode, void* stream) {
+  return moe_layer(e, d_x, tokens, d_router_w, top_k, d_out, mode, stream, [&](const float* lg, int* ids, float* w) {
+    return re_moe_route_dev(lg, tokens, e->n_experts, top_k, gate, ids, w, stream);
+  });
+}
+
+int re_moe_layer_group_dev(re_moe* e, const float* d_x, size_t tokens, const float* d_router_w, size_t top_k,
+                           int gate, const float* d_bias, size_t bias_len, size_t n_groups, size_t top_k_group,
+                           float* d_out, int mode, void* stream) {
+  return moe_layer(e, d_x, tokens, d_router_w, top_k, d_out, mode, stream, [&](const float* lg, int* ids, float* w) {
+    return re_moe_route_group_dev(lg, tokens, e->n_experts, top_k, gate, d_bias, bias_len, n_groups, top_k_group,
+                                  ids, w, stream);
+  });
 }
 
 int re_moe_forward_dev(re_moe* e, const float* d_x, size_t tokens, size_t top_k, const uint32_t* ids,

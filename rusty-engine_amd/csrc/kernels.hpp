@@ -245,6 +245,10 @@ hipError_t launch_pos_add(int* pos, int delta, hipStream_t s);
 // logits, 1 = per-expert sigmoid renormalised over the chosen
 hipError_t launch_moe_route(const float* logits, int tokens, int n_experts, int k, int gate, int* ids,
                             float* weights, hipStream_t s);
+// route_group (top2 = 0) / route_noaux_tc (top2 = 1) of moe.rs:126-268; top_k_group 0 = every group
+hipError_t launch_moe_route_group(const float* logits, int tokens, int n_experts, int k, int top2, const float* bias,
+                                  int bias_len, int n_groups, int top_k_group, int* ids, float* weights,
+                                  hipStream_t s);
 // logits[t][e] = router_w[e] . x[t] (f32)
 hipError_t launch_moe_router_logits(const float* x, const float* router_w, int tokens, int hidden, int n_experts,
                                     float* logits, hipStream_t s);

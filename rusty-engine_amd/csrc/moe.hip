@@ -3,6 +3,8 @@
 // the experts receive few rows each.
 #include <hip/hip_runtime.h>
 
+#include <cfloat>
+
 #include "deq.hpp"
 #include "kernels.hpp"
 
@@ -142,6 +144,110 @@ __global__ __launch_bounds__(64) void moe_route_kernel(const float* __restrict__
   const int t = blockIdx.x;
   route_token<EPL>(logits + (size_t)t * n_experts, n_experts, k, gate, threadIdx.x, topv, topi, ids + (size_t)t * k,
                    weights + (size_t)t * k);
+}
+
+// Bias-corrected group routing of one token per wave (route_group / route_noaux_tc,
+// moe.rs:126-268). Scores sigmoid(logit + bias[e]) (bias entries past bias_len are 0) go to
+// LDS; lane g then scores group g, the experts e with e * ng / n == g, walking them in index order
+// as the reference does: their sum from 0.0 (top2 = 0), or the sum of the two best with the
+// reference's update rule (top2 = 1). The top_k_group best groups (ties to the lower group, the
+// stable descending sort; 0 = every group) are picked by repeated wave argmax, experts outside them
+// are excluded, and the top k of the rest are picked the same way and renormalised over their
+// scores, summed in rank order. When the eligible groups hold fewer than k experts the remaining
+// slots get id -1 and weight 0 (the reference returns the shorter list; an id out of range
+// contributes nothing downstream). NaN scores rank as -inf.
+template <int EPL>
+__global__ __launch_bounds__(64) void moe_route_group_kernel(const float* __restrict__ logits, int n_experts, int k,
+                                                             int top2, const float* __restrict__ bias, int bias_len,
+                                                             int ng, int tkg, int* __restrict__ ids,
+                                                             float* __restrict__ weights) {
+  __shared__ float sc[kRouteMaxExperts];
+  __shared__ float gs[kRouteMaxExperts];
+  __shared__ int allowed[kRouteMaxExperts];
+  __shared__ float topv[kRouteMaxExperts];
+  __shared__ int topi[kRouteMaxExperts];
+  const int t = blockIdx.x, lane = threadIdx.x;
+  const float* row = logits + (size_t)t * n_experts;
+  for (int e = lane; e < n_experts; e += 64) {
+    const float x = row[e] + (bias && e < bias_len ? bias[e] : 0.0f);
+    float s = 1.0f / (1.0f + expf(-x));                // sigmoid (moe.rs:43-46)
+    if (s != s) s = -INFINITY;
+    sc[e] = s;
+  }
+  __syncthreads();
+  for (int g = lane; g < ng; g += 64) {
+    const int lo = (int)(((long long)g * n_experts + ng - 1) / ng);
+    const int hi = (int)(((long long)(g + 1) * n_experts + ng - 1) / ng);
+    float sum = 0.0f, t1 = -FLT_MAX, t2 = -FLT_MAX;
+    for (int i = lo; i < hi; ++i) {
+      const float v = sc[i];
+      if (!top2) {
+        sum += v;
+      } else if (v >= t1) {
+        t2 = t1;
+        t1 = v;
+      } else if (v > t2) {
+        t2 = v;
+      }
+    }
+    gs[g] = top2 ? t1 + (t2 == -FLT_MAX ? 0.0f : t2) : sum;
+    allowed[g] = tkg == 0;
+  }
+  __syncthreads();
+  const int take = tkg < ng ? tkg : ng;
+  for (int r = 0; r < take; ++r) {
+    float bv = -INFINITY;
+    int bg = 0x7fffffff;
+    for (int g = lane; g < ng; g += 64)
+      if (!allowed[g] && (gs[g] > bv || (gs[g] == bv && g < bg))) { bv = gs[g]; bg = g; }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      const float ov = __shfl_xor(bv, off, 64);
+      const int og = __shfl_xor(bg, off, 64);
+      if (ov > bv || (ov == bv && og < bg)) { bv = ov; bg = og; }
+    }
+    if (lane == 0 && bg < ng) allowed[bg] = 1;
+    __syncthreads();
+  }
+  const int epl = (n_experts + 63) / 64;
+  float v[EPL];
+  bool taken[EPL];
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) {
+    const int e = lane + 64 * j;
+    const bool in = j < epl && e < n_experts;
+    v[j] = in ? sc[e] : -INFINITY;
+    taken[j] = !in || !allowed[(int)((long long)e * ng / n_experts)];
+  }
+  for (int r = 0; r < k; ++r) {
+    float bv = -INFINITY;
+    int be = 0x7fffffff;
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) {
+      if (j >= epl) break;                             // uniform
+      const int e = lane + 64 * j;
+      if (!taken[j] && (v[j] > bv || (v[j] == bv && e < be))) { bv = v[j]; be = e; }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      const float ov = __shfl_xor(bv, off, 64);
+      const int oe = __shfl_xor(be, off, 64);
+      if (ov > bv || (ov == bv && oe < be)) { bv = ov; be = oe; }
+    }
+#pragma unroll
+    for (int j = 0; j < EPL; ++j)
+      if (lane + 64 * j == be) taken[j] = true;
+    if (lane == 0) { topv[r] = bv; topi[r] = be; }
+  }
+  if (lane != 0) return;
+  int kk = 0;                                          // eligible experts found (a prefix of the ranks)
+  while (kk < k && topi[kk] < n_experts) ++kk;
+  float ws = 0.0f;
+  for (int r = 0; r < kk; ++r) ws += topv[r];
+  for (int r = 0; r < k; ++r) {
+    ids[(size_t)t * k + r] = r < kk ? topi[r] : -1;
+    weights[(size_t)t * k + r] = r < kk && ws != 0.0f ? topv[r] / ws : 0.0f;
+  }
 }
 
 // logits[t][e] = router_w[e] . x[t] (the f32 matvec of moe.rs:367): x[t] staged in LDS, one wave
@@ -360,6 +466,22 @@ hipError_t launch_moe_route(const float* logits, int tokens, int n_experts, int 
   else
     hipLaunchKernelGGL(moe_route_kernel<kRouteMaxExperts / 64>, dim3((unsigned)tokens), dim3(64), 0, s, logits, n_experts, k,
                        gate, ids, weights);
+  return hipGetLastError();
+}
+
+hipError_t launch_moe_route_group(const float* logits, int tokens, int n_experts, int k, int top2, const float* bias,
+                                  int bias_len, int n_groups, int top_k_group, int* ids, float* weights,
+                                  hipStream_t s) {
+  const int epl = (n_experts + 63) / 64;
+#define RE_ROUTE_GROUP(E)                                                                                        \
+  hipLaunchKernelGGL(moe_route_group_kernel<E>, dim3((unsigned)tokens), dim3(64), 0, s, logits, n_experts, k, top2, \
+                     bias, bias_len, n_groups, top_k_group, ids, weights)
+  if (epl <= 1) RE_ROUTE_GROUP(1);
+  else if (epl <= 2) RE_ROUTE_GROUP(2);
+  else if (epl <= 4) RE_ROUTE_GROUP(4);
+  else if (epl <= 8) RE_ROUTE_GROUP(8);
+  else RE_ROUTE_GROUP(kRouteMaxExperts / 64);
+#undef RE_ROUTE_GROUP
   return hipGetLastError();
 }
 

@@ -24,6 +24,8 @@
 #include <string>
 #include <utility>
 #include <vector>
+#include <cfloat>
+#include <optional>
 
 #include "../../include/rehip.h"
 
@@ -274,6 +276,59 @@ inline std::vector<ExpertScore> top_k_sigmoid(const std::vector<float>& scores, 
 
 inline std::vector<ExpertScore> route(const std::vector<float>& logits, RouterConfig cfg) {
   return cfg.gate == Gate::Softmax ? top_k(logits, cfg.top_k) : top_k_sigmoid(logits, cfg.top_k);
+}
+
+// Bias-corrected group routing (moe.rs:126-268): scores sigmoid(logit + bias[i]) (missing bias
+// entries count as 0), n_groups contiguous groups (group i * ng / n), only the top_k_group best
+// groups eligible (nullopt: every group), the top_k best eligible experts renormalised over their
+// scores. noaux_tc scores a group by its two best members, route_group by the sum of all.
+inline std::vector<ExpertScore> route_groups(const std::vector<float>& logits, const std::vector<float>& bias,
+                                             size_t n_groups, size_t top_k, std::optional<size_t> top_k_group,
+                                             bool top2) {
+  const size_t n = logits.size();
+  if (n == 0) return {};
+  std::vector<float> ex(n);
+  for (size_t i = 0; i < n; ++i) ex[i] = sigmoid(logits[i] + (i < bias.size() ? bias[i] : 0.0f));
+  const size_t ng = std::min(std::max<size_t>(n_groups, 1), n);
+  std::vector<float> gscore(ng, 0.0f), t1(ng, -FLT_MAX), t2(ng, -FLT_MAX);
+  for (size_t i = 0; i < n; ++i) {
+    const size_t g = i * ng / n;
+    if (!top2) {
+      gscore[g] += ex[i];
+    } else if (ex[i] >= t1[g]) {
+      t2[g] = t1[g];
+      t1[g] = ex[i];
+    } else if (ex[i] > t2[g]) {
+      t2[g] = ex[i];
+    }
+  }
+  if (top2)
+    for (size_t g = 0; g < ng; ++g) gscore[g] = t1[g] + (t2[g] == -FLT_MAX ? 0.0f : t2[g]);
+  std::vector<bool> allowed(ng, !top_k_group.has_value());
+  if (top_k_group) {
+    const auto order = order_desc(gscore);
+    for (size_t j = 0; j < std::min(*top_k_group, ng); ++j) allowed[order[j]] = true;
+  }
+  std::vector<size_t> cand;
+  for (size_t i = 0; i < n; ++i)
+    if (allowed[i * ng / n]) cand.push_back(i);
+  std::stable_sort(cand.begin(), cand.end(), [&](size_t a, size_t b) { return ex[a] > ex[b]; });
+  const size_t k = std::min(top_k, cand.size());
+  float wsum = 0.0f;
+  for (size_t j = 0; j < k; ++j) wsum += ex[cand[j]];
+  std::vector<ExpertScore> out(k);
+  for (size_t j = 0; j < k; ++j) out[j] = {cand[j], wsum == 0.0f ? 0.0f : ex[cand[j]] / wsum};
+  return out;
+}
+
+inline std::vector<ExpertScore> route_group(const std::vector<float>& logits, const std::vector<float>& bias,
+                                            size_t n_groups, size_t top_k, std::optional<size_t> top_k_group) {
+  return route_groups(logits, bias, n_groups, top_k, top_k_group, false);
+}
+
+inline std::vector<ExpertScore> route_noaux_tc(const std::vector<float>& logits, const std::vector<float>& bias,
+                                               size_t n_groups, size_t top_k, std::optional<size_t> top_k_group) {
+  return route_groups(logits, bias, n_groups, top_k, top_k_group, true);
 }
 
 // ---- MoE experts on the GPU --------------------------------------------------------------------

@@ -52,7 +52,7 @@ EXPORTS = ("re_init", "re_last_error", "re_version", "re_row_bytes", "re_tiled_b
            "re_gguf_find_tensor", "re_gguf_tensor_data", "re_qmat_from_gguf", "re_moe_from_gguf",
            "re_quantize_q8_act", "re_quantize_q8_act_dev", "re_qmat_matmul_i8", "re_qmat_matmul_i8_dev",
            "re_attention_decode_dev", "re_qmat_gemv_plan", "re_qmat_matmul_noalloc_dev", "re_moe_set_shared",
-           "re_rope_table_dev")
+           "re_rope_table_dev", "re_moe_route_group_dev", "re_moe_layer_group_dev")
 GEMV_KERNELS = {0: "split", 1: "rows", 2: "tile", 3: "dense"}
 
 
@@ -106,6 +106,8 @@ def lib() -> C.CDLL:
         L.re_moe_route_dev.argtypes = [_vp, _sz, _sz, _sz, C.c_int, _vp, _vp, _vp]
         L.re_moe_forward_routed_dev.argtypes = [_vp, _vp, _sz, _sz, _vp, _vp, _vp, C.c_int, _vp]
         L.re_moe_layer_dev.argtypes = [_vp, _vp, _sz, _vp, _sz, C.c_int, _vp, C.c_int, _vp]
+        L.re_moe_route_group_dev.argtypes = [_vp, _sz, _sz, _sz, C.c_int, _vp, _sz, _sz, _sz, _vp, _vp, _vp]
+        L.re_moe_layer_group_dev.argtypes = [_vp, _vp, _sz, _vp, _sz, C.c_int, _vp, _sz, _sz, _sz, _vp, C.c_int, _vp]
         L.re_qmat_create_stacked.argtypes = [C.c_uint32, _vp, _sz, _sz, _sz, _sz, C.POINTER(_vp)]
         L.re_qmat_count.argtypes = [_vp]
         L.re_qmat_count.restype = _sz
@@ -372,7 +374,7 @@ def kv_append_dev(k, v, rows, kv_dim, kcache, vcache, max_seq, pos, stream=None)
                                   _stream_ptr(stream)))
 
 
-GATE_SOFTMAX, GATE_SIGMOID = 0, 1
+GATE_SOFTMAX, GATE_SIGMOID, GATE_GROUP, GATE_NOAUX_TC = 0, 1, 2, 3
 
 
 def moe_router_logits_dev(x, router_w, tokens, hidden, n_experts, logits, stream=None):
@@ -383,6 +385,14 @@ def moe_router_logits_dev(x, router_w, tokens, hidden, n_experts, logits, stream
 def moe_route_dev(logits, tokens, n_experts, top_k, gate, ids, weights, stream=None):
     _check(lib().re_moe_route_dev(_p(logits), tokens, n_experts, top_k, gate, _p(ids), _p(weights),
                                   _stream_ptr(stream)))
+
+
+def moe_route_group_dev(logits, tokens, n_experts, top_k, gate, bias, bias_len, n_groups, top_k_group, ids,
+                        weights, stream=None):
+    """route_group (GATE_GROUP) / route_noaux_tc (GATE_NOAUX_TC) of moe.rs:126-268 on the device;
+    bias: None or a device buffer of bias_len f32; top_k_group None or 0 = every group."""
+    _check(lib().re_moe_route_group_dev(_p(logits), tokens, n_experts, top_k, gate, _p(bias), bias_len if bias else 0,
+                                        n_groups, top_k_group or 0, _p(ids), _p(weights), _stream_ptr(stream)))
 
 
 def attention_work_bytes(rows, n_heads, head_dim, max_seq) -> int:
@@ -529,6 +539,14 @@ class MoeExperts:
         """Router logits, top-k routing and the expert FFN, all on the device (moe.rs:360-388)."""
         _check(lib().re_moe_layer_dev(self._h, _dev_ptr(x_dev), tokens, _dev_ptr(router_w_dev), top_k, gate,
                                       _dev_ptr(out_dev), mode, _stream_ptr(stream)))
+
+    def layer_group_dev(self, x_dev, tokens, router_w_dev, top_k, gate, bias_dev, bias_len, n_groups, top_k_group,
+                        out_dev, mode=MODE_BF16, stream=None) -> None:
+        """Router logits, bias-corrected group routing (GATE_GROUP / GATE_NOAUX_TC) and the expert
+        FFN on the device."""
+        _check(lib().re_moe_layer_group_dev(self._h, _dev_ptr(x_dev), tokens, _dev_ptr(router_w_dev), top_k, gate,
+                                            _p(bias_dev), bias_len if bias_dev else 0, n_groups, top_k_group or 0,
+                                            _dev_ptr(out_dev), mode, _stream_ptr(stream)))
 
     def close(self) -> None:
         if self._h:

@@ -156,6 +156,31 @@ static void test_unknown_type_is_an_error() {  // kernel.rs:2006, 2027 panic -> 
   CHECK(threw, "no EngineError for type 99");
 }
 
+static void test_group_routers_match_oracle() {  // moe.rs:675-720, then random logits vs the oracle
+  std::printf("group_routers_match_oracle\n");
+  const std::vector<float> l8 = {5.0f, 2.0f, -9.0f, -9.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+  CHECK(route_noaux_tc(l8, {}, 2, 1, 1)[0].id == 0, "noaux_tc picks the dominant pair");
+  const auto lite = route_group(l8, {}, 2, 1, 1);
+  CHECK(lite[0].id >= 4 && lite[0].id <= 7, "route_group picks the larger sum");
+  CHECK(route_noaux_tc({}, {}, 2, 1, 1).empty(), "empty input");
+  std::mt19937 rng(91);
+  std::normal_distribution<float> nd;
+  for (int trial = 0; trial < 50; ++trial) {
+    std::vector<float> logits(128), bias(100);
+    for (auto& v : logits) v = std::round(nd(rng) * 2.0f) / 2.0f;
+    for (auto& v : bias) v = nd(rng) * 0.25f;
+    for (int top2 = 0; top2 < 2; ++top2) {
+      const auto mine = top2 ? route_noaux_tc(logits, bias, 8, 8, 4) : route_group(logits, bias, 8, 8, 4);
+      uint32_t ids[8];
+      float w[8];
+      const size_t n = (top2 ? orc_route_noaux_tc : orc_route_group)(logits.data(), logits.size(), bias.data(),
+                                                                     bias.size(), 8, 8, 4, ids, w);
+      CHECK(n == mine.size(), "group route count");
+      for (size_t j = 0; j < n; ++j) CHECK(mine[j].id == ids[j] && mine[j].weight == w[j], "group route vs oracle");
+    }
+  }
+}
+
 static void test_router_matches_oracle() {  // moe.rs:631-662
   std::printf("router_top_k_matches_oracle\n");
   auto s = top_k({0.1f, 0.9f, 0.2f, 0.8f}, 2);
@@ -393,6 +418,7 @@ int main() {
     test_matmul_matches_rowwise_matvec();
     test_matvec_is_deterministic();
     test_every_type_against_oracle();
+    test_group_routers_match_oracle();
     test_router_matches_oracle();
     test_moe_layer_routes_to_best_expert();
     test_moe_layer_adds_shared_expert();

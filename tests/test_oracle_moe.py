@@ -8,6 +8,7 @@ f64 evaluation of the whole layer pins the batched path on random experts.
 import math
 
 import numpy as np
+import pytest
 
 import oracle as O
 from blockpack import pack_q8_0
@@ -165,3 +166,103 @@ def test_moe_ffn_matches_f64_brute_force():
             want += float(w[t * k + j]) * (D[e] @ a)
         scale = np.abs(want).max() + 1e-3
         assert np.all(np.abs(out[t * hidden:(t + 1) * hidden] - want) <= 1e-4 * scale), t
+
+
+# ---- bias-corrected group routers (moe.rs:126-268) ----------------------------------------------
+EPS = 1e-5
+
+
+def test_route_group_restricts_to_best_group():           # moe.rs:675-686
+    ids, w = O.route_group([0.0, 0.0, 0.0, 5.0, 4.0, 3.0], None, 2, 2, 1)
+    assert len(ids) == 2 and all(3 <= i <= 5 for i in ids)
+    assert abs(w.sum() - 1.0) < EPS
+
+
+def test_route_noaux_tc_uses_top2_group_score_not_group_sum():   # moe.rs:688-701
+    logits = [5.0, 2.0, -9.0, -9.0, 0.0, 0.0, 0.0, 0.0]
+    ids, w = O.route_noaux_tc(logits, None, 2, 1, 1)
+    assert ids[0] == 0 and abs(w[0] - 1.0) < EPS
+    ids, _ = O.route_group(logits, None, 2, 1, 1)
+    assert 4 <= ids[0] <= 7
+
+
+def test_route_noaux_tc_renormalizes_top_k():             # moe.rs:703-712
+    ids, w = O.route_noaux_tc([5.0, 2.0, -9.0, -9.0, 0.0, 0.0, 0.0, 0.0], None, 2, 2, 1)
+    assert list(ids) == [0, 1] and abs(w.sum() - 1.0) < EPS
+
+
+def test_route_noaux_tc_empty_input():                    # moe.rs:714-717
+    assert O.route_noaux_tc([], None, 2, 1, 1)[0].size == 0
+    assert O.route_group([], None, 2, 1, 1)[0].size == 0
+
+
+@pytest.mark.parametrize("router", [O.route_group, O.route_noaux_tc])
+@pytest.mark.parametrize("n,ng,k", [(128, 8, 8), (64, 1, 6), (256, 8, 8), (10, 3, 4)])
+def test_every_group_eligible_is_top_k_sigmoid(router, n, ng, k):
+    # top_k_group None (and = ng) keeps every expert: the selection and the weights are those of
+    # top_k_sigmoid (moe.rs:97-117), bit for bit, ties included (quantised logits)
+    rng = np.random.default_rng(500 + n + ng)
+    logits = (np.round(rng.standard_normal(n) * 4) / 4).astype(np.float32)
+    want = O.top_k_sigmoid(logits, k)
+    for tkg in (None, ng):
+        got = router(logits, None, ng, k, tkg)
+        assert np.array_equal(got[0], want[0]) and np.array_equal(got[1], want[1]), tkg
+
+
+@pytest.mark.parametrize("router", [O.route_group, O.route_noaux_tc])
+def test_bias_is_added_to_the_logits(router):
+    # sigmoid(logit + bias[i]): passing the bias equals passing logits + bias (same f32 sum);
+    # entries past the bias's length count as 0 (bias.get(i).unwrap_or(0.0))
+    rng = np.random.default_rng(510)
+    logits = rng.standard_normal(128).astype(np.float32)
+    bias = (rng.standard_normal(128) * 0.5).astype(np.float32)
+    a = router(logits, bias, 8, 8, 4)
+    b = router((logits + bias).astype(np.float32), None, 8, 8, 4)
+    assert np.array_equal(a[0], b[0]) and np.array_equal(a[1], b[1])
+    short = bias[:40]
+    a = router(logits, short, 8, 8, 4)
+    b = router(logits, np.concatenate([short, np.zeros(88, np.float32)]), 8, 8, 4)
+    assert np.array_equal(a[0], b[0]) and np.array_equal(a[1], b[1])
+
+
+def brute_force_route(logits, n_groups, k, tkg, top2):
+    """Independent restatement by sets and numpy's stable argsort: group i * ng // n; group score
+    = sum (route_group) or sum of the two best (route_noaux_tc) of the oracle's sigmoid scores;
+    the tkg best groups (ties to the lower group) are eligible; the k best eligible experts (ties
+    to the lower index)."""
+    n = len(logits)
+    sc = np.array([O.sigmoid(float(x)) for x in logits], np.float32)
+    ng = max(1, min(n_groups, n))
+    grp = np.arange(n) * ng // n
+    gs = []
+    for g in range(ng):
+        v = sc[grp == g]
+        if top2:
+            v = np.sort(v)[::-1][:2]
+        acc = np.float32(0.0)
+        for x in (v if top2 else sc[grp == g]):
+            acc = np.float32(acc + x)
+        gs.append(acc)
+    gs = np.array(gs, np.float32)
+    order = np.argsort(-gs, kind="stable")
+    allowed = set(order[:min(tkg, ng)].tolist())
+    cand = np.array([i for i in range(n) if grp[i] in allowed])
+    pick = cand[np.argsort(-sc[cand], kind="stable")][:min(k, len(cand))]
+    return pick
+
+
+@pytest.mark.parametrize("top2", [False, True])
+@pytest.mark.parametrize("n,ng,k,tkg", [(128, 8, 8, 4), (256, 8, 8, 4), (10, 3, 4, 1), (96, 12, 6, 3),
+                                        (8, 4, 4, 1)])
+def test_group_routing_matches_brute_force(top2, n, ng, k, tkg):
+    rng = np.random.default_rng(520 + n + ng + 7 * top2)
+    for trial in range(20):
+        # quantised logits: equal scores (ties) inside and across groups
+        logits = (np.round(rng.standard_normal(n) * 2) / 2).astype(np.float32)
+        ids, w = (O.route_noaux_tc if top2 else O.route_group)(logits, None, ng, k, tkg)
+        want = brute_force_route(logits, ng, k, tkg, top2)
+        assert list(ids) == list(want), (trial, list(ids), list(want))
+        assert abs(float(w.sum()) - 1.0) < EPS
+    # fewer eligible experts than k: (8 experts, 4 groups of 2, one group) -> 2 results
+    if (n, ng, tkg) == (8, 4, 1):
+        assert len(want) == 2
