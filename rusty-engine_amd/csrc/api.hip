@@ -244,6 +244,15 @@ bool moe_qmma_path(const re_moe* e, const float* d_x, size_t tokens, int mode) {
          env_size("REHIP_MOE_QMMA", 1) != 0;
 }
 
+// f32 mode with one gate/up type and more rows than the expert GEMV serves: the same register-
+// decoded grouped GEMMs with split bf16 operands (three MFMAs per product, each operand held to
+// 2^-16 relative, far inside the f32 bar of 2^-10 * sum|w x|): at 512 tokens on the
+// Qwen3-30B-A3B shape they replace the LDS-staged f32 MFMA GEMMs. REHIP_MOE_SPLIT=0 turns it off.
+bool moe_split_path(const re_moe* e, const float* d_x, size_t tokens, int mode, bool few) {
+  return mode == RE_MODE_F32 && !few && tokens > 1 && e->gg.type == e->gu.type && e->hidden % 8 == 0 &&
+         e->inter % 8 == 0 && aligned16(d_x) && env_size("REHIP_MOE_SPLIT", 1) != 0;
+}
+
 // Gathered rows per grouped-GEMM task: 32 (one token tile) while the experts get few rows each,
 // else 64; REHIP_MOE_CHUNK = 32 / 64 overrides for the register-decoded GEMMs.
 int moe_qmma_chunk(bool qmma, bool few) {
@@ -1169,14 +1178,17 @@ int moe_qmma_down_rows(int chunk) { return moe_qmma_down_pair(chunk) == kQmmaTwo
 // their device counts (nullptr: the launch count is exact) come from the host or device planner
 hipError_t moe_qmma_ffn(re_moe* e, size_t tokens, size_t pairs, int chunk, const int* xrow, const GemmTask* t_gu,
                         const int* n_gu_dev, int n_gu, const GemmTask* t_d, const int* n_d_dev, int n_d,
-                        hipStream_t s) {
+                        hipStream_t s, bool split = false) {
+  // split: e->sxb holds x's hi then lo halves, and h goes to e->sh as hi then lo (the f32 size)
   GemmArgs a{};
   a.W = e->d_gate;
   a.W2 = e->d_up;
   a.w_bytes = (uint32_t)(e->gg.bytes * e->n_experts);
   a.w_stride = e->gg.bytes;
   a.X = e->sxb.p;
-  a.x_bytes = (uint32_t)(tokens * e->hidden * 2);
+  a.x_bytes = (uint32_t)(tokens * e->hidden * 2 * (split ? 2 : 1));
+  a.x_lo = (uint32_t)(tokens * e->hidden * 2);
+  a.y_lo = pairs * e->inter;
   a.xrow = xrow;
   a.Y = (float*)e->sh.p;
   a.m = (int)e->inter;
@@ -1186,14 +1198,15 @@ hipError_t moe_qmma_ffn(re_moe* e, size_t tokens, size_t pairs, int chunk, const
   a.ldy = (int)e->inter;
   a.tasks = t_gu;
   a.ntasks = n_gu_dev;
-  hipError_t err = launch_moe_qmma(e->gg.type, kQmmaGateUp, chunk, a, n_gu, s);
+  hipError_t err = launch_moe_qmma(e->gg.type, kQmmaGateUp, chunk, a, n_gu, s, split);
   if (err != hipSuccess) return err;
   GemmArgs d{};
   d.W = e->d_down;
   d.w_bytes = (uint32_t)(e->gd.bytes * e->n_experts);
   d.w_stride = e->gd.bytes;
   d.X = e->sh.p;
-  d.x_bytes = (uint32_t)(pairs * e->inter * 2);
+  d.x_bytes = (uint32_t)(pairs * e->inter * 2 * (split ? 2 : 1));
+  d.x_lo = (uint32_t)(pairs * e->inter * 2);
   d.xrow = nullptr;
   d.Y = (float*)e->syp.p;
   d.m = (int)e->hidden;
@@ -1203,7 +1216,7 @@ hipError_t moe_qmma_ffn(re_moe* e, size_t tokens, size_t pairs, int chunk, const
   d.ldy = (int)e->hidden;
   d.tasks = t_d;
   d.ntasks = n_d_dev;
-  return launch_moe_qmma(e->gd.type, moe_qmma_down_pair(chunk), chunk, d, n_d, s);
+  return launch_moe_qmma(e->gd.type, moe_qmma_down_pair(chunk), chunk, d, n_d, s, split);
 }
 
 }  // namespace
@@ -1271,13 +1284,14 @@ int re_moe_forward_routed_dev(re_moe* e, const float* d_x, size_t tokens, size_t
   // register-decoded grouped GEMMs take 32-row chunks there (one token tile) and 64 beyond
   const bool few = pairs <= 2 * e->n_experts;
   const bool qmma = moe_qmma_path(e, d_x, tokens, mode);
-  const bool gemv = !qmma && few && moe_gemv_fits(e);
+  const bool split = !qmma && moe_split_path(e, d_x, tokens, mode, few);
+  const bool gemv = !qmma && !split && few && moe_gemv_fits(e);
   MoePlanShape sh{};
   sh.pairs = (int)pairs;
   sh.k = (int)top_k;
   sh.n_experts = (int)e->n_experts;
   sh.gemv = gemv;
-  sh.chunk = gemv ? (tokens == 1 ? 1 : kMoeGemvBatch) : moe_qmma_chunk(qmma, few);
+  sh.chunk = gemv ? (tokens == 1 ? 1 : kMoeGemvBatch) : moe_qmma_chunk(qmma || split, few);
   if (gemv) {
     const int rd = moe_gemv_rows_down();
     const int rgu = tokens == 1 && e->gg.type == e->gu.type ? moe_gemv_rows_gu1() : kMoeGemvRows;
@@ -1288,7 +1302,7 @@ int re_moe_forward_routed_dev(re_moe* e, const float* d_x, size_t tokens, size_t
   } else {
     sh.rows_gu = sh.rows_d = kMoeTile;
     sh.tiles_gu = (int)((e->inter + kMoeTile - 1) / kMoeTile);
-    const int rows_d = qmma ? moe_qmma_down_rows(sh.chunk) : kMoeTile;
+    const int rows_d = qmma || split ? moe_qmma_down_rows(sh.chunk) : kMoeTile;
     sh.tiles_d = (int)((e->hidden + rows_d - 1) / rows_d);
   }
   const int max_chunks = (int)((pairs + sh.chunk - 1) / sh.chunk + std::min(pairs, e->n_experts));
@@ -1303,9 +1317,9 @@ int re_moe_forward_routed_dev(re_moe* e, const float* d_x, size_t tokens, size_t
   if (!dual && ((rc = e->sg.ensure(act)) || (rc = e->su.ensure(act)))) return rc;
   // the bf16 copy of X (grouped GEMMs in bf16 mode) is made by the planning launch
   const bool xb = !gemv && moe_bf16_acts(e, d_x, mode);
-  if (xb && (rc = e->sxb.ensure(tokens * e->hidden * 2))) return rc;
+  if ((xb || split) && (rc = e->sxb.ensure(tokens * e->hidden * 2 * (split ? 2 : 1)))) return rc;
   int* dm = (int*)e->dmeta.p;
-  HIP_TRY(launch_moe_plan(d_ids, sh, dm, d_x, xb ? e->sxb.p : nullptr, tokens * e->hidden, s));
+  HIP_TRY(launch_moe_plan(d_ids, sh, dm, d_x, xb || split ? e->sxb.p : nullptr, tokens * e->hidden, s, split));
   const int* xrow = dm;
   const int* pos = dm + pairs;
   const int* ntasks = dm + 2 * pairs;
@@ -1355,10 +1369,10 @@ int re_moe_forward_routed_dev(re_moe* e, const float* d_x, size_t tokens, size_t
     d.KB = (int)e->gd.kb;
     d.ldy = (int)e->hidden;
     HIP_TRY(launch_moe_gemv(e->gd.type, false, d, sh.max_d, s));
-  } else if (qmma) {
+  } else if (qmma || split) {
     const GemmTask* tg = (const GemmTask*)tasks;
     HIP_TRY(moe_qmma_ffn(e, tokens, pairs, sh.chunk, xrow, tg, ntasks, sh.max_gu, tg + sh.max_gu, ntasks + 1,
-                         sh.max_d, s));
+                         sh.max_d, s, split));
   } else {
     const GemmTask* tg = (const GemmTask*)tasks;
     GemmArgs a{};
@@ -1544,8 +1558,9 @@ int re_moe_forward_dev(re_moe* e, const float* d_x, size_t tokens, size_t top_k,
   // grouped GEMMs (bf16 mode) take chunks of 32 rows while the rows per expert are few, else 64.
   const bool few = pairs <= (size_t)kMoeGemvBatch * touched;
   const bool qmma = moe_qmma_path(e, d_x, tokens, mode);
-  const bool gemv = !qmma && few && moe_gemv_fits(e);
-  const int chunk = moe_qmma_chunk(qmma, few);
+  const bool split = !qmma && moe_split_path(e, d_x, tokens, mode, few);
+  const bool gemv = !qmma && !split && few && moe_gemv_fits(e);
+  const int chunk = moe_qmma_chunk(qmma || split, few);
   int max_rows = 0;
   for (size_t x = 0; x < e->n_experts; ++x) max_rows = std::max(max_rows, std::min(count[x], kMoeGemvBatch));
   // 16-row gate/up tasks exist for single-row tasks only (a repeated expert id gives 2+ rows)
@@ -1561,7 +1576,7 @@ int re_moe_forward_dev(re_moe* e, const float* d_x, size_t tokens, size_t top_k,
           v_d.push_back({(int)x, (int)row, start[x] + r, np});
       }
   } else {
-    const int rows_d = qmma ? moe_qmma_down_rows(chunk) : kMoeTile;
+    const int rows_d = qmma || split ? moe_qmma_down_rows(chunk) : kMoeTile;
     const int mt_gu = (int)((e->inter + kMoeTile - 1) / kMoeTile), mt_d = (int)((e->hidden + rows_d - 1) / rows_d);
     for (size_t x = 0; x < e->n_experts; ++x) {
       for (int r = 0; r < count[x]; r += chunk) {
@@ -1651,11 +1666,12 @@ int re_moe_forward_dev(re_moe* e, const float* d_x, size_t tokens, size_t top_k,
     d.KB = (int)e->gd.kb;
     d.ldy = (int)e->hidden;
     HIP_TRY(launch_moe_gemv(e->gd.type, false, d, (int)n_d, s));
-  } else if (qmma) {
-    if ((rc = e->sxb.ensure(tokens * e->hidden * 2))) return rc;
-    HIP_TRY(launch_x_to_bf16(d_x, e->sxb.p, tokens * e->hidden, s));
+  } else if (qmma || split) {
+    if ((rc = e->sxb.ensure(tokens * e->hidden * 2 * (split ? 2 : 1)))) return rc;
+    if (split) HIP_TRY(launch_x_to_bf16_split(d_x, e->sxb.p, tokens * e->hidden, s));
+    else HIP_TRY(launch_x_to_bf16(d_x, e->sxb.p, tokens * e->hidden, s));
     HIP_TRY(moe_qmma_ffn(e, tokens, pairs, chunk, (const int*)dm, (const GemmTask*)(dm + off_tgu), nullptr, (int)n_gu,
-                         (const GemmTask*)(dm + off_td), nullptr, (int)n_d, s));
+                         (const GemmTask*)(dm + off_td), nullptr, (int)n_d, s, split));
   } else {
     GemmArgs a{};
     a.X = d_x;

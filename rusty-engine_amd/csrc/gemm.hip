@@ -578,6 +578,23 @@ __global__ __launch_bounds__(256) void x_to_bf16_kernel(const float4* __restrict
   }
 }
 
+// the split form: hi = bf16(x) at xb[i], lo = bf16(x - hi) at xb[n8 + i] (8 elements per unit)
+__global__ __launch_bounds__(256) void x_to_bf16_split_kernel(const float4* __restrict__ x, bf16x8_t* __restrict__ xb,
+                                                              size_t n8) {
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n8; i += (size_t)gridDim.x * 256) {
+    const float4 a = x[2 * i], b = x[2 * i + 1];
+    const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    bf16x8_t hi, lo;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      hi[j] = (__bf16)v[j];
+      lo[j] = (__bf16)(v[j] - (float)hi[j]);
+    }
+    xb[i] = hi;
+    xb[n8 + i] = lo;
+  }
+}
+
 template <int T, bool F32, int BM, int BN, int WM, int WN, int KG, bool GROUPED>
 static hipError_t launch_shape(const GemmArgs& a, int ntasks, hipStream_t s) {
   constexpr int NT = WM * WN * 64 * KG;
@@ -712,6 +729,15 @@ hipError_t launch_x_to_bf16(const float* x, void* xb, size_t n, hipStream_t s) {
   const size_t n8 = n / 8;
   const unsigned grid = (unsigned)std::min<size_t>((n8 + 255) / 256, 4096);
   hipLaunchKernelGGL(x_to_bf16_kernel, dim3(grid), dim3(256), 0, s, (const float4*)x, (bf16x8_t*)xb, n8);
+  return hipGetLastError();
+}
+
+hipError_t launch_x_to_bf16_split(const float* x, void* xb, size_t n, hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  if (n % 8) return hipErrorInvalidValue;
+  const size_t n8 = n / 8;
+  const unsigned grid = (unsigned)std::min<size_t>((n8 + 255) / 256, 4096);
+  hipLaunchKernelGGL(x_to_bf16_split_kernel, dim3(grid), dim3(256), 0, s, (const float4*)x, (bf16x8_t*)xb, n8);
   return hipGetLastError();
 }
 

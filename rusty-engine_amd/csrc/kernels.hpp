@@ -125,6 +125,11 @@ struct GemmArgs {
   const GemmTask* tasks;   // grouped launch: one task per workgroup (nullptr = dense grid)
   const int* xrow;         // grouped: X row of gathered row p (nullptr = p itself)
   const int* ntasks;       // grouped: nullptr, or the task count on the device (larger grids exit early)
+  // split bf16 operands (register-decoded expert GEMMs in f32 mode): X holds the bf16 rounding of
+  // each activation (hi) and, x_lo bytes further, the bf16 rounding of what hi leaves (lo); a
+  // gate/up pair writes h's hi to Y and its lo y_lo elements further
+  uint32_t x_lo;
+  size_t y_lo;
 };
 
 struct GemmPlan {
@@ -142,6 +147,9 @@ hipError_t launch_gemm(uint32_t type, int mode, const GemmArgs& a, int ntasks, G
                        hipStream_t s);
 // xb[i] = bf16(x[i]), round to nearest even; n a multiple of 8, both buffers 16-byte aligned
 hipError_t launch_x_to_bf16(const float* x, void* xb, size_t n, hipStream_t s);
+// split form: xb[i] = hi = bf16(x[i]) and xb[n + i] = lo = bf16(x[i] - hi), both rounded to nearest
+// even, so hi + lo holds x to 2^-16 relative
+hipError_t launch_x_to_bf16_split(const float* x, void* xb, size_t n, hipStream_t s);
 
 // Grouped expert GEMV (few gathered rows per expert): one task per workgroup
 struct MoeGemvTask {
@@ -208,8 +216,12 @@ hipError_t launch_moe_gemv(uint32_t type, bool dual, const MoeGemvArgs& a, int n
 //                  as bf16;
 //   kQmmaTwoTiles  128 rows (tiles 2 mtile, 2 mtile + 1) of W, Y receives f32.
 // Uses W, W2, w_bytes, w_stride, X, x_bytes, xrow, Y, m, K, KB, ldy, tasks, ntasks of GemmArgs.
+// split (f32 mode): every product is hi(x) hi(w) + hi(x) lo(w) + lo(x) hi(w), three bf16 MFMAs
+// accumulated in f32 (each operand split as launch_x_to_bf16_split does; x_lo / y_lo locate
+// the lo halves, and a gate/up pair writes h as hi and lo).
 constexpr int kQmmaOneTile = 0, kQmmaGateUp = 1, kQmmaTwoTiles = 2;
-hipError_t launch_moe_qmma(uint32_t type, int pair, int max_rows, const GemmArgs& a, int ntasks, hipStream_t s);
+hipError_t launch_moe_qmma(uint32_t type, int pair, int max_rows, const GemmArgs& a, int ntasks, hipStream_t s,
+                           bool split = false);
 
 // Dense transformer steps on device buffers (layer.hip)
 hipError_t launch_rmsnorm(const float* x, const float* w, int rows, int d, float eps, float* out, hipStream_t s);
@@ -265,9 +277,10 @@ struct MoePlanShape {
   int max_gu, max_d;            // capacity of the task lists
 };
 size_t moe_meta_bytes(const MoePlanShape& sh);
-// x / xb / n: also round the n floats of x to bf16 into xb (n % 8 == 0), or xb = nullptr
+// x / xb / n: also round the n floats of x to bf16 into xb (n % 8 == 0), or xb = nullptr;
+// split: xb also receives the lo halves at xb + n (as launch_x_to_bf16_split)
 hipError_t launch_moe_plan(const int* ids, const MoePlanShape& sh, void* meta, const float* x, void* xb, size_t n,
-                           hipStream_t s);
+                           hipStream_t s, bool split = false);
 hipError_t launch_swiglu(const float* g, const float* u, float* h, size_t n, hipStream_t s);
 hipError_t launch_swiglu_bf16(const float* g, const float* u, void* h, size_t n, hipStream_t s);
 hipError_t launch_combine(const float* yp, const int* pos, const float* w, float* out, int tokens,

@@ -433,17 +433,25 @@ __device__ __forceinline__ void moe_plan_body(const int* __restrict__ ids, const
 __global__ __launch_bounds__(64 * kPlanWaves) void moe_plan_convert_kernel(const int* __restrict__ ids,
                                                                            MoePlanShape sh, int* __restrict__ meta,
                                                                            const float4* __restrict__ x,
-                                                                           bf16x8_t* __restrict__ xb, size_t n8) {
+                                                                           bf16x8_t* __restrict__ xb, size_t n8,
+                                                                           int split) {
   if (blockIdx.x == 0) {
     moe_plan_body(ids, sh, meta);
     return;
   }
   for (size_t i = (size_t)(blockIdx.x - 1) * 1024 + threadIdx.x; i < n8; i += (size_t)(gridDim.x - 1) * 1024) {
     const float4 a = x[2 * i], b = x[2 * i + 1];
+    const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
     bf16x8_t o;
-    o[0] = (__bf16)a.x; o[1] = (__bf16)a.y; o[2] = (__bf16)a.z; o[3] = (__bf16)a.w;
-    o[4] = (__bf16)b.x; o[5] = (__bf16)b.y; o[6] = (__bf16)b.z; o[7] = (__bf16)b.w;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[j] = (__bf16)v[j];
     xb[i] = o;
+    if (split) {                          // the lo halves, as x_to_bf16_split_kernel
+      bf16x8_t l;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) l[j] = (__bf16)(v[j] - (float)o[j]);
+      xb[n8 + i] = l;
+    }
   }
 }
 
@@ -555,12 +563,12 @@ hipError_t launch_moe_router_logits(const float* x, const float* router_w, int t
 }
 
 hipError_t launch_moe_plan(const int* ids, const MoePlanShape& sh, void* meta, const float* x, void* xb, size_t n,
-                           hipStream_t s) {
+                           hipStream_t s, bool split) {
   if (xb && n % 8) return hipErrorInvalidValue;
   const size_t n8 = xb ? n / 8 : 0;
   const unsigned conv = (unsigned)std::min<size_t>((n8 + 1023) / 1024, 255);
   hipLaunchKernelGGL(moe_plan_convert_kernel, dim3(1 + conv), dim3(64 * kPlanWaves), 0, s, ids, sh, (int*)meta,
-                     (const float4*)x, (bf16x8_t*)xb, n8);
+                     (const float4*)x, (bf16x8_t*)xb, n8, split ? 1 : 0);
   return hipGetLastError();
 }
 

@@ -40,10 +40,9 @@ __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
 }
 
 // The 16 values of a run (scale * q - offset, each exact in f32 as in the reference's
-// dequantizer) rounded to bf16 pairs: lo = elements 0-7, hi = elements 8-15.
+// dequantizer) in f32.
 template <int T>
-__device__ __forceinline__ void run_bf16(const Run& r, uint32_t lo[4], uint32_t hi[4]) {
-  float v[16];
+__device__ __forceinline__ void run_f32(const Run& r, float v[16]) {
   if constexpr (kNibble<T>) {
     // 4-bit quants as fp8 e4m3 bytes are exactly q * 2^-9 (two per instruction)
     const float sc = r.scale * 512.0f;
@@ -60,10 +59,34 @@ __device__ __forceinline__ void run_bf16(const Run& r, uint32_t lo[4], uint32_t 
 #pragma unroll
     for (int i = 0; i < 16; ++i) v[i] = run_value(r, i);
   }
+}
+
+// The run rounded to bf16 pairs: lo = elements 0-7, hi = elements 8-15.
+template <int T>
+__device__ __forceinline__ void run_bf16(const Run& r, uint32_t lo[4], uint32_t hi[4]) {
+  float v[16];
+  run_f32<T>(r, v);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     lo[i] = pack_bf16(v[2 * i], v[2 * i + 1]);
     hi[i] = pack_bf16(v[8 + 2 * i], v[8 + 2 * i + 1]);
+  }
+}
+
+// Split form (f32 mode): the bf16 rounding of each value (lo / hi as run_bf16) and the bf16
+// rounding of what that leaves (rlo / rhi), so each value is held to 2^-16 relative.
+template <int T>
+__device__ __forceinline__ void run_bf16_split(const Run& r, uint32_t lo[4], uint32_t hi[4], uint32_t rlo[4],
+                                               uint32_t rhi[4]) {
+  float v[16];
+  run_f32<T>(r, v);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    lo[i] = pack_bf16(v[2 * i], v[2 * i + 1]);
+    hi[i] = pack_bf16(v[8 + 2 * i], v[8 + 2 * i + 1]);
+    const bf16x2_t l = __builtin_bit_cast(bf16x2_t, lo[i]), h = __builtin_bit_cast(bf16x2_t, hi[i]);
+    rlo[i] = pack_bf16(v[2 * i] - (float)l[0], v[2 * i + 1] - (float)l[1]);
+    rhi[i] = pack_bf16(v[8 + 2 * i] - (float)h[0], v[8 + 2 * i + 1] - (float)h[1]);
   }
 }
 
@@ -100,6 +123,22 @@ __device__ __forceinline__ void decode_frags(const typename Blk<T>::CR& raw, int
   halves_to_frags(lo, hi, f.b0, f.b1);
   f.ea = a.e;
   f.eb = b.e;
+}
+
+// both parts of the split form: f (the bf16 roundings) and fr (the remainders)
+template <int T>
+__device__ __forceinline__ void decode_frags_split(const typename Blk<T>::CR& raw, int cc, Frags& f, Frags& fr) {
+  Run a, b;
+  Blk<T>::decode_chunk(raw, cc, a, b);
+  uint32_t lo[4], hi[4], rlo[4], rhi[4];
+  run_bf16_split<T>(a, lo, hi, rlo, rhi);
+  halves_to_frags(lo, hi, f.a0, f.a1);
+  halves_to_frags(rlo, rhi, fr.a0, fr.a1);
+  run_bf16_split<T>(b, lo, hi, rlo, rhi);
+  halves_to_frags(lo, hi, f.b0, f.b1);
+  halves_to_frags(rlo, rhi, fr.b0, fr.b1);
+  f.ea = fr.ea = a.e;
+  f.eb = fr.eb = b.e;
 }
 
 // Half tile (32 weight rows per wave): lanes 0-31 decode run a of rows 0-31, lanes 32-63 run b of
@@ -226,11 +265,14 @@ __device__ __forceinline__ bf16x8_t ld_x(__amdgpu_buffer_rsrc_t r, uint32_t off)
 // H (staged activations only, one K wave): two waves share the task, each taking 32 of the
 // tile's rows (half = wave), and one staging of the activation rows in LDS, each wave copying
 // half of every stage.
+// SP (f32 mode): split operands, three MFMAs per product (the activations' and the weights' bf16
+// roundings and remainders: hi hi + hi lo + lo hi), activations read from L2.
 constexpr int kOneTile = 0, kGateUp = 1, kTwoTiles = 2;
-template <int T, int PAIR, int NT, int KS, bool XL, bool H>
+template <int T, int PAIR, int NT, int KS, bool XL, bool H, bool SP>
 __device__ __forceinline__ void qmma_task(const GemmArgs& p, const GemmTask& t, uint8_t* xs) {
   using B = Blk<T>;
   static_assert(!H || (XL && KS == 1 && PAIR != kTwoTiles), "half tiles: staged activations, one K wave, one tile");
+  static_assert(!SP || (!XL && !H), "split operands: activations from L2, whole tiles");
   constexpr int NCH = B::NCH;                       // 32-element chunks per block
   constexpr int RG = H ? 1 : 2;                     // 32-row groups per weight set
   const int lane = threadIdx.x & 63;
@@ -296,7 +338,7 @@ __device__ __forceinline__ void qmma_task(const GemmArgs& p, const GemmTask& t, 
     }
   };
   // A operands of chunk c: runs a and b of every token tile
-  struct XOps { bf16x8_t a[NT], b[NT]; };
+  struct XOps { bf16x8_t a[NT], b[NT], al[SP ? NT : 1], bl[SP ? NT : 1]; };
   // (runs at or past K, the padding of rows stored as whole blocks, read zeros: K % 16 == 0, so a
   // run is wholly inside or outside)
   auto load_x = [&](int c, int ea, int eb, XOps& x) {
@@ -305,8 +347,14 @@ __device__ __forceinline__ void qmma_task(const GemmArgs& p, const GemmTask& t, 
     const bool in_a = c < nch && ka < p.K, in_b = c < nch && kbe < p.K;
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
-      x.a[j] = ld_x(xr, j < nt && in_a ? xoff[j] + (uint32_t)ka * 2u : kQOob);
-      x.b[j] = ld_x(xr, j < nt && in_b ? xoff[j] + (uint32_t)kbe * 2u : kQOob);
+      const uint32_t oa = j < nt && in_a ? xoff[j] + (uint32_t)ka * 2u : kQOob;
+      const uint32_t ob = j < nt && in_b ? xoff[j] + (uint32_t)kbe * 2u : kQOob;
+      x.a[j] = ld_x(xr, oa);
+      x.b[j] = ld_x(xr, ob);
+      if constexpr (SP) {
+        x.al[j] = ld_x(xr, oa == kQOob ? kQOob : oa + p.x_lo);
+        x.bl[j] = ld_x(xr, ob == kQOob ? kQOob : ob + p.x_lo);
+      }
     }
   };
   // run element offsets of chunk cc (the Blk<T>::dec layouts; the same for every row)
@@ -334,6 +382,20 @@ __device__ __forceinline__ void qmma_task(const GemmArgs& p, const GemmTask& t, 
       if constexpr (!H) a[RG - 1][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x.b[j], f.b1, a[RG - 1][j], 0, 0, 0);
     }
   };
+  // split operands: the cross terms x_hi w_lo and x_lo w_hi after the x_hi w_hi products
+  auto mma_rest = [&](const XOps& x, const Frags& f, const Frags& fr, f32x16_t (&a)[RG][NT]) {
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      a[0][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x.a[j], fr.a0, a[0][j], 0, 0, 0);
+      a[RG - 1][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x.a[j], fr.a1, a[RG - 1][j], 0, 0, 0);
+      a[0][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x.al[j], f.a0, a[0][j], 0, 0, 0);
+      a[RG - 1][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x.al[j], f.a1, a[RG - 1][j], 0, 0, 0);
+      a[0][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x.b[j], fr.b0, a[0][j], 0, 0, 0);
+      a[RG - 1][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x.b[j], fr.b1, a[RG - 1][j], 0, 0, 0);
+      a[0][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x.bl[j], f.b0, a[0][j], 0, 0, 0);
+      a[RG - 1][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x.bl[j], f.b1, a[RG - 1][j], 0, 0, 0);
+    }
+  };
   auto decode = [&](const typename B::CR& raw, int cc, Frags& f) {
     if constexpr (H) decode_frags_half<T>(raw, cc, f);
     else decode_frags<T>(raw, cc, f);
@@ -346,13 +408,26 @@ __device__ __forceinline__ void qmma_task(const GemmArgs& p, const GemmTask& t, 
     load_x(c, ea, eb, x);
   };
   auto step = [&](int c, const typename B::CR& r, const typename B::CR& q, const XOps& x) {
-    Frags f;
-    decode(with_head<T>(r, hc), c % NCH, f);
-    mma(x, f, acc);
-    if constexpr (DUAL) {
-      Frags f2;
-      decode(with_head<T>(q, hc2), c % NCH, f2);
-      mma(x, f2, acc2);
+    if constexpr (SP) {
+      Frags f, fr;
+      decode_frags_split<T>(with_head<T>(r, hc), c % NCH, f, fr);
+      mma(x, f, acc);
+      mma_rest(x, f, fr, acc);
+      if constexpr (DUAL) {
+        Frags f2, fr2;
+        decode_frags_split<T>(with_head<T>(q, hc2), c % NCH, f2, fr2);
+        mma(x, f2, acc2);
+        mma_rest(x, f2, fr2, acc2);
+      }
+    } else {
+      Frags f;
+      decode(with_head<T>(r, hc), c % NCH, f);
+      mma(x, f, acc);
+      if constexpr (DUAL) {
+        Frags f2;
+        decode(with_head<T>(q, hc2), c % NCH, f2);
+        mma(x, f2, acc2);
+      }
     }
   };
   // U chunks per iteration, a whole number of blocks, unrolled so that every chunk's position in
@@ -527,7 +602,10 @@ __device__ __forceinline__ void qmma_task(const GemmArgs& p, const GemmTask& t, 
         if (i >= rn) continue;
         const size_t o = (size_t)(t.r0 + i) * (size_t)p.ldy + (size_t)row;
         if constexpr (PAIR == kGateUp) {
-          reinterpret_cast<__bf16*>(p.Y)[o] = (__bf16)silu_mul(acc[g][j][r], acc2[g][j][r]);
+          const float hv = silu_mul(acc[g][j][r], acc2[g][j][r]);
+          const __bf16 hh = (__bf16)hv;
+          reinterpret_cast<__bf16*>(p.Y)[o] = hh;
+          if constexpr (SP) reinterpret_cast<__bf16*>(p.Y)[o + p.y_lo] = (__bf16)(hv - (float)hh);
         } else if constexpr (PAIR == kTwoTiles) {
           p.Y[o] = g < 2 ? acc[g & 1][j][r] : acc2[g & 1][j][r];
         } else {
@@ -541,7 +619,7 @@ __device__ __forceinline__ void qmma_task(const GemmArgs& p, const GemmTask& t, 
 // A task of at most 32 rows runs the one-tile body (no MFMAs on an empty second token tile).
 // XL: activations staged in LDS (two stage buffers per wave).
 // H: two waves per task (32 weight rows each) sharing three stage buffers.
-template <int T, int PAIR, int NT, int KS, bool XL, bool H>
+template <int T, int PAIR, int NT, int KS, bool XL, bool H, bool SP = false>
 __global__ __launch_bounds__(64 * KS * (H ? 2 : 1)) void moe_qmma_kernel(GemmArgs p) {
   if (p.ntasks && (int)blockIdx.x >= *p.ntasks) return;   // grid sized for the most tasks
   const GemmTask t = p.tasks[blockIdx.x];
@@ -549,16 +627,20 @@ __global__ __launch_bounds__(64 * KS * (H ? 2 : 1)) void moe_qmma_kernel(GemmArg
   uint8_t* mine = xs + (XL && !H ? (threadIdx.x >> 6) * 2 * NT * 32 * 128 : 0);
   if constexpr (NT == 2) {
     if (t.rn <= 32) {
-      qmma_task<T, PAIR, 1, KS, XL, H>(p, t, mine);
+      qmma_task<T, PAIR, 1, KS, XL, H, SP>(p, t, mine);
       return;
     }
   }
-  qmma_task<T, PAIR, NT, KS, XL, H>(p, t, mine);
+  qmma_task<T, PAIR, NT, KS, XL, H, SP>(p, t, mine);
 }
 
 template <int T, int PA, int NT, int KS>
-static void launch_qmma_v(bool xl, bool h, int ntasks, hipStream_t s, const GemmArgs& a) {
+static void launch_qmma_v(bool xl, bool h, int ntasks, hipStream_t s, const GemmArgs& a, bool sp) {
   const dim3 grid((unsigned)ntasks);
+  if (sp) {
+    hipLaunchKernelGGL((moe_qmma_kernel<T, PA, NT, KS, false, false, true>), grid, dim3(64 * KS), 0, s, a);
+    return;
+  }
   if constexpr (PA != kTwoTiles && KS == 1) {
     if (h) {
       hipLaunchKernelGGL((moe_qmma_kernel<T, PA, NT, 1, true, true>), grid, dim3(128), 0, s, a);
@@ -569,7 +651,8 @@ static void launch_qmma_v(bool xl, bool h, int ntasks, hipStream_t s, const Gemm
   else hipLaunchKernelGGL((moe_qmma_kernel<T, PA, NT, KS, false, false>), grid, dim3(64 * KS), 0, s, a);
 }
 
-hipError_t launch_moe_qmma(uint32_t type, int pair, int max_rows, const GemmArgs& a, int ntasks, hipStream_t s) {
+hipError_t launch_moe_qmma(uint32_t type, int pair, int max_rows, const GemmArgs& a, int ntasks, hipStream_t s,
+                           bool split) {
   if (ntasks <= 0) return hipSuccess;
   if (max_rows < 1 || max_rows > 64 || pair < kOneTile || pair > kTwoTiles) return hipErrorInvalidValue;
   const bool one = max_rows <= 32;
@@ -593,11 +676,11 @@ hipError_t launch_moe_qmma(uint32_t type, int pair, int max_rows, const GemmArgs
   bool h = pair == kGateUp && !one;
   if (hv && (hv[0] == '0' || hv[0] == '1') && !hv[1]) h = hv[0] == '1';
   h = h && ks == 1 && pair != kTwoTiles;
-#define REHIP_QMMA_P(TT, PA)                                                         \
-  if (one) { if (ks == 2) launch_qmma_v<TT, PA, 1, 2>(xl, h, ntasks, s, a);          \
-             else launch_qmma_v<TT, PA, 1, 1>(xl, h, ntasks, s, a); }                \
-  else { if (ks == 2) launch_qmma_v<TT, PA, 2, 2>(xl, h, ntasks, s, a);              \
-         else launch_qmma_v<TT, PA, 2, 1>(xl, h, ntasks, s, a); }
+#define REHIP_QMMA_P(TT, PA)                                                               \
+  if (one) { if (ks == 2) launch_qmma_v<TT, PA, 1, 2>(xl, h, ntasks, s, a, split);           \
+             else launch_qmma_v<TT, PA, 1, 1>(xl, h, ntasks, s, a, split); }                 \
+  else { if (ks == 2) launch_qmma_v<TT, PA, 2, 2>(xl, h, ntasks, s, a, split);               \
+         else launch_qmma_v<TT, PA, 2, 1>(xl, h, ntasks, s, a, split); }
 #define REHIP_QMMA(TT)                                                     \
   case TT:                                                                 \
     if (pair == kGateUp) { REHIP_QMMA_P(TT, kGateUp) }                     \
