@@ -451,6 +451,58 @@ int gemm_enqueue(re_qmat* q, const float* d_x, size_t rows, float* d_y, int mode
   const size_t xbytes = rows * q->g.n * sizeof(float);
   if (xbytes >= (1ull << 31) || q->g.bytes >= (1ull << 31))
     return fail(RE_ERR_SIZE, "GEMM operands must stay below 2 GiB (X %zu B, W %zu B)", xbytes, q->g.bytes);
+  // few rows: the few-row GEMM (weights decoded in registers, one workgroup per 64-row tile and
+  // K slice, K slices for ~256 workgroups). It is faster than the tiled GEMM for 2..32 rows in bf16
+  // mode (one 32-row token tile) and for 2..64 rows in f32 mode, where the tiled GEMM stages f32
+  // tiles. REHIP_SKINNY=0 keeps the tiled GEMM for A/B runs.
+  const size_t skinny_max = mode == RE_MODE_F32 ? 64 : 32;
+  if (rows >= 2 && rows <= skinny_max && aligned16(d_x) && env_size("REHIP_SKINNY", 1) != 0 &&
+      !env_size("REHIP_GEMM_TILE", 0)) {
+    const SkinnyPlan sp = plan_skinny((int)q->g.m, (int)q->g.n, (int)q->g.qk);
+    SkinnyArgs a{};
+    a.W = q->d_w;
+    a.w_bytes = (uint32_t)q->g.bytes;
+    a.X = d_x;
+    a.x_bytes = (uint32_t)xbytes;
+    a.Y = d_y;
+    a.N = (int)rows;
+    a.m = (int)q->g.m;
+    a.K = (int)q->g.n;
+    a.KB = (int)q->g.kb;
+    a.tiles = (int)q->g.tiles;
+    a.ldy = (int)q->g.m;
+    a.blocks_per_split = sp.blocks_per_split;
+    a.splits = sp.splits;
+    const size_t part_bytes = (size_t)a.splits * rows * q->g.m * sizeof(float);
+    if (a.splits > 1) {
+      if (fixed_partial) {
+        if (part_bytes > fixed_cap)
+          return fail(RE_ERR_SIZE, "GEMM %zu x %zu x %zu with %d K slices needs %zu bytes of split scratch; the "
+                      "static scratch holds %zu", rows, q->g.m, q->g.n, a.splits, part_bytes, fixed_cap);
+        a.partial = fixed_partial;
+      } else if (part_bytes > q->spart.cap) {
+        // grown on first use; under stream capture nothing may be allocated, so an un-warmed shape
+        // runs as one K slice (same result up to summation order)
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        HIP_TRY(hipStreamIsCapturing(s, &cs));
+        if (cs != hipStreamCaptureStatusNone) {
+          a.blocks_per_split = (int)q->g.kb;
+          a.splits = 1;
+        } else {
+          int rc = q->spart.ensure(part_bytes);
+          if (rc) return rc;
+        }
+      }
+      if (!fixed_partial && a.splits > 1) a.partial = (float*)q->spart.p;
+    }
+    if (a.splits == 1 && (size_t)a.blocks_per_split * q->g.qk > (size_t)kSkinnyMaxK) {
+      // one slice of more than the staging holds: the tiled GEMM below
+    } else {
+      HIP_TRY(launch_gemm_skinny(q->g.type, a, mode == RE_MODE_F32, s));
+      if (a.splits > 1) HIP_TRY(launch_gemm_reduce(a.partial, d_y, rows * q->g.m, a.splits, s));
+      return RE_OK;
+    }
+  }
   GemmPlan pl = plan_gemm((int)q->g.m, (int)rows, (int)q->g.n, mode);
   // tuning knobs: REHIP_GEMM_TILE (1 64x64, 2 128x128, 3 128x256, 4 256x128, 5 128x192), REHIP_GEMM_KG,
   // REHIP_GEMM_SPLITS; a combination the library does not build fails at launch

@@ -540,16 +540,18 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(const V* __restrict__ 
                                                           int splits) {
   const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= n) return;
+  // up to sixteen slices' loads in flight per round trip (the slice count is uniform, so the
+  // guards are scalar branches); the sum runs in slice order
   V s = partial[i];
-  int sp = 1;
-  for (; sp + 8 <= splits; sp += 8) {
-    V v[8];
+  for (int sp = 1; sp < splits; sp += 16) {
+    V v[16];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) v[j] = partial[(size_t)(sp + j) * n + i];
+    for (int j = 0; j < 16; ++j)
+      if (sp + j < splits) v[j] = partial[(size_t)(sp + j) * n + i];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) s = vadd(s, v[j]);
+    for (int j = 0; j < 16; ++j)
+      if (sp + j < splits) s = vadd(s, v[j]);
   }
-  for (; sp < splits; ++sp) s = vadd(s, partial[(size_t)sp * n + i]);
   store_final(y + i, s);
 }
 
@@ -563,6 +565,10 @@ static hipError_t launch_reduce(const float* partial, float* y, size_t n, int sp
                        splits);
   }
   return hipGetLastError();
+}
+
+hipError_t launch_gemm_reduce(const float* partial, float* y, size_t n, int splits, hipStream_t s) {
+  return launch_reduce(partial, y, n, splits, s);
 }
 
 // x[i] -> bf16 with round to nearest even (the rounding the bf16-mode GEMM applies to f32 X), 8

@@ -145,6 +145,31 @@ GemmPlan plan_gemm(int m, int n, int K, int mode);
 int gemm_kgroups(GemmTile tile, int mode, long workgroups, int steps);
 hipError_t launch_gemm(uint32_t type, int mode, const GemmArgs& a, int ntasks, GemmTile tile, int kgroups,
                        hipStream_t s);
+// Few-row dense GEMM (skinny.hip): Y[N x m] = X[N x K] W^T for N <= 64 rows of f32 X, a 64-row
+// weight tile and a K slice of blocks_per_split whole blocks per workgroup; splits > 1 writes
+// partial[split][N][ldy] for the split-K reduce (launch with launch_gemm_reduce).
+struct SkinnyArgs {
+  const uint8_t* W;        // tiled slabs
+  uint32_t w_bytes;
+  const float* X;          // N x K f32 rows
+  uint32_t x_bytes;
+  float* Y;                // splits == 1: N x ldy
+  float* partial;          // splits > 1: splits x N x ldy
+  int N, m, K, KB, tiles, ldy;
+  int blocks_per_split, splits;
+};
+struct SkinnyPlan {
+  int blocks_per_split = 1;
+  int splits = 1;
+};
+constexpr int kSkinnyMaxK = 512;          // staged k per slice (LDS)
+SkinnyPlan plan_skinny(int m, int K, int qk);
+size_t skinny_lds_bytes(int staged_k, bool split_operands);
+// split_operands: f32 mode (split bf16 operands, three MFMAs per product)
+hipError_t launch_gemm_skinny(uint32_t type, const SkinnyArgs& a, bool split_operands, hipStream_t s);
+// y = sum over splits, in split order, of partial[split] (n floats each), streaming stores
+hipError_t launch_gemm_reduce(const float* partial, float* y, size_t n, int splits, hipStream_t s);
+
 // xb[i] = bf16(x[i]), round to nearest even; n a multiple of 8, both buffers 16-byte aligned
 hipError_t launch_x_to_bf16(const float* x, void* xb, size_t n, hipStream_t s);
 // split form: xb[i] = hi = bf16(x[i]) and xb[n + i] = lo = bf16(x[i] - hi), both rounded to nearest
