@@ -63,8 +63,10 @@ int re_repack(uint32_t ggml_type, const uint8_t *bytes, size_t nbytes, size_t m,
 /* ---- QMat (src/qmat.rs:30-42) ---------------------------------------------------------- */
 /* Upload and repack once. nbytes must equal m * re_row_bytes(type, n). F32 (0), F16 (1) and
  * BF16 (30) bytes are QMat::F32 / the no-fused-kernel arms (qmat.rs:45-49, 128-151): kept
- * row-major, nbytes = m * n * element size, f32 products in every mode; they do not stack and
- * take neither the norm/argmax epilogues of re_qmat_matvec_ex_dev nor re_ffn_create. */
+ * row-major, nbytes = m * n * element size; they do not stack. Below 16 activation rows their
+ * products are f32 in every mode; from 16 rows (n a multiple of 8) an MFMA GEMM, with bf16
+ * operands in bf16 mode and f32 ones in f32 mode. re_qmat_matvec_ex_dev's RMS-norm runs as its own
+ * launch into a buffer the matrix owns, and re_ffn_create pairs two dense matrices of one type. */
 int re_qmat_create(uint32_t ggml_type, const uint8_t *bytes, size_t nbytes, size_t m, size_t n,
                    re_qmat **out);
 /* A stack of `count` same-type, same-shape matrices (nbytes = count * m * row bytes, one after
@@ -276,8 +278,9 @@ int re_embed_dev(const float *d_table, size_t n_vocab, size_t d, const int *d_to
 /* *d_pos += delta on the stream. */
 int re_pos_add_dev(int *d_pos, int delta, void *stream);
 /* A gate/up pair (same type and shape, inter x hidden) read side by side for one activation row:
- * h = silu(gate x) * (up x) in one launch (the SwiGLU FFN input, forward.rs:100-105). The pair
- * keeps references to the two matrices, which must outlive it. */
+ * h = silu(gate x) * (up x) in one launch (the SwiGLU FFN input, forward.rs:100-105). Dense
+ * (F32/F16/BF16) pairs run the norm, the two products and SwiGLU as four launches through a buffer
+ * the pair owns. The pair keeps references to the two matrices, which must outlive it. */
 int re_ffn_create(re_qmat *gate, re_qmat *up, re_ffn **out);
 void re_ffn_destroy(re_ffn *f);
 /* d_norm_w: NULL, or x is RMS-normalised first (the FFN norm, forward.rs:479). */

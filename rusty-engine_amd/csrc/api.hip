@@ -173,6 +173,7 @@ struct re_qmat {
   uint8_t* d_w = nullptr;                 // count matrices, w_stride bytes apart
   size_t count = 1, w_stride = 0;
   float* d_partial = nullptr;
+  float* d_norm = nullptr;                // dense weights: the RMS-normed x of matvec_ex (n floats)
   int splits = 1, kb_per_split = 1, waves = 4;
   int rows_per_group = 0, groups = 0;   // row-group GEMV launch (0 = split launch)
   std::mutex mu;
@@ -616,7 +617,7 @@ int create_dense(uint32_t ggml_type, const uint8_t* bytes, size_t nbytes, size_t
   q->g.m = m;
   q->g.n = n;
   q->count = 1;
-  if (hipMalloc(&q->d_w, nbytes) != hipSuccess) {
+  if (hipMalloc(&q->d_w, nbytes) != hipSuccess || hipMalloc(&q->d_norm, n * sizeof(float)) != hipSuccess) {
     re_qmat_destroy(q);
     return fail(RE_ERR_HIP, "hipMalloc(%zu) failed", nbytes);
   }
@@ -677,6 +678,7 @@ void re_qmat_destroy(re_qmat* q) {
   if (q->stream) (void)hipStreamSynchronize(q->stream);
   if (q->d_w) (void)hipFree(q->d_w);
   if (q->d_partial) (void)hipFree(q->d_partial);
+  if (q->d_norm) (void)hipFree(q->d_norm);
   q->sx.release();
   q->sy.release();
   q->spart.release();
@@ -693,7 +695,8 @@ uint32_t re_qmat_type(const re_qmat* q) { return q ? q->g.type : 0; }
 int re_qmat_matvec_dev(re_qmat* q, const float* d_x, float* d_y, void* stream) {
   if (!q || !d_x || !d_y) return fail(RE_ERR_ARG, "null pointer");
   if (q->dense) {
-    HIP_TRY(launch_dense_gemm(q->g.type, q->d_w, d_x, d_y, (int)q->g.m, (int)q->g.n, 1, nullptr, (hipStream_t)stream));
+    HIP_TRY(launch_dense_gemm(q->g.type, q->d_w, d_x, d_y, (int)q->g.m, (int)q->g.n, 1, nullptr, RE_MODE_F32,
+                              nullptr, nullptr, 1, (hipStream_t)stream));
     return RE_OK;
   }
   return gemv_enqueue(q, d_x, d_y, (hipStream_t)stream);
@@ -792,10 +795,15 @@ int re_qmat_matvec_ex_dev(re_qmat* q, const float* d_x, const float* d_norm_w, f
                           float* d_y, unsigned long long* d_best, void* stream) {
   if (!q || !d_x || !d_y) return fail(RE_ERR_ARG, "null pointer");
   if (d_norm_w && !(eps >= 0.0f)) return fail(RE_ERR_ARG, "norm eps must be >= 0");
-  if (q->dense) {
-    if (d_norm_w || d_best)
-      return fail(RE_ERR_TYPE, "%s weights take the plain product and the residual add only", type_name(q->g.type));
-    HIP_TRY(launch_dense_gemm(q->g.type, q->d_w, d_x, d_y, (int)q->g.m, (int)q->g.n, 1, d_add, (hipStream_t)stream));
+  if (q->dense) {                        // RMS-norm into the matrix's own buffer, then the plain product
+    const hipStream_t s = (hipStream_t)stream;
+    const float* xin = d_x;
+    if (d_norm_w) {
+      HIP_TRY(launch_rmsnorm(d_x, d_norm_w, 1, (int)q->g.n, eps, q->d_norm, s));
+      xin = q->d_norm;
+    }
+    HIP_TRY(launch_dense_gemm(q->g.type, q->d_w, xin, d_y, (int)q->g.m, (int)q->g.n, 1, d_add, RE_MODE_F32, d_best,
+                              nullptr, 1, s));
     return RE_OK;
   }
   return gemv_enqueue(q, d_x, d_y, (hipStream_t)stream, d_add, d_norm_w, eps, d_best);
@@ -806,10 +814,25 @@ int re_qmat_matmul_dev(re_qmat* q, const float* d_x, size_t rows, float* d_y, in
   if (mode != RE_MODE_BF16 && mode != RE_MODE_F32) return fail(RE_ERR_ARG, "unknown mode %d", mode);
   if (rows == 0) return RE_OK;
   if (rows > (1u << 24)) return fail(RE_ERR_SIZE, "rows = %zu too large", rows);
-  if (q->dense) {                        // f32 products in either mode (the reference's f32 matvec)
+  if (q->dense) {                        // below 16 rows f32 products in either mode (the reference's
+    // f32 matvec); from 16 rows the MFMA GEMM, bf16 operands in bf16 mode and f32 in f32 mode
     if (rows > 65535u * 4u) return fail(RE_ERR_SIZE, "rows = %zu too large for dense weights", rows);
-    HIP_TRY(launch_dense_gemm(q->g.type, q->d_w, d_x, d_y, (int)q->g.m, (int)q->g.n, (int)rows, nullptr,
-                              (hipStream_t)stream));
+    const hipStream_t s = (hipStream_t)stream;
+    int splits = 1;
+    if (dense_mma_rows((int)q->g.n, (int)rows, d_x)) {
+      // few output tiles: K slices into the matrix's partial buffer, grown on first use (under
+      // stream capture an unwarmed shape runs as one slice: the same result up to summation order)
+      splits = dense_mma_splits((int)q->g.m, (int)q->g.n, (int)rows);
+      const size_t need = (size_t)splits * rows * q->g.m * sizeof(float);
+      if (splits > 1 && need > q->spart.cap) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        HIP_TRY(hipStreamIsCapturing(s, &cs));
+        if (cs != hipStreamCaptureStatusNone || need > (32u << 20)) splits = 1;
+        else if (int rc = q->spart.ensure(need)) return rc;
+      }
+    }
+    HIP_TRY(launch_dense_gemm(q->g.type, q->d_w, d_x, d_y, (int)q->g.m, (int)q->g.n, (int)rows, nullptr, mode,
+                              nullptr, splits > 1 ? (float*)q->spart.p : nullptr, splits, s));
     return RE_OK;
   }
   if (rows == 1) return gemv_enqueue(q, d_x, d_y, (hipStream_t)stream);
@@ -1824,6 +1847,8 @@ int re_moe_forward(re_moe* e, const float* x, size_t tokens, size_t top_k, const
 struct re_ffn {
   re_qmat *gate = nullptr, *up = nullptr;
   int ntasks = 0;
+  float* d_tmp = nullptr;                 // dense gate/up: normed x, gate and up outputs
+  size_t x_off = 0, g_off = 0, u_off = 0;
 };
 
 int re_rmsnorm_dev(const float* d_x, const float* d_w, size_t rows, size_t d, float eps, float* d_out, void* stream) {
@@ -1975,14 +2000,27 @@ int re_pos_add_dev(int* d_pos, int delta, void* stream) {
 int re_ffn_create(re_qmat* gate, re_qmat* up, re_ffn** out) {
   if (!gate || !up || !out) return fail(RE_ERR_ARG, "null pointer");
   *out = nullptr;
-  if (gate->dense || up->dense) return fail(RE_ERR_TYPE, "ffn: quantized gate and up only");
+  if (gate->dense != up->dense) return fail(RE_ERR_TYPE, "ffn: gate and up both quantized or both dense");
   if (gate->g.type != up->g.type || gate->g.m != up->g.m || gate->g.n != up->g.n)
     return fail(RE_ERR_SIZE, "ffn: gate and up must share type and shape");
-  if (gate->g.n > (size_t)kGemvRowsMaxK) return fail(RE_ERR_SIZE, "ffn: rows longer than %d", kGemvRowsMaxK);
+  if (!gate->dense && gate->g.n > (size_t)kGemvRowsMaxK)
+    return fail(RE_ERR_SIZE, "ffn: rows longer than %d", kGemvRowsMaxK);
   re_ffn* f = new (std::nothrow) re_ffn();
   if (!f) return fail(RE_ERR_ARG, "out of memory");
   f->gate = gate;
   f->up = up;
+  if (gate->dense) {
+    // dense weights: RMS-norm, the two products and SwiGLU as four launches, through a buffer
+    // owned by the pair (so a captured decode step allocates nothing)
+    auto pad = [](size_t v) { return (v + 63) / 64 * 64; };
+    f->x_off = 0;
+    f->g_off = pad(gate->g.n);
+    f->u_off = f->g_off + pad(gate->g.m);
+    if (hipMalloc(&f->d_tmp, (f->u_off + pad(gate->g.m)) * sizeof(float)) != hipSuccess) {
+      delete f;
+      return fail(RE_ERR_HIP, "ffn: hipMalloc failed");
+    }
+  }
   // one workgroup per kFfnGemvRows weight rows; the kernel derives its rows from the workgroup
   // index (no task list to load)
   f->ntasks = (int)((gate->g.m + kFfnGemvRows - 1) / kFfnGemvRows);
@@ -1992,12 +2030,33 @@ int re_ffn_create(re_qmat* gate, re_qmat* up, re_ffn** out) {
 
 void re_ffn_destroy(re_ffn* f) {
   if (!f) return;
+  if (f->d_tmp) {
+    (void)hipDeviceSynchronize();
+    (void)hipFree(f->d_tmp);
+  }
   delete f;
 }
 
 int re_ffn_forward_dev(re_ffn* f, const float* d_x, const float* d_norm_w, float eps, float* d_h, void* stream) {
   if (!f || !d_x || !d_h) return fail(RE_ERR_ARG, "null pointer");
   if (!aligned16(d_x) || !aligned16(d_norm_w)) return fail(RE_ERR_ARG, "x and norm weights must be 16-byte aligned");
+  if (f->gate->dense) {
+    const hipStream_t s = (hipStream_t)stream;
+    const int m = (int)f->gate->g.m, n = (int)f->gate->g.n;
+    const float* xin = d_x;
+    if (d_norm_w) {
+      HIP_TRY(launch_rmsnorm(d_x, d_norm_w, 1, n, eps, f->d_tmp + f->x_off, s));
+      xin = f->d_tmp + f->x_off;
+    }
+    float* gy = f->d_tmp + f->g_off;
+    float* uy = f->d_tmp + f->u_off;
+    HIP_TRY(launch_dense_gemm(f->gate->g.type, f->gate->d_w, xin, gy, m, n, 1, nullptr, RE_MODE_F32, nullptr, nullptr,
+                              1, s));
+    HIP_TRY(launch_dense_gemm(f->up->g.type, f->up->d_w, xin, uy, m, n, 1, nullptr, RE_MODE_F32, nullptr, nullptr, 1,
+                              s));
+    HIP_TRY(launch_swiglu(gy, uy, d_h, (size_t)m, s));
+    return RE_OK;
+  }
   MoeGemvArgs g{};
   g.rows_per_task = kFfnGemvRows;
   g.norm_w = d_norm_w;

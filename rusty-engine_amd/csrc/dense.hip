@@ -1,8 +1,10 @@
 // Dense (unquantized) weights: F32, F16 and BF16 matrices stored row-major as the GGUF file holds
 // them (QMat::F32 and the no-fused-kernel fallback of src/qmat.rs:128-151, the float arms of
 // quant::dequant, src/quant.rs:363-392). Every element widens exactly to f32 (F16 by bit
-// widening with subnormals and NaN payloads kept, BF16 by a 16-bit shift); products accumulate in
-// f32 per lane in element order and fold over the wave with a fixed xor tree (deterministic).
+// widening with subnormals and NaN payloads kept, BF16 by a 16-bit shift). Up to 15 activation
+// rows: products accumulate in f32 per lane in element order and fold over the wave with a fixed
+// xor tree (deterministic); from 16 rows, an MFMA GEMM (bf16 operands in bf16 mode, f32 in f32
+// mode).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -50,10 +52,12 @@ __device__ __forceinline__ float wave_sum_xor(float v) {
 
 // Y[t][r] = sum_k W[r][k] x[t][k] (+ add[r] when given): one wave per weight row, TT activation
 // rows per workgroup, lanes striding the row so every weight load is a contiguous 64-element run.
+// One row (TT = 1) may also fold the greedy argmax of y into best (the quantized GEMV's slots).
 template <uint32_t T, int TT>
 __global__ __launch_bounds__(256) void dense_gemm_kernel(const typename DenseElem<T>::S* __restrict__ W,
                                                          const float* __restrict__ x, float* __restrict__ y, int m,
-                                                         int n, int rows, const float* __restrict__ add) {
+                                                         int n, int rows, const float* __restrict__ add,
+                                                         unsigned long long* __restrict__ best) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = blockIdx.x * 4 + wave;
   if (r >= m) return;                    // no workgroup barrier below
@@ -71,28 +75,195 @@ __global__ __launch_bounds__(256) void dense_gemm_kernel(const typename DenseEle
   }
 #pragma unroll
   for (int t = 0; t < TT; ++t) acc[t] = wave_sum_xor(acc[t]);
+  unsigned long long key = 0;
   if (lane == 0) {
 #pragma unroll
-    for (int t = 0; t < TT; ++t)
-      if (t < nt) y[(size_t)(t0 + t) * m + r] = add ? acc[t] + add[r] : acc[t];
+    for (int t = 0; t < TT; ++t) {
+      if (t < nt) {
+        const float v = add ? acc[t] + add[r] : acc[t];
+        y[(size_t)(t0 + t) * m + r] = v;
+        if (TT == 1) key = argmax_key(v, r);
+      }
+    }
+  }
+  if (TT == 1 && best) wave_argmax_fold(key, best);
+}
+
+// Many activation rows: an MFMA GEMM over 64 x 64 output tiles (64 weight rows x 64 activation
+// rows), four waves of one 32 x 32 tile each, K in steps of 32. Each step's weights and activations
+// go through LDS: every element is widened exactly to f32 and, in bf16 mode, rounded to bf16 (RNE)
+// for v_mfma_f32_32x32x16_bf16; f32 mode keeps f32 and uses v_mfma_f32_32x32x2_f32. The next
+// step's global loads are in flight while a step multiplies. Needs n % 8 == 0 (whole 8-element
+// runs per thread) and 16-byte aligned activation rows; K beyond n and rows beyond m / rows read
+// zeros. The result of an output depends only on its row, column and the mode (fixed K order).
+constexpr int kDenseBM = 64, kDenseBN = 64, kDenseBK = 32;
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16_t;
+
+template <bool F32> struct DenseLds;
+template <> struct DenseLds<false> {
+  using E = __bf16;
+  static constexpr int LD = kDenseBK + 8;     // 80 bytes per row: 16-byte aligned, banks spread
+};
+template <> struct DenseLds<true> {
+  using E = float;
+  static constexpr int LD = kDenseBK + 4;     // 144 bytes per row
+};
+
+// the 8 elements k0 .. k0 + 7 of weight row r (zeros past the matrix), widened to f32
+template <uint32_t T>
+__device__ __forceinline__ void dense_load8(const typename DenseElem<T>::S* W, int m, int n, int r, int k0, float (&v)[8]) {
+  if (r >= m || k0 >= n) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = 0.0f;
+    return;
+  }
+  const typename DenseElem<T>::S* p = W + (size_t)r * n + k0;
+  if constexpr (T == 0) {
+    const float4 a = *reinterpret_cast<const float4*>(p), b = *reinterpret_cast<const float4*>(p + 4);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  } else {
+    const uint4 u = *reinterpret_cast<const uint4*>(p);
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = DenseElem<T>::get((uint16_t)(w[i] & 0xFFFFu));
+      v[2 * i + 1] = DenseElem<T>::get((uint16_t)(w[i] >> 16));
+    }
+  }
+}
+
+__device__ __forceinline__ void dense_loadx8(const float* x, int rows, int n, int t, int k0, float (&v)[8]) {
+  if (t >= rows || k0 >= n) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = 0.0f;
+    return;
+  }
+  const float* p = x + (size_t)t * n + k0;
+  const float4 a = *reinterpret_cast<const float4*>(p), b = *reinterpret_cast<const float4*>(p + 4);
+  v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+
+template <bool F32>
+__device__ __forceinline__ void dense_store8(typename DenseLds<F32>::E* dst, const float (&v)[8]) {
+  if constexpr (F32) {
+    *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+    *reinterpret_cast<float4*>(dst + 4) = make_float4(v[4], v[5], v[6], v[7]);
+  } else {
+    bf16x8_t b;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) b[i] = (__bf16)v[i];
+    *reinterpret_cast<bf16x8_t*>(dst) = b;
+  }
+}
+
+template <uint32_t T, bool F32>
+__global__ __launch_bounds__(256) void dense_mma_kernel(const typename DenseElem<T>::S* __restrict__ W,
+                                                        const float* __restrict__ x, float* __restrict__ y, int m,
+                                                        int n, int rows, const float* __restrict__ add,
+                                                        float* __restrict__ partial, int steps_per_split) {
+  using L = DenseLds<F32>;
+  using E = typename L::E;
+  constexpr int LD = L::LD;
+  __shared__ __attribute__((aligned(16))) E ws[kDenseBM * LD];
+  __shared__ __attribute__((aligned(16))) E xs[kDenseBN * LD];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave & 1, wn = wave >> 1;             // the wave's 32 weight rows / 32 activation rows
+  const int m0 = blockIdx.x * kDenseBM, t0 = blockIdx.y * kDenseBN;
+  // K slice of this workgroup (blockIdx.z; one slice when the grid has no z)
+  const int steps_all = (n + kDenseBK - 1) / kDenseBK;
+  const int s0 = blockIdx.z * steps_per_split, s1 = min(steps_all, s0 + steps_per_split);
+  // staging: thread t takes row t / 4 of both tiles, elements 8 (t % 4) .. + 7 of the step
+  const int sr = tid >> 2, sk = 8 * (tid & 3);
+  float wv[8], xv[8];
+  dense_load8<T>(W, m, n, m0 + sr, s0 * kDenseBK + sk, wv);
+  dense_loadx8(x, rows, n, t0 + sr, s0 * kDenseBK + sk, xv);
+  f32x16_t acc;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+  for (int st = s0; st < s1; ++st) {
+    dense_store8<F32>(ws + sr * LD + sk, wv);
+    dense_store8<F32>(xs + sr * LD + sk, xv);
+    __syncthreads();
+    if (st + 1 < s1) {                   // the next step's loads fly under this step's MFMAs
+      dense_load8<T>(W, m, n, m0 + sr, (st + 1) * kDenseBK + sk, wv);
+      dense_loadx8(x, rows, n, t0 + sr, (st + 1) * kDenseBK + sk, xv);
+    }
+    const E* wa = ws + (32 * wm + (lane & 31)) * LD;
+    const E* xb = xs + (32 * wn + (lane & 31)) * LD;
+    if constexpr (F32) {
+      // MFMA q of the 8-k slice kk takes k = 8 kk + q (lanes 0-31) and 8 kk + 4 + q (lanes 32-63)
+#pragma unroll
+      for (int kk = 0; kk < kDenseBK / 8; ++kk) {
+        const float4 a = *reinterpret_cast<const float4*>(wa + 8 * kk + 4 * (lane >> 5));
+        const float4 b = *reinterpret_cast<const float4*>(xb + 8 * kk + 4 * (lane >> 5));
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.x, b.x, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.y, b.y, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.z, b.z, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.w, b.w, acc, 0, 0, 0);
+      }
+    } else {
+#pragma unroll
+      for (int kk = 0; kk < kDenseBK / 16; ++kk) {
+        const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(wa + 16 * kk + 8 * (lane >> 5));
+        const bf16x8_t b = *reinterpret_cast<const bf16x8_t*>(xb + 16 * kk + 8 * (lane >> 5));
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc, 0, 0, 0);
+      }
+    }
+    __syncthreads();                     // every wave is done reading the step
+  }
+  // D[i][j]: weight row i = 8 (r / 4) + 4 (lane / 32) + r % 4 of the wave's 32, activation row
+  // j = lane % 32: four consecutive registers are four consecutive outputs of one activation row
+  // (K slices: each writes its partial tile; the reduce adds them in slice order)
+  const int t = t0 + 32 * wn + (lane & 31);
+  if (t >= rows) return;
+  float* yr = (gridDim.z > 1 ? partial + (size_t)blockIdx.z * rows * m : y) + (size_t)t * m;
+  const float* ad = gridDim.z > 1 ? nullptr : add;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const int r0 = m0 + 32 * wm + 8 * g + 4 * (lane >> 5);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int r = r0 + e;
+      if (r < m) yr[r] = ad ? acc[4 * g + e] + ad[r] : acc[4 * g + e];
+    }
   }
 }
 
 template <uint32_t T>
-hipError_t launch_dense_t(const void* W, const float* x, float* y, int m, int n, int rows, const float* add,
-                          hipStream_t s) {
+hipError_t launch_dense_t(const void* W, const float* x, float* y, int m, int n, int rows, const float* add, int mode,
+                          unsigned long long* best, float* partial, int splits, hipStream_t s) {
   using S = typename DenseElem<T>::S;
+  if (best && rows != 1) return hipErrorInvalidValue;
+  if (dense_mma_rows(n, rows, x)) {
+    const int steps = (n + kDenseBK - 1) / kDenseBK;
+    if (splits < 1 || (splits > 1 && (!partial || add))) return hipErrorInvalidValue;
+    const int sps = (steps + splits - 1) / splits;
+    splits = (steps + sps - 1) / sps;
+    const dim3 grid((unsigned)((m + kDenseBM - 1) / kDenseBM), (unsigned)((rows + kDenseBN - 1) / kDenseBN),
+                    (unsigned)splits);
+    if (mode == 1)
+      hipLaunchKernelGGL((dense_mma_kernel<T, true>), grid, dim3(256), 0, s, (const S*)W, x, y, m, n, rows, add,
+                         partial, sps);
+    else
+      hipLaunchKernelGGL((dense_mma_kernel<T, false>), grid, dim3(256), 0, s, (const S*)W, x, y, m, n, rows, add,
+                         partial, sps);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || splits == 1) return e;
+    return launch_gemm_reduce(partial, y, (size_t)rows * m, splits, s);
+  }
   const unsigned gx = (unsigned)((m + 3) / 4);
   // 1, 4 or 16 activation rows per workgroup: W is read once per row group, and every output keeps
   // the same per-lane order and fold whatever the group
   if (rows == 1)
-    hipLaunchKernelGGL((dense_gemm_kernel<T, 1>), dim3(gx, 1u), dim3(256), 0, s, (const S*)W, x, y, m, n, rows, add);
+    hipLaunchKernelGGL((dense_gemm_kernel<T, 1>), dim3(gx, 1u), dim3(256), 0, s, (const S*)W, x, y, m, n, rows, add,
+                       best);
   else if (rows < 16)
     hipLaunchKernelGGL((dense_gemm_kernel<T, 4>), dim3(gx, (unsigned)((rows + 3) / 4)), dim3(256), 0, s, (const S*)W,
-                       x, y, m, n, rows, add);
+                       x, y, m, n, rows, add, nullptr);
   else
     hipLaunchKernelGGL((dense_gemm_kernel<T, 16>), dim3(gx, (unsigned)((rows + 15) / 16)), dim3(256), 0, s,
-                       (const S*)W, x, y, m, n, rows, add);
+                       (const S*)W, x, y, m, n, rows, add, nullptr);
   return hipGetLastError();
 }
 
@@ -101,13 +272,27 @@ hipError_t launch_dense_t(const void* W, const float* x, float* y, int m, int n,
 bool dense_type(uint32_t type) { return type == 0 || type == 1 || type == 30; }
 size_t dense_elem_bytes(uint32_t type) { return type == 0 ? 4 : 2; }
 
+bool dense_mma_rows(int n, int rows, const float* x) {
+  return rows >= kDenseMmaMinRows && n % 8 == 0 && ((uintptr_t)x & 15) == 0;
+}
+
+int dense_mma_splits(int m, int n, int rows) {
+  // K slices until ~512 workgroups run (two per CU: a workgroup's K loop is bound by its load
+  // latency), each slice at least 4 steps of 32
+  const long tiles = (long)((m + kDenseBM - 1) / kDenseBM) * ((rows + kDenseBN - 1) / kDenseBN);
+  const int steps = (n + kDenseBK - 1) / kDenseBK;
+  if (tiles >= 512) return 1;
+  return (int)std::max<long>(1, std::min<long>((512 + tiles - 1) / tiles, steps / 4));
+}
+
 hipError_t launch_dense_gemm(uint32_t type, const void* W, const float* x, float* y, int m, int n, int rows,
-                             const float* add, hipStream_t s) {
+                             const float* add, int mode, unsigned long long* best, float* partial, int splits,
+                             hipStream_t s) {
   if (rows == 0 || m == 0) return hipSuccess;
   switch (type) {
-    case 0: return launch_dense_t<0>(W, x, y, m, n, rows, add, s);
-    case 1: return launch_dense_t<1>(W, x, y, m, n, rows, add, s);
-    case 30: return launch_dense_t<30>(W, x, y, m, n, rows, add, s);
+    case 0: return launch_dense_t<0>(W, x, y, m, n, rows, add, mode, best, partial, splits, s);
+    case 1: return launch_dense_t<1>(W, x, y, m, n, rows, add, mode, best, partial, splits, s);
+    case 30: return launch_dense_t<30>(W, x, y, m, n, rows, add, mode, best, partial, splits, s);
     default: return hipErrorInvalidValue;
   }
 }

@@ -77,9 +77,16 @@ hipError_t launch_dequant(uint32_t type, const uint8_t* W, float* out, int m, in
 // Dense F32 / F16 / BF16 weights (dense.hip): row-major as stored, m x n elements
 bool dense_type(uint32_t type);                  // ggml types 0, 1, 30
 size_t dense_elem_bytes(uint32_t type);
-// Y (rows x m) = X (rows x n) W^T (+ add[r] per output row when given)
+// Y (rows x m) = X (rows x n) W^T (+ add[r] per output row when given). From kDenseMmaMinRows
+// rows (n % 8 == 0, 16-byte aligned x) an MFMA GEMM: mode 1 (f32) f32 MFMA, else bf16 operands.
+// best (one row only): the greedy argmax of y folded into the kArgmaxSlots slots. The MFMA GEMM may
+// split K over `splits` slices (partial: splits x rows x m floats, no add), added in slice order.
+constexpr int kDenseMmaMinRows = 16;
+bool dense_mma_rows(int n, int rows, const float* x);     // the MFMA GEMM takes this call
+int dense_mma_splits(int m, int n, int rows);             // its planned K slices
 hipError_t launch_dense_gemm(uint32_t type, const void* W, const float* x, float* y, int m, int n, int rows,
-                             const float* add, hipStream_t s);
+                             const float* add, int mode, unsigned long long* best, float* partial, int splits,
+                             hipStream_t s);
 hipError_t launch_dense_to_f32(uint32_t type, const void* src, float* dst, size_t count, hipStream_t s);
 // Int8 activations (i8.hip): Q8Activation::from_f32 of rows x n f32 (n % 32 == 0, x 16-byte
 // aligned) into scales (rows x n/32) and qs (rows x n, 16-byte aligned); and the Q8_0 x i8 GEMM

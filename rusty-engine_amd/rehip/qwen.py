@@ -561,29 +561,28 @@ class DeviceDecoder:
     @staticmethod
     def _check_supported(mb: ModelBytes) -> None:
         """The shapes and types the device-resident step covers, checked before anything is
-        allocated: quantized projections (the fused norm / residual / SwiGLU / argmax epilogues
-        exist for the quant GEMVs only; dense F32/F16/BF16 models run on DenseDecoder with
-        HipBackend), one type for q, k and v (one fused matrix) and one for gate and up (one
-        paired launch), rows a multiple of 32 elements, and head_dim a multiple of 4 up to 256 (the
-        attention kernels). Raises ValueError naming what is outside."""
-        from . import GEOM
+        allocated: projections quantized (Q4_0/Q5_0/Q8_0/Q4_K/Q5_K/Q6_K, the fused norm / residual /
+        SwiGLU / argmax epilogues) or dense (F32/F16/BF16: the norm and SwiGLU as launches of their
+        own), one type for q, k and v (one fused matrix) and one for gate and up (one pair), rows a
+        multiple of 32 elements, and head_dim a multiple of 4 up to 256 (the attention kernels).
+        Raises ValueError naming what is outside."""
+        from . import BF16, F16, F32, GEOM
         g = mb.geom
-        out_t = mb.output_type if mb.output_type is not None else mb.embed_type
-        for name, t in (("attention", mb.attn_type), ("ffn", mb.ffn_type), ("down", mb.down_type),
-                        ("embedding", mb.embed_type), ("output", out_t)):
-            if t not in GEOM:
-                raise ValueError(f"DeviceDecoder: the {name} weights are ggml type {t}, which has no fused "
-                                 "GEMV kernel (quantized Q4_0/Q5_0/Q8_0/Q4_K/Q5_K/Q6_K only); run dense models "
-                                 "on DenseDecoder with HipBackend")
-        for i, b in enumerate(mb.blocks):
-            if b.types:
-                raise ValueError(f"DeviceDecoder: block {i} overrides tensor types {sorted(b.types)}; the device "
-                                 "step takes one attention type (fused q|k|v) and one ffn type (paired gate/up)")
         if g.d_model % g.n_heads or g.head_dim % 4 or g.head_dim > 256 or g.n_heads % g.n_kv_heads:
             raise ValueError(f"DeviceDecoder: head_dim {g.d_model}/{g.n_heads} with {g.n_kv_heads} KV heads; the "
                              "attention kernels take head_dim a multiple of 4 up to 256 and whole query groups")
         if g.d_model % 32 or g.d_ff % 32:
             raise ValueError(f"DeviceDecoder: d_model {g.d_model} and d_ff {g.d_ff} must be multiples of 32")
+        out_t = mb.output_type if mb.output_type is not None else mb.embed_type
+        for name, t in (("attention", mb.attn_type), ("ffn", mb.ffn_type), ("down", mb.down_type),
+                        ("embedding", mb.embed_type), ("output", out_t)):
+            if t not in GEOM and t not in (F32, F16, BF16):
+                raise ValueError(f"DeviceDecoder: the {name} weights are ggml type {t}, which has no GEMV kernel "
+                                 "(Q4_0/Q5_0/Q8_0/Q4_K/Q5_K/Q6_K and F32/F16/BF16 only)")
+        for i, b in enumerate(mb.blocks):
+            if b.types:
+                raise ValueError(f"DeviceDecoder: block {i} overrides tensor types {sorted(b.types)}; the device "
+                                 "step takes one attention type (fused q|k|v) and one ffn type (paired gate/up)")
 
     # -- pieces ----------------------------------------------------------------------------
     def _qkv_post(self, blk, rows):

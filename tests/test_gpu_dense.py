@@ -72,15 +72,41 @@ def test_dense_matvec_matmul(t, m, n):
     x = rng.standard_normal(n).astype(np.float32)
     got = q.matvec(x)
     _check_product(got, t, raw, m, n, x, 1)
-    for rows in (2, 5, 17):
+    for rows in (2, 5, 15):
         xs = rng.standard_normal((rows, n)).astype(np.float32)
-        for mode in (rehip.MODE_F32, rehip.MODE_BF16):     # f32 products in either mode
+        for mode in (rehip.MODE_F32, rehip.MODE_BF16):     # below 16 rows: f32 products in either mode
             y = q.matmul(xs, rows, mode)
             _check_product(y, t, raw, m, n, xs, rows)
         # a row's output does not depend on the rows beside it, nor on the row-group size
-        # (1, 4 or 16 rows per workgroup)
+        # (1 or 4 rows per workgroup)
         assert np.array_equal(q.matmul(xs[:1], 1, rehip.MODE_F32), q.matvec(xs[0]))
         assert np.array_equal(q.matmul(xs[:2], 2, rehip.MODE_F32), q.matmul(xs, rows, rehip.MODE_F32)[:2 * m])
+    q.close()
+
+
+@pytest.mark.parametrize("t", DENSE)
+@pytest.mark.parametrize("m,n,rows", [(896, 896, 961), (130, 200, 16), (64, 4864, 65), (333, 96, 100),
+                                      (896, 4864, 64)])
+def test_dense_mfma_gemm(t, m, n, rows):
+    """16 rows and up (n % 8 == 0): the MFMA GEMM (with K slices when it has few output tiles). f32
+    mode (f32 MFMA) within 2^-10 sum|w x| of the oracle's sequential sum; bf16 mode (operands
+    rounded to bf16) within 1e-2 of the norm of an f64 product; a row's outputs do not depend on the
+    call's other activation rows."""
+    rng = np.random.default_rng(m + n + rows + t)
+    raw = _raw(t, rng.standard_normal((m, n)).astype(np.float32))
+    q = rehip.QMat.from_bytes(t, raw, m, n)
+    xs = rng.standard_normal((rows, n)).astype(np.float32)
+    y = q.matmul(xs, rows, rehip.MODE_F32)
+    _check_product(y, t, raw, m, n, xs, rows)
+    exact = (xs.astype(np.float64) @ O.dequant(t, raw).astype(np.float64).reshape(m, n).T).reshape(-1)
+    yb = q.matmul(xs, rows, rehip.MODE_BF16)
+    assert np.linalg.norm(yb - exact) / np.linalg.norm(exact) <= 1e-2
+    xs2 = xs.copy()
+    xs2[1:] = rng.standard_normal((rows - 1, n)).astype(np.float32)
+    for mode in (rehip.MODE_F32, rehip.MODE_BF16):
+        full = q.matmul(xs, rows, mode)
+        other = q.matmul(xs2, rows, mode)
+        assert np.array_equal(other[:m], full[:m]), mode
     q.close()
 
 
@@ -100,8 +126,16 @@ def test_dense_device_entry_points(t):
     q.matvec_ex_dev(dx, dy, add=da)
     hip.synchronize()
     assert np.array_equal(dy.download(), plain + add)        # one f32 add after the product
-    with pytest.raises(rehip.RehipError, match="plain product"):
-        q.matvec_ex_dev(dx, dy, norm_w=da, eps=1e-6)
+    # the RMS-norm prologue: re_rmsnorm_dev's normed x, then the plain product (bit for bit)
+    nw = B.from_array((1 + 0.1 * rng.standard_normal(n)).astype(np.float32))
+    dn = B(n * 4)
+    rehip.rmsnorm_dev(dx, nw, 1, n, 1e-6, dn)
+    q.matvec_dev(dn, dy)
+    hip.synchronize()
+    normed = dy.download()
+    q.matvec_ex_dev(dx, dy, norm_w=nw, eps=1e-6, add=da)
+    hip.synchronize()
+    assert np.array_equal(dy.download(), normed + add)
     out = B(m * n * 4)
     q.dequant_dev(out)
     hip.synchronize()
@@ -124,8 +158,12 @@ def test_dense_errors():
     q = rehip.QMat.from_f32(w, 2, 3)
     with pytest.raises(rehip.RehipError):
         q.matmul_i8(np.zeros(0, np.float32), np.zeros(0, np.int8), 0)  # needs Q8_0
-    with pytest.raises(rehip.RehipError, match="quantized gate and up"):
-        rehip.Ffn(q, q)
+    q8 = rehip.QMat.from_bytes(rehip.Q8_0, np.zeros(2 * 34, np.uint8), 2, 32)
+    d32 = rehip.QMat.from_f32(np.zeros(64, np.float32), 2, 32)
+    with pytest.raises(rehip.RehipError, match="both quantized or both dense"):
+        rehip.Ffn(q8, d32)
+    q8.close()
+    d32.close()
     q.close()
 
 

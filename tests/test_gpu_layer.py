@@ -309,8 +309,8 @@ def test_ffn_pair(t, inter, hidden):
     U.close()
 
 
-def cpu_tokens(mb, prompt, steps):
-    r = qwen.DenseRunner(mb, CpuBackend())
+def cpu_tokens(mb, prompt, steps, backend=None):
+    r = qwen.DenseRunner(mb, backend or CpuBackend())
     dec = qwen.DenseDecoder(r, len(prompt) + steps)
     logits = dec.prefill(prompt)
     first = logits.copy()
@@ -321,6 +321,51 @@ def cpu_tokens(mb, prompt, steps):
 
 
 TINY = qwen.Geometry(d_model=256, n_heads=4, n_kv_heads=2, d_ff=512, rope_freq_base=1e4, rms_eps=1e-5)
+
+
+def dense_model(seed, geom, n_layers, n_vocab):
+    """Seeded random weights stored unquantized: F16 attention, BF16 gate/up, F32 down, embedding
+    and lm_head (entries N(0, 1/K), embedding/output 0.1 N(0, 1))."""
+    rng = np.random.default_rng(seed)
+
+    def raw(t, m, n, std):
+        w = (rng.standard_normal((m, n)) * std).astype(np.float32)
+        if t == rehip.F32:
+            return w.view(np.uint8).reshape(-1)
+        if t == rehip.F16:
+            return w.astype(np.float16).view(np.uint8).reshape(-1)
+        return (w.view(np.uint32) >> 16).astype(np.uint16).view(np.uint8).reshape(-1)
+    d, kv, ff = geom.d_model, geom.n_kv_heads * geom.head_dim, geom.d_ff
+    wd, wf = 1.0 / np.sqrt(d), 1.0 / np.sqrt(ff)
+    A, F, D = rehip.F16, rehip.BF16, rehip.F32
+    blocks = [qwen.BlockBytes(q=raw(A, d, d, wd), k=raw(A, kv, d, wd), v=raw(A, kv, d, wd), o=raw(A, d, d, wd),
+                              gate=raw(F, ff, d, wd), up=raw(F, ff, d, wd), down=raw(D, d, ff, wf),
+                              attn_norm=(1 + 0.1 * rng.standard_normal(d)).astype(np.float32),
+                              ffn_norm=(1 + 0.1 * rng.standard_normal(d)).astype(np.float32),
+                              q_bias=(0.1 * rng.standard_normal(d)).astype(np.float32),
+                              k_bias=(0.1 * rng.standard_normal(kv)).astype(np.float32),
+                              v_bias=(0.1 * rng.standard_normal(kv)).astype(np.float32))
+              for _ in range(n_layers)]
+    return qwen.ModelBytes(geom, n_vocab, raw(D, n_vocab, d, 0.1), raw(D, n_vocab, d, 0.1),
+                           (1 + 0.1 * rng.standard_normal(d)).astype(np.float32), blocks,
+                           attn_type=A, ffn_type=F, down_type=D, embed_type=D, output_type=D)
+
+
+@pytest.mark.parametrize("use_graph", [False, True])
+def test_device_decoder_dense_weights_match_cpu_path(use_graph):
+    """Unquantized weights through the device-resident decoder (the dense GEMV with its norm and
+    argmax, the dense gate/up pair, the dense MFMA GEMM in the f32 prefill) against the greedy
+    tokens of the oracle's QMat (the CPU kernels cover the quantized types only)."""
+    import test_qwen_gguf as T
+    mb = dense_model(11, TINY, n_layers=3, n_vocab=1000)
+    prompt = list(np.random.default_rng(12).integers(0, 1000, 40))      # 40 rows: the MFMA GEMM
+    want, lg = cpu_tokens(mb, prompt, 20, T.OracleQMatBackend())          # the oracle's dense QMat
+    dd = qwen.DeviceDecoder(mb, max_seq=80, prefill_rows=40, use_graph=use_graph)
+    first = dd.prefill(prompt)
+    np.testing.assert_allclose(dd.logits(), lg, rtol=0, atol=1e-4 * np.abs(lg).max())
+    got = [first] + [dd.step() for _ in range(19)]
+    dd.close()
+    assert got == want
 
 
 @pytest.mark.parametrize("use_graph", [False, True])

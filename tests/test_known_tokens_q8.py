@@ -10,8 +10,8 @@ answers follow from the construction alone, not from any implementation:
     (infer.rs:217-223).
 Q8_0 holds every weight exactly (1 = 32/32, 2 = 64/32; 0.1 as 100 * f16(0.001)).
 The CPU test checks the construction with the oracle-backed host decoder and that DeviceDecoder
-refuses the reference's own F32 fixture (head_dim 2, dense weights) with a clear error; the GPU
-tests run the device-resident decoder and the HIP host-step path."""
+refuses the reference's own F32 fixture (head_dim 2: the attention kernels take multiples of 4)
+with a clear error; the GPU tests run the device-resident decoder and the HIP host-step path."""
 import numpy as np
 import pytest
 
@@ -70,12 +70,13 @@ def test_construction_on_the_oracle_host_path():
 
 
 def test_device_decoder_refuses_the_dense_head_dim_2_fixture(tmp_path):
+    # dense F32 weights are covered; head_dim 2 is not (the attention kernels take multiples of 4)
     import test_qwen_gguf as T
     path = tmp_path / "dense_gen.gguf"
     path.write_bytes(T.synth_dense_gguf())
     g = rehip.Gguf(path)
     mb = qwen.model_from_gguf(g)
-    with pytest.raises(ValueError, match="no fused GEMV kernel"):
+    with pytest.raises(ValueError, match="head_dim"):
         qwen.DeviceDecoder(mb, max_seq=8)
     g.close()
 
