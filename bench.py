@@ -30,7 +30,7 @@ X[N x 4864]:
 
 Inputs are synthetic and seeded (numpy PCG64), uploaded before timing.
 
---sweep gemv|gemm|moe|decode|i8|load|calib prints JSON records of a measurement sweep instead
+--sweep gemv|gemm|dense|moe|decode|i8|load|calib prints JSON records of a measurement sweep instead
 (the decode GEMV sweep over the Qwen2.5-0.5B projections in every type; the prefill GEMMs; the
 MoE FFN; the decode step; the int8 activation path; GGUF ingest; and machine calibration:
 streaming HBM read, bf16 MFMA stream, per-launch floor of a kernel graph).
@@ -137,6 +137,32 @@ def time_gemm(t, m, k, n, mode, launches, seed, check=True):
     q.close()
     s.destroy()
     return r
+
+
+def time_dense(t, m, k, n, mode, launches, seed):
+    """One GEMM over unquantized (F32 / F16 / BF16) weights, row-major as stored (re_qmat_matmul_dev:
+    the MFMA GEMM from 16 rows), as a graph of `launches` launches. Weights N(0, 1/k)."""
+    import rehip
+    from rehip import hip
+    rng = np.random.default_rng(seed)
+    w = (rng.standard_normal((m, k)) / np.sqrt(k)).astype(np.float32)
+    if t == rehip.F32:
+        raw = w.view(np.uint8).reshape(-1)
+    elif t == rehip.F16:
+        raw = w.astype(np.float16).view(np.uint8).reshape(-1)
+    else:
+        raw = (w.view(np.uint32) >> 16).astype(np.uint16).view(np.uint8).reshape(-1)
+    q = rehip.QMat.from_bytes(t, raw, m, k)
+    dx = hip.DeviceBuffer.from_array(rng.standard_normal((n, k)).astype(np.float32))
+    dy = hip.DeviceBuffer(n * m * 4)
+    s = hip.Stream()
+    us = graph_time_us(s, lambda: q.matmul_dev(dx, n, dy, mode, stream=s), launches)
+    flop = 2.0 * n * m * k
+    peak = BF16_PEAK_TFLOPS if mode == rehip.MODE_BF16 else F32_MFMA_PEAK_TFLOPS
+    q.close()
+    s.destroy()
+    return {"type": rehip.TYPE_NAMES[t], "m": m, "k": k, "n": n, "mode": "bf16" if mode == rehip.MODE_BF16 else "f32",
+            "us": us, "tflops": flop / (us * 1e-6) / 1e12, "frac_mfma_peak": flop / (us * 1e-6) / 1e12 / peak}
 
 
 def moe_weights(seed):
@@ -636,6 +662,12 @@ def run_sweep(args):
                     r = time_gemm(t, m, k, n, mode, args.launches, seed=101 + n, check=False)
                     r["name"] = name
                     emit(r)
+    elif args.sweep == "dense":
+        for t in (rehip.F16, rehip.BF16, rehip.F32):
+            for m, k in ((4864, 896), (896, 4864), (896, 896)):
+                for n in (int(v) for v in args.rows.split(",") if v):
+                    for mode in ({"bf16": 0, "f32": 1}[v] for v in args.modes.split(",") if v):
+                        emit(time_dense(t, m, k, n, mode, min(args.launches, 100), seed=700 + n))
     elif args.sweep == "moe":
         weights = moe_weights(403)
         moe = rehip.MoeExperts(rehip.Q4_K, weights[0], rehip.Q4_K, weights[1], rehip.Q6_K, weights[2],
@@ -675,7 +707,7 @@ def main():
                     help="decode steps of the CPU-matmul end-to-end run (parity and CPU tok/s)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="first run one 256 MiB device-to-device copy (calibrates profiler byte counters)")
-    ap.add_argument("--sweep", default="", help="gemv | gemm | moe | decode | i8 | load | calib")
+    ap.add_argument("--sweep", default="", help="gemv | gemm | dense | moe | decode | i8 | load | calib")
     ap.add_argument("--types", default="Q4_0,Q5_0,Q8_0,Q4_K,Q5_K,Q6_K")
     ap.add_argument("--launches", type=int, default=300)
     ap.add_argument("--rows", default="64,961")
