@@ -117,9 +117,15 @@ def time_gemm(t, m, k, n, mode, launches, seed, check=True):
     us = graph_time_us(s, lambda: q.matmul_dev(dx, n, dy, mode, stream=s), launches)
     flop = 2.0 * n * m * k
     nbytes = algorithmic_bytes(t, m, k, n)
-    peak = BF16_PEAK_TFLOPS if mode == rehip.MODE_BF16 else F32_MFMA_PEAK_TFLOPS
+    # f32 mode runs bf16 MFMAs on split operands (three per product: hi*hi, hi*lo, lo*hi) unless
+    # REHIP_GEMM_SP=0 keeps f32 MFMAs above 64 rows: the MFMA work is priced at the peak of the
+    # instructions issued
+    split = mode == rehip.MODE_F32 and (n <= 64 or os.environ.get("REHIP_GEMM_SP", "1") != "0")
+    peak = BF16_PEAK_TFLOPS if mode == rehip.MODE_BF16 or split else F32_MFMA_PEAK_TFLOPS
+    mfma_flop = 3 * flop if split else flop
     r = {"type": rehip.TYPE_NAMES[t], "m": m, "k": k, "n": n, "mode": "bf16" if mode == rehip.MODE_BF16 else "f32",
-         "us": us, "tflops": flop / (us * 1e-6) / 1e12, "frac_mfma_peak": flop / (us * 1e-6) / 1e12 / peak,
+         "mfma": "bf16 x3 (split operands)" if split else ("bf16" if mode == rehip.MODE_BF16 else "f32"),
+         "us": us, "tflops": flop / (us * 1e-6) / 1e12, "frac_mfma_peak": mfma_flop / (us * 1e-6) / 1e12 / peak,
          "peak_tflops": peak, "gbs": nbytes / (us * 1e-6) / 1e9, "frac_hbm": nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS,
          "flop": flop, "bytes": nbytes}
     if check:

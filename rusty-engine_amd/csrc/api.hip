@@ -504,7 +504,9 @@ int gemm_enqueue(re_qmat* q, const float* d_x, size_t rows, float* d_y, int mode
       return RE_OK;
     }
   }
-  GemmPlan pl = plan_gemm((int)q->g.m, (int)rows, (int)q->g.n, mode);
+  // f32 mode on bf16 MFMAs with split operands (REHIP_GEMM_SP=0: the f32 MFMA tiles)
+  const int kmode = mode == RE_MODE_F32 && env_size("REHIP_GEMM_SP", 1) != 0 ? kGemmModeSplit : mode;
+  GemmPlan pl = plan_gemm((int)q->g.m, (int)rows, (int)q->g.n, kmode);
   // tuning knobs: REHIP_GEMM_TILE (1 64x64, 2 128x128, 3 128x256, 4 256x128, 5 128x192), REHIP_GEMM_KG,
   // REHIP_GEMM_SPLITS; a combination the library does not build fails at launch
   if (const size_t t = env_size("REHIP_GEMM_TILE", 0); t >= 1 && t <= 5) {
@@ -555,7 +557,7 @@ int gemm_enqueue(re_qmat* q, const float* d_x, size_t rows, float* d_y, int mode
       a.partial = (float*)q->spart.p;
     }
   }
-  HIP_TRY(launch_gemm(q->g.type, mode, a, 0, pl.tile, pl.kgroups, s));
+  HIP_TRY(launch_gemm(q->g.type, kmode, a, 0, pl.tile, pl.kgroups, s));
   return RE_OK;
 }
 

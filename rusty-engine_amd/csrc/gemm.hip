@@ -88,6 +88,25 @@ __device__ __forceinline__ void pack_run(const Run& r, DecChunk<F32>& d, int h) 
   }
 }
 
+// split form (f32 mode on bf16 MFMAs): the bf16 rounding of each value into hi, the bf16 rounding
+// of what it leaves into lo, so hi + lo holds the value to 2^-16 relative
+template <int T>
+__device__ __forceinline__ void pack_run_split(const Run& r, DecChunk<false>& hi, DecChunk<false>& lo, int h) {
+  float v[16];
+  run_values<T>(r, v);
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    bf16x8_t oh, ol;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      oh[i] = (__bf16)v[8 * k + i];
+      ol[i] = (__bf16)(v[8 * k + i] - (float)oh[i]);
+    }
+    hi.v[2 * h + k] = oh;
+    lo.v[2 * h + k] = ol;
+  }
+}
+
 template <bool F32>
 __device__ __forceinline__ void store_dec(typename Elem<F32>::T* row, const DecChunk<F32>& d) {
   if constexpr (F32) {
@@ -120,11 +139,13 @@ __device__ __forceinline__ typename DecX<F32>::T cvt_x(float4 v) {
 
 constexpr uint32_t kOob = 0x80000000u;   // a byte offset past every buffer: the load returns 0
 
-template <int T, bool F32, bool GROUPED, int BM, int BN, int WM, int WN, int KG, bool XB = false, bool DUAL = false>
+template <int T, bool F32, bool GROUPED, int BM, int BN, int WM, int WN, int KG, bool XB = false, bool DUAL = false,
+          bool SP = false>
 __global__ __launch_bounds__(WM* WN * 64 * KG) void gemm_kernel(GemmArgs p) {
   using B = Blk<T>;
   using E = typename Elem<F32>::T;
   static_assert(!XB || !F32, "bf16 activations feed the bf16 mode only");
+  static_assert(!SP || (!F32 && !GROUPED && !XB && !DUAL && KG == 1), "split operands: dense bf16-MFMA launches");
   static_assert(!DUAL || (GROUPED && XB && KG == 1), "gate/up pairs: grouped bf16 launches, one K-group");
   constexpr int NW = DUAL ? 2 : 1;                 // weight tiles per step (gate, up)
   constexpr int GT = WM * WN * 64;                 // threads of one K-group
@@ -139,7 +160,8 @@ __global__ __launch_bounds__(WM* WN * 64 * KG) void gemm_kernel(GemmArgs p) {
   constexpr int STAGE = (NW * BM + BN) * LD;       // LDS elements of one group
   static_assert(WJOBS >= 1 && XV >= 1 && TM >= 1 && TN >= 1, "tile shape");
   static_assert((KG - 1) * BM * BN * 4 <= KG * STAGE * (int)sizeof(E), "K-group partials fit in LDS");
-  __shared__ __attribute__((aligned(16))) E smem[KG * STAGE];
+  // SP: a second stage of the same shape holds the remainders (lo) of the weights and activations
+  __shared__ __attribute__((aligned(16))) E smem[KG * STAGE * (SP ? 2 : 1)];
 
   const int grp = __builtin_amdgcn_readfirstlane(threadIdx.x / GT);
   const int tid = threadIdx.x - grp * GT;          // thread inside the K-group
@@ -149,6 +171,8 @@ __global__ __launch_bounds__(WM* WN * 64 * KG) void gemm_kernel(GemmArgs p) {
   E* const Ws = smem + grp * STAGE;
   E* const Ws2 = Ws + BM * LD;                     // up tile (pairs only)
   E* const Xs = Ws + NW * BM * LD;
+  E* const Wl = Ws + STAGE;                       // SP: remainder planes
+  E* const Xl = Xs + STAGE;
 
   int mtile, r0, rn, split = 0;
   uint32_t wbase = 0;
@@ -273,6 +297,16 @@ __global__ __launch_bounds__(WM* WN * 64 * KG) void gemm_kernel(GemmArgs p) {
                                     __int_as_float(v[3])));
     }
   };
+  // SP: the remainders' decoded chunks and activations (one element otherwise, unused)
+  DecChunk<F32> dec_lo[SP ? WJOBS : 1];
+  XD xdec_lo[SP ? XV : 1];
+  // SP: the remainder of an activation after its bf16 rounding, rounded to bf16
+  auto cvt_lo = [&](const i32x4_t& v, const XD& hi) -> XD {
+    XD o;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = (__bf16)(__int_as_float(v[i]) - (float)hi[i]);
+    return o;
+  };
   auto decode = [&](int s, const typename B::CR (&raw)[WJOBS], DecChunk<F32> (&dec)[WJOBS]) {
 #pragma unroll
     for (int rep = 0; rep < WJOBS; ++rep) {
@@ -282,8 +316,15 @@ __global__ __launch_bounds__(WM* WN * 64 * KG) void gemm_kernel(GemmArgs p) {
       else { cc = 4 * (s & 1) + c; kl = -128 * (s & 1); }
       Run a, b;
       B::decode_chunk(raw[rep], cc, a, b);
-      pack_run<T, F32>(a, dec[rep], 0);
-      pack_run<T, F32>(b, dec[rep], 1);
+      if constexpr (SP) {
+        pack_run_split<T>(a, dec[rep], dec_lo[rep], 0);
+        pack_run_split<T>(b, dec[rep], dec_lo[rep], 1);
+        dec_lo[rep].ea = kl + a.e;
+        dec_lo[rep].eb = kl + b.e;
+      } else {
+        pack_run<T, F32>(a, dec[rep], 0);
+        pack_run<T, F32>(b, dec[rep], 1);
+      }
       dec[rep].ea = kl + a.e;
       dec[rep].eb = kl + b.e;
     }
@@ -297,6 +338,13 @@ __global__ __launch_bounds__(WM* WN * 64 * KG) void gemm_kernel(GemmArgs p) {
     }
 #pragma unroll
     for (int jj = 0; jj < XV; ++jj) *reinterpret_cast<XD*>(Xs + (XR * jj + tid / (BK / XE)) * LD + xk) = xd[jj];
+    if constexpr (SP) {
+#pragma unroll
+      for (int rep = 0; rep < WJOBS; ++rep) store_dec<false>(Wl + ((tid + GT * rep) % BM) * LD, dec_lo[rep]);
+#pragma unroll
+      for (int jj = 0; jj < XV; ++jj)
+        *reinterpret_cast<XD*>(Xl + (XR * jj + tid / (BK / XE)) * LD + xk) = xdec_lo[jj];
+    }
   };
 
   typename B::CR rawA[WJOBS], rawB[WJOBS];
@@ -317,6 +365,10 @@ __global__ __launch_bounds__(WM* WN * 64 * KG) void gemm_kernel(GemmArgs p) {
   if constexpr (DUAL) decode(s0, rawA2, dec2);
 #pragma unroll
   for (int jj = 0; jj < XV; ++jj) xdec[jj] = cvt(xraw[jj]);
+  if constexpr (SP) {
+#pragma unroll
+    for (int jj = 0; jj < XV; ++jj) xdec_lo[jj] = cvt_lo(xraw[jj], xdec[jj]);
+  }
   write_lds(dec, dec2, xdec);
 #pragma unroll
   for (int rep = 0; rep < WJOBS; ++rep) rawA[rep] = rawB[rep];
@@ -339,6 +391,14 @@ __global__ __launch_bounds__(WM* WN * 64 * KG) void gemm_kernel(GemmArgs p) {
       const E* wsrc2 = wsrc + BM * LD;     // the up tile's same row and slice (pairs only)
       const E* xsrc = Xs + (BN / WN * wn + (lane & 31)) * LD + 8 * (lane >> 5);
       bf16x8_t av[2][TM], bv[2][TN], av2[2][DUAL ? TM : 1];
+      // SP: the remainder fragments at the same places of the remainder stage
+      bf16x8_t al[2][SP ? TM : 1], bl[2][SP ? TN : 1];
+      if constexpr (SP) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i) al[0][i] = *reinterpret_cast<const bf16x8_t*>(wsrc + STAGE + 32 * i * LD);
+#pragma unroll
+        for (int j = 0; j < TN; ++j) bl[0][j] = *reinterpret_cast<const bf16x8_t*>(xsrc + STAGE + 32 * j * LD);
+      }
 #pragma unroll
       for (int i = 0; i < TM; ++i) av[0][i] = *reinterpret_cast<const bf16x8_t*>(wsrc + 32 * i * LD);
       if constexpr (DUAL) {
@@ -362,12 +422,31 @@ __global__ __launch_bounds__(WM* WN * 64 * KG) void gemm_kernel(GemmArgs p) {
 #pragma unroll
           for (int j = 0; j < TN; ++j)
             bv[nxt][j] = *reinterpret_cast<const bf16x8_t*>(xsrc + 32 * j * LD + 16 * (kk + 1));
+          if constexpr (SP) {
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+              al[nxt][i] = *reinterpret_cast<const bf16x8_t*>(wsrc + STAGE + 32 * i * LD + 16 * (kk + 1));
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+              bl[nxt][j] = *reinterpret_cast<const bf16x8_t*>(xsrc + STAGE + 32 * j * LD + 16 * (kk + 1));
+          }
         }
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
           for (int j = 0; j < TN; ++j)
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[cur][i], bv[cur][j], acc[i][j], 0, 0, 0);
+        if constexpr (SP) {
+          // w_hi x_lo + w_lo x_hi after the w_hi x_hi products (the lo x lo term, ~2^-16
+          // relative, is left out)
+#pragma unroll
+          for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[cur][i], bl[cur][j], acc[i][j], 0, 0, 0);
+              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[cur][i], bv[cur][j], acc[i][j], 0, 0, 0);
+            }
+        }
         if constexpr (DUAL) {
 #pragma unroll
           for (int i = 0; i < TM; ++i)
@@ -411,6 +490,10 @@ __global__ __launch_bounds__(WM* WN * 64 * KG) void gemm_kernel(GemmArgs p) {
     }
 #pragma unroll
     for (int jj = 0; jj < XV; ++jj) xdec[jj] = cvt(xraw[jj]);
+    if constexpr (SP) {
+#pragma unroll
+      for (int jj = 0; jj < XV; ++jj) xdec_lo[jj] = cvt_lo(xraw[jj], xdec[jj]);
+    }
     __syncthreads();                      // every wave is done reading step s
     write_lds(dec, dec2, xdec);           // step s + KG (zeros past the end)
     __syncthreads();
@@ -601,7 +684,7 @@ __global__ __launch_bounds__(256) void x_to_bf16_split_kernel(const float4* __re
   }
 }
 
-template <int T, bool F32, int BM, int BN, int WM, int WN, int KG, bool GROUPED>
+template <int T, bool F32, int BM, int BN, int WM, int WN, int KG, bool GROUPED, bool SP = false>
 static hipError_t launch_shape(const GemmArgs& a, int ntasks, hipStream_t s) {
   constexpr int NT = WM * WN * 64 * KG;
   if constexpr (GROUPED) {
@@ -627,7 +710,8 @@ static hipError_t launch_shape(const GemmArgs& a, int ntasks, hipStream_t s) {
   } else {
     const int total = ((a.m + BM - 1) / BM) * ((a.N + BN - 1) / BN) * a.splits;
     const int grid = (total + 7) / 8 * 8;
-    hipLaunchKernelGGL((gemm_kernel<T, F32, false, BM, BN, WM, WN, KG>), dim3((unsigned)grid), dim3(NT), 0, s, a);
+    hipLaunchKernelGGL((gemm_kernel<T, F32, false, BM, BN, WM, WN, KG, false, false, SP>), dim3((unsigned)grid),
+                       dim3(NT), 0, s, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || a.splits == 1) return e;
     return launch_reduce(a.partial, a.Y, (size_t)a.N * a.ldy, a.splits, s);
@@ -665,8 +749,18 @@ static hipError_t launch_t(const GemmArgs& a, int ntasks, GemmTile tile, int kg,
   }
 }
 
+// f32 mode on bf16 MFMAs (split operands): dense launches, 128 x 128 or 64 x 64 tiles, one K-group
+template <int T>
+static hipError_t launch_t_split(const GemmArgs& a, GemmTile tile, int kg, hipStream_t s) {
+  if (a.tasks || a.x_bf16 || a.W2 || kg != 1) return hipErrorInvalidValue;
+  if (tile == GemmTile::k128x128) return launch_shape<T, false, 128, 128, 2, 2, 1, false, true>(a, 0, s);
+  if (tile == GemmTile::k64x64) return launch_shape<T, false, 64, 64, 2, 2, 1, false, true>(a, 0, s);
+  return hipErrorInvalidValue;
+}
+
 template <int T>
 static hipError_t launch_mode(int mode, const GemmArgs& a, int ntasks, GemmTile tile, int kg, hipStream_t s) {
+  if (mode == kGemmModeSplit) return launch_t_split<T>(a, tile, kg, s);
   return mode == 1 ? launch_t<T, true>(a, ntasks, tile, kg, s) : launch_t<T, false>(a, ntasks, tile, kg, s);
 }
 
@@ -683,6 +777,28 @@ int gemm_kgroups(GemmTile tile, int mode, long workgroups, int steps) {
 GemmPlan plan_gemm(int m, int n, int K, int mode) {
   GemmPlan pl;
   const int steps = (K + kGemmBK - 1) / kGemmBK;
+  if (mode == kGemmModeSplit) {
+    // split operands (f32 mode on bf16 MFMAs). Many tiles: 64 x 64 (two workgroups per CU; C1 at
+    // 961 rows 50.7 us against 61.3 on 128 x 128). Fewer: 128 x 128 on four waves of 64 x 64 (the
+    // tiles and their remainders fill 139 KiB of LDS), K split toward 224 workgroups while the
+    // partial tiles stay <= 32 MiB (C2 at 961 rows: 4 splits 50.2 us, 3 59.5, 5 75.7, 8 57.2)
+    pl.kgroups = 1;
+    const long t64 = (long)((m + 63) / 64) * ((n + 63) / 64);
+    if (t64 >= 512) {
+      pl.tile = GemmTile::k64x64;
+    } else {
+      pl.tile = GemmTile::k128x128;
+      const long tiles = (long)((m + 127) / 128) * ((n + 127) / 128);
+      if (tiles < 200 && steps >= 4) {
+        long splits = std::min<long>((224 + tiles - 1) / tiles, steps / 2);
+        while (splits > 1 && splits * (long)n * m * 4 > (32l << 20)) --splits;
+        pl.splits = (int)std::max<long>(1, splits);
+      }
+    }
+    pl.steps_per_split = (steps + pl.splits - 1) / pl.splits;
+    pl.splits = (steps + pl.steps_per_split - 1) / pl.steps_per_split;
+    return pl;
+  }
   const long t128 = (long)((m + 127) / 128) * ((n + 127) / 128);
   const long t256 = (long)((m + 127) / 128) * ((n + 255) / 256);
   const long t64 = (long)((m + 63) / 64) * ((n + 63) / 64);

@@ -147,6 +147,10 @@ struct GemmPlan {
 };
 
 // tile, K-groups and K split of a dense m x n-row launch over K (mode 0 bf16, 1 f32)
+// launch mode of the tiled GEMM beside RE_MODE_BF16 / RE_MODE_F32: f32 mode computed with bf16
+// MFMAs on split operands (each operand's bf16 rounding and the bf16 rounding of its remainder;
+// products hi*hi + hi*lo + lo*hi, each within 2^-16 relative)
+constexpr int kGemmModeSplit = 2;
 GemmPlan plan_gemm(int m, int n, int K, int mode);
 // K-groups for `workgroups` tiles of `tile` over `steps` K steps
 int gemm_kgroups(GemmTile tile, int mode, long workgroups, int steps);

@@ -349,6 +349,27 @@ def test_gemm_forced_tiles(t, tile, kg, splits, monkeypatch):
     q.close()
 
 
+@pytest.mark.parametrize("t", rehip.QUANT_TYPES)
+@pytest.mark.parametrize("tile,splits", [(1, 1), (2, 1), (1, 3), (2, 4)])
+def test_gemm_f32_split_operand_tiles(t, tile, splits, monkeypatch):
+    # f32 mode on bf16 MFMAs (split operands) at both tiles, whole K and K split over workgroups,
+    # on a ragged shape (300 weight rows, 500 activation rows, K = 1280): the f32 bar, and the same
+    # bits on a repeat
+    monkeypatch.setenv("REHIP_GEMM_TILE", str(tile))
+    monkeypatch.setenv("REHIP_GEMM_KG", "1")
+    monkeypatch.setenv("REHIP_GEMM_SPLITS", str(splits))
+    m, n, rows = 300, 1280, 500
+    rng = np.random.default_rng(9100 + 10 * t + tile)
+    w = synth.weight_bytes(rng, t, m, n)
+    x = synth.activations(rng, rows, n)
+    q = qmat(t, w, m, n)
+    exact, absd = f64_product(t, w, m, n, x, rows)
+    got = q.matmul(x, rows, rehip.MODE_F32)
+    assert np.all(np.abs(got - exact.reshape(-1)) <= F32_TOL * absd.reshape(-1))
+    assert np.array_equal(q.matmul(x, rows, rehip.MODE_F32), got)
+    q.close()
+
+
 @pytest.mark.parametrize("t", [rehip.Q4_0, rehip.Q8_0, rehip.Q4_K, rehip.Q6_K])
 def test_gemm_large_tiles_ragged_edges(t):
     # 3136 weight rows (not a multiple of 128) x 2085 activation rows (not a multiple of 256):
