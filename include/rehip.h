@@ -41,7 +41,8 @@ extern "C" {
 #define RE_ERR_NODEV 5     /* no usable gfx950 device */
 
 #define RE_MODE_BF16 0     /* GEMM: bf16 MFMA, f32 accumulate (|err| <= 1e-2 rel-to-norm) */
-#define RE_MODE_F32 1      /* GEMM: f32 MFMA strict mode (|err| <= 2^-10 sum|w*x|) */
+#define RE_MODE_F32 1      /* GEMM: f32-accurate mode (|err| <= 2^-10 sum|w*x|): quantized weights run bf16
+                              MFMAs on split operands (hi*hi + hi*lo + lo*hi), dense weights f32 MFMAs */
 
 typedef struct re_qmat re_qmat;
 typedef struct re_moe re_moe;
