@@ -164,11 +164,14 @@ def time_dense(t, m, k, n, mode, launches, seed):
     s = hip.Stream()
     us = graph_time_us(s, lambda: q.matmul_dev(dx, n, dy, mode, stream=s), launches)
     flop = 2.0 * n * m * k
-    peak = BF16_PEAK_TFLOPS if mode == rehip.MODE_BF16 else F32_MFMA_PEAK_TFLOPS
+    # f32 mode from 16 rows: bf16 MFMAs on split operands (three per product, two for BF16 weights)
+    split = mode == rehip.MODE_F32 and n >= 16 and os.environ.get("REHIP_GEMM_SP", "1") != "0"
+    peak = BF16_PEAK_TFLOPS if mode == rehip.MODE_BF16 or split else F32_MFMA_PEAK_TFLOPS
+    mfma_flop = (2 if t == rehip.BF16 else 3) * flop if split else flop
     q.close()
     s.destroy()
     return {"type": rehip.TYPE_NAMES[t], "m": m, "k": k, "n": n, "mode": "bf16" if mode == rehip.MODE_BF16 else "f32",
-            "us": us, "tflops": flop / (us * 1e-6) / 1e12, "frac_mfma_peak": flop / (us * 1e-6) / 1e12 / peak}
+            "us": us, "tflops": flop / (us * 1e-6) / 1e12, "frac_mfma_peak": mfma_flop / (us * 1e-6) / 1e12 / peak}
 
 
 def moe_weights(seed):

@@ -817,7 +817,8 @@ int re_qmat_matmul_dev(re_qmat* q, const float* d_x, size_t rows, float* d_y, in
   if (rows == 0) return RE_OK;
   if (rows > (1u << 24)) return fail(RE_ERR_SIZE, "rows = %zu too large", rows);
   if (q->dense) {                        // below 16 rows f32 products in either mode (the reference's
-    // f32 matvec); from 16 rows the MFMA GEMM, bf16 operands in bf16 mode and f32 in f32 mode
+    // f32 matvec); from 16 rows the MFMA GEMM, bf16 operands in bf16 mode and split operands on
+    // bf16 MFMAs in f32 mode (REHIP_GEMM_SP=0: f32 MFMAs)
     if (rows > 65535u * 4u) return fail(RE_ERR_SIZE, "rows = %zu too large for dense weights", rows);
     const hipStream_t s = (hipStream_t)stream;
     int splits = 1;
@@ -833,7 +834,8 @@ int re_qmat_matmul_dev(re_qmat* q, const float* d_x, size_t rows, float* d_y, in
         else if (int rc = q->spart.ensure(need)) return rc;
       }
     }
-    HIP_TRY(launch_dense_gemm(q->g.type, q->d_w, d_x, d_y, (int)q->g.m, (int)q->g.n, (int)rows, nullptr, mode,
+    const int kmode = mode == RE_MODE_F32 && env_size("REHIP_GEMM_SP", 1) != 0 ? kGemmModeSplit : mode;
+    HIP_TRY(launch_dense_gemm(q->g.type, q->d_w, d_x, d_y, (int)q->g.m, (int)q->g.n, (int)rows, nullptr, kmode,
                               nullptr, splits > 1 ? (float*)q->spart.p : nullptr, splits, s));
     return RE_OK;
   }

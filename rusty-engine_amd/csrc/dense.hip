@@ -144,6 +144,19 @@ __device__ __forceinline__ void dense_loadx8(const float* x, int rows, int n, in
   v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
 }
 
+// the bf16 roundings of 8 values into hi and (LO) the bf16 roundings of their remainders into lo
+template <bool LO>
+__device__ __forceinline__ void dense_store8_split(__bf16* hi, __bf16* lo, const float (&v)[8]) {
+  bf16x8_t h, l;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    h[i] = (__bf16)v[i];
+    l[i] = (__bf16)(v[i] - (float)h[i]);
+  }
+  *reinterpret_cast<bf16x8_t*>(hi) = h;
+  if constexpr (LO) *reinterpret_cast<bf16x8_t*>(lo) = l;
+}
+
 template <bool F32>
 __device__ __forceinline__ void dense_store8(typename DenseLds<F32>::E* dst, const float (&v)[8]) {
   if constexpr (F32) {
@@ -157,7 +170,11 @@ __device__ __forceinline__ void dense_store8(typename DenseLds<F32>::E* dst, con
   }
 }
 
-template <uint32_t T, bool F32>
+// SP (f32 mode on bf16 MFMAs, split operands): the weights and activations are staged as their
+// bf16 roundings (hi) and, in a second plane, the bf16 roundings of what hi leaves (lo); each
+// product is w_hi x_hi + w_hi x_lo + w_lo x_hi, each term within 2^-16 relative (BF16 weights are
+// their own rounding: w_lo = 0, two MFMAs)
+template <uint32_t T, bool F32, bool SP = false>
 __global__ __launch_bounds__(256) void dense_mma_kernel(const typename DenseElem<T>::S* __restrict__ W,
                                                         const float* __restrict__ x, float* __restrict__ y, int m,
                                                         int n, int rows, const float* __restrict__ add,
@@ -165,8 +182,10 @@ __global__ __launch_bounds__(256) void dense_mma_kernel(const typename DenseElem
   using L = DenseLds<F32>;
   using E = typename L::E;
   constexpr int LD = L::LD;
-  __shared__ __attribute__((aligned(16))) E ws[kDenseBM * LD];
-  __shared__ __attribute__((aligned(16))) E xs[kDenseBN * LD];
+  static_assert(!(F32 && SP), "split operands run on bf16 MFMAs");
+  constexpr bool WLO = SP && T != 30;                  // the weights have a remainder (not BF16)
+  __shared__ __attribute__((aligned(16))) E ws[kDenseBM * LD * (WLO ? 2 : 1)];
+  __shared__ __attribute__((aligned(16))) E xs[kDenseBN * LD * (SP ? 2 : 1)];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave & 1, wn = wave >> 1;             // the wave's 32 weight rows / 32 activation rows
   const int m0 = blockIdx.x * kDenseBM, t0 = blockIdx.y * kDenseBN;
@@ -182,8 +201,13 @@ __global__ __launch_bounds__(256) void dense_mma_kernel(const typename DenseElem
 #pragma unroll
   for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
   for (int st = s0; st < s1; ++st) {
-    dense_store8<F32>(ws + sr * LD + sk, wv);
-    dense_store8<F32>(xs + sr * LD + sk, xv);
+    if constexpr (SP) {
+      dense_store8_split<WLO>(ws + sr * LD + sk, ws + kDenseBM * LD + sr * LD + sk, wv);
+      dense_store8_split<true>(xs + sr * LD + sk, xs + kDenseBN * LD + sr * LD + sk, xv);
+    } else {
+      dense_store8<F32>(ws + sr * LD + sk, wv);
+      dense_store8<F32>(xs + sr * LD + sk, xv);
+    }
     __syncthreads();
     if (st + 1 < s1) {                   // the next step's loads fly under this step's MFMAs
       dense_load8<T>(W, m, n, m0 + sr, (st + 1) * kDenseBK + sk, wv);
@@ -208,6 +232,14 @@ __global__ __launch_bounds__(256) void dense_mma_kernel(const typename DenseElem
         const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(wa + 16 * kk + 8 * (lane >> 5));
         const bf16x8_t b = *reinterpret_cast<const bf16x8_t*>(xb + 16 * kk + 8 * (lane >> 5));
         acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc, 0, 0, 0);
+        if constexpr (SP) {
+          const bf16x8_t bl = *reinterpret_cast<const bf16x8_t*>(xb + kDenseBN * LD + 16 * kk + 8 * (lane >> 5));
+          acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bl, acc, 0, 0, 0);
+          if constexpr (WLO) {
+            const bf16x8_t al = *reinterpret_cast<const bf16x8_t*>(wa + kDenseBM * LD + 16 * kk + 8 * (lane >> 5));
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, b, acc, 0, 0, 0);
+          }
+        }
       }
     }
     __syncthreads();                     // every wave is done reading the step
@@ -242,7 +274,10 @@ hipError_t launch_dense_t(const void* W, const float* x, float* y, int m, int n,
     splits = (steps + sps - 1) / sps;
     const dim3 grid((unsigned)((m + kDenseBM - 1) / kDenseBM), (unsigned)((rows + kDenseBN - 1) / kDenseBN),
                     (unsigned)splits);
-    if (mode == 1)
+    if (mode == kGemmModeSplit)
+      hipLaunchKernelGGL((dense_mma_kernel<T, false, true>), grid, dim3(256), 0, s, (const S*)W, x, y, m, n, rows,
+                         add, partial, sps);
+    else if (mode == 1)
       hipLaunchKernelGGL((dense_mma_kernel<T, true>), grid, dim3(256), 0, s, (const S*)W, x, y, m, n, rows, add,
                          partial, sps);
     else
