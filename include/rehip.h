@@ -41,8 +41,9 @@ extern "C" {
 #define RE_ERR_NODEV 5     /* no usable gfx950 device */
 
 #define RE_MODE_BF16 0     /* GEMM: bf16 MFMA, f32 accumulate (|err| <= 1e-2 rel-to-norm) */
-#define RE_MODE_F32 1      /* GEMM: f32-accurate mode (|err| <= 2^-10 sum|w*x|): quantized weights run bf16
-                              MFMAs on split operands (hi*hi + hi*lo + lo*hi), dense weights f32 MFMAs */
+#define RE_MODE_F32 1      /* GEMM: f32-accurate mode (|err| <= 2^-10 sum|w*x|): GEMMs run bf16 MFMAs on
+                              split operands (hi*hi + hi*lo + lo*hi; two MFMAs for BF16 weights, whose
+                              low part is zero); REHIP_GEMM_SP=0 keeps f32 MFMAs above 64 rows */
 
 typedef struct re_qmat re_qmat;
 typedef struct re_moe re_moe;
