@@ -49,12 +49,17 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs p) {
   const uint8_t* tbase = p.W + (size_t)tile * p.KB * B::SLAB;
   const int u_end = kb1 * NCH;
   const int u0 = kb0 * NCH + wave;
+  // ring loads go through a buffer resource over the tile: a chunk past the end reads at an
+  // offset past the resource (zeros, no memory traffic) instead of being skipped under a branch,
+  // which made the compiler wait for each load where the branch joins (one round trip per entry)
+  const __amdgpu_buffer_rsrc_t wr = make_rsrc(tbase, (uint32_t)p.KB * (uint32_t)B::SLAB);
+  auto load = [&](int u, typename B::CR& r) {
+    const uint32_t off = u < u_end ? (uint32_t)(u / NCH) * (uint32_t)B::SLAB : 0x80000000u;
+    B::bload_chunk(wr, off, lane, u % NCH, r);
+  };
   typename B::CR ring[D];
 #pragma unroll
-  for (int i = 0; i < D; ++i) {
-    const int u = u0 + i * WAVES;
-    if (u < u_end) B::load_chunk(tbase + (size_t)(u / NCH) * B::SLAB, lane, u % NCH, ring[i]);
-  }
+  for (int i = 0; i < D; ++i) load(u0 + i * WAVES, ring[i]);
 
   // stage this split's x (float4, zero past K) and its per-16 sums
   const int x0 = kb0 * B::QK;
@@ -100,7 +105,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs p) {
         Run a, b;
         B::decode_chunk(ring[i], c, a, b);
         const int un = u + D * WAVES;
-        if (un < u_end) B::load_chunk(tbase + (size_t)(un / NCH) * B::SLAB, lane, un % NCH, ring[i]);
+        if (un < u_end) load(un, ring[i]);
         const float* xb = xl + (kb - kb0) * B::QK;
         const float* xs = xs16 + (kb - kb0) * (B::QK / 16);
         const int valid = p.K - kb * B::QK;   // K is a multiple of 32: a run is wholly in or out
@@ -140,11 +145,13 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs p) {
 // over the lane groups with a fixed xor-shuffle tree, then over the waves in wave order
 // (deterministic). Row groups that share cache lines are given to the same XCD (workgroup w
 // runs on XCD w % 8).
-template <int T, int R, int WAVES>
+// ONE: every slot has at most one chunk (KB * NCH <= slots per workgroup, the usual case for
+// decode-sized matrices): a one-entry ring, no refill.
+template <int T, int R, int WAVES, bool ONE>
 __global__ __launch_bounds__(WAVES * 64) void gemv_rows_kernel(GemvArgs p) {
   using B = Blk<T>;
   constexpr int NCH = B::NCH;
-  constexpr int D = WAVES == 16 ? 2 : kGemvDepth;   // 16 waves: 128 VGPRs per lane
+  constexpr int D = ONE ? 1 : (WAVES == 16 ? 2 : kGemvDepth);   // 16 waves: 128 VGPRs per lane
   constexpr int G = 64 / R;              // lane groups per wave
   constexpr int S = WAVES * G;           // slots per workgroup
   // LDS: x[KB * QK] (zero past K), xs16[KB * QK / 16], red[WAVES * R], ssred[WAVES]
@@ -180,12 +187,16 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_rows_kernel(GemvArgs p) {
     if (p.norm_w) w0 = *reinterpret_cast<const float4*>(p.norm_w + 4 * threadIdx.x);
   }
   __builtin_amdgcn_sched_barrier(0);
+  // ring loads through a buffer resource over the tile, as in gemv_kernel: a slot past the end
+  // reads at an offset past the resource (no branch, one round trip for the whole ring)
+  const __amdgpu_buffer_rsrc_t wr = make_rsrc(tbase, (uint32_t)p.KB * (uint32_t)B::SLAB);
+  auto load = [&](int u, typename B::CR& r) {
+    const uint32_t off = u < u_end ? (uint32_t)(u / NCH) * (uint32_t)B::SLAB : 0x80000000u;
+    B::bload_chunk(wr, off, rr, u % NCH, r);
+  };
   typename B::CR ring[D];
 #pragma unroll
-  for (int i = 0; i < D; ++i) {
-    const int u = slot + i * S;
-    if (u < u_end) B::load_chunk(tbase + (size_t)(u / NCH) * B::SLAB, rr, u % NCH, ring[i]);
-  }
+  for (int i = 0; i < D; ++i) load(slot + i * S, ring[i]);
   __builtin_amdgcn_sched_barrier(0);
 
   // RMS-norm prologue: x * w is staged and the sum of squares kept per thread; the row's
@@ -231,7 +242,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_rows_kernel(GemvArgs p) {
         Run a, b;
         B::decode_chunk(ring[i], c, a, b);
         const int un = u + D * S;
-        if (un < u_end) B::load_chunk(tbase + (size_t)(un / NCH) * B::SLAB, rr, un % NCH, ring[i]);
+        if (!ONE && un < u_end) load(un, ring[i]);
         const float* xb = xl + kb * B::QK;
         const float* xs = xs16 + kb * (B::QK / 16);
         const int valid = p.K - kb * B::QK;   // K is a multiple of 32: a run is wholly in or out
@@ -491,17 +502,24 @@ __global__ __launch_bounds__(64) void dequant_kernel(const uint8_t* __restrict__
   }
 }
 
+template <int T, int R, bool ONE>
+static void launch_rows_w(const GemvArgs& a, int waves, unsigned grid, size_t lds, hipStream_t s) {
+  if (waves == 16) {
+    hipLaunchKernelGGL((gemv_rows_kernel<T, R, 16, ONE>), dim3(grid), dim3(1024), lds, s, a);
+  } else if (waves == 8) {
+    hipLaunchKernelGGL((gemv_rows_kernel<T, R, 8, ONE>), dim3(grid), dim3(512), lds, s, a);
+  } else {
+    hipLaunchKernelGGL((gemv_rows_kernel<T, R, 4, ONE>), dim3(grid), dim3(256), lds, s, a);
+  }
+}
+
 template <int T, int R>
 static hipError_t launch_rows(const GemvArgs& a, int waves, hipStream_t s) {
   const size_t lds = ((size_t)a.KB * Blk<T>::QK * 17 / 16 + 16 * R + 16) * sizeof(float);
   const unsigned grid = (unsigned)(((size_t)a.groups * (a.batch > 1 ? a.batch : 1) + 7) / 8 * 8);
-  if (waves == 16) {
-    hipLaunchKernelGGL((gemv_rows_kernel<T, R, 16>), dim3(grid), dim3(1024), lds, s, a);
-  } else if (waves == 8) {
-    hipLaunchKernelGGL((gemv_rows_kernel<T, R, 8>), dim3(grid), dim3(512), lds, s, a);
-  } else {
-    hipLaunchKernelGGL((gemv_rows_kernel<T, R, 4>), dim3(grid), dim3(256), lds, s, a);
-  }
+  const int w = waves == 16 || waves == 8 ? waves : 4;
+  if ((size_t)a.KB * Blk<T>::NCH <= (size_t)w * 64 / R) launch_rows_w<T, R, true>(a, w, grid, lds, s);
+  else launch_rows_w<T, R, false>(a, w, grid, lds, s);
   return hipGetLastError();
 }
 

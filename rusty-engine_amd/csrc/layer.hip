@@ -79,15 +79,48 @@ __global__ __launch_bounds__(256) void kv_append_kernel(const float* __restrict_
 // Cache rows past the last visible one are never read (loads clamp to it), so rows of the cache
 // that were never written do not enter the result.
 
+// v of lane (lane ^ OFF) without the LDS pipe: v_permlane32_swap / v_permlane16_swap exchange
+// 32- / 16-lane halves (each returns both halves; the lane keeps the one that came from its
+// partner), DPP row moves do the rest (row_ror:8 = xor 8 within a 16-lane row, quad_perm
+// [3,2,1,0] then row_half_mirror = xor 4, quad_perm [2,3,0,1] / [1,0,3,2] = xor 2 / xor 1).
+// The pairs are those of __shfl_xor(v, OFF, 64), so a butterfly over them keeps its bits.
+template <int OFF>
+__device__ __forceinline__ float lane_xor(float v) {
+  const int u = __float_as_int(v);
+  if constexpr (OFF == 32) {
+    const auto s = __builtin_amdgcn_permlane32_swap((unsigned)u, (unsigned)u, false, false);
+    return __uint_as_float((threadIdx.x & 32) ? s[0] : s[1]);
+  } else if constexpr (OFF == 16) {
+    const auto s = __builtin_amdgcn_permlane16_swap((unsigned)u, (unsigned)u, false, false);
+    return __uint_as_float((threadIdx.x & 16) ? s[0] : s[1]);
+  } else if constexpr (OFF == 8) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, u, 0x128, 0xF, 0xF, false));
+  } else if constexpr (OFF == 4) {
+    const int r = __builtin_amdgcn_update_dpp(0, u, 0x1B, 0xF, 0xF, false);
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, r, 0x141, 0xF, 0xF, false));
+  } else if constexpr (OFF == 2) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, u, 0x4E, 0xF, 0xF, false));
+  } else {
+    static_assert(OFF == 1, "lane_xor: OFF is a power of two up to 32");
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, u, 0xB1, 0xF, 0xF, false));
+  }
+}
+// butterfly max / sum over the wave (every lane ends with the result), pairs xor 32, 16, .., 1
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-  return v;
+  v = fmaxf(v, lane_xor<32>(v));
+  v = fmaxf(v, lane_xor<16>(v));
+  v = fmaxf(v, lane_xor<8>(v));
+  v = fmaxf(v, lane_xor<4>(v));
+  v = fmaxf(v, lane_xor<2>(v));
+  return fmaxf(v, lane_xor<1>(v));
 }
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
+  v += lane_xor<32>(v);
+  v += lane_xor<16>(v);
+  v += lane_xor<8>(v);
+  v += lane_xor<4>(v);
+  v += lane_xor<2>(v);
+  return v + lane_xor<1>(v);
 }
 
 // Few rows (decode), or head sizes other than 64: one 1024-thread workgroup per (query head,
