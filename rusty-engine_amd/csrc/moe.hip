@@ -615,11 +615,11 @@ hipError_t launch_combine(const float* yp, const int* pos, const float* w, float
 // is read once per task. DUAL: the gate and up matrices are read side by side and the task
 // writes silu(gate) * up (SwiGLU, moe.rs:280-283) directly. Sums fold over lane groups by a
 // fixed xor tree and over waves in wave order (deterministic).
-template <int T, int R, int WAVES, int NB, bool DUAL>
+template <int T, int R, int WAVES, int NB, bool DUAL, bool ONE>
 __global__ __launch_bounds__(WAVES * 64) void moe_gemv_kernel(MoeGemvArgs a) {
   using B = Blk<T>;
   constexpr int NCH = B::NCH;
-  constexpr int D = 2;                   // units in flight per slot
+  constexpr int D = ONE ? 1 : 2;         // units in flight per slot (ONE: a slot has at most one)
   constexpr int G = 64 / R;
   constexpr int S = WAVES * G;
   constexpr int NM = DUAL ? 2 : 1;
@@ -644,13 +644,25 @@ __global__ __launch_bounds__(WAVES * 64) void moe_gemv_kernel(MoeGemvArgs a) {
   float* red = xs16 + NB * (KP / 16);    // [WAVES][NM][NB][R]
   float* ssred = red + WAVES * NM * NB * R;   // [WAVES][NB]
 
-  const int row = task.row0 + (lane % R);          // weight row inside the expert
-  const int tile = row >> 6, rr = row & 63;
-  const size_t wofs = (size_t)task.expert * a.w_stride + (size_t)tile * a.KB * B::SLAB;
-  const uint8_t* t0 = a.W0 + wofs;
-  const uint8_t* t1 = DUAL ? a.W1 + wofs : nullptr;
+  // the task's R rows lie in one 64-row tile (row0 is a multiple of R, R divides 64), so the
+  // tile and the weight resources are uniform
+  const int row0 = __builtin_amdgcn_readfirstlane(task.row0);
+  const int expert = __builtin_amdgcn_readfirstlane(task.expert);
+  const int tile = row0 >> 6, rr = (row0 & 63) + (lane % R);
+  const size_t wofs = (size_t)expert * a.w_stride + (size_t)tile * a.KB * B::SLAB;
+  const uint32_t tbytes = (uint32_t)a.KB * (uint32_t)B::SLAB;
+  const __amdgpu_buffer_rsrc_t w0r = make_rsrc(a.W0 + wofs, tbytes);
+  const __amdgpu_buffer_rsrc_t w1r = make_rsrc(DUAL ? a.W1 + wofs : a.W0 + wofs, tbytes);
   const int slot = wave * G + lane / R;
   const int u_end = a.KB * NCH;
+  // a chunk past the end reads at an offset past the resource (zeros, no memory traffic): the
+  // ring's first loads need no branch, which made the compiler wait for each load where the
+  // branch joins (one memory round trip per entry)
+  auto load = [&](int u, typename B::CR& r0, typename B::CR& r1) {
+    const uint32_t off = u < u_end ? (uint32_t)(u / NCH) * (uint32_t)B::SLAB : 0x80000000u;
+    B::bload_chunk(w0r, off, rr, u % NCH, r0);
+    if constexpr (DUAL) B::bload_chunk(w1r, off, rr, u % NCH, r1);
+  };
 
   // this thread's first activation (and norm weight) goes out before the weight loads: loads
   // retire in order, so the staging below then waits for it alone and overlaps the weights'
@@ -669,13 +681,7 @@ __global__ __launch_bounds__(WAVES * 64) void moe_gemv_kernel(MoeGemvArgs a) {
   __builtin_amdgcn_sched_barrier(0);
   typename B::CR ring0[D], ring1[D];
 #pragma unroll
-  for (int i = 0; i < D; ++i) {
-    const int u = slot + i * S;
-    if (u < u_end) {
-      B::load_chunk(t0 + (size_t)(u / NCH) * B::SLAB, rr, u % NCH, ring0[i]);
-      if constexpr (DUAL) B::load_chunk(t1 + (size_t)(u / NCH) * B::SLAB, rr, u % NCH, ring1[i]);
-    }
-  }
+  for (int i = 0; i < D; ++i) load(slot + i * S, ring0[i], ring1[i]);
   __builtin_amdgcn_sched_barrier(0);
 
   // stage the task's activation rows (zero past K and past np); with an RMS-norm, x * w is
@@ -729,10 +735,7 @@ __global__ __launch_bounds__(WAVES * 64) void moe_gemv_kernel(MoeGemvArgs a) {
         B::decode_chunk(ring0[i], c, a0, b0);
         if constexpr (DUAL) B::decode_chunk(ring1[i], c, a1, b1);
         const int un = u + D * S;
-        if (un < u_end) {
-          B::load_chunk(t0 + (size_t)(un / NCH) * B::SLAB, rr, un % NCH, ring0[i]);
-          if constexpr (DUAL) B::load_chunk(t1 + (size_t)(un / NCH) * B::SLAB, rr, un % NCH, ring1[i]);
-        }
+        if (!ONE && un < u_end) load(un, ring0[i], ring1[i]);
         const int valid = a.K - kb * B::QK;   // K is a multiple of 32: a run is wholly in or out
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
@@ -1002,7 +1005,10 @@ template <int T, bool DUAL, int NB, int R = kMoeGemvRows, int W = kMoeGemvWaves>
 static hipError_t launch_moe_gemv_nb(const MoeGemvArgs& a, int ntasks, hipStream_t s) {
   const int KP = a.KB * Blk<T>::QK;
   const size_t lds = ((size_t)NB * KP * 17 / 16 + (size_t)W * (DUAL ? 2 : 1) * NB * R + (size_t)W * NB) * sizeof(float);
-  hipLaunchKernelGGL((moe_gemv_kernel<T, R, W, NB, DUAL>), dim3((unsigned)ntasks), dim3(W * 64), lds, s, a);
+  if ((size_t)a.KB * Blk<T>::NCH <= (size_t)W * 64 / R)
+    hipLaunchKernelGGL((moe_gemv_kernel<T, R, W, NB, DUAL, true>), dim3((unsigned)ntasks), dim3(W * 64), lds, s, a);
+  else
+    hipLaunchKernelGGL((moe_gemv_kernel<T, R, W, NB, DUAL, false>), dim3((unsigned)ntasks), dim3(W * 64), lds, s, a);
   return hipGetLastError();
 }
 
