@@ -862,11 +862,11 @@ __global__ __launch_bounds__(WAVES * 64) void moe_down_combine_kernel(MoeDownCom
   typename B::CR ring[D];
 #pragma unroll
   for (int i = 0; i < D; ++i) {
-    const int u = slot + i * S;
-    if (u < u_end) {
-      const int j = u / u_pair, c = u - j * u_pair;
-      B::load_chunk(base_of(j) + (size_t)(c / NCH) * B::SLAB, rr, c % NCH, ring[i]);
-    }
+    // unconditional (a slot past the end reloads the last unit, never used): a load under a
+    // branch made the compiler wait for it where the branch joins, one round trip per entry
+    const int u = min(slot + i * S, u_end - 1);
+    const int j = u / u_pair, c = u - j * u_pair;
+    B::load_chunk(base_of(j) + (size_t)(c / NCH) * B::SLAB, rr, c % NCH, ring[i]);
   }
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
