@@ -409,14 +409,17 @@ template <> struct Blk<T_Q6_K> {
     r.t0 = sld2(rs, lane * 2, soff + 1024 * 13);
     r.t1 = 0;
   }
-  // the planes chunks 4H .. 4H + 3 read (their ql planes, qh planes 8 + 2H and 9 + 2H, sc, d)
+  // the planes chunks 4H .. 4H + 3 read (sc, d, then their ql planes and qh planes 8 + 2H and
+  // 9 + 2H). The scales go first: loads complete in order, and the compiler converts d as soon as
+  // it can, so a d issued last made that conversion wait for the whole half.
   template <int H> __device__ static void sload_half(__amdgpu_buffer_rsrc_t rs, uint32_t soff, int lane, R& r) {
+    r.p[12] = sld16(rs, lane * 16, soff + 1024 * 12);
+    r.t0 = sld2(rs, lane * 2, soff + 1024 * 13);
+    __builtin_amdgcn_sched_barrier(0);   // keeps the scale loads ahead of the planes
 #pragma unroll
     for (int j = 0; j < 4; ++j) r.p[4 * H + j] = sld16(rs, lane * 16, soff + 1024 * (4 * H + j));
     r.p[8 + 2 * H] = sld16(rs, lane * 16, soff + 1024 * (8 + 2 * H));
     r.p[9 + 2 * H] = sld16(rs, lane * 16, soff + 1024 * (9 + 2 * H));
-    r.p[12] = sld16(rs, lane * 16, soff + 1024 * 12);
-    r.t0 = sld2(rs, lane * 2, soff + 1024 * 13);
   }
   __device__ static void decode(const R& r, int c, Run& a, Run& b) {
     dec(r.p[c], r.p[8 + 2 * (c >> 2) + (c & 1)], r.p[12], r.t0, c, a, b);

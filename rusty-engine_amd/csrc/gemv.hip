@@ -16,6 +16,8 @@
 // cheaper on gfx950 than an agent-scope release per workgroup (an L2 write-back).
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "deq.hpp"
 #include "kernels.hpp"
 
@@ -391,10 +393,14 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_tile_kernel(GemvArgs p) {
   if constexpr (B::NCH == 8 && HALF) {
     // super-blocks: the pipeline runs on half blocks (chunks 0-3 / 4-7), so one block's worth
     // of registers keeps the next half in flight
-#pragma unroll 1
-    for (int st = wave; st < nsteps; st += WAVES) {
+    // one step: its second half loads while the first is consumed, then (PF) the next step's
+    // first half while the second is. The last step runs as a copy without the prefetch: with
+    // the prefetch under a branch, the two paths left different loads outstanding and the
+    // compiler waited for all of them (the prefetch included) before the second half.
+    auto half_step = [&](int st, auto pf) {
       const uint32_t so = (uint32_t)(st * B::SLAB);
       B::template sload_half<1>(rs, so, lane, r1[0]);
+      __builtin_amdgcn_sched_barrier(0);   // the loads go out before any of the first half's decode
       const float* xb = xl + st * B::QK;
       const float* xs = xs16 + st * (B::QK / 16);
 #pragma unroll
@@ -405,7 +411,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_tile_kernel(GemvArgs p) {
         acc += run_dot<T>(a, xb + z, xs + z);
         acc += run_dot<T>(b, xb + z, xs + z);
       }
-      if (st + WAVES < nsteps) B::template sload_half<0>(rs, (uint32_t)((st + WAVES) * B::SLAB), lane, r0[0]);
+      if constexpr (decltype(pf)::value) B::template sload_half<0>(rs, (uint32_t)((st + WAVES) * B::SLAB), lane, r0[0]);
 #pragma unroll
       for (int c = 4; c < 8; ++c) {
         Run a, b;
@@ -414,7 +420,11 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_tile_kernel(GemvArgs p) {
         acc += run_dot<T>(a, xb + z, xs + z);
         acc += run_dot<T>(b, xb + z, xs + z);
       }
-    }
+    };
+    int st = wave;
+#pragma unroll 1
+    for (; st + WAVES < nsteps; st += WAVES) half_step(st, std::true_type{});
+    if (st < nsteps) half_step(st, std::false_type{});
   } else {
     for (int st = wave; st < nsteps; st += 2 * WAVES) {
       if (st + WAVES < nsteps) load_step(st + WAVES, r1);
