@@ -426,12 +426,23 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_tile_kernel(GemvArgs p) {
     for (; st + WAVES < nsteps; st += WAVES) half_step(st, std::true_type{});
     if (st < nsteps) half_step(st, std::false_type{});
   } else {
-    for (int st = wave; st < nsteps; st += 2 * WAVES) {
-      if (st + WAVES < nsteps) load_step(st + WAVES, r1);
+    // steady state while both prefetches exist (unconditional: a prefetch under a branch left
+    // the two paths with different loads outstanding, and the compiler then waited for all of
+    // them, the prefetch included, inside the current step), then the last one or two steps
+    int st = wave;
+#pragma unroll 1
+    for (; st + 2 * WAVES < nsteps; st += 2 * WAVES) {
+      load_step(st + WAVES, r1);
       step(st, r0);
-      if (st + WAVES >= nsteps) break;
-      if (st + 2 * WAVES < nsteps) load_step(st + 2 * WAVES, r0);
+      load_step(st + 2 * WAVES, r0);
       step(st + WAVES, r1);
+    }
+    if (st + WAVES < nsteps) {
+      load_step(st + WAVES, r1);
+      step(st, r0);
+      step(st + WAVES, r1);
+    } else if (st < nsteps) {
+      step(st, r0);
     }
   }
 
