@@ -345,7 +345,10 @@ __device__ __forceinline__ float4 add4(float4 a, float4 b) { return make_float4(
 // TAB (with QKV, hd % 8 == 0, dq.rope given): each lane rotates its own dims of q, and the team
 // holding the new key those of k, in registers with the table's (cos, sin); no LDS pass or barrier
 // comes before the scores.
-template <int NC, bool QKV, bool TAB = false>   // kc / vc are not __restrict__: with QKV the new row is stored through dq
+// FULL: hd == 64 NC, so every lane's dims are inside the head and the K/V loads need no guard (a
+// guarded load is a branch, and the compiler then waited for every K load before issuing the V
+// loads: two memory round trips instead of one)
+template <int NC, bool QKV, bool TAB = false, bool FULL = false>   // kc / vc are not __restrict__: with QKV the new row is stored through dq
 __global__ __launch_bounds__(256) void attention_split_kernel(const float* __restrict__ q, const float* kc,
                                                               const float* vc, int heads, int kv_heads,
                                                               int hd, int max_seq, const int* __restrict__ pos,
@@ -377,6 +380,29 @@ __global__ __launch_bounds__(256) void attention_split_kernel(const float* __res
   const bool has_new = QKV && p0 >= 0 && p0 < max_seq && p0 >= j0 && p0 < j0 + jn;
   const int half = hd >> 1, t = threadIdx.x;
   float qx0 = 0.0f, qx1 = 0.0f, kx0 = 0.0f, kx1 = 0.0f, vx = 0.0f;
+  // keys j0 + 16 u + team, u < U: all loads of K and V issued first, ahead of the epilogue's
+  // (whose bias and table loads sit under branches, after which the compiler waits for every
+  // load issued so far: issued later, K and V took a second memory round trip). With QKV the new
+  // key's row, not yet written, is replaced after the epilogue.
+  float4 kv[U][NC], vv[U][NC];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const size_t row = (size_t)(j0 + min(16 * u + team, jn - 1)) * kv_dim;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int d = 4 * tl + 64 * c;
+      kv[u][c] = FULL || d < hd ? *reinterpret_cast<const float4*>(kbase + row + d) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const size_t row = (size_t)(j0 + min(16 * u + team, jn - 1)) * kv_dim;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int d = 4 * tl + 64 * c;
+      vv[u][c] = FULL || d < hd ? *reinterpret_cast<const float4*>(vbase + row + d) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  }
   // TAB: raw q of this lane's dims and their partners (biased), the new key's and value's (every
   // team of the split holding key p0: teams past the split's last key, jn - 1, read that row too),
   // and the (cos, sin) of their pairs
@@ -384,42 +410,58 @@ __global__ __launch_bounds__(256) void attention_split_kernel(const float* __res
   const bool newteam = TAB && has_new;
   if constexpr (TAB) {
     const bool from_tab = p0 >= 0 && p0 < dq.rope_rows;
+    const int prow = from_tab ? p0 : 0;  // a position past the table reads row 0 (not used)
+    const float* qr = q + (size_t)h * hd;
+    const float* kr = dq.ks + (size_t)kvh * hd;
+    const float* vr = dq.vs + (size_t)kvh * hd;
+    // an absent bias reads its row instead (readable; the values are not used)
+    const float* bqr = dq.bq ? dq.bq + (size_t)h * hd : qr;
+    const float* bkr = dq.bk ? dq.bk + (size_t)kvh * hd : kr;
+    const float* bvr = dq.bv ? dq.bv + (size_t)kvh * hd : vr;
+    float4 bq0[NC], bq1[NC], bk0[NC], bk1[NC], bv0[NC];
+    // every load first and none under a branch: after a branch the compiler waited for all the
+    // loads issued so far, one memory round trip per branch
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
       const int d = 4 * tl + 64 * c;
       const int dd = d < hd ? d : 0;
       const bool lo = dd < half;
       const int dp = lo ? dd + half : dd - half, i0 = lo ? dd : dd - half;
-      const float* qr = q + (size_t)h * hd;
       tq[c] = *reinterpret_cast<const float4*>(qr + dd);
       tqp[c] = *reinterpret_cast<const float4*>(qr + dp);
+      bq0[c] = *reinterpret_cast<const float4*>(bqr + dd);
+      bq1[c] = *reinterpret_cast<const float4*>(bqr + dp);
+      const float2* cs = dq.rope + (size_t)prow * half + i0;
+      tc0[c] = *reinterpret_cast<const float4*>(cs);
+      tc1[c] = *reinterpret_cast<const float4*>(cs + 2);
+      tk[c] = *reinterpret_cast<const float4*>(kr + dd);
+      tkp[c] = *reinterpret_cast<const float4*>(kr + dp);
+      tv[c] = *reinterpret_cast<const float4*>(vr + dd);
+      bk0[c] = *reinterpret_cast<const float4*>(bkr + dd);
+      bk1[c] = *reinterpret_cast<const float4*>(bkr + dp);
+      bv0[c] = *reinterpret_cast<const float4*>(bvr + dd);
+    }
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
       if (dq.bq) {
-        tq[c] = add4(tq[c], *reinterpret_cast<const float4*>(dq.bq + (size_t)h * hd + dd));
-        tqp[c] = add4(tqp[c], *reinterpret_cast<const float4*>(dq.bq + (size_t)h * hd + dp));
+        tq[c] = add4(tq[c], bq0[c]);
+        tqp[c] = add4(tqp[c], bq1[c]);
       }
-      if (from_tab) {
-        const float2* cs = dq.rope + (size_t)p0 * half + i0;
-        tc0[c] = *reinterpret_cast<const float4*>(cs);
-        tc1[c] = *reinterpret_cast<const float4*>(cs + 2);
-      } else {                           // a position past the table: computed here
+      if (!from_tab) {                   // a position past the table: computed here
+        const int d = 4 * tl + 64 * c;
+        const int dd = d < hd ? d : 0;
+        const int i0 = dd < half ? dd : dd - half;
         float cv[4], sv[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) rope_cs(i0 + j, hd, p0, dq.base, cv[j], sv[j]);
         tc0[c] = make_float4(cv[0], sv[0], cv[1], sv[1]);
         tc1[c] = make_float4(cv[2], sv[2], cv[3], sv[3]);
       }
-      if (newteam) {
-        const float* kr = dq.ks + (size_t)kvh * hd;
-        const float* vr = dq.vs + (size_t)kvh * hd;
-        tk[c] = *reinterpret_cast<const float4*>(kr + dd);
-        tkp[c] = *reinterpret_cast<const float4*>(kr + dp);
-        tv[c] = *reinterpret_cast<const float4*>(vr + dd);
-        if (dq.bk) {
-          tk[c] = add4(tk[c], *reinterpret_cast<const float4*>(dq.bk + (size_t)kvh * hd + dd));
-          tkp[c] = add4(tkp[c], *reinterpret_cast<const float4*>(dq.bk + (size_t)kvh * hd + dp));
-        }
-        if (dq.bv) tv[c] = add4(tv[c], *reinterpret_cast<const float4*>(dq.bv + (size_t)kvh * hd + dd));
+      if (dq.bk) {                       // (the new key and value are used by the new team only)
+        tk[c] = add4(tk[c], bk0[c]);
+        tkp[c] = add4(tkp[c], bk1[c]);
       }
+      if (dq.bv) tv[c] = add4(tv[c], bv0[c]);
     }
   } else if constexpr (QKV) {
     if (t < half) {
@@ -441,27 +483,6 @@ __global__ __launch_bounds__(256) void attention_split_kernel(const float* __res
       }
     }
     if (has_new && t < hd) vx = dq.bv ? dq.vs[(size_t)kvh * hd + t] + dq.bv[(size_t)kvh * hd + t] : dq.vs[(size_t)kvh * hd + t];
-  }
-  // keys j0 + 16 u + team, u < U: all loads of K and V issued up front (V lands under the scores;
-  // with QKV the new key's row, not yet written, is replaced after the epilogue)
-  float4 kv[U][NC], vv[U][NC];
-#pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const size_t row = (size_t)(j0 + min(16 * u + team, jn - 1)) * kv_dim;
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      const int d = 4 * tl + 64 * c;
-      kv[u][c] = d < hd ? *reinterpret_cast<const float4*>(kbase + row + d) : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-  }
-#pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const size_t row = (size_t)(j0 + min(16 * u + team, jn - 1)) * kv_dim;
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      const int d = 4 * tl + 64 * c;
-      vv[u][c] = d < hd ? *reinterpret_cast<const float4*>(vbase + row + d) : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
   }
   float4 qv[NC];
   if constexpr (TAB) {
@@ -987,7 +1008,10 @@ hipError_t launch_attention_decode(const float* q, const float* k, const float* 
   const DecodeQkv dq{k, v, bq, bk, bv, base, kc, vc, reinterpret_cast<const float2*>(rope), max_seq};
   auto a16 = [](const void* x) { return ((uintptr_t)x & 15) == 0; };   // null passes
   if (rope && hd % 8 == 0 && a16(rope) && a16(q) && a16(k) && a16(v) && a16(bq) && a16(bk) && a16(bv)) {
-    if (hd <= 64)
+    if (hd == 64)
+      hipLaunchKernelGGL((attention_split_kernel<1, true, true, true>), grid, dim3(256), 0, s, q, kc, vc, heads,
+                         kv_heads, hd, max_seq, pos, work, dq);
+    else if (hd <= 64)
       hipLaunchKernelGGL((attention_split_kernel<1, true, true>), grid, dim3(256), 0, s, q, kc, vc, heads, kv_heads,
                          hd, max_seq, pos, work, dq);
     else if (hd <= 128)
