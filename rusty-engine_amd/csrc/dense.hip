@@ -67,11 +67,27 @@ __global__ __launch_bounds__(256) void dense_gemm_kernel(const typename DenseEle
   float acc[TT];
 #pragma unroll
   for (int t = 0; t < TT; ++t) acc[t] = 0.0f;
-  for (int k = lane; k < n; k += 64) {
-    const float w = DenseElem<T>::get(wr[k]);
+  // U of the lane's k at a time: their weight and activation loads go out together (a loop that
+  // loads and multiplies one k at a time waits a memory round trip per k), then the FMAs in the
+  // same ascending-k order, so the sums keep their bits. Activation rows past nt read row nt - 1
+  // (their sums are not stored).
+  // A k past the row loads index n - 1 and skips its FMAs (a branch around arithmetic only).
+  constexpr int U = TT >= 16 ? 2 : TT >= 4 ? 4 : 8;
+  for (int k = lane; k < n; k += 64 * U) {
+    float w[U], xv[U][TT];
 #pragma unroll
-    for (int t = 0; t < TT; ++t)
-      if (t < nt) acc[t] = __builtin_fmaf(w, x[(size_t)(t0 + t) * n + k], acc[t]);
+    for (int j = 0; j < U; ++j) w[j] = DenseElem<T>::get(wr[min(k + 64 * j, n - 1)]);
+#pragma unroll
+    for (int j = 0; j < U; ++j)
+#pragma unroll
+      for (int t = 0; t < TT; ++t) xv[j][t] = x[(size_t)(t0 + min(t, nt - 1)) * n + min(k + 64 * j, n - 1)];
+#pragma unroll
+    for (int j = 0; j < U; ++j) {
+      if (k + 64 * j < n) {
+#pragma unroll
+        for (int t = 0; t < TT; ++t) acc[t] = __builtin_fmaf(w[j], xv[j][t], acc[t]);
+      }
+    }
   }
 #pragma unroll
   for (int t = 0; t < TT; ++t) acc[t] = wave_sum_xor(acc[t]);
