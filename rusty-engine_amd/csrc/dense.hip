@@ -160,6 +160,36 @@ __device__ __forceinline__ void dense_loadx8(const float* x, int rows, int n, in
   v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
 }
 
+// 8 raw elements through a buffer resource (F32: two 16-byte loads, F16/BF16: one); an offset past
+// the resource reads zeros, so the tile edges need no branch
+struct DenseRaw { i32x4_t a, b; };
+template <uint32_t T>
+__device__ __forceinline__ DenseRaw dense_bload8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  DenseRaw v;
+  v.a = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+  if constexpr (T == 0) v.b = __builtin_amdgcn_raw_buffer_load_b128(r, (int)(off + 16u), 0, 0);
+  else v.b = i32x4_t{0, 0, 0, 0};
+  return v;
+}
+// the 8 elements widened exactly to f32
+template <uint32_t T>
+__device__ __forceinline__ void dense_widen8(const DenseRaw& u, float (&v)[8]) {
+  if constexpr (T == 0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[i] = __int_as_float(u.a[i]);
+      v[4 + i] = __int_as_float(u.b[i]);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t w = (uint32_t)u.a[i];
+      v[2 * i] = DenseElem<T>::get((uint16_t)(w & 0xFFFFu));
+      v[2 * i + 1] = DenseElem<T>::get((uint16_t)(w >> 16));
+    }
+  }
+}
+
 // the bf16 roundings of 8 values into hi and (LO) the bf16 roundings of their remainders into lo
 template <bool LO>
 __device__ __forceinline__ void dense_store8_split(__bf16* hi, __bf16* lo, const float (&v)[8]) {
@@ -210,13 +240,27 @@ __global__ __launch_bounds__(256) void dense_mma_kernel(const typename DenseElem
   const int s0 = blockIdx.z * steps_per_split, s1 = min(steps_all, s0 + steps_per_split);
   // staging: thread t takes row t / 4 of both tiles, elements 8 (t % 4) .. + 7 of the step
   const int sr = tid >> 2, sk = 8 * (tid & 3);
-  float wv[8], xv[8];
-  dense_load8<T>(W, m, n, m0 + sr, s0 * kDenseBK + sk, wv);
-  dense_loadx8(x, rows, n, t0 + sr, s0 * kDenseBK + sk, xv);
+  // buffer resources over the workgroup's weight rows and activation rows: a row past the matrix
+  // lies past the resource, a k past the row (or past the split) takes an offset past it, so
+  // every load is unconditional. Loaded under branches, the next step's loads had been waited for
+  // right away (the compiler copied them where the branches join), before this step's MFMAs.
+  using S = typename DenseElem<T>::S;
+  const int wrows = min(kDenseBM, m - m0), xrows = min(kDenseBN, rows - t0);
+  const __amdgpu_buffer_rsrc_t wrs = make_rsrc(W + (size_t)m0 * n, (uint32_t)((size_t)wrows * n * sizeof(S)));
+  const __amdgpu_buffer_rsrc_t xrs = make_rsrc(x + (size_t)t0 * n, (uint32_t)((size_t)xrows * n * sizeof(float)));
+  auto off = [&](int st, uint32_t es) -> uint32_t {
+    const int k0 = st * kDenseBK + sk;
+    return st < s1 && k0 < n ? ((uint32_t)sr * (uint32_t)n + (uint32_t)k0) * es : 0x80000000u;
+  };
+  DenseRaw wraw = dense_bload8<T>(wrs, off(s0, sizeof(S)));
+  DenseRaw xraw = dense_bload8<0>(xrs, off(s0, sizeof(float)));
   f32x16_t acc;
 #pragma unroll
   for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
   for (int st = s0; st < s1; ++st) {
+    float wv[8], xv[8];
+    dense_widen8<T>(wraw, wv);
+    dense_widen8<0>(xraw, xv);
     if constexpr (SP) {
       dense_store8_split<WLO>(ws + sr * LD + sk, ws + kDenseBM * LD + sr * LD + sk, wv);
       dense_store8_split<true>(xs + sr * LD + sk, xs + kDenseBN * LD + sr * LD + sk, xv);
@@ -225,10 +269,8 @@ __global__ __launch_bounds__(256) void dense_mma_kernel(const typename DenseElem
       dense_store8<F32>(xs + sr * LD + sk, xv);
     }
     __syncthreads();
-    if (st + 1 < s1) {                   // the next step's loads fly under this step's MFMAs
-      dense_load8<T>(W, m, n, m0 + sr, (st + 1) * kDenseBK + sk, wv);
-      dense_loadx8(x, rows, n, t0 + sr, (st + 1) * kDenseBK + sk, xv);
-    }
+    wraw = dense_bload8<T>(wrs, off(st + 1, sizeof(S)));     // the next step's loads fly under this
+    xraw = dense_bload8<0>(xrs, off(st + 1, sizeof(float)));  // step's MFMAs (past s1: zeros)
     const E* wa = ws + (32 * wm + (lane & 31)) * LD;
     const E* xb = xs + (32 * wn + (lane & 31)) * LD;
     if constexpr (F32) {
