@@ -516,13 +516,31 @@ __global__ __launch_bounds__(256) void moe_router_tile_kernel(const float* __res
 #pragma unroll
   for (int t = 0; t < TT; ++t) acc[0][t] = acc[1][t] = 0.0f;
   const int nv = hidden / 4;
-  for (int v = lane; v < nv; v += 64) {
-    const float4 a = w0[v], b = w1[v];
+  // U of the lane's float4 at a time: their loads go out together, then the FMAs in the same
+  // order (one float4 at a time waited an L2 round trip per step); past the row a lane loads the
+  // last float4 and skips its FMAs
+  constexpr int U = TT == 1 ? 8 : 4;
+  for (int v0 = lane; v0 < nv; v0 += 64 * U) {
+    float4 a[U], b[U], q[U][TT];
 #pragma unroll
-    for (int t = 0; t < TT; ++t) {
-      const float4 q = xr[t][v];
-      acc[0][t] = __builtin_fmaf(a.w, q.w, __builtin_fmaf(a.z, q.z, __builtin_fmaf(a.y, q.y, __builtin_fmaf(a.x, q.x, acc[0][t]))));
-      acc[1][t] = __builtin_fmaf(b.w, q.w, __builtin_fmaf(b.z, q.z, __builtin_fmaf(b.y, q.y, __builtin_fmaf(b.x, q.x, acc[1][t]))));
+    for (int j = 0; j < U; ++j) {
+      const int v = min(v0 + 64 * j, nv - 1);
+      a[j] = w0[v];
+      b[j] = w1[v];
+#pragma unroll
+      for (int t = 0; t < TT; ++t) q[j][t] = xr[t][v];
+    }
+#pragma unroll
+    for (int j = 0; j < U; ++j) {
+      if (v0 + 64 * j < nv) {
+#pragma unroll
+        for (int t = 0; t < TT; ++t) {
+          acc[0][t] = __builtin_fmaf(a[j].w, q[j][t].w, __builtin_fmaf(a[j].z, q[j][t].z,
+                      __builtin_fmaf(a[j].y, q[j][t].y, __builtin_fmaf(a[j].x, q[j][t].x, acc[0][t]))));
+          acc[1][t] = __builtin_fmaf(b[j].w, q[j][t].w, __builtin_fmaf(b[j].z, q[j][t].z,
+                      __builtin_fmaf(b[j].y, q[j][t].y, __builtin_fmaf(b[j].x, q[j][t].x, acc[1][t]))));
+        }
+      }
     }
   }
 #pragma unroll
